@@ -1,0 +1,197 @@
+"""Benchmark of the DSA hot path on one MI355X.
+
+Headline (``value``): lightning_indexer (score + stable top-k) rows/s on
+BASELINE config 2 -- BSND 1x8192, 64 indexer heads, D=128, top-k 2048, causal.
+One step = one lightning_indexer call over the whole 8192-row batch, inputs
+resident in HBM. The same JSON line carries:
+  roofline      -- the indexer score kernel (dominant) against bf16 dense MFMA peak,
+                   timed with HIP events on the launch stream;
+  cpu_baseline  -- the numpy oracle (a port of the reference golden) on a stride
+                   sample of the same rows, timed on this host;
+  breakdown     -- top-k kernel, SFA prefill (config 3), SFA paged decode (config 4),
+                   the TND indexer->SFA pipeline (config 5) and the small config 1.
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+METRIC = "indexer+topk rows/s & TFLOP/s; SFA fwd TFLOP/s (prefill), KV GB/s (decode), % roof"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def timed(fn, steps, warmup, torch):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def event_time(fns, reps, torch):
+    """Average device time (ms) of each callable, bracketed by HIP events on the
+    current stream (the stream every kernel here is launched on)."""
+    tot = [0.0] * len(fns)
+    for _ in range(reps):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(fns) + 1)]
+        ev[0].record()
+        for i, f in enumerate(fns):
+            f()
+            ev[i + 1].record()
+        torch.cuda.synchronize()
+        for i in range(len(fns)):
+            tot[i] += ev[i].elapsed_time(ev[i + 1])
+    return [t / reps for t in tot]
+
+
+def cpu_baseline_indexer(inp, c, torch, budget_s=20.0):
+    """Oracle (numpy port of lightning_indexer_numpy.py) on a stride sample of C2 rows."""
+    import numpy as np
+    from oracle import lightning_indexer_ref as LIO
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+    except Exception:
+        threads = 1
+    q = inp.query.float().cpu().numpy()
+    k = inp.key.float().cpu().numpy()
+    w = inp.weights.float().cpu().numpy()
+    S = c["S1"]
+    stride = 32
+    rows = [(0, s) for s in range(stride // 2, S, stride)]
+    # calibrate on a few rows so the sample stays within the time budget
+    t0 = time.perf_counter()
+    LIO.li_golden_bsnd(q, k, w, [S], [S], c["sparse_count"], 3, True, rows=rows[-4:])
+    per_row_max = (time.perf_counter() - t0) / 4
+    n = len(rows)
+    while n > 16 and per_row_max * n / 2 > budget_s:
+        rows = rows[::2]
+        n = len(rows)
+    t0 = time.perf_counter()
+    LIO.li_golden_bsnd(q, k, w, [S], [S], c["sparse_count"], 3, True, rows=rows)
+    dt = time.perf_counter() - t0
+    return {"value": round(len(rows) / dt, 2), "unit": "rows/s", "cores": int(threads), "kind": "port",
+            "sample": f"{len(rows)} of {S} query rows (every {S // len(rows)}th, spanning the causal "
+                      f"triangle) of config 2 through the numpy oracle; {dt:.1f} s; "
+                      f"extrapolated full call {S / (len(rows) / dt):.0f} s"}
+
+
+def bench_indexer_c2(args, torch, W, dsa):
+    from dsa_triton_ascend_amd.lightning_indexer import IndexerPlan
+    dev = torch.device("cuda:0")
+    c = dict(W.C2)
+    inp = W.indexer_inputs(**c, device=dev, seed=42)
+    plan = IndexerPlan(inp.query, inp.key, inp.weights, sparse_count=c["sparse_count"],
+                       sparse_mode=3, return_value=True)
+    sec = timed(plan.run, args.steps, args.warmup, torch)
+    t_score, t_topk = event_time([plan.score, plan.topk], max(3, args.steps // 2), torch)
+    S = c["S1"]
+    pairs = S * (S + 1) // 2
+    flop = 2.0 * pairs * c["N1"] * c["D"]
+    return inp, c, sec, t_score, t_topk, flop
+
+
+def bench_sfa(plan_kwargs, steps, warmup, torch):
+    from dsa_triton_ascend_amd.sparse_flash_attention import AttentionPlan
+    plan = AttentionPlan(**plan_kwargs)
+    sec = timed(plan.run, steps, warmup, torch)
+    (ms,) = event_time([plan.run], max(3, steps // 2), torch)
+    return sec, ms
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--quick", action="store_true", help="headline only (no breakdown, no CPU baseline)")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import dsa_triton_ascend_amd as dsa
+    from dsa_triton_ascend_amd import workloads as W
+
+    log("[bench] C2 lightning_indexer ...")
+    inp, c, sec, t_score, t_topk, flop = bench_indexer_c2(args, torch, W, dsa)
+    rows = c["S1"]
+    achieved = flop / (t_score * 1e-3) / 1e12
+    result = {
+        "metric": METRIC,
+        "value": round(rows / sec, 1),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sec * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) bf16 inputs of the BASELINE config shapes)",
+        "config": {"workload": "C2: lightning_indexer BSND B=1 S1=S2=8192 N1=64 N2=1 D=128 "
+                               "sparse_count=2048 sparse_mode=3 return_value=True",
+                   "rows": rows, "indexer_tflops": round(flop / sec / 1e12, 2)},
+        "roofline": {"kernel": "li_score_kernel", "bound": "mfma", "achieved": round(achieved, 2),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None, "kernel_ms": round(t_score, 4),
+                     "algorithmic_flop": flop},
+    }
+    breakdown = {"li_topk_kernel_ms": round(t_topk, 4),
+                 "li_topk_rows_per_s": round(rows / (t_topk * 1e-3), 1)}
+    if not args.quick:
+        steps = max(3, args.steps // 4)
+        try:
+            log("[bench] C3 SFA prefill ...")
+            si = W.sfa_prefill_inputs(device="cuda:0", seed=42)
+            kw = dict(query=si.query, key=si.key, value=si.key, sparse_indices=si.sparse_indices, **si.kwargs())
+            s3, ms3 = bench_sfa(kw, steps, 1, torch)
+            f3 = 6292480 * 128 * (576 + 512) * 2.0
+            breakdown["sfa_prefill_c3"] = {"ms": round(ms3, 4), "tflops": round(f3 / ms3 / 1e9, 2),
+                                           "frac_mfma": round(f3 / ms3 / 1e9 / PEAK_BF16_TFLOPS, 4),
+                                           "algorithmic_flop": f3}
+            del si, kw
+            torch.cuda.empty_cache()
+            log("[bench] C4 SFA decode ...")
+            sd = W.sfa_decode_inputs(device="cuda:0", seed=42)
+            kw = dict(query=sd.query, key=sd.key, value=sd.key, sparse_indices=sd.sparse_indices, **sd.kwargs())
+            s4, ms4 = bench_sfa(kw, max(5, args.steps), 2, torch)
+            kv_bytes = 64 * 2048 * 576 * 2
+            breakdown["sfa_decode_c4"] = {"ms": round(ms4, 4), "kv_gbs": round(kv_bytes / ms4 / 1e6, 1),
+                                          "frac_hbm": round(kv_bytes / ms4 / 1e6 / PEAK_HBM_GBS, 4),
+                                          "gathered_kv_bytes": kv_bytes}
+            del sd, kw
+            torch.cuda.empty_cache()
+        except Exception as e:  # report, keep the headline
+            breakdown["sfa_error"] = repr(e)[:300]
+    if not (args.quick or args.no_cpu):
+        log("[bench] CPU baseline (oracle sample) ...")
+        result["cpu_baseline"] = cpu_baseline_indexer(inp, c, torch)
+    else:
+        result["cpu_baseline"] = None
+    result["breakdown"] = breakdown
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,143 @@
+// C ABI of libdsa_mi355x.so: argument validation, error reporting, dispatch.
+//
+// Validation mirrors the ValueError conditions of the reference operators
+// (lightning_indexer_triton.py:501-502, :524-525; sparse_flash_attention_triton.py
+// :1341-1351, :1377-1378, :1391-1398) so a bad call fails here with a message
+// instead of reaching a kernel; the Python layer raises the same conditions first.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/dsa_mi355x.h"
+#include "dsa_common.hpp"
+
+bool li_score_supported_d(int d);
+
+namespace {
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) {
+    g_err[0] = 0;
+    return DSA_OK;
+  }
+  return fail(DSA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool is16(int dt) { return dt == DSA_DTYPE_BF16 || dt == DSA_DTYPE_F16; }
+}  // namespace
+
+extern "C" {
+
+int dsa_abi_version(void) { return 1; }
+
+const char* dsa_last_error(void) { return g_err; }
+
+int dsa_li_score(const void* query, const void* key, const void* weights, int io_dtype,
+                 int w_dtype, const int32_t* row_start, const int32_t* key_start,
+                 const int32_t* act_q, const int32_t* act_k, int batch, int total_rows, int n1,
+                 int n2, int d, int s2, int max_rows_per_batch, int max_kv, int sparse_mode,
+                 uint16_t* scores, int64_t score_ld, void* stream) {
+  if (!query || !key || !weights || !row_start || !key_start || !act_q || !act_k || !scores)
+    return fail(DSA_ERR_INVALID, "dsa_li_score: null pointer argument");
+  if (!is16(io_dtype)) return fail(DSA_ERR_INVALID, "dsa_li_score: io_dtype must be fp16 or bf16");
+  if (!is16(w_dtype) && w_dtype != DSA_DTYPE_F32)
+    return fail(DSA_ERR_INVALID, "dsa_li_score: weights dtype must be fp16, bf16 or fp32");
+  if (batch <= 0 || total_rows < 0 || n1 <= 0 || n2 <= 0 || s2 < 0 || max_rows_per_batch < 0)
+    return fail(DSA_ERR_INVALID, "dsa_li_score: non-positive shape");
+  if (n1 % n2 != 0) return fail(DSA_ERR_INVALID, "N1(%d) must be divisible by N2(%d)", n1, n2);
+  if (n1 / n2 > 128) return fail(DSA_ERR_UNSUPPORTED, "dsa_li_score: group size N1/N2=%d > 128", n1 / n2);
+  if (!li_score_supported_d(d))
+    return fail(DSA_ERR_UNSUPPORTED, "dsa_li_score: D=%d not in {64, 96, 128, 256, 512}", d);
+  if (sparse_mode != 0 && sparse_mode != 3)
+    return fail(DSA_ERR_INVALID, "dsa_li_score: sparse_mode must be 0 or 3");
+  if (score_ld < s2) return fail(DSA_ERR_INVALID, "dsa_li_score: score_ld < S2");
+  if (batch > 65535 || n2 > 65535) return fail(DSA_ERR_UNSUPPORTED, "dsa_li_score: batch or N2 > 65535");
+  LiScoreArgs a{query, key, weights, io_dtype, w_dtype, row_start, key_start, act_q, act_k,
+                batch, total_rows, n1, n2, d, s2, max_rows_per_batch, max_kv, sparse_mode,
+                scores, score_ld};
+  return hip_status(launch_li_score(a, (hipStream_t)stream), "dsa_li_score launch");
+}
+
+int dsa_li_topk(const uint16_t* scores, int64_t score_ld, int io_dtype, const int32_t* row_start,
+                const int32_t* act_q, const int32_t* act_k, int batch, int total_rows, int n2,
+                int s2, int sparse_mode, int sparse_count, int32_t* indices, uint16_t* values,
+                void* stream) {
+  if (!scores || !row_start || !act_q || !act_k || !indices)
+    return fail(DSA_ERR_INVALID, "dsa_li_topk: null pointer argument");
+  if (!is16(io_dtype)) return fail(DSA_ERR_INVALID, "dsa_li_topk: io_dtype must be fp16 or bf16");
+  if (batch <= 0 || total_rows < 0 || n2 <= 0 || s2 < 0)
+    return fail(DSA_ERR_INVALID, "dsa_li_topk: non-positive shape");
+  if (sparse_count <= 0) return fail(DSA_ERR_INVALID, "dsa_li_topk: sparse_count must be positive");
+  if (sparse_count > 8192)
+    return fail(DSA_ERR_UNSUPPORTED, "dsa_li_topk: sparse_count=%d > 8192", sparse_count);
+  if (s2 > 65536) return fail(DSA_ERR_UNSUPPORTED, "dsa_li_topk: S2=%d > 65536", s2);
+  if (sparse_mode != 0 && sparse_mode != 3)
+    return fail(DSA_ERR_INVALID, "dsa_li_topk: sparse_mode must be 0 or 3");
+  if (score_ld < s2) return fail(DSA_ERR_INVALID, "dsa_li_topk: score_ld < S2");
+  LiTopkArgs a{scores, score_ld, io_dtype, row_start, act_q, act_k, batch, total_rows, n2, s2,
+               sparse_mode, sparse_count, indices, values};
+  return hip_status(launch_li_topk(a, (hipStream_t)stream), "dsa_li_topk launch");
+}
+
+size_t dsa_sfa_workspace_bytes(int total_rows, int n1, int d, int sparse_count,
+                               int sparse_block_size, int kv_splits) {
+  if (total_rows <= 0 || sparse_count <= 0 || sparse_block_size <= 0) return 0;
+  return sfa_workspace_bytes(total_rows, n1, d, sparse_count, sparse_block_size, kv_splits);
+}
+
+int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key, const void* key_rope,
+                int io_dtype, const int32_t* sparse_indices, int sparse_count,
+                int sparse_block_size, const int32_t* block_table, int max_blocks,
+                int page_block_size, const int32_t* row_start, const int32_t* key_start,
+                const int32_t* act_q, const int32_t* act_k, int batch, int total_rows, int n1,
+                int d, int dr, int s2, int64_t key_rows, int sparse_mode, float scale, void* out,
+                float* sm_max,
+                float* sm_sum, void* workspace, size_t workspace_bytes, int kv_splits,
+                void* stream) {
+  if (!query || !query_rope || !key || !key_rope || !sparse_indices || !row_start || !act_q ||
+      !act_k || !out)
+    return fail(DSA_ERR_INVALID, "dsa_sfa_fwd: null pointer argument");
+  if (!block_table && !key_start)
+    return fail(DSA_ERR_INVALID, "dsa_sfa_fwd: key_start required without block_table");
+  if (!is16(io_dtype)) return fail(DSA_ERR_INVALID, "dsa_sfa_fwd: io_dtype must be fp16 or bf16");
+  if (sparse_mode != 0 && sparse_mode != 3)
+    return fail(DSA_ERR_INVALID, "Only sparse_mode 0 (full) / 3 (rightDownCausal) supported");
+  if (sparse_block_size < 1 || (sparse_block_size & (sparse_block_size - 1)) != 0 ||
+      sparse_block_size > 128)
+    return fail(DSA_ERR_INVALID, "sparse_block_size must be a power of 2 in [1,128]");
+  if (d != 128 && d != 256 && d != 512)
+    return fail(DSA_ERR_INVALID, "D must be one of (128, 256, 512), got %d", d);
+  if (dr != 64) return fail(DSA_ERR_INVALID, "rope dim must be 64, got %d", dr);
+  if (n1 < 1 || n1 > 128 || (n1 & (n1 - 1)) != 0)
+    return fail(DSA_ERR_INVALID, "N1 must be one of (1, 2, 4, 8, 16, 32, 64, 128), got %d", n1);
+  if (batch <= 0 || total_rows < 0 || sparse_count <= 0 || key_rows < 0)
+    return fail(DSA_ERR_INVALID, "dsa_sfa_fwd: non-positive shape");
+  if (block_table && (max_blocks <= 0 || page_block_size <= 0))
+    return fail(DSA_ERR_INVALID, "dsa_sfa_fwd: PA_BSND needs max_blocks and block_size > 0");
+  if ((sm_max == nullptr) != (sm_sum == nullptr))
+    return fail(DSA_ERR_INVALID, "dsa_sfa_fwd: sm_max and sm_sum must both be given or both NULL");
+  if ((int64_t)sparse_count * sparse_block_size > (1 << 20))
+    return fail(DSA_ERR_UNSUPPORTED, "dsa_sfa_fwd: sparse_count*sparse_block_size > 2^20 tokens");
+  const size_t need = sfa_workspace_bytes(total_rows, n1, d, sparse_count, sparse_block_size, kv_splits);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail(DSA_ERR_INVALID, "dsa_sfa_fwd: workspace of %zu bytes required, %zu given", need,
+                workspace_bytes);
+  SfaArgs a{query, query_rope, key, key_rope, io_dtype, sparse_indices, sparse_count,
+            sparse_block_size, block_table, max_blocks, page_block_size, row_start, key_start,
+            act_q, act_k, batch, total_rows, n1, d, dr, s2, key_rows, sparse_mode, scale, out, sm_max,
+            sm_sum, workspace, workspace_bytes, kv_splits};
+  return hip_status(launch_sfa_fwd(a, (hipStream_t)stream), "dsa_sfa_fwd launch");
+}
+
+}  // extern "C"

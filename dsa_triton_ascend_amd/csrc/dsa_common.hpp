@@ -1,0 +1,132 @@
+// Shared device helpers for the gfx950 (CDNA4) DSA kernels.
+//
+// 16-bit floats are moved as raw uint16 bit patterns; the MFMA operands are
+// 8-wide bf16 / fp16 vectors built from one 16-byte load. Conversions that the
+// reference goldens define bit-exactly (fp32 -> bf16 round-to-nearest-even,
+// lightning_indexer_numpy.py:20-24) are restated here on the bit pattern.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/dsa_mi355x.h"
+
+namespace dsa {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+enum IoType { IO_F16 = DSA_DTYPE_F16, IO_BF16 = DSA_DTYPE_BF16 };
+
+// ------------------------------------------------------------------ conversions
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(((uint32_t)h) << 16);
+}
+// Round-to-nearest-even fp32 -> bf16 on the bit pattern: add 0x7FFF plus the
+// lsb of the kept half, then truncate (same rule as the numpy golden).
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+__device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);  // v_cvt_f16_f32, RNE
+}
+
+template <int IO> __device__ __forceinline__ float to_f32(uint16_t h) {
+  return IO == IO_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+}
+template <int IO> __device__ __forceinline__ uint16_t from_f32(float f) {
+  return IO == IO_BF16 ? f32_to_bf16_rne(f) : f32_to_f16_rne(f);
+}
+
+// Monotone map of a 16-bit float pattern to an unsigned key: larger float ->
+// larger key; +0 and -0 map to the same key (the goldens compare them equal).
+__device__ __forceinline__ uint32_t ord16(uint16_t h) {
+  if (h == 0x8000u) h = 0;
+  return (h & 0x8000u) ? (uint32_t)(uint16_t)(~h) : (uint32_t)(h | 0x8000u);
+}
+__device__ __forceinline__ uint16_t unord16(uint32_t k) {
+  return (k & 0x8000u) ? (uint16_t)(k & 0x7FFFu) : (uint16_t)(~k);
+}
+
+// ------------------------------------------------------------------ MFMA
+template <int IO> struct Mfma;
+template <> struct Mfma<IO_BF16> {
+  static __device__ __forceinline__ f32x16 m32(uint4 a, uint4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 m16(uint4 a, uint4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+template <> struct Mfma<IO_F16> {
+  static __device__ __forceinline__ f32x16 m32(uint4 a, uint4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 m16(uint4 a, uint4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+
+// Output layouts (CDNA3/CDNA4 MFMA, 64 lanes):
+//  32x32: lane l, acc[r] (r < 16) holds C[row = (r/4)*8 + (l/32)*4 + r%4][col = l%32]
+//  16x16: lane l, acc[r] (r < 4)  holds C[row = (l/16)*4 + r][col = l%16]
+// Operands: lane l supplies 8 consecutive K values of A row (l%32 | l%16) and of
+// B column (l%32 | l%16); the K group is l/32 (32x32x16) or l/16 (16x16x32).
+__device__ __forceinline__ int m32_row(int r, int lane) { return (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3); }
+__device__ __forceinline__ int m16_row(int r, int lane) { return (lane >> 4) * 4 + r; }
+
+// ------------------------------------------------------------------ misc
+__device__ __forceinline__ uint4 ldg16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ void stg16(void* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
+
+__device__ __forceinline__ int batch_of_row(const int32_t* row_start, int batch, int r) {
+  // largest b with row_start[b] <= r (row_start has batch+1 ascending entries)
+  int lo = 0, hi = batch - 1;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if (row_start[mid] <= r) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+}  // namespace dsa
+
+// ------------------------------------------------------------------ launchers
+// Host-side launch entry points implemented by each kernel translation unit
+// and called by the C-ABI layer after argument validation.
+struct LiScoreArgs {
+  const void* q; const void* k; const void* w; int io; int wdt;
+  const int32_t* row_start; const int32_t* key_start; const int32_t* act_q; const int32_t* act_k;
+  int batch, total_rows, n1, n2, d, s2, max_rows_per_batch, max_kv, sparse_mode;
+  uint16_t* scores; int64_t ld;
+};
+struct LiTopkArgs {
+  const uint16_t* scores; int64_t ld; int io;
+  const int32_t* row_start; const int32_t* act_q; const int32_t* act_k;
+  int batch, total_rows, n2, s2, sparse_mode, k;
+  int32_t* idx; uint16_t* val;
+};
+struct SfaArgs {
+  const void* q; const void* qr; const void* k; const void* kr; int io;
+  const int32_t* sidx; int topk; int sbs;
+  const int32_t* block_table; int max_blocks; int page_bs;
+  const int32_t* row_start; const int32_t* key_start; const int32_t* act_q; const int32_t* act_k;
+  int batch, total_rows, n1, d, dr, s2; int64_t key_rows; int sparse_mode; float scale;
+  void* out; float* sm_max; float* sm_sum;
+  void* ws; size_t ws_bytes; int kv_splits;
+};
+hipError_t launch_li_score(const LiScoreArgs& a, hipStream_t s);
+hipError_t launch_li_topk(const LiTopkArgs& a, hipStream_t s);
+hipError_t launch_sfa_fwd(const SfaArgs& a, hipStream_t s);
+size_t sfa_workspace_bytes(int total_rows, int n1, int d, int topk, int sbs, int kv_splits);

@@ -1,0 +1,141 @@
+/*
+ * dsa_mi355x.h — C ABI of the MI355X (gfx950) DeepSeek-Sparse-Attention hot path.
+ *
+ * The reference binds its device work through two MindSpore `_ms_pyfunc`
+ * cores plus a library top-k; each entry point below replaces one of them:
+ *
+ *   dsa_li_score   <- _lightning_indexer_score_core   lightning_indexer_triton.py:386-417
+ *                     (+ _lightning_indexer_score_kernel :180-284)
+ *   dsa_li_topk    <- _stable_topk                     lightning_indexer_triton.py:343-361
+ *                     with the golden's ordering       lightning_indexer_numpy.py:92-105
+ *   dsa_sfa_fwd    <- _sfa_core                        sparse_flash_attention_triton.py:1160-1289
+ *                     (+ _sfa_kernel :324-604, _sfa_gather_kernel :611-679,
+ *                        _sfa_kernel_gathered :710-962, _pa_to_bsnd :1012-1033,
+ *                        _expand_block_indices :1036-1051)
+ *   dsa_sfa_workspace_bytes <- the workspace sizing of _sfa_core :1218-1250
+ *                     (the caller allocates; the library keeps no cache)
+ *
+ * Conventions
+ *  - Every pointer is device memory unless stated; the caller owns every buffer.
+ *  - `stream` is a hipStream_t passed as void* (NULL = the null stream). Calls
+ *    are asynchronous on that stream.
+ *  - Return 0 on success, DSA_ERR_* (< 0) otherwise; dsa_last_error() gives a
+ *    thread-local message for the last failing call on the calling thread.
+ *  - Query rows are "packed rows": BSND row r = b*S1 + s1, TND row r = cu_q[b-1] + s1.
+ *    row_start[B+1] gives the first packed row of each batch (BSND: b*S1,
+ *    TND: 0, cu_q[0], ...); key_start[B] the first packed key row (BSND: b*S2,
+ *    TND: 0, cu_k[0], ...). act_q / act_k are per-batch lengths.
+ */
+#ifndef DSA_MI355X_H
+#define DSA_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DSA_DTYPE_F16 0
+#define DSA_DTYPE_BF16 1
+#define DSA_DTYPE_F32 2
+
+#define DSA_OK 0
+#define DSA_ERR_INVALID (-1)     /* argument outside the documented domain */
+#define DSA_ERR_UNSUPPORTED (-2) /* valid for the reference, not implemented here */
+#define DSA_ERR_HIP (-3)         /* a HIP runtime call failed */
+
+/* ABI version of this header (bumped on any signature change). */
+int dsa_abi_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* dsa_last_error(void);
+
+/*
+ * Indexer scores (replaces _lightning_indexer_score_core,
+ * lightning_indexer_triton.py:386-417).
+ *
+ *   score[r*N2+n2, s2] = sum_{g < G} relu(q[r, n2*G+g, :] . k[key_start[b]+s2, n2, :]) * w[r, n2*G+g]
+ *
+ * quantised to the io dtype (bf16 RNE / fp16) and written as 16-bit patterns to
+ * scores[(r*N2+n2)*score_ld + s2] for the visible prefix s2 < L(r) only, where
+ * L = min(max(act_k-act_q+s1+1, 0), S2, act_k) for sparse_mode 3 and
+ * min(act_k, S2) for sparse_mode 0 (lightning_indexer_numpy.py:85-90).
+ * Rows with s1 >= act_q[b] are not written.
+ *   query  [total_rows, N1, D] io dtype;  key [.., N2, D] io dtype;
+ *   weights[total_rows, N1] in w_dtype (fp16 / bf16 / fp32);
+ *   io_dtype DSA_DTYPE_BF16 or DSA_DTYPE_F16;  D a multiple of 32 up to 512;
+ *   N1 % N2 == 0;  sparse_mode 0 or 3;  score_ld >= S2.
+ *   max_rows_per_batch = max_b(row_start[b+1]-row_start[b]) (host-known bound);
+ *   max_kv = max_b act_k[b] (host-known bound, <= S2).
+ */
+int dsa_li_score(const void* query, const void* key, const void* weights, int io_dtype,
+                 int w_dtype, const int32_t* row_start, const int32_t* key_start,
+                 const int32_t* act_q, const int32_t* act_k, int batch, int total_rows, int n1,
+                 int n2, int d, int s2, int max_rows_per_batch, int max_kv, int sparse_mode,
+                 uint16_t* scores, int64_t score_ld, void* stream);
+
+/*
+ * Stable top-k over the quantised score rows (replaces _stable_topk,
+ * lightning_indexer_triton.py:343-361, with the golden's order,
+ * lightning_indexer_numpy.py:92-105): per score row, entries of the visible
+ * prefix ordered by score descending then index ascending; the first
+ * min(L, sparse_count) are written to indices[(r*N2+n2)*sparse_count + i]
+ * (int32) and, if `values` is not NULL, their 16-bit score to values[...];
+ * the remaining slots get index -1 and value 0. Rows with s1 >= act_q are all -1 / 0.
+ * Requires S2 <= 65536.
+ */
+int dsa_li_topk(const uint16_t* scores, int64_t score_ld, int io_dtype,
+                const int32_t* row_start, const int32_t* act_q, const int32_t* act_k,
+                int batch, int total_rows, int n2, int s2, int sparse_mode, int sparse_count,
+                int32_t* indices, uint16_t* values, void* stream);
+
+/*
+ * Bytes of device workspace dsa_sfa_fwd needs for this problem
+ * (0 when no split-KV partials are used). kv_splits <= 0 selects the library's choice.
+ */
+size_t dsa_sfa_workspace_bytes(int total_rows, int n1, int d, int sparse_count,
+                               int sparse_block_size, int kv_splits);
+
+/*
+ * Sparse flash attention forward, MLA-absorb (replaces _sfa_core,
+ * sparse_flash_attention_triton.py:1160-1289; semantics of
+ * sparse_flash_attention_numpy.py:38-160).
+ *
+ * For each packed query row r (batch b, s1 = r - row_start[b], s1 < act_q[b]):
+ *   threshold = act_k (mode 0) | act_k - act_q + s1 + 1 (mode 3; rows with
+ *   s1 < act_q - act_k are skipped); the first min(count, ceil(threshold/bs))
+ *   ids of sparse_indices[r, :] are scanned, stopping at the first -1; id i
+ *   expands to tokens [i*bs, min(i*bs+bs, act_k, threshold)).
+ *   score[h, t] = (q[r,h,:D].k[t,:D] + q_rope[r,h,:].k_rope[t,:]) * scale
+ *   out[r, h, :] = softmax_t(score[h, :]) @ k[t, :D]       (value = key)
+ *   sm_max[r*N1+h] = max_t score,  sm_sum[r*N1+h] = sum_t exp(score - max)
+ * Skipped rows / rows without tokens get out = 0, sm = 0.
+ *
+ *   query [total_rows, N1, D], query_rope [total_rows, N1, Dr], io dtype;
+ *   key / key_rope: BSND or TND [.., 1, D|Dr] with token t at row key_start[b]+t,
+ *     or PA_BSND [num_blocks, page_block_size, 1, D|Dr] when block_table != NULL:
+ *     token t of batch b lives in block block_table[b*max_blocks + t/page_block_size]
+ *     (-1 block -> a zero row, like the reference's de-paging);
+ *   sparse_indices [total_rows, sparse_count] int32 block ids;
+ *   key_rows: rows held by key / key_rope (num_blocks*page_block_size for PA_BSND);
+ *     a gathered token outside [0, key_rows) reads as a zero row (never out of bounds).
+ *   N1 <= 128, D in {128, 256, 512}, Dr = 64, sparse_block_size a power of 2 <= 128.
+ *   sm_max / sm_sum may be NULL (not requested).
+ *   workspace: >= dsa_sfa_workspace_bytes(...) bytes (may be NULL when that is 0).
+ */
+int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key,
+                const void* key_rope, int io_dtype, const int32_t* sparse_indices,
+                int sparse_count, int sparse_block_size, const int32_t* block_table,
+                int max_blocks, int page_block_size, const int32_t* row_start,
+                const int32_t* key_start, const int32_t* act_q, const int32_t* act_k, int batch,
+                int total_rows, int n1, int d, int dr, int s2, int64_t key_rows, int sparse_mode,
+                float scale,
+                void* out, float* sm_max, float* sm_sum, void* workspace,
+                size_t workspace_bytes, int kv_splits, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSA_MI355X_H */

@@ -1,0 +1,97 @@
+"""C-ABI boundary checks that need no GPU: the library loads, exports every
+symbol include/dsa_mi355x.h declares, and rejects invalid arguments with a
+non-zero status and a message before touching the device; the Python entry
+points raise the reference's ValueErrors before any device work."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from dsa_triton_ascend_amd import _lib
+from dsa_triton_ascend_amd import lightning_indexer, sparse_flash_attention
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "dsa_mi355x.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dsa_\w+)\s*\(", text)))
+
+
+def test_header_symbols_exported():
+    lib = _lib.load()
+    syms = declared_symbols()
+    assert {"dsa_li_score", "dsa_li_topk", "dsa_sfa_fwd", "dsa_sfa_workspace_bytes",
+            "dsa_last_error", "dsa_abi_version"} <= set(syms)
+    for s in syms:
+        assert hasattr(lib, s), f"{s} declared in the header but not exported"
+        assert s in _lib.SIGNATURES, f"{s} has no ctypes signature"
+    assert lib.dsa_abi_version() == 1
+
+
+def test_invalid_arguments_return_status_without_gpu():
+    lib = _lib.load()
+    st = lib.dsa_li_score(None, None, None, 1, 2, None, None, None, None, 1, 1, 8, 1, 128, 16,
+                          1, 16, 3, None, 16, None)
+    assert st == _lib.DSA_ERR_INVALID
+    assert b"null pointer" in lib.dsa_last_error()
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    st = lib.dsa_li_score(p, p, p, 1, 2, p, p, p, p, 1, 1, 8, 3, 128, 16, 1, 16, 3, p, 16, None)
+    assert st == _lib.DSA_ERR_INVALID and b"divisible" in lib.dsa_last_error()
+    st = lib.dsa_li_score(p, p, p, 1, 2, p, p, p, p, 1, 1, 8, 1, 100, 16, 1, 16, 3, p, 16, None)
+    assert st == _lib.DSA_ERR_UNSUPPORTED
+    st = lib.dsa_li_topk(p, 70000, 1, p, p, p, 1, 1, 1, 70000, 3, 64, p, None, None)
+    assert st == _lib.DSA_ERR_UNSUPPORTED and b"65536" in lib.dsa_last_error()
+    base = [p, p, p, p, 1, p, 64, 1, None, 0, 0, p, p, p, p, 1, 1, 128, 512, 64, 16, 16, 3, 0.1,
+            p, None, None, p, 1 << 30, 0, None]
+    # `base` itself is valid and is never called: each case below breaks one field
+    bad = list(base)
+    bad[18] = 100
+    assert lib.dsa_sfa_fwd(*bad) == _lib.DSA_ERR_INVALID and b"D must be one of" in lib.dsa_last_error()
+    bad = list(base)
+    bad[7] = 3
+    assert lib.dsa_sfa_fwd(*bad) == _lib.DSA_ERR_INVALID and b"power of 2" in lib.dsa_last_error()
+    bad = list(base)
+    bad[17] = 96
+    assert lib.dsa_sfa_fwd(*bad) == _lib.DSA_ERR_INVALID and b"N1 must be one of" in lib.dsa_last_error()
+    bad = list(base)
+    bad[22] = 1
+    assert lib.dsa_sfa_fwd(*bad) == _lib.DSA_ERR_INVALID and b"sparse_mode" in lib.dsa_last_error()
+    bad = list(base)
+    bad[27], bad[28] = None, 0
+    assert lib.dsa_sfa_fwd(*bad) == _lib.DSA_ERR_INVALID and b"workspace" in lib.dsa_last_error()
+    assert lib.dsa_sfa_workspace_bytes(4096, 128, 512, 2048, 1, 0) >= 4096 * 2048 * 4
+
+
+def test_python_validation_matches_reference():
+    q = torch.zeros(1, 4, 8, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="block_table"):
+        lightning_indexer(q, q[:, :, :1], torch.zeros(1, 4, 8), block_table=torch.zeros(1, 1))
+    k = torch.zeros(1, 16, 1, 512, dtype=torch.bfloat16)
+    qs = torch.zeros(1, 4, 8, 512, dtype=torch.bfloat16)
+    qr = torch.zeros(1, 4, 8, 64, dtype=torch.bfloat16)
+    kr = torch.zeros(1, 16, 1, 64, dtype=torch.bfloat16)
+    si = torch.zeros(1, 4, 1, 8, dtype=torch.int32)
+    cases = [(dict(attention_mode=1), "attention_mode"), (dict(sparse_mode=1), "sparse_mode"),
+             (dict(pre_tokens=5), "pre_tokens"), (dict(sparse_block_size=3), "power of 2"),
+             (dict(query_rope=None), "query_rope")]
+    for kw, msg in cases:
+        args = dict(query_rope=qr, key_rope=kr)
+        args.update(kw)
+        with pytest.raises(ValueError, match=msg):
+            sparse_flash_attention(qs, k, k, si, **args)
+    with pytest.raises(ValueError, match="block_table"):
+        sparse_flash_attention(qs, k, k, si, query_rope=qr, key_rope=kr, layout_kv="PA_BSND")
+    # CPU tensors are refused (no silent CPU path)
+    with pytest.raises(ValueError, match="GPU"):
+        sparse_flash_attention(qs, k, k, si, query_rope=qr, key_rope=kr)
+    with pytest.raises(ValueError, match="GPU"):
+        lightning_indexer(q, q[:, :, :1], torch.zeros(1, 4, 8))
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(RuntimeError, match="missing"):
+        _lib.load(tmp_path / "nope.so")

@@ -1,0 +1,210 @@
+"""GPU parity: sparse_flash_attention (HIP) vs the oracle
+(oracle/sparse_flash_attention_ref.py).
+
+Shape matrix follows the reference's test_golden (test_sfa_triton.py:129-169):
+token-wise and block-wise (bs 2, 4), S1=1, topK=2048, multi-batch,
+D in {128,256,512}, fp16 / bf16, plus mode 0, TND and PA_BSND cases the
+reference never tests. Tolerances: outputs within rtol=atol=1e-2 (io dtype),
+softmax_max / softmax_sum within rtol 1e-4 (fp32).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from dsa_triton_ascend_amd import SparseFlashAttention, sparse_flash_attention
+from dsa_triton_ascend_amd import workloads as W
+from oracle import sparse_flash_attention_ref as SFA
+
+pytestmark = pytest.mark.gpu
+
+DT = {"bf16": torch.bfloat16, "fp16": torch.float16}
+OUT_TOL = dict(rtol=1e-2, atol=1e-2)
+LSE_TOL = dict(rtol=1e-4, atol=1e-5)
+
+
+def _np(t):
+    return t.float().cpu().numpy()
+
+
+def _ref_indices(B, S1, S2, count, bs, mode, seed=7):
+    """Reference index generator (test_sfa_triton.py:64-85), same RandomState(7) stream."""
+    rng = np.random.RandomState(seed)
+    si = np.full((B, S1, 1, count), -1, dtype=np.int32)
+    for b in range(B):
+        for s1 in range(S1):
+            thr = S2 if mode == 0 else S2 - S1 + s1 + 1
+            if thr <= 0:
+                continue
+            nb = int(np.ceil(thr / bs))
+            n = min(count, nb)
+            si[b, s1, 0, :n] = np.sort(rng.permutation(nb)[:n]).astype(np.int32)
+    return si
+
+
+def _inputs(B, S1, S2, N1, D, dtype, seed=42):
+    """Reference generator semantics (test_sfa_triton.py:47-61): randn -> fp16 -> dtype."""
+    rng = np.random.RandomState(seed)
+    t = lambda *s: torch.from_numpy(rng.randn(*s).astype(np.float16)).to(DT[dtype])
+    q, k, v, qr, kr = t(B, S1, N1, D), t(B, S2, 1, D), t(B, S2, 1, D), t(B, S1, N1, 64), t(B, S2, 1, 64)
+    return q, k, v, qr, kr
+
+
+def compare(out, smax, ssum, o_out, o_max, o_sum, what):
+    go, gm, gs = _np(out), _np(smax), _np(ssum)
+    assert go.shape == o_out.shape and gm.shape == o_max.shape
+    assert np.all(np.isfinite(go))
+    np.testing.assert_allclose(go, o_out, err_msg=f"{what}: attention_out", **OUT_TOL)
+    np.testing.assert_allclose(gm, o_max, err_msg=f"{what}: softmax_max", **LSE_TOL)
+    np.testing.assert_allclose(gs, o_sum, err_msg=f"{what}: softmax_sum", **LSE_TOL)
+    err = np.abs(go - o_out).max()
+    print(f"[sfa parity] {what}: max|out-oracle|={err:.3e} "
+          f"max|lse rel|={np.max(np.abs(gs - o_sum) / np.maximum(np.abs(o_sum), 1e-30)):.2e}")
+
+
+GOLDEN = [(1, 4, 128, 8, 64, 1, 3), (2, 16, 256, 16, 128, 1, 3), (1, 8, 128, 8, 32, 2, 3),
+          (1, 8, 256, 16, 32, 4, 3), (1, 1, 128, 8, 16, 1, 3), (1, 4, 2048, 8, 2048, 1, 3),
+          (1, 4, 128, 8, 64, 1, 0), (1, 4, 2048, 8, 2048, 1, 0)]
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("D", [128, 256, 512])
+@pytest.mark.parametrize("B,S1,S2,N1,count,bs,mode", GOLDEN)
+def test_golden_matrix(dev, B, S1, S2, N1, count, bs, mode, D, dtype):
+    q, k, v, qr, kr = _inputs(B, S1, S2, N1, D, dtype)
+    si = _ref_indices(B, S1, S2, count, bs, mode)
+    scale = 1.0 / math.sqrt(D + 64)
+    mod = SparseFlashAttention(scale_value=scale, sparse_block_size=bs, sparse_mode=mode,
+                               return_softmax_lse=True)
+    out, smax, ssum = mod(q.to(dev), k.to(dev), v.to(dev), torch.from_numpy(si).to(dev),
+                          query_rope=qr.to(dev), key_rope=kr.to(dev))
+    torch.cuda.synchronize()
+    o = SFA.sparse_flash_attention(_np(q), _np(k), None, si, scale, query_rope=_np(qr),
+                                   key_rope=_np(kr), sparse_block_size=bs, sparse_mode=mode,
+                                   return_softmax_lse=True, io_dtype=dtype)
+    assert out.dtype == q.dtype and smax.shape == (B, 1, S1, N1)
+    compare(out, smax, ssum, *o, what=f"B{B} S1={S1} S2={S2} N1={N1} k={count} bs={bs} m{mode} D{D} {dtype}")
+
+
+@pytest.mark.parametrize("N1", [1, 2, 32, 64, 128])
+def test_head_counts(dev, N1):
+    B, S1, S2, D, count = 1, 6, 96, 512, 48
+    q, k, v, qr, kr = _inputs(B, S1, S2, N1, D, "bf16", seed=5)
+    si = _ref_indices(B, S1, S2, count, 1, 3, seed=8)
+    out, smax, ssum = sparse_flash_attention(q.to(dev), k.to(dev), v.to(dev), torch.from_numpy(si).to(dev),
+                                             scale_value=0.05, query_rope=qr.to(dev), key_rope=kr.to(dev),
+                                             sparse_mode=3, return_softmax_lse=True)
+    o = SFA.sparse_flash_attention(_np(q), _np(k), None, si, 0.05, query_rope=_np(qr), key_rope=_np(kr),
+                                   sparse_mode=3, return_softmax_lse=True, io_dtype="bf16")
+    compare(out, smax, ssum, *o, what=f"N1={N1}")
+
+
+def test_actual_lengths_and_skips(dev):
+    """act_q > act_k (mode-3 leading rows skipped), a -1 in the middle of a row
+    (scan stops), duplicate ids, ids beyond the threshold."""
+    B, S1, S2, N1, D, count = 2, 8, 64, 16, 128, 12
+    q, k, v, qr, kr = _inputs(B, S1, S2, N1, D, "bf16", seed=9)
+    rng = np.random.RandomState(1)
+    si = rng.randint(0, 64, size=(B, S1, 1, count)).astype(np.int32)
+    si[0, 3, 0, 5] = -1
+    si[1, 2, 0, :] = 7
+    act_q, act_k = [8, 6], [5, 64]
+    for mode in (0, 3):
+        out, smax, ssum = sparse_flash_attention(q.to(dev), k.to(dev), v.to(dev), torch.from_numpy(si).to(dev),
+                                                 scale_value=0.07, actual_seq_lengths_query=act_q,
+                                                 actual_seq_lengths_kv=act_k, query_rope=qr.to(dev),
+                                                 key_rope=kr.to(dev), sparse_mode=mode,
+                                                 return_softmax_lse=True)
+        o = SFA.sparse_flash_attention(_np(q), _np(k), None, si, 0.07, None, act_q, act_k, _np(qr),
+                                       _np(kr), 1, "BSND", "BSND", mode, True, io_dtype="bf16")
+        compare(out, smax, ssum, *o, what=f"act lengths mode {mode}")
+
+
+def test_lse_not_requested_gives_zeros(dev):
+    q, k, v, qr, kr = _inputs(1, 4, 64, 8, 128, "bf16")
+    si = _ref_indices(1, 4, 64, 16, 1, 3)
+    out, smax, ssum = sparse_flash_attention(q.to(dev), k.to(dev), v.to(dev), torch.from_numpy(si).to(dev),
+                                             scale_value=0.1, query_rope=qr.to(dev), key_rope=kr.to(dev),
+                                             sparse_mode=3, return_softmax_lse=False)
+    assert not smax.any() and not ssum.any() and out.abs().sum() > 0
+
+
+def test_tnd(dev):
+    lens_q, lens_k = [5, 1, 40, 17], [64, 9, 40, 100]
+    N1, D, count = 16, 512, 32
+    rng = np.random.RandomState(2)
+    T1, T2 = sum(lens_q), sum(lens_k)
+    f = lambda *s: torch.from_numpy(rng.randn(*s).astype(np.float32)).bfloat16()
+    q, qr, k, kr = f(T1, N1, D), f(T1, N1, 64), f(T2, 1, D), f(T2, 1, 64)
+    si = np.full((T1, 1, count), -1, np.int32)
+    r = 0
+    for b in range(4):
+        for s in range(lens_q[b]):
+            thr = lens_k[b] - lens_q[b] + s + 1
+            if thr > 0:
+                n = min(count, thr)
+                si[r, 0, :n] = np.sort(rng.permutation(thr)[:n])
+            r += 1
+    cq, ck = np.cumsum(lens_q).tolist(), np.cumsum(lens_k).tolist()
+    out, smax, ssum = sparse_flash_attention(q.to(dev), k.to(dev), k.to(dev), torch.from_numpy(si).to(dev),
+                                             scale_value=0.04, actual_seq_lengths_query=cq,
+                                             actual_seq_lengths_kv=ck, query_rope=qr.to(dev),
+                                             key_rope=kr.to(dev), layout_query="TND", layout_kv="TND",
+                                             sparse_mode=3, return_softmax_lse=True)
+    assert out.shape == (T1, N1, D) and smax.shape == (1, T1, N1)
+    o = SFA.sparse_flash_attention(_np(q), _np(k), None, si, 0.04, None, cq, ck, _np(qr), _np(kr), 1,
+                                   "TND", "TND", 3, True, io_dtype="bf16")
+    compare(out, smax, ssum, *o, what="TND")
+
+
+def test_pa_decode_small(dev):
+    """PA_BSND decode with a shuffled block table and a -1 (missing) block."""
+    inp = W.sfa_decode_inputs(B=4, N1=128, len_lo=300, len_hi=700, block_size=64, sparse_count=128,
+                              device="cpu", seed=3)
+    bt = inp.block_table.clone()
+    bt[1, 2] = -1   # tokens of this block read as zeros, like the reference's de-paging
+    out, smax, ssum = sparse_flash_attention(inp.query.to(dev), inp.key.to(dev), inp.key.to(dev),
+                                             inp.sparse_indices.to(dev), scale_value=inp.scale_value,
+                                             block_table=bt.to(dev),
+                                             actual_seq_lengths_kv=inp.actual_seq_lengths_kv,
+                                             query_rope=inp.query_rope.to(dev), key_rope=inp.key_rope.to(dev),
+                                             layout_kv="PA_BSND", sparse_mode=3, return_softmax_lse=True,
+                                             block_size=64)
+    o = SFA.sparse_flash_attention(_np(inp.query), _np(inp.key), None, inp.sparse_indices.numpy(),
+                                   inp.scale_value, bt.numpy(), None, inp.actual_seq_lengths_kv,
+                                   _np(inp.query_rope), _np(inp.key_rope), 1, "BSND", "PA_BSND", 3, True,
+                                   block_size=64, io_dtype="bf16")
+    compare(out, smax, ssum, *o, what="PA decode small")
+
+
+def test_c4_decode_full(dev):
+    """BASELINE config 4 at full size (64 rows: the oracle runs every row)."""
+    inp = W.sfa_decode_inputs(device=dev, seed=42)
+    out, smax, ssum = sparse_flash_attention(inp.query, inp.key, inp.key, inp.sparse_indices,
+                                             **inp.kwargs())
+    torch.cuda.synchronize()
+    sel = list(range(0, 64, 4))
+    o = SFA.sparse_flash_attention(_np(inp.query[sel]), _np(inp.key), None,
+                                   inp.sparse_indices[sel].cpu().numpy(), inp.scale_value,
+                                   inp.block_table[sel].cpu().numpy(), None,
+                                   [inp.actual_seq_lengths_kv[b] for b in sel], _np(inp.query_rope[sel]),
+                                   _np(inp.key_rope), 1, "BSND", "PA_BSND", 3, True,
+                                   block_size=inp.block_size, io_dtype="bf16")
+    compare(out[sel], smax[sel], ssum[sel], *o, what="C4 decode (16 sampled batches)")
+
+
+@pytest.mark.slow
+def test_c3_prefill_sampled(dev):
+    """BASELINE config 3 at full size; oracle on stride-sampled rows."""
+    inp = W.sfa_prefill_inputs(device=dev, seed=42)
+    out, smax, ssum = sparse_flash_attention(inp.query, inp.key, inp.key, inp.sparse_indices,
+                                             **inp.kwargs())
+    torch.cuda.synchronize()
+    rows = [(0, s) for s in (0, 1, 2047, 2048, 4095)] + [(0, s) for s in range(3, 4096, 511)]
+    o = SFA.sparse_flash_attention(_np(inp.query), _np(inp.key), None, inp.sparse_indices.cpu().numpy(),
+                                   inp.scale_value, query_rope=_np(inp.query_rope), key_rope=_np(inp.key_rope),
+                                   sparse_mode=3, return_softmax_lse=True, io_dtype="bf16", rows=rows)
+    s = [r[1] for r in rows]
+    compare(out[:, s], smax[:, :, s], ssum[:, :, s], o[0][:, s], o[1][:, :, s], o[2][:, :, s],
+            what="C3 prefill (sampled rows)")
