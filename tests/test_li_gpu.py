@@ -70,7 +70,9 @@ def run_case(dev, B, S1, S2, N1, N2, D, K, mode=3, dtype="bf16", act_q=None, act
     stats = check_li(gi, gv, _np(q), _np(k), _np(w), aq, ak, K, mode, dtype,
                      rows=_rows(B, S1, max_rows))
     print(f"[li parity] B={B} S1={S1} S2={S2} N1={N1} N2={N2} D={D} K={K} mode={mode} {dtype}: {stats}")
-    assert stats.flip_rows <= max(2, 0.2 * stats.rows), stats
+    # every flip is justified element by element; a kernel biased within E would
+    # still show up as a high flip rate
+    assert stats.flips <= max(4, 0.02 * stats.elements), stats
     return stats
 
 
@@ -146,7 +148,7 @@ def test_tnd(dev, layout_key):
     gi, gv = idx.cpu().numpy(), val.float().cpu().numpy()
     # exact agreement expected at these sizes; fall back to the rounding-aware check per row
     if not (np.array_equal(gi, o_idx) and np.array_equal(gv, o_val)):
-        from tests.parity import check_li_row, LiParityStats
+        from tests.parity import check_li_row, LiParityStats, row_error_bound
         act_q = np.diff([0] + cu_q)
         act_k = np.diff([0] + cu_k)
         stats = LiParityStats()
@@ -158,9 +160,10 @@ def test_tnd(dev, layout_key):
             for s in range(act_q[b]):
                 s32 = LI.li_row_scores(qb, kb, wb, b, s, 0, act_q, act_k, 3)
                 s64 = LI.li_row_scores_f64(qb, kb, wb, b, s, 0, act_q, act_k, 3)
-                check_li_row(gi[r, 0], gv[r, 0], s32, s64, int(act_k[b]), K, "bf16", stats)
+                err = row_error_bound(qb, kb, wb, b, s, 0)
+                check_li_row(gi[r, 0], gv[r, 0], s32, s64, int(act_k[b]), K, "bf16", stats, err=err)
                 r += 1
-        assert stats.flip_rows <= 3, stats
+        assert stats.flips <= max(4, 0.02 * stats.elements), stats
 
 
 @pytest.mark.slow
@@ -180,4 +183,4 @@ def test_c2_full_size_sampled(dev):
     stats = check_li(gi, gv, _np(inp.query), _np(inp.key), _np(inp.weights), [S], [S], K, 3,
                      "bf16", rows=rows)
     print(f"[li parity C2] {stats}")
-    assert stats.flip_rows <= max(2, 0.5 * stats.rows)
+    assert stats.flips <= max(4, 0.01 * stats.elements), stats

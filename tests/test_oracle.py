@@ -303,3 +303,53 @@ def test_causal_index_generator_contract():
                 assert np.all(row[n:] == -1)
                 v = row[:n]
                 assert np.all(np.diff(v) > 0) and v.min() >= 0 and v.max() < nb
+
+
+@pytest.mark.parametrize("vd", ["bf16", "fp16"])
+def test_parity_checker_accepts_other_fp32_order(vd):
+    """An independent fp32 evaluation (d summed in 4 blocks, heads reversed) of the
+    same scores must satisfy the parity rule -- the error bound covers real fp32
+    reordering noise, including heavy cancellation with unscaled weights."""
+    from tests.parity import check_li_row, row_error_bound
+    rng = np.random.RandomState(21)
+    S2, N1, D, K = 256, 64, 128, 64
+    q = quantize(rng.randn(1, 24, N1, D).astype(np.float32), vd)
+    k = quantize(rng.randn(1, S2, 1, D).astype(np.float32), vd)
+    w = quantize(rng.randn(1, 24, N1).astype(np.float32), vd)
+    stats = LiParityStats()
+    for s1 in range(24):
+        dots = np.zeros((S2, N1), np.float32)
+        for blk in range(4):
+            sl = slice(blk * 32, (blk + 1) * 32)
+            dots += k[0, :, 0, sl] @ q[0, s1, :, sl].T
+        alt = np.zeros(S2, np.float32)
+        for g in reversed(range(N1)):
+            alt += np.maximum(dots[:, g], 0) * w[0, s1, g]
+        aq = quantize(alt, vd)
+        gi, gv = LI.select_topk(aq, S2, K)
+        s32 = LI.li_row_scores(q, k, w, 0, s1, 0, [24], [S2], 0)
+        s64 = LI.li_row_scores_f64(q, k, w, 0, s1, 0, [24], [S2], 0)
+        check_li_row(gi, gv, s32, s64, S2, K, vd, stats, err=row_error_bound(q, k, w, 0, s1, 0))
+    assert stats.rows == 24
+
+
+def test_parity_checker_rejects_dropped_head():
+    """Planted mistake: scores missing one head's contribution must fail the rule."""
+    from tests.parity import check_li_row, row_error_bound
+    rng = np.random.RandomState(22)
+    S2, N1, D, K = 128, 16, 64, 32
+    q = round_bf16(rng.randn(1, 8, N1, D).astype(np.float32))
+    k = round_bf16(rng.randn(1, S2, 1, D).astype(np.float32))
+    w = (rng.randn(1, 8, N1) / 4).astype(np.float32)
+    failures = 0
+    for s1 in range(8):
+        s32 = LI.li_row_scores(q, k, w, 0, s1, 0, [8], [S2], 0)
+        wrong = s32 - np.maximum(k[0, :, 0] @ q[0, s1, 5], 0) * w[0, s1, 5]
+        gi, gv = LI.select_topk(quantize(wrong, "bf16"), S2, K)
+        s64 = LI.li_row_scores_f64(q, k, w, 0, s1, 0, [8], [S2], 0)
+        try:
+            check_li_row(gi, gv, s32, s64, S2, K, "bf16", LiParityStats(),
+                         err=row_error_bound(q, k, w, 0, s1, 0))
+        except AssertionError:
+            failures += 1
+    assert failures == 8
