@@ -3,33 +3,42 @@
 // Semantics: sparse_flash_attention_numpy.py:38-160 (the golden) with the
 // layouts of sparse_flash_attention_triton.py:1353-1450.
 //
-// Two kernels:
-//  1. sfa_tokens_kernel  -- one work-group per packed query row: applies the
+// Kernels:
+//  1. sfa_tokens_kernel -- one work-group per packed query row: applies the
 //     row-skip rules and the golden's gatherKV scan (first
 //     min(count, ceil(threshold/bs)) ids, stop at the first -1, expand id to
-//     [id*bs, min(id*bs+bs, act_k, threshold))), and writes the row's token
-//     list as PHYSICAL key rows (key_start offset, or the PA block-table
-//     lookup; a -1 block gives -1 = zero row) into the workspace.  This is the
-//     work the reference does with _expand_block_indices / _pa_to_bsnd on the
-//     host plus its masked loads (:1012-1051, :392-398).
-//  2. sfa_attn_kernel -- one work-group (4 waves) per (query row, block of 64
-//     heads). Per tile of 32 tokens the gathered rows [D | Dr] are staged in
-//     LDS with 16-byte loads; each wave computes S = Q K^T for 16 heads with
-//     v_mfma_f32_16x16x32 (Q resident in VGPRs), runs the online softmax in
-//     fp32 (row max via lane shuffles, row sums kept per lane), writes P (io
-//     dtype) and the rescale factors to LDS; then each wave accumulates
-//     O[64 heads, D/4 columns] += P V with v_mfma_f32_32x32x16, V being the
-//     same LDS rows (value = key). O never leaves VGPRs until the epilogue
-//     divides by the row sum and stores the io-dtype output and LSE stats.
+//     [id*bs, min(id*bs+bs, act_k, threshold))) and writes the row's token list
+//     as PHYSICAL key rows (key_start offset, or the PA block-table lookup; a -1
+//     block or an out-of-range row becomes the zero row). Replaces the
+//     reference's host-side _expand_block_indices / _pa_to_bsnd (:1012-1051)
+//     and its masked loads (:392-398).
+//  2. sfa_attn_kernel -- one work-group (4 waves, one per SIMD) per (query row,
+//     KV split) covering all (up to 128) heads, so every gathered KV row is
+//     fetched once per row:
+//       * tokens are processed in tiles of 32; a tile's [D | Dr] rows are
+//         gathered with direct-to-LDS 16-byte loads (no VGPR staging) into one
+//         of two LDS buffers while the previous tile is being computed;
+//       * S^T = K Q^T on v_mfma_f32_32x32x16 with tokens as M and 32 heads per
+//         wave as N (Q^T resident in VGPRs): a lane then holds 16 tokens of one
+//         head, so the softmax row max is in-lane plus one lane swap;
+//       * online softmax in fp32 with lazy rescaling: the exponent reference
+//         m_used only moves when a tile's max exceeds it by more than 8 ln 2,
+//         so O is rarely rescaled; the true max is tracked for softmax_max;
+//       * P (io dtype) goes to LDS as [head][token]; each wave then owns a
+//         D/4-column slice of O[128 heads, D] and accumulates P V on
+//         v_mfma_f32_32x32x16, the V^T operand read with ds_read_b64_tr_b16
+//         straight from the gathered rows (value = key);
+//       * O stays in registers; the epilogue divides by the row sum (or, with
+//         several KV splits, writes unnormalised partials for the combine).
+//  3. sfa_combine_kernel -- merges KV-split partials (log-sum-exp weights).
+// Unlike the reference (sparse_flash_attention_triton.py:509-525) the fp32
+// accumulator never round-trips through HBM for unsplit rows.
 #include "dsa_common.hpp"
 
 namespace dsa {
 namespace {
 
 constexpr int DR = 64;
-constexpr int HB = 64;   // heads per work-group
-constexpr int BN = 32;   // tokens per tile
-constexpr int NWAVE = 4;
 
 struct RowInfo {
   int b, s1, aq, ak, threshold;
@@ -49,18 +58,52 @@ __device__ __forceinline__ RowInfo row_info(const SfaArgs& a, int r) {
   return ri;
 }
 
+// ---------------------------------------------------------------- workspace
+struct Ws {
+  int32_t* counts;   // [rows]
+  int32_t* tokens;   // [rows, cap]
+  uint16_t* zero;    // one zero KV row: 512 + Dr elements
+  float* part_o;     // [rows, splits, N1, D]   (splits > 1)
+  float* part_s;     // [rows, splits, N1, 3]   m_used, m_true, l
+};
+
+__host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+__host__ __device__ inline Ws ws_layout(void* base, int rows, int cap, int n1, int d, int splits,
+                                        size_t* total) {
+  char* p = reinterpret_cast<char*>(base);
+  size_t off = 0;
+  Ws w;
+  w.counts = reinterpret_cast<int32_t*>(p + off);
+  off += align256((size_t)rows * 4);
+  w.tokens = reinterpret_cast<int32_t*>(p + off);
+  off += align256((size_t)rows * cap * 4);
+  w.zero = reinterpret_cast<uint16_t*>(p + off);
+  off += align256((size_t)(512 + DR) * 2);
+  w.part_o = reinterpret_cast<float*>(p + off);
+  w.part_s = nullptr;
+  if (splits > 1) {
+    off += align256((size_t)rows * splits * n1 * d * 4);
+    w.part_s = reinterpret_cast<float*>(p + off);
+    off += align256((size_t)rows * splits * n1 * 3 * 4);
+  }
+  if (total) *total = off;
+  return w;
+}
+
 // ---------------------------------------------------------------- kernel 1
 constexpr int TOK_TPB = 256;
 
-__global__ __launch_bounds__(TOK_TPB) void sfa_tokens_kernel(SfaArgs a, int cap, int32_t* counts,
-                                                             int32_t* tokens) {
+__global__ __launch_bounds__(TOK_TPB) void sfa_tokens_kernel(SfaArgs a, int cap, Ws ws) {
   __shared__ int s_first_neg;
   __shared__ int wsum[TOK_TPB / 64];
   const int r = blockIdx.x;
-  const RowInfo ri = row_info(a, r);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (r == 0)
+    for (int i = tid; i < 512 + DR; i += TOK_TPB) ws.zero[i] = 0;
+  const RowInfo ri = row_info(a, r);
   if (!ri.active) {
-    if (tid == 0) counts[r] = 0;
+    if (tid == 0) ws.counts[r] = 0;
     return;
   }
   const int bs = a.sbs;
@@ -86,7 +129,6 @@ __global__ __launch_bounds__(TOK_TPB) void sfa_tokens_kernel(SfaArgs a, int cap,
     const int64_t e = begin + bs < end_lim ? begin + bs : end_lim;
     if (e > begin) my += (int)(e - begin);
   }
-  // block exclusive scan of `my`
   int v = my;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
@@ -102,7 +144,7 @@ __global__ __launch_bounds__(TOK_TPB) void sfa_tokens_kernel(SfaArgs a, int cap,
     tot += wsum[w];
   }
   int pos = off + v - my;
-  int32_t* out = tokens + (int64_t)r * cap;
+  int32_t* out = ws.tokens + (int64_t)r * cap;
   for (int i = i0; i < i1; ++i) {
     const int id = ids[i];
     if (id < 0) continue;
@@ -110,244 +152,424 @@ __global__ __launch_bounds__(TOK_TPB) void sfa_tokens_kernel(SfaArgs a, int cap,
     if (begin >= ri.threshold) continue;
     const int64_t e = begin + bs < end_lim ? begin + bs : end_lim;
     for (int64_t t = begin; t < e; ++t) {
-      int32_t phys;
+      int64_t p;
       if (a.block_table) {
         const int64_t bi = t / a.page_bs;
         const int blk = bi < a.max_blocks ? a.block_table[(int64_t)ri.b * a.max_blocks + bi] : -1;
-        const int64_t p = blk < 0 ? -1 : (int64_t)blk * a.page_bs + t % a.page_bs;
-        phys = (p >= 0 && p < a.key_rows) ? (int32_t)p : -1;
+        p = blk < 0 ? -1 : (int64_t)blk * a.page_bs + t % a.page_bs;
       } else {
-        const int64_t p = (int64_t)a.key_start[ri.b] + t;
-        phys = (t < a.s2 && p < a.key_rows) ? (int32_t)p : -1;
+        p = t < a.s2 ? (int64_t)a.key_start[ri.b] + t : -1;
       }
-      out[pos++] = phys;
+      out[pos++] = (p >= 0 && p < a.key_rows) ? (int32_t)p : -1;
     }
   }
-  if (tid == 0) counts[r] = tot;
+  if (tid == 0) ws.counts[r] = tot;
 }
 
 // ---------------------------------------------------------------- kernel 2
-template <int D> struct AttnCfg {
-  static constexpr int DK = D + DR;           // contraction length of Q K^T
-  static constexpr int KS = DK / 32;          // 16x16x32 k-steps
-  static constexpr int PITCH = DK + 8;        // LDS row pitch (elements)
-  static constexpr int CH_ROW = DK / 8;       // 16-byte chunks per token row
-  static constexpr int CH_TILE = BN * CH_ROW;
-  static constexpr int DW = D / NWAVE;        // output columns per wave
-  static constexpr int NT = DW / 32;          // 32-wide N tiles per wave
-  static constexpr int PP = BN + 8;           // P tile pitch (elements)
+constexpr int NWV = 4;      // waves per work-group (one per SIMD)
+constexpr int HB = 128;     // heads per work-group (N1 <= 128, padded)
+constexpr int BN = 32;      // tokens per tile
+constexpr int PP = BN + 8;  // P tile pitch (elements)
+constexpr int QRP = DR + 8; // Q-rope LDS pitch (elements): 144-byte rows, conflict-free 16-byte reads
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float TAU = 5.545177444479562f;  // 8 ln 2: lazy-rescale threshold
+
+template <int D> struct Cfg {
+  static constexpr int KS = (D + DR) / 16;      // 32x32x16 k-steps of S^T
+  static constexpr int KSN = D / 16;            // of which in the nope part
+  static constexpr int ROW = D * 2 + 128;       // LDS bytes reserved per gathered nope row
+  static constexpr int NOPE = BN * ROW;         // bytes per nope buffer
+  static constexpr int ROPE = BN * DR * 2;      // bytes per rope buffer (4 groups of 8 tokens)
+  static constexpr int DW = D / NWV;            // O columns per wave
+  static constexpr int NT = DW / 32;            // 32-wide N tiles per wave
+  static constexpr int LANES_ROW = D / 8;       // lanes that load one nope row
 };
 
+// Start of token t's nope row inside a buffer: rows are ROW bytes apart and
+// shifted by 32*(t%4) + 16*((t/4)%2) bytes so that (a) the S^T operand reads
+// (8 lanes = 8 tokens, same column) and (b) the transposed V reads (4 tokens x
+// 32 bytes per 16-lane group) both land on distinct LDS banks.
+template <int D> __device__ __forceinline__ int nope_off(int t) {
+  return t * Cfg<D>::ROW + 32 * (t & 3) + 16 * ((t >> 2) & 1);
+}
+// Rope chunk c (8 elements) of token t: groups of 8 tokens, [chunk][token] order,
+// which is what one direct-to-LDS instruction writes for 8 tokens.
+__device__ __forceinline__ int rope_off(int t, int c) { return (t >> 3) * 1024 + (c * 8 + (t & 7)) * 16; }
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint2 ds_read_tr(const void* lds_ptr) {
+  s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(const_cast<void*>(lds_ptr)));
+  return __builtin_bit_cast(uint2, v);
+}
+
+__device__ __forceinline__ void lds_dma16(const void* gptr, void* lds_base) {
+  __builtin_amdgcn_global_load_lds(gptr, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
+}
+
+// Token indices of one tile for this wave: 8 wave-uniform nope rows (scalar
+// loads) and one per-lane rope row (lane -> token wave*8 + lane%8). Loaded one
+// tile ahead so issuing the gather never waits on them.
+struct TileIdx {
+  int nope[8];
+  int rope;
+};
+
+__device__ __forceinline__ TileIdx load_idx(const int32_t* toks, int nvalid, int wave_u, int lane) {
+  TileIdx ix;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int t = wave_u * 8 + i;
+    ix.nope[i] = __builtin_amdgcn_readfirstlane(toks[t < nvalid ? t : 0]);  // tail slots re-read a valid row
+  }
+  const int t = wave_u * 8 + (lane & 7);
+  ix.rope = toks[t < nvalid ? t : 0];
+  return ix;
+}
+
+// Issue the gather of one tile: wave w loads tokens 8w..8w+7 (one nope row per
+// instruction, D/8 lanes) and their rope chunks (one instruction for the 8 tokens).
+template <int D>
+__device__ __forceinline__ void gather_tile(const uint16_t* kb, const uint16_t* krb,
+                                            const uint16_t* zero, const TileIdx& ix, uint8_t* nope,
+                                            uint8_t* rope, int wave_u, int lane) {
+  using C = Cfg<D>;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int phys = ix.nope[i];
+    const uint16_t* src = phys >= 0 ? kb + (int64_t)phys * D : zero;
+    if (lane < C::LANES_ROW) lds_dma16(src + lane * 8, nope + nope_off<D>(wave_u * 8 + i));
+  }
+  const uint16_t* src = ix.rope >= 0 ? krb + (int64_t)ix.rope * DR : zero + 512;
+  lds_dma16(src + (lane >> 3) * 8, rope + wave_u * 1024);
+}
+
+// o *= f on an accumulator element kept in an AGPR (VALU cannot read AGPRs):
+// read it into one temporary VGPR, scale, write it back.
+__device__ __forceinline__ float agpr_scale(float o, float f) {
+  float t;
+  asm volatile("v_accvgpr_read_b32 %1, %0\n\tv_mul_f32 %1, %1, %2\n\tv_accvgpr_write_b32 %0, %1"
+               : "+a"(o), "=&v"(t)
+               : "v"(f));
+  return o;
+}
+
+__device__ __forceinline__ void wait_all() { __builtin_amdgcn_s_waitcnt(0); }  // vm, lgkm, exp counters 0
+
 template <int IO, int D>
-__global__ __launch_bounds__(NWAVE * 64) void sfa_attn_kernel(SfaArgs a, int cap,
-                                                              const int32_t* counts,
-                                                              const int32_t* tokens) {
-  using C = AttnCfg<D>;
-  __shared__ __attribute__((aligned(16))) uint16_t kv[BN * C::PITCH];
-  __shared__ __attribute__((aligned(16))) uint16_t pt[HB * C::PP];
+__global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, int splits, Ws ws) {
+  using C = Cfg<D>;
+  __shared__ __attribute__((aligned(16))) uint8_t nope0[C::NOPE];
+  __shared__ __attribute__((aligned(16))) uint8_t nope1[C::NOPE];
+  __shared__ __attribute__((aligned(16))) uint8_t rope0[C::ROPE];
+  __shared__ __attribute__((aligned(16))) uint8_t rope1[C::ROPE];
+  __shared__ __attribute__((aligned(16))) uint16_t pt[HB * PP];
+  __shared__ __attribute__((aligned(16))) uint16_t qrs[HB * QRP];   // Q rope of all heads
   __shared__ float s_alpha[HB];
   __shared__ float s_l[HB];
-  __shared__ int s_tok[BN];
+  __shared__ int s_flag[2];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = blockIdx.x;
-  const int h0 = blockIdx.y * HB;
-  const int ntok = counts[r];
-  const int32_t* toks = tokens + (int64_t)r * cap;
+  const int sp = blockIdx.y;
+  const int ntok_all = ws.counts[r];
+  // this split's token range, in whole tiles
+  const int per = ((ntok_all + splits - 1) / splits + BN - 1) / BN * BN;
+  const int t_beg = sp * per;
+  const int t_end = (t_beg + per < ntok_all ? t_beg + per : ntok_all);
+  const int ntok = t_end > t_beg ? t_end - t_beg : 0;
+  const int32_t* toks = ws.tokens + (int64_t)r * cap + t_beg;
   uint16_t* out = reinterpret_cast<uint16_t*>(a.out);
+  const int n1 = a.n1;
 
-  if (ntok == 0) {  // skipped row: zeros (out, stats)
-    for (int i = threadIdx.x; i < HB * D; i += NWAVE * 64) {
-      const int h = h0 + i / D;
-      if (h < a.n1) out[((int64_t)r * a.n1 + h) * D + (i % D)] = 0;
-    }
-    if (a.sm_max && threadIdx.x < HB && h0 + (int)threadIdx.x < a.n1) {
-      a.sm_max[(int64_t)r * a.n1 + h0 + threadIdx.x] = 0.f;
-      a.sm_sum[(int64_t)r * a.n1 + h0 + threadIdx.x] = 0.f;
+  if (ntok == 0) {
+    if (splits == 1) {  // skipped row: zeros (out, stats)
+      for (int i = threadIdx.x; i < n1 * D; i += NWV * 64) out[(int64_t)r * n1 * D + i] = 0;
+      if (a.sm_max)
+        for (int h = threadIdx.x; h < n1; h += NWV * 64) {
+          a.sm_max[(int64_t)r * n1 + h] = 0.f;
+          a.sm_sum[(int64_t)r * n1 + h] = 0.f;
+        }
+    } else {
+      float* ps = ws.part_s + ((int64_t)r * splits + sp) * n1 * 3;
+      for (int h = threadIdx.x; h < n1; h += NWV * 64) {
+        ps[h * 3 + 0] = -INFINITY;
+        ps[h * 3 + 1] = -INFINITY;
+        ps[h * 3 + 2] = 0.f;
+      }
     }
     return;
   }
 
-  // ---- Q fragments (A of S = Q K^T): 16 heads per wave, 16x16x32 layout
-  const int hq = h0 + wave * 16 + (lane & 15);
-  const uint16_t* qn = reinterpret_cast<const uint16_t*>(a.q) + ((int64_t)r * a.n1 + hq) * D;
-  const uint16_t* qr = reinterpret_cast<const uint16_t*>(a.qr) + ((int64_t)r * a.n1 + hq) * DR;
-  uint4 qf[C::KS];
+  const uint16_t* kb = reinterpret_cast<const uint16_t*>(a.k);
+  const uint16_t* krb = reinterpret_cast<const uint16_t*>(a.kr);
+  const int ntiles = (ntok + BN - 1) / BN;
+
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  // ---- start the first gather, then load Q^T (B operand of S^T) for this wave's 32 heads
+  TileIdx ix_next = load_idx(toks, ntok < BN ? ntok : BN, wave_u, lane);
+  gather_tile<D>(kb, krb, ws.zero, ix_next, nope0, rope0, wave_u, lane);
+  if (ntiles > 1) ix_next = load_idx(toks + BN, ntok - BN < BN ? ntok - BN : BN, wave_u, lane);
+
+  const int hq = wave * 32 + (lane & 31);
+  const uint16_t* qn = reinterpret_cast<const uint16_t*>(a.q) + ((int64_t)r * n1 + hq) * D;
+  uint4 qf[C::KSN];   // nope part in VGPRs; the rope part goes to LDS (qrs)
 #pragma unroll
-  for (int ks = 0; ks < C::KS; ++ks) {
-    const int e = ks * 32 + (lane >> 4) * 8;
-    if (hq < a.n1)
-      qf[ks] = e < D ? ldg16(qn + e) : ldg16(qr + (e - D));
-    else
-      qf[ks] = make_uint4(0, 0, 0, 0);
+  for (int ks = 0; ks < C::KSN; ++ks)
+    qf[ks] = hq < n1 ? ldg16(qn + ks * 16 + (lane >> 5) * 8) : make_uint4(0, 0, 0, 0);
+  for (int c = threadIdx.x; c < HB * (DR / 8); c += NWV * 64) {
+    const int h = c / (DR / 8), e = (c % (DR / 8)) * 8;
+    *reinterpret_cast<uint4*>(qrs + h * QRP + e) =
+        h < n1 ? ldg16(reinterpret_cast<const uint16_t*>(a.qr) + ((int64_t)r * n1 + h) * DR + e)
+               : make_uint4(0, 0, 0, 0);
   }
 
-  constexpr float LOG2E = 1.4426950408889634f;
-  float m_run[4], l_part[4];
+  float m_used = -INFINITY, m_true = -INFINITY, l_part = 0.f;
+  {
+    // An AGPR operand makes the backend select the AGPR-accumulator MFMA form,
+    // so O lives in AGPRs and the 256 arch VGPRs stay free for Q^T and operands.
+    float agpr_hint = 0.f;
+    asm volatile("" : "+a"(agpr_hint));
+  }
+  f32x16 o[4][C::NT];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) { m_run[i] = -INFINITY; l_part[i] = 0.f; }
-  f32x16 o[2][C::NT];
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+  for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int nt = 0; nt < C::NT; ++nt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) o[mt][nt][i] = 0.f;
+  if (threadIdx.x < 2) s_flag[threadIdx.x] = 0;
 
-  const uint16_t* kbase = reinterpret_cast<const uint16_t*>(a.k);
-  const uint16_t* krbase = reinterpret_cast<const uint16_t*>(a.kr);
-  const int ntiles = (ntok + BN - 1) / BN;
-
-  for (int t = 0; t < ntiles; ++t) {
+  auto tile = [&](int t, const uint8_t* nope, const uint8_t* rope, uint8_t* nope_nx,
+                  uint8_t* rope_nx) {
+    wait_all();
+    __syncthreads();  // tile t resident; every wave finished tile t-1 (pt, s_alpha, other buffer free)
     const int tb = t * BN;
     const int nvalid = ntok - tb < BN ? ntok - tb : BN;
-    if (threadIdx.x < BN) s_tok[threadIdx.x] = threadIdx.x < nvalid ? toks[tb + threadIdx.x] : -1;
-    __syncthreads();
-    // ---- gather the tile's rows [D | Dr] into LDS
-    for (int ch = threadIdx.x; ch < C::CH_TILE; ch += NWAVE * 64) {
-      const int tk = ch / C::CH_ROW, part = ch % C::CH_ROW;
-      const int phys = s_tok[tk];
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (phys >= 0) {
-        const int e = part * 8;
-        v = e < D ? ldg16(kbase + (int64_t)phys * D + e) : ldg16(krbase + (int64_t)phys * DR + (e - D));
+    if (threadIdx.x == 0) s_flag[(t + 1) & 1] = 0;
+    if (t + 1 < ntiles) {
+      gather_tile<D>(kb, krb, ws.zero, ix_next, nope_nx, rope_nx, wave_u, lane);
+      if (t + 2 < ntiles) {
+        const int tb2 = tb + 2 * BN;
+        ix_next = load_idx(toks + tb2, ntok - tb2 < BN ? ntok - tb2 : BN, wave_u, lane);
       }
-      *reinterpret_cast<uint4*>(&kv[tk * C::PITCH + part * 8]) = v;
     }
-    __syncthreads();
-
-    // ---- S = Q K^T for this wave's 16 heads x 32 tokens
-    f32x4 s[2];
+    // ---- S^T[32 tokens, 32 heads] for this wave
+    f32x16 s = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const int tr = lane & 31, kg = lane >> 5;
+    const uint8_t* arow = nope + nope_off<D>(tr) + kg * 16;
+    // operand loads run 4 k-steps ahead of the MFMA chain; the sched barrier
+    // keeps that order (hoisting every load would cost ~4 VGPRs per k-step)
+    auto a_frag = [&](int ks) -> uint4 {
+      return ks < C::KSN ? *reinterpret_cast<const uint4*>(arow + ks * 32)
+                         : *reinterpret_cast<const uint4*>(rope + rope_off(tr, (ks - C::KSN) * 2 + kg));
+    };
+    uint4 af[4];
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      s[sub] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const uint16_t* bp = &kv[(sub * 16 + (lane & 15)) * C::PITCH + (lane >> 4) * 8];
+    for (int j = 0; j < 4; ++j) af[j] = a_frag(j);
 #pragma unroll
-      for (int ks = 0; ks < C::KS; ++ks)
-        s[sub] = Mfma<IO>::m16(qf[ks], *reinterpret_cast<const uint4*>(bp + ks * 32), s[sub]);
+    for (int ks = 0; ks < C::KS; ++ks) {
+      const uint4 bq = ks < C::KSN ? qf[ks]
+                                   : *reinterpret_cast<const uint4*>(qrs + hq * QRP + (ks - C::KSN) * 16 + kg * 8);
+      s = Mfma<IO>::m32(af[ks & 3], bq, s);
+      if (ks + 4 < C::KS) af[ks & 3] = a_frag(ks + 4);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    // lane holds heads wave*16 + (lane>>4)*4 + i, tokens sub*16 + (lane&15)
-    float alpha[4];
+    // ---- online softmax for head hq over this tile (lane holds 16 tokens)
+    float mx = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      // x = score * scale in natural units, so m_run is exactly the golden's max
-      const float x0 = (lane & 15) < nvalid ? s[0][i] * a.scale : -INFINITY;
-      const float x1 = 16 + (lane & 15) < nvalid ? s[1][i] * a.scale : -INFINITY;
-      float mx = fmaxf(x0, x1);
-#pragma unroll
-      for (int o2 = 1; o2 < 16; o2 <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o2));
-      const float mnew = fmaxf(m_run[i], mx);  // finite: token 0 of every tile is valid
-      alpha[i] = exp2f((m_run[i] - mnew) * LOG2E);
-      m_run[i] = mnew;
-      const float p0 = exp2f((x0 - mnew) * LOG2E), p1 = exp2f((x1 - mnew) * LOG2E);
-      l_part[i] = l_part[i] * alpha[i] + p0 + p1;
-      const int hl = wave * 16 + (lane >> 4) * 4 + i;
-      pt[hl * C::PP + (lane & 15)] = from_f32<IO>(p0);
-      pt[hl * C::PP + 16 + (lane & 15)] = from_f32<IO>(p1);
-      if ((lane & 15) == 0) s_alpha[hl] = alpha[i];
+    for (int i = 0; i < 16; ++i) {
+      const int tk = (i >> 2) * 8 + kg * 4 + (i & 3);
+      s[i] = tk < nvalid ? s[i] * a.scale : -INFINITY;
+      mx = fmaxf(mx, s[i]);
     }
-    __syncthreads();
-
-    // ---- O[64 heads, this wave's D/4 columns] = alpha * O + P V
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      float al[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) al[i] = s_alpha[mt * 32 + m32_row(i, lane)];
-#pragma unroll
-      for (int nt = 0; nt < C::NT; ++nt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) o[mt][nt][i] *= al[i];
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    m_true = fmaxf(m_true, mx);
+    float alpha = 1.f;
+    if (mx > m_used + TAU) {
+      alpha = exp2f((m_used - mx) * LOG2E);
+      m_used = mx;
     }
+    float psum = 0.f;
+    uint16_t* prow = pt + hq * PP + kg * 4;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      uint32_t w2[2];
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const float p0 = exp2f((s[g * 4 + h2 * 2] - m_used) * LOG2E);
+        const float p1 = exp2f((s[g * 4 + h2 * 2 + 1] - m_used) * LOG2E);
+        psum += p0 + p1;
+        w2[h2] = (uint32_t)from_f32<IO>(p0) | ((uint32_t)from_f32<IO>(p1) << 16);
+      }
+      *reinterpret_cast<uint2*>(prow + g * 8) = make_uint2(w2[0], w2[1]);
+    }
+    l_part = l_part * alpha + psum;
+    if (lane < 32) s_alpha[hq] = alpha;
+    if (alpha != 1.f) s_flag[t & 1] = 1;
+    __syncthreads();  // P, alpha and the flag of tile t complete
+    // ---- O[128 heads, this wave's D/4 columns] = alpha * O + P V
+    if (s_flag[t & 1]) {
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float al = s_alpha[mt * 32 + m32_row(i, lane)];
+#pragma unroll
+          for (int nt = 0; nt < C::NT; ++nt) o[mt][nt][i] = agpr_scale(o[mt][nt][i], al);
+        }
+    }
+    const int g16 = lane >> 4, c16 = lane & 15;
 #pragma unroll
     for (int kq = 0; kq < BN / 16; ++kq) {
-      uint4 pa[2];
+      uint4 pa[4];
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-        pa[mt] = *reinterpret_cast<const uint4*>(&pt[(mt * 32 + (lane & 31)) * C::PP + kq * 16 + (lane >> 5) * 8]);
+      for (int mt = 0; mt < 4; ++mt)
+        pa[mt] = *reinterpret_cast<const uint4*>(pt + (mt * 32 + (lane & 31)) * PP + kq * 16 + kg * 8);
 #pragma unroll
       for (int nt = 0; nt < C::NT; ++nt) {
-        const int dcol = wave * C::DW + nt * 32 + (lane & 31);
-        const uint16_t* vp = &kv[(kq * 16 + (lane >> 5) * 8) * C::PITCH + dcol];
-        uint32_t w[4];
+        const int col = wave * C::DW + nt * 32 + (g16 & 1) * 16 + 4 * (c16 & 3);
+        const int tok0 = kq * 16 + (g16 >> 1) * 8 + (c16 >> 2);
+        const uint2 lo = ds_read_tr(nope + nope_off<D>(tok0) + col * 2);
+        const uint2 hi = ds_read_tr(nope + nope_off<D>(tok0 + 4) + col * 2);
+        const uint4 vb = make_uint4(lo.x, lo.y, hi.x, hi.y);
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          w[j] = (uint32_t)vp[(2 * j) * C::PITCH] | ((uint32_t)vp[(2 * j + 1) * C::PITCH] << 16);
-        const uint4 vb = make_uint4(w[0], w[1], w[2], w[3]);
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) o[mt][nt] = Mfma<IO>::m32(pa[mt], vb, o[mt][nt]);
+        for (int mt = 0; mt < 4; ++mt) o[mt][nt] = Mfma<IO>::m32(pa[mt], vb, o[mt][nt]);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
-    __syncthreads();
+  };
+
+  for (int t = 0; t < ntiles; t += 2) {
+    tile(t, nope0, rope0, nope1, rope1);
+    if (t + 1 < ntiles) tile(t + 1, nope1, rope1, nope0, rope0);
   }
 
-  // ---- epilogue: finish row sums, normalise, store
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float l = l_part[i];
-#pragma unroll
-    for (int o2 = 1; o2 < 16; o2 <<= 1) l += __shfl_xor(l, o2);
-    const int hl = wave * 16 + (lane >> 4) * 4 + i;
-    if ((lane & 15) == 0) {
-      s_l[hl] = l;
-      const int h = h0 + hl;
-      if (a.sm_max && h < a.n1) {
-        a.sm_max[(int64_t)r * a.n1 + h] = m_run[i];
-        a.sm_sum[(int64_t)r * a.n1 + h] = l;
-      }
+  // ---- epilogue
+  const float l_tot = l_part + __shfl_xor(l_part, 32);
+  __syncthreads();  // all PV reads of s_alpha / pt done before s_l is written
+  if (lane < 32) s_l[hq] = l_tot;
+  if (splits == 1) {
+    if (lane < 32 && hq < n1 && a.sm_max) {
+      a.sm_max[(int64_t)r * n1 + hq] = m_true;
+      a.sm_sum[(int64_t)r * n1 + hq] = l_tot * exp2f((m_used - m_true) * LOG2E);
     }
+  } else if (lane < 32 && hq < n1) {
+    float* ps = ws.part_s + (((int64_t)r * splits + sp) * n1 + hq) * 3;
+    ps[0] = m_used;
+    ps[1] = m_true;
+    ps[2] = l_tot;
   }
   __syncthreads();
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
+  for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int hl = mt * 32 + m32_row(i, lane);
-      const int h = h0 + hl;
-      if (h >= a.n1) continue;
-      const float inv = 1.f / s_l[hl];
+      const int h = mt * 32 + m32_row(i, lane);
+      if (h >= n1) continue;
+      if (splits == 1) {
+        const float inv = 1.f / s_l[h];
+        uint16_t* orow = out + ((int64_t)r * n1 + h) * D + wave * C::DW + (lane & 31);
 #pragma unroll
-      for (int nt = 0; nt < C::NT; ++nt) {
-        const int dcol = wave * C::DW + nt * 32 + (lane & 31);
-        out[((int64_t)r * a.n1 + h) * D + dcol] = from_f32<IO>(o[mt][nt][i] * inv);
+        for (int nt = 0; nt < C::NT; ++nt) orow[nt * 32] = from_f32<IO>(o[mt][nt][i] * inv);
+      } else {
+        float* prow = ws.part_o + (((int64_t)r * splits + sp) * n1 + h) * D + wave * C::DW + (lane & 31);
+#pragma unroll
+        for (int nt = 0; nt < C::NT; ++nt) prow[nt * 32] = o[mt][nt][i];
       }
     }
   }
 }
 
+// ---------------------------------------------------------------- kernel 3
 template <int IO>
-hipError_t launch_attn(const SfaArgs& a, hipStream_t s, int cap, const int32_t* counts,
-                       const int32_t* tokens) {
-  dim3 grid(a.total_rows, (a.n1 + HB - 1) / HB), block(NWAVE * 64);
-  switch (a.d) {
-    case 128: hipLaunchKernelGGL((sfa_attn_kernel<IO, 128>), grid, block, 0, s, a, cap, counts, tokens); break;
-    case 256: hipLaunchKernelGGL((sfa_attn_kernel<IO, 256>), grid, block, 0, s, a, cap, counts, tokens); break;
-    case 512: hipLaunchKernelGGL((sfa_attn_kernel<IO, 512>), grid, block, 0, s, a, cap, counts, tokens); break;
-    default: return hipErrorInvalidValue;
+__global__ __launch_bounds__(256) void sfa_combine_kernel(SfaArgs a, int splits, Ws ws) {
+  const int r = blockIdx.x;
+  const int h = blockIdx.y;
+  const int n1 = a.n1, D = a.d;
+  const float* ps = ws.part_s + (int64_t)r * splits * n1 * 3;
+  float M = -INFINITY, mt = -INFINITY;
+  for (int s = 0; s < splits; ++s) {
+    const float* q = ps + ((int64_t)s * n1 + h) * 3;
+    if (q[2] > 0.f) {
+      M = fmaxf(M, q[0]);
+      mt = fmaxf(mt, q[1]);
+    }
   }
+  float L = 0.f;
+  for (int s = 0; s < splits; ++s) {
+    const float* q = ps + ((int64_t)s * n1 + h) * 3;
+    if (q[2] > 0.f) L += q[2] * exp2f((q[0] - M) * LOG2E);
+  }
+  uint16_t* orow = reinterpret_cast<uint16_t*>(a.out) + ((int64_t)r * n1 + h) * D;
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  for (int d = threadIdx.x; d < D; d += 256) {
+    float acc = 0.f;
+    for (int s = 0; s < splits; ++s) {
+      const float* q = ps + ((int64_t)s * n1 + h) * 3;
+      if (q[2] > 0.f)
+        acc += ws.part_o[(((int64_t)r * splits + s) * n1 + h) * D + d] * exp2f((q[0] - M) * LOG2E);
+    }
+    orow[d] = from_f32<IO>(acc * inv);
+  }
+  if (threadIdx.x == 0 && a.sm_max) {
+    a.sm_max[(int64_t)r * n1 + h] = L > 0.f ? mt : 0.f;
+    a.sm_sum[(int64_t)r * n1 + h] = L > 0.f ? L * exp2f((M - mt) * LOG2E) : 0.f;
+  }
+}
+
+template <int IO, int D>
+hipError_t launch_attn_d(const SfaArgs& a, hipStream_t s, int cap, int splits, Ws ws) {
+  hipLaunchKernelGGL((sfa_attn_kernel<IO, D>), dim3(a.total_rows, splits), dim3(NWV * 64), 0, s, a,
+                     cap, splits, ws);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || splits == 1) return e;
+  hipLaunchKernelGGL((sfa_combine_kernel<IO>), dim3(a.total_rows, a.n1), dim3(256), 0, s, a, splits, ws);
   return hipGetLastError();
+}
+
+template <int IO>
+hipError_t launch_attn(const SfaArgs& a, hipStream_t s, int cap, int splits, Ws ws) {
+  switch (a.d) {
+    case 128: return launch_attn_d<IO, 128>(a, s, cap, splits, ws);
+    case 256: return launch_attn_d<IO, 256>(a, s, cap, splits, ws);
+    case 512: return launch_attn_d<IO, 512>(a, s, cap, splits, ws);
+  }
+  return hipErrorInvalidValue;
 }
 
 }  // namespace
 }  // namespace dsa
 
-static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+// KV splits: unsplit for prefill-sized row counts; few rows (decode) are split so
+// the grid covers the 256 CUs, keeping at least 4 tiles per split.
+static int sfa_splits(int total_rows, int cap, int kv_splits) {
+  if (kv_splits > 0) return kv_splits;
+  if (total_rows >= 256) return 1;
+  int s = (256 + total_rows - 1) / total_rows;
+  const int max_s = cap / (4 * 32);
+  if (s > max_s) s = max_s;
+  if (s > 16) s = 16;
+  return s < 1 ? 1 : s;
+}
 
 size_t sfa_workspace_bytes(int total_rows, int n1, int d, int topk, int sbs, int kv_splits) {
-  (void)n1; (void)d; (void)kv_splits;
-  const size_t cap = (size_t)topk * (size_t)sbs;
-  return align256((size_t)total_rows * 4) + align256((size_t)total_rows * cap * 4);
+  const int cap = topk * sbs;
+  size_t total = 0;
+  dsa::ws_layout(nullptr, total_rows, cap, n1, d, sfa_splits(total_rows, cap, kv_splits), &total);
+  return total;
 }
 
 hipError_t launch_sfa_fwd(const SfaArgs& a, hipStream_t s) {
   if (a.total_rows <= 0) return hipSuccess;
   const int cap = a.topk * a.sbs;
-  int32_t* counts = reinterpret_cast<int32_t*>(a.ws);
-  int32_t* tokens = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(a.ws) + align256((size_t)a.total_rows * 4));
-  hipLaunchKernelGGL(dsa::sfa_tokens_kernel, dim3(a.total_rows), dim3(dsa::TOK_TPB), 0, s, a, cap,
-                     counts, tokens);
+  const int splits = sfa_splits(a.total_rows, cap, a.kv_splits);
+  dsa::Ws ws = dsa::ws_layout(a.ws, a.total_rows, cap, a.n1, a.d, splits, nullptr);
+  hipLaunchKernelGGL(dsa::sfa_tokens_kernel, dim3(a.total_rows), dim3(dsa::TOK_TPB), 0, s, a, cap, ws);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  return a.io == dsa::IO_BF16 ? dsa::launch_attn<dsa::IO_BF16>(a, s, cap, counts, tokens)
-                              : dsa::launch_attn<dsa::IO_F16>(a, s, cap, counts, tokens);
+  return a.io == dsa::IO_BF16 ? dsa::launch_attn<dsa::IO_BF16>(a, s, cap, splits, ws)
+                              : dsa::launch_attn<dsa::IO_F16>(a, s, cap, splits, ws);
 }
