@@ -26,8 +26,14 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
 SOURCES = ["li_score.hip", "li_topk.hip", "sfa_fwd.hip", "capi.cpp"]
 
 
+# Kernels whose float code never relies on NaN propagation: lets fmaxf lower to a
+# single v_max_f32 without the IEEE-mode canonicalisation of each operand.
+NO_NANS = {"li_score.hip", "sfa_fwd.hip"}
+
+
 def _compile(src: Path, obj: Path) -> None:
-    cmd = [HIPCC, *COMMON, "-x", "hip", "-c", str(src), "-o", str(obj)]
+    extra = ["-fno-honor-nans"] if src.name in NO_NANS else []
+    cmd = [HIPCC, *COMMON, *extra, "-x", "hip", "-c", str(src), "-o", str(obj)]
     p = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in p.stderr.splitlines() if noise not in l)

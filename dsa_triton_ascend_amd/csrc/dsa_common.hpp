@@ -24,18 +24,30 @@ enum IoType { IO_F16 = DSA_DTYPE_F16, IO_BF16 = DSA_DTYPE_BF16 };
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __uint_as_float(((uint32_t)h) << 16);
 }
-// Round-to-nearest-even fp32 -> bf16 on the bit pattern: add 0x7FFF plus the
-// lsb of the kept half, then truncate (same rule as the numpy golden).
+// Round-to-nearest-even fp32 -> bf16 (gfx950 v_cvt_pk_bf16_f32). For finite
+// inputs this equals the golden's bit rule (add 0x7FFF plus the lsb of the kept
+// half, then truncate), lightning_indexer_numpy.py:20-24.
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
-  uint32_t u = __float_as_uint(f);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {
   return (float)__builtin_bit_cast(_Float16, h);
 }
 __device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
   return __builtin_bit_cast(uint16_t, (_Float16)f);  // v_cvt_f16_f32, RNE
+}
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two fp32 values -> two RNE-rounded 16-bit values packed in one dword (lo = a).
+template <int IO> __device__ __forceinline__ uint32_t pack2(float a, float b) {
+  const f32x2_t v = {a, b};
+  if constexpr (IO == DSA_DTYPE_BF16)
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+  else
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_t));
 }
 
 template <int IO> __device__ __forceinline__ float to_f32(uint16_t h) {

@@ -9,17 +9,22 @@
 //
 // Mapping onto CDNA4:
 //  * one wave owns one query row; the row's G heads are the MFMA M dimension
-//    (MT tiles of 32 heads), keys are N (32 per MFMA), D is the contraction.
-//    v_mfma_f32_32x32x16_{bf16,f16}, fp32 accumulation.
-//  * the row's Q fragments stay in VGPRs for the whole key sweep (MT*D <= 512),
+//    (MT tiles of 32 heads), keys are N (32 per MFMA), D is the contraction:
+//    v_mfma_f32_32x32x16_{bf16,f16} with fp32 accumulation;
+//  * the row's Q fragments stay in VGPRs for the whole key sweep (MT <= 2, MT*D <= 512),
 //    otherwise they are re-read from L2 per key tile;
 //  * a work-group = NW waves = NW consecutive query rows of one (batch, n2);
-//    they share each K tile, staged global -> VGPR -> LDS with a one-tile
-//    register prefetch and two LDS buffers (one barrier per tile); LDS rows are
-//    padded by 16 B so the 16-byte B-fragment reads are conflict-free;
+//    they share each 64-key K tile, staged global -> VGPR -> LDS with a
+//    one-tile register prefetch and two LDS buffers (one barrier per tile);
+//    LDS rows are padded by 16 B so the 16-byte B-fragment reads are
+//    conflict-free;
+//  * per tile a wave issues its B-fragment reads ahead of the MFMAs and keeps
+//    one accumulator set per 32-key subtile, so the epilogue of one subtile can
+//    overlap the MFMAs of the next;
 //  * the epilogue is fused: relu(acc) * w[head] summed over the 16 heads a lane
-//    holds and the MT tiles, then one cross-lane add (lanes l and l^32) gives
-//    the per-key score; fully causal-masked tiles are never loaded or computed;
+//    holds and the MT tiles (four independent partial sums), then one
+//    cross-lane add (lanes l and l^32) gives the per-key score; fully causal-
+//    masked tiles are never loaded or computed;
 //  * row blocks are issued heaviest-first (largest s1 first) to flatten the
 //    causal triangle's tail.
 #include "dsa_common.hpp"
@@ -28,14 +33,13 @@ namespace dsa {
 
 namespace {
 
-constexpr int NW = 4;  // waves (= query rows) per work-group
+constexpr int NW = 8;  // waves (= query rows) per work-group
 
 template <int D> struct LiTile {
   static constexpr int BN = D <= 128 ? 64 : 32;        // keys per LDS tile
   static constexpr int PITCH = D + 8;                  // uint16 elements per LDS key row
   static constexpr int CHUNKS = BN * D / 8;            // 16-byte chunks per tile
-  static constexpr int CPT = CHUNKS / (NW * 64);       // chunks per thread
-  static_assert(CHUNKS % (NW * 64) == 0, "tile must split evenly over the work-group");
+  static constexpr int CPT = (CHUNKS + NW * 64 - 1) / (NW * 64);   // chunks per thread
 };
 
 __device__ __forceinline__ float load_w(const void* w, int wdt, int64_t i) {
@@ -61,7 +65,8 @@ template <int IO, int D, int MT>
 __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
   using T = LiTile<D>;
   constexpr int KK = D / 16;                 // MFMA k-steps
-  constexpr bool QREG = MT * D <= 512;       // Q fragments resident in VGPRs
+  constexpr int NSUB = T::BN / 32;           // 32-key subtiles per tile
+  constexpr bool QREG = MT <= 2 && MT * D <= 512;   // Q fragments resident in VGPRs
   __shared__ __attribute__((aligned(16))) uint16_t kt[2][T::BN * T::PITCH];
 
   const int lane = threadIdx.x & 63;
@@ -83,33 +88,14 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
   const int s1 = s1_0 + wave;
   const bool row_ok = s1 < nrows;
   const int L_row = row_ok ? visible_len(s1, aq, ak, a.s2, a.sparse_mode) : 0;
-  const int64_t r = (int64_t)a.row_start[b] + s1;
+  const int64_t r = (int64_t)a.row_start[b] + (row_ok ? s1 : s1_0);
 
   const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.q) + (r * a.n1 + (int64_t)n2 * G) * D;
   const uint16_t* kbase = reinterpret_cast<const uint16_t*>(a.k) +
                           ((int64_t)a.key_start[b] * a.n2 + n2) * D;
   const int64_t kstride = (int64_t)a.n2 * D;
 
-  // ---- per-row operands: Q fragments (A) and head weights
-  uint4 qf[QREG ? MT : 1][QREG ? KK : 1];
-  float wv[MT][16];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = mt * 32 + (lane & 31);
-    if constexpr (QREG) {
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk)
-        qf[mt][kk] = (row_ok && m < G) ? ldg16(qrow + (int64_t)m * D + kk * 16 + (lane >> 5) * 8)
-                                       : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int h = mt * 32 + m32_row(i, lane);
-      wv[mt][i] = (row_ok && h < G) ? load_w(a.w, a.wdt, r * a.n1 + (int64_t)n2 * G + h) : 0.f;
-    }
-  }
-
-  // ---- K tile staging
+  // ---- K tile staging (started first so its latency overlaps the Q / w loads)
   const int ntiles = (L_blk + T::BN - 1) / T::BN;
   uint4 pre[T::CPT];
   auto fetch = [&](int tile) {
@@ -118,59 +104,107 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
       const int ch = threadIdx.x + c * NW * 64;
       const int key = ch / (D / 8), off = (ch % (D / 8)) * 8;
       const int s2 = tile * T::BN + key;
-      pre[c] = s2 < L_blk ? ldg16(kbase + (int64_t)s2 * kstride + off) : make_uint4(0, 0, 0, 0);
+      pre[c] = (ch < T::CHUNKS && s2 < L_blk) ? ldg16(kbase + (int64_t)s2 * kstride + off)
+                                              : make_uint4(0, 0, 0, 0);
     }
   };
   auto stash = [&](int buf) {
 #pragma unroll
     for (int c = 0; c < T::CPT; ++c) {
       const int ch = threadIdx.x + c * NW * 64;
-      const int key = ch / (D / 8), off = (ch % (D / 8)) * 8;
-      *reinterpret_cast<uint4*>(&kt[buf][key * T::PITCH + off]) = pre[c];
+      if (ch < T::CHUNKS) {
+        const int key = ch / (D / 8), off = (ch % (D / 8)) * 8;
+        *reinterpret_cast<uint4*>(&kt[buf][key * T::PITCH + off]) = pre[c];
+      }
     }
   };
+  fetch(0);
+
+  // ---- per-row operands: Q fragments (A) and head weights
+  uint4 qf[QREG ? MT : 1][QREG ? KK : 1];
+  if constexpr (QREG) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = mt * 32 + (lane & 31);
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk)
+        qf[mt][kk] = (row_ok && m < G) ? ldg16(qrow + (int64_t)m * D + kk * 16 + (lane >> 5) * 8)
+                                       : make_uint4(0, 0, 0, 0);
+    }
+  }
+  // weights: one coalesced load per lane (head = lane + 64 j), then each lane
+  // gathers the 16 heads it holds in the MFMA output layout with lane shuffles
+  float wv[MT][16];
+  {
+    constexpr int WJ = (MT * 32 + 63) / 64;
+    float wl[WJ];
+#pragma unroll
+    for (int j = 0; j < WJ; ++j) {
+      const int h = lane + 64 * j;
+      wl[j] = (row_ok && h < G) ? load_w(a.w, a.wdt, r * a.n1 + (int64_t)n2 * G + h) : 0.f;
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int h = mt * 32 + m32_row(i, lane);
+        const float v = __shfl(wl[(mt * 32) / 64], h & 63);
+        wv[mt][i] = v;
+      }
+  }
 
   uint16_t* srow = a.scores + (r * a.n2 + n2) * a.ld;
-  fetch(0);
   stash(0);
   __syncthreads();
   for (int t = 0; t < ntiles; ++t) {
     const int buf = t & 1;
     if (t + 1 < ntiles) fetch(t + 1);
+    if (t * T::BN < L_row) {  // wave-uniform: this row sees part of the tile
+      f32x16 acc[NSUB][MT];
 #pragma unroll
-    for (int sub = 0; sub < T::BN / 32; ++sub) {
-      const int key0 = t * T::BN + sub * 32;
-      if (key0 >= L_row) continue;  // wave-uniform: fully masked for this row
-      f32x16 acc[MT];
+      for (int sub = 0; sub < NSUB; ++sub)
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) acc[mt][i] = 0.f;
-      const uint16_t* bp = &kt[buf][(sub * 32 + (lane & 31)) * T::PITCH + (lane >> 5) * 8];
+          for (int i = 0; i < 16; ++i) acc[sub][mt][i] = 0.f;
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
-        const uint4 bf = *reinterpret_cast<const uint4*>(bp + kk * 16);
+      for (int sub = 0; sub < NSUB; ++sub) {
+        const uint16_t* bp = &kt[buf][(sub * 32 + (lane & 31)) * T::PITCH + (lane >> 5) * 8];
+        constexpr int KC = KK < 8 ? KK : 8;   // fragments issued ahead of their MFMAs
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          uint4 af;
-          if constexpr (QREG) {
-            af = qf[mt][kk];
-          } else {
-            const int m = mt * 32 + (lane & 31);
-            af = (row_ok && m < G) ? ldg16(qrow + (int64_t)m * D + kk * 16 + (lane >> 5) * 8)
-                                   : make_uint4(0, 0, 0, 0);
+        for (int k0 = 0; k0 < KK; k0 += KC) {
+          uint4 bf[KC];
+#pragma unroll
+          for (int j = 0; j < KC; ++j) bf[j] = *reinterpret_cast<const uint4*>(bp + (k0 + j) * 16);
+#pragma unroll
+          for (int j = 0; j < KC; ++j) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+              uint4 af;
+              if constexpr (QREG) {
+                af = qf[mt][k0 + j];
+              } else {
+                const int m = mt * 32 + (lane & 31);
+                af = (row_ok && m < G) ? ldg16(qrow + (int64_t)m * D + (k0 + j) * 16 + (lane >> 5) * 8)
+                                       : make_uint4(0, 0, 0, 0);
+              }
+              acc[sub][mt] = Mfma<IO>::m32(af, bf[j], acc[sub][mt]);
+            }
           }
-          acc[mt] = Mfma<IO>::m32(af, bf, acc[mt]);
         }
       }
-      float p = 0.f;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+      for (int sub = 0; sub < NSUB; ++sub) {
+        float p4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 16; ++i) p += fmaxf(acc[mt][i], 0.f) * wv[mt][i];
-      p += __shfl_xor(p, 32);
-      const int s2 = key0 + (lane & 31);
-      if (lane < 32 && s2 < L_row) srow[s2] = from_f32<IO>(p);
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) p4[i & 3] += fmaxf(acc[sub][mt][i], 0.f) * wv[mt][i];
+        float p = (p4[0] + p4[1]) + (p4[2] + p4[3]);
+        p += __shfl_xor(p, 32);
+        const int s2 = t * T::BN + sub * 32 + (lane & 31);
+        if (lane < 32 && s2 < L_row) srow[s2] = from_f32<IO>(p);
+      }
     }
     if (t + 1 < ntiles) stash(buf ^ 1);
     __syncthreads();

@@ -6,24 +6,31 @@
 // and quantised score), the other slots get -1 / 0. The reference's device
 // path calls mint.topk / mint.sort here (lightning_indexer_triton.py:343-361).
 //
-// Because every entry is a 16-bit float, (score, index) packs into one unique
-// 32-bit key  key = ord16(score) << 16 | (0xFFFF - index)  whose descending
-// order is exactly the golden's order (S2 <= 65536). Per score row, one
-// work-group of 256 threads:
-//   1. L <= k: every visible entry is selected.
-//   2. L >  k: radix-select the k-th largest 16-bit score T with two 8-bit
-//      LDS histogram passes (the row is re-read from L2), giving cnt_gt
-//      (entries > T) and need = k - cnt_gt. Entries > T are appended with an
-//      LDS atomic; entries == T are ranked in index order with wave ballots
-//      + popcount prefixes and a running block total, the first `need` kept.
-//   3. bitonic sort of the k selected unique keys in LDS (descending), then
-//      one coalesced pass writes indices and values.
+// One 256-thread work-group per score row:
+//   1. Thread t owns the contiguous index range [32t, 32t+32) of the row; the
+//      16-bit scores are mapped to order-preserving keys u (ord16) and kept in
+//      VGPRs (rows longer than 8192 entries are streamed from memory instead).
+//   2. L > k: the k-th largest key T is found by a 16-step binary search over
+//      the key bits, each step a block-wide count of u >= candidate (wave
+//      reductions + one LDS exchange; no atomics, so no contention on the few
+//      crowded high-score bins).
+//   3. Order-preserving compaction: entries with u > T and the first
+//      k - count(u > T) entries with u == T (in index order) are written, in
+//      index order, as keys (u << 16 | index) into LDS; per-thread positions come
+//      from block exclusive scans of the per-thread counts.
+//   4. A stable LSD radix sort on the 16-bit score (4 passes of 4 bits, digits
+//      of the inverted key so larger scores come first; per-thread counter
+//      columns in LDS, no atomics). Stability preserves the index order of
+//      equal scores, which is exactly the golden's tie rule.
+//   5. One pass writes the indices and 16-bit values in rank order.
 #include "dsa_common.hpp"
 
 namespace dsa {
 namespace {
 
 constexpr int TPB = 256;
+constexpr int RPT = 32;                 // row entries per thread held in VGPRs
+constexpr int ROW_CACHED = TPB * RPT;   // 8192
 
 __device__ __forceinline__ int visible_len(int s1, int aq, int ak, int S2, int mode) {
   int L;
@@ -38,43 +45,116 @@ __device__ __forceinline__ int visible_len(int s1, int aq, int ak, int S2, int m
   return L < 0 ? 0 : L;
 }
 
-// Block-wide inclusive scan of one uint32 per thread (TPB threads).
-__device__ __forceinline__ uint32_t block_incl_scan(uint32_t v, uint32_t* wsum) {
+__device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// Block-wide sum (all threads get the total). `red` holds TPB/64 words.
+__device__ __forceinline__ uint32_t block_sum(uint32_t v, uint32_t* red) {
+  v = wave_sum(v);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  uint32_t t = 0;
+#pragma unroll
+  for (int w = 0; w < TPB / 64; ++w) t += red[w];
+  return t;
+}
+
+// Block-wide exclusive scan; also returns the total.
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* red, uint32_t* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t x = v;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
-    uint32_t n = __shfl_up(v, o);
-    if (lane >= o) v += n;
+    const uint32_t n = __shfl_up(x, o);
+    if (lane >= o) x += n;
   }
-  if (lane == 63) wsum[wave] = v;
   __syncthreads();
-  uint32_t off = 0;
+  if (lane == 63) red[wave] = x;
+  __syncthreads();
+  uint32_t off = 0, tot = 0;
 #pragma unroll
-  for (int w = 0; w < TPB / 64; ++w) off += (w < wave) ? wsum[w] : 0u;
-  __syncthreads();
-  return v + off;
-}
-
-// Given a 256-bin histogram, find the bin holding the k-th largest element:
-// returns via LDS the bin and the number of elements in strictly higher bins.
-__device__ __forceinline__ void select_bin(const uint32_t* hist, uint32_t k, uint32_t* wsum,
-                                           uint32_t* res_bin, uint32_t* res_gt) {
-  const int t = threadIdx.x;
-  const uint32_t v = hist[255 - t];
-  const uint32_t incl = block_incl_scan(v, wsum);
-  const uint32_t excl = incl - v;
-  if (excl < k && incl >= k) {
-    *res_bin = 255 - t;
-    *res_gt = excl;
+  for (int w = 0; w < TPB / 64; ++w) {
+    off += (w < wave) ? red[w] : 0u;
+    tot += red[w];
   }
-  __syncthreads();
+  *total = tot;
+  return off + x - v;
 }
 
+__device__ __forceinline__ void load_keys(const uint16_t* row, int L, int base, uint32_t (&u)[RPT]) {
+  const int i0 = base + threadIdx.x * RPT;
+  if (i0 + RPT <= L) {
+#pragma unroll
+    for (int c = 0; c < RPT / 8; ++c) {
+      const uint4 v = ldg16(row + i0 + c * 8);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        u[c * 8 + 2 * j] = ord16((uint16_t)(w[j] & 0xFFFFu));
+        u[c * 8 + 2 * j + 1] = ord16((uint16_t)(w[j] >> 16));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < RPT; ++e) u[e] = (i0 + e < L) ? ord16(row[i0 + e]) : 0u;  // 0 < every real key
+  }
+}
+
+// Stable LSD radix sort of E keys per thread (blocked: thread t holds ranks
+// [E t, E t + E)), ascending on the inverted upper 16 bits = score descending.
+template <int E>
+__device__ __forceinline__ void radix_sort_desc16(uint32_t (&key)[E], uint32_t* sbuf, uint16_t* cnt,
+                                                  uint32_t* red) {
+  const int t = threadIdx.x;
+#pragma unroll 1
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 16 + 4 * pass;
+#pragma unroll
+    for (int d = 0; d < 16; ++d) cnt[d * TPB + t] = 0;
+    uint16_t lrank[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int d = ((~key[e]) >> shift) & 15;
+      const uint16_t r = cnt[d * TPB + t];
+      lrank[e] = r;
+      cnt[d * TPB + t] = r + 1;
+    }
+    __syncthreads();
+    // exclusive scan over cnt in [digit][thread] order: thread t scans entries 16t..16t+15
+    uint32_t loc[16];
+    uint32_t s = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      loc[j] = s;
+      s += cnt[t * 16 + j];
+    }
+    uint32_t tot;
+    const uint32_t off = block_excl_scan(s, red, &tot);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) cnt[t * 16 + j] = (uint16_t)(off + loc[j]);
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int d = ((~key[e]) >> shift) & 15;
+      sbuf[cnt[d * TPB + t] + lrank[e]] = key[e];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < E; ++e) key[e] = sbuf[E * t + e];
+    __syncthreads();
+  }
+}
+
+template <int E>
 __global__ __launch_bounds__(TPB) void li_topk_kernel(LiTopkArgs a) {
-  extern __shared__ __attribute__((aligned(16))) uint32_t sel[];  // next_pow2(k) keys
-  __shared__ uint32_t hist[256];
-  __shared__ uint32_t wsum[TPB / 64];
-  __shared__ uint32_t s_bin, s_gt, s_cnt, s_tie;
+  __shared__ __attribute__((aligned(16))) uint32_t sbuf[E * TPB];
+  __shared__ uint16_t cnt[16 * TPB];
+  __shared__ uint32_t red[TPB / 64];
 
   const int sr = blockIdx.x;
   const int r = sr / a.n2;
@@ -87,97 +167,93 @@ __global__ __launch_bounds__(TPB) void li_topk_kernel(LiTopkArgs a) {
   int32_t* iout = a.idx + (int64_t)sr * k;
   uint16_t* vout = a.val ? a.val + (int64_t)sr * k : nullptr;
   const uint16_t* row = a.scores + (int64_t)sr * a.ld;
-  const int tid = threadIdx.x;
+  const int t = threadIdx.x;
 
   if (nout == 0) {
-    for (int i = tid; i < k; i += TPB) {
+    for (int i = t; i < k; i += TPB) {
       iout[i] = -1;
       if (vout) vout[i] = 0;
     }
     return;
   }
 
-  int P = 1;
-  while (P < nout) P <<= 1;
-
-  if (L <= k) {
-    for (int i = tid; i < L; i += TPB) sel[i] = (ord16(row[i]) << 16) | (0xFFFFu - (uint32_t)i);
-  } else {
-    // ---- pass A: high byte of the 16-bit key
-    hist[tid] = 0;
-    __syncthreads();
-    for (int i = tid; i < L; i += TPB) atomicAdd(&hist[ord16(row[i]) >> 8], 1u);
-    __syncthreads();
-    select_bin(hist, (uint32_t)k, wsum, &s_bin, &s_gt);
-    const uint32_t bhi = s_bin, gt_hi = s_gt;
-    __syncthreads();
-    // ---- pass B: low byte inside the selected high bin
-    hist[tid] = 0;
-    __syncthreads();
-    for (int i = tid; i < L; i += TPB) {
-      const uint32_t u = ord16(row[i]);
-      if ((u >> 8) == bhi) atomicAdd(&hist[u & 0xFFu], 1u);
-    }
-    __syncthreads();
-    select_bin(hist, (uint32_t)k - gt_hi, wsum, &s_bin, &s_gt);
-    const uint32_t T = (bhi << 8) | s_bin;
-    const uint32_t cnt_gt = gt_hi + s_gt;
-    const uint32_t need = (uint32_t)k - cnt_gt;
-    if (tid == 0) { s_cnt = 0; s_tie = 0; }
-    __syncthreads();
-    // ---- pass C: compaction; ties ranked in index order
-    const int lane = tid & 63, wave = tid >> 6;
-    for (int base = 0; base < L; base += TPB) {
-      const int i = base + tid;
-      const uint32_t u = i < L ? ord16(row[i]) : 0u;
-      const uint32_t key = (u << 16) | (0xFFFFu - (uint32_t)i);
-      if (i < L && u > T) sel[atomicAdd(&s_cnt, 1u)] = key;
-      const bool tie = i < L && u == T;
-      const uint64_t m = __ballot(tie);
-      const uint32_t pre = __popcll(m & ((1ull << lane) - 1ull));
-      if (lane == 0) wsum[wave] = (uint32_t)__popcll(m);
-      __syncthreads();
-      uint32_t woff = 0, tot = 0;
+  // ---- selection + order-preserving compaction into sbuf[0, nout)
+  const int nchunks = (L + ROW_CACHED - 1) / ROW_CACHED;
+  uint32_t u[RPT];
+  if (nchunks == 1) load_keys(row, L, 0, u);
+  uint32_t T = 0;  // keys > T are all taken; keys == T up to `need`
+  uint32_t need = 0xFFFFFFFFu;
+  if (L > k) {
+#pragma unroll 1
+    for (int bit = 15; bit >= 0; --bit) {
+      const uint32_t cand = T | (1u << bit);
+      uint32_t c = 0;
+#pragma unroll 1
+      for (int ch = 0; ch < nchunks; ++ch) {
+        if (nchunks > 1) load_keys(row, L, ch * ROW_CACHED, u);
 #pragma unroll
-      for (int w = 0; w < TPB / 64; ++w) {
-        woff += (w < wave) ? wsum[w] : 0u;
-        tot += wsum[w];
+        for (int e = 0; e < RPT; ++e) c += u[e] >= cand ? 1u : 0u;
       }
-      const uint32_t rank = s_tie + woff + pre;
-      if (tie && rank < need) sel[cnt_gt + rank] = key;
-      __syncthreads();
-      if (tid == 0) s_tie += tot;
-      __syncthreads();
+      if (block_sum(c, red) >= (uint32_t)k) T = cand;
     }
+    uint32_t g = 0;
+#pragma unroll 1
+    for (int ch = 0; ch < nchunks; ++ch) {
+      if (nchunks > 1) load_keys(row, L, ch * ROW_CACHED, u);
+#pragma unroll
+      for (int e = 0; e < RPT; ++e) g += u[e] > T ? 1u : 0u;
+    }
+    need = (uint32_t)k - block_sum(g, red);
   }
-  for (int i = nout + tid; i < P; i += TPB) sel[i] = 0u;  // pads sort last
+  // positions: selected-before = greater-before + min(ties-before, need)
+  uint32_t run_g = 0, run_e = 0;  // totals of previous chunks
+#pragma unroll 1
+  for (int ch = 0; ch < nchunks; ++ch) {
+    if (nchunks > 1) load_keys(row, L, ch * ROW_CACHED, u);
+    uint32_t cg = 0, ce = 0;
+#pragma unroll
+    for (int e = 0; e < RPT; ++e) {
+      cg += u[e] > T ? 1u : 0u;
+      ce += (u[e] == T && T != 0) ? 1u : 0u;
+    }
+    uint32_t tot_g, tot_e;
+    uint32_t pg = block_excl_scan(cg, red, &tot_g) + run_g;
+    uint32_t pe = block_excl_scan(ce, red, &tot_e) + run_e;
+    const int i0 = ch * ROW_CACHED + t * RPT;
+#pragma unroll
+    for (int e = 0; e < RPT; ++e) {
+      const uint32_t key = (u[e] << 16) | (0xFFFFu - (uint32_t)(i0 + e));
+      if (u[e] > T) {
+        sbuf[pg + (pe < need ? pe : need)] = key;
+        ++pg;
+      } else if (u[e] == T && T != 0) {
+        if (pe < need) sbuf[pg + pe] = key;
+        ++pe;
+      }
+    }
+    run_g += tot_g;
+    run_e += tot_e;
+  }
+  for (int i = nout + t; i < E * TPB; i += TPB) sbuf[i] = 0u;  // pads sort last
   __syncthreads();
 
-  // ---- bitonic sort, descending
-  for (int k2 = 2; k2 <= P; k2 <<= 1) {
-    for (int j = k2 >> 1; j > 0; j >>= 1) {
-      for (int i = tid; i < (P >> 1); i += TPB) {
-        const int lo = ((i & ~(j - 1)) << 1) | (i & (j - 1));
-        const int hi = lo + j;
-        const uint32_t x = sel[lo], y = sel[hi];
-        const bool desc = (lo & k2) == 0;
-        if (desc ? (x < y) : (x > y)) {
-          sel[lo] = y;
-          sel[hi] = x;
-        }
+  // ---- stable radix sort of the selected keys, then write in rank order
+  uint32_t key[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) key[e] = sbuf[E * t + e];
+  __syncthreads();
+  radix_sort_desc16<E>(key, sbuf, cnt, red);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = E * t + e;
+    if (i < k) {
+      if (i < nout) {
+        iout[i] = (int32_t)(0xFFFFu - (key[e] & 0xFFFFu));
+        if (vout) vout[i] = unord16(key[e] >> 16);
+      } else {
+        iout[i] = -1;
+        if (vout) vout[i] = 0;
       }
-      __syncthreads();
-    }
-  }
-
-  for (int i = tid; i < k; i += TPB) {
-    if (i < nout) {
-      const uint32_t key = sel[i];
-      iout[i] = (int32_t)(0xFFFFu - (key & 0xFFFFu));
-      if (vout) vout[i] = unord16(key >> 16);
-    } else {
-      iout[i] = -1;
-      if (vout) vout[i] = 0;
     }
   }
 }
@@ -185,16 +261,16 @@ __global__ __launch_bounds__(TPB) void li_topk_kernel(LiTopkArgs a) {
 }  // namespace
 }  // namespace dsa
 
-size_t li_topk_lds_bytes(int k) {
-  size_t P = 1;
-  while (P < (size_t)k) P <<= 1;
-  return P * 4;
-}
-
 hipError_t launch_li_topk(const LiTopkArgs& a, hipStream_t s) {
   const int64_t rows = (int64_t)a.total_rows * a.n2;
   if (rows <= 0) return hipSuccess;
-  hipLaunchKernelGGL(dsa::li_topk_kernel, dim3((unsigned)rows), dim3(dsa::TPB),
-                     li_topk_lds_bytes(a.k), s, a);
+  const int e = (a.k + dsa::TPB - 1) / dsa::TPB;
+  const dim3 grid((unsigned)rows), block(dsa::TPB);
+  if (e <= 1) hipLaunchKernelGGL(dsa::li_topk_kernel<1>, grid, block, 0, s, a);
+  else if (e <= 2) hipLaunchKernelGGL(dsa::li_topk_kernel<2>, grid, block, 0, s, a);
+  else if (e <= 4) hipLaunchKernelGGL(dsa::li_topk_kernel<4>, grid, block, 0, s, a);
+  else if (e <= 8) hipLaunchKernelGGL(dsa::li_topk_kernel<8>, grid, block, 0, s, a);
+  else if (e <= 16) hipLaunchKernelGGL(dsa::li_topk_kernel<16>, grid, block, 0, s, a);
+  else hipLaunchKernelGGL(dsa::li_topk_kernel<32>, grid, block, 0, s, a);
   return hipGetLastError();
 }

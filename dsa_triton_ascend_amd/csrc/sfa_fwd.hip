@@ -173,7 +173,11 @@ constexpr int BN = 32;      // tokens per tile
 constexpr int PP = BN + 8;  // P tile pitch (elements)
 constexpr int QRP = DR + 8; // Q-rope LDS pitch (elements): 144-byte rows, conflict-free 16-byte reads
 constexpr float LOG2E = 1.4426950408889634f;
-constexpr float TAU = 5.545177444479562f;  // 8 ln 2: lazy-rescale threshold
+// Lazy-rescale threshold (natural units): the exponent reference m_used only
+// moves when a tile's max exceeds it by more than TAU, so P = exp(x - m_used)
+// stays below e^40 (exact in relative terms in fp32 / bf16 / fp16-free paths)
+// and O is practically never rescaled.
+constexpr float TAU = 40.f;
 
 template <int D> struct Cfg {
   static constexpr int KS = (D + DR) / 16;      // 32x32x16 k-steps of S^T
@@ -379,32 +383,40 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
     }
     // ---- online softmax for head hq over this tile (lane holds 16 tokens)
     float mx = -INFINITY;
+    if (nvalid == BN) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int tk = (i >> 2) * 8 + kg * 4 + (i & 3);
-      s[i] = tk < nvalid ? s[i] * a.scale : -INFINITY;
-      mx = fmaxf(mx, s[i]);
+      for (int i = 0; i < 16; ++i) {
+        s[i] *= a.scale;
+        mx = fmaxf(mx, s[i]);
+      }
+    } else {  // partial last tile: mask the slots past the token list
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int tk = (i >> 2) * 8 + kg * 4 + (i & 3);
+        s[i] = tk < nvalid ? s[i] * a.scale : -INFINITY;
+        mx = fmaxf(mx, s[i]);
+      }
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     m_true = fmaxf(m_true, mx);
     float alpha = 1.f;
     if (mx > m_used + TAU) {
-      alpha = exp2f((m_used - mx) * LOG2E);
+      // first tile: O and l are still zero, nothing to rescale (alpha stays 1)
+      if (m_used != -INFINITY) alpha = __builtin_amdgcn_exp2f((m_used - mx) * LOG2E);
       m_used = mx;
     }
+    const float mb = m_used * LOG2E;
     float psum = 0.f;
     uint16_t* prow = pt + hq * PP + kg * 4;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      uint32_t w2[2];
+      float p[4];
 #pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        const float p0 = exp2f((s[g * 4 + h2 * 2] - m_used) * LOG2E);
-        const float p1 = exp2f((s[g * 4 + h2 * 2 + 1] - m_used) * LOG2E);
-        psum += p0 + p1;
-        w2[h2] = (uint32_t)from_f32<IO>(p0) | ((uint32_t)from_f32<IO>(p1) << 16);
+      for (int j = 0; j < 4; ++j) {
+        p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[g * 4 + j], LOG2E, -mb));
+        psum += p[j];
       }
-      *reinterpret_cast<uint2*>(prow + g * 8) = make_uint2(w2[0], w2[1]);
+      *reinterpret_cast<uint2*>(prow + g * 8) = make_uint2(pack2<IO>(p[0], p[1]), pack2<IO>(p[2], p[3]));
     }
     l_part = l_part * alpha + psum;
     if (lane < 32) s_alpha[hq] = alpha;
