@@ -33,10 +33,16 @@ namespace dsa {
 
 namespace {
 
-constexpr int NW = 8;  // waves (= query rows) per work-group
+#ifndef DSA_LI_NW
+#define DSA_LI_NW 8
+#endif
+#ifndef DSA_LI_BN
+#define DSA_LI_BN 64
+#endif
+constexpr int NW = DSA_LI_NW;  // waves (= query rows) per work-group
 
 template <int D> struct LiTile {
-  static constexpr int BN = D <= 128 ? 64 : 32;        // keys per LDS tile
+  static constexpr int BN = D <= 128 ? DSA_LI_BN : 32;  // keys per LDS tile
   static constexpr int PITCH = D + 8;                  // uint16 elements per LDS key row
   static constexpr int CHUNKS = BN * D / 8;            // 16-byte chunks per tile
   static constexpr int CPT = (CHUNKS + NW * 64 - 1) / (NW * 64);   // chunks per thread
@@ -154,61 +160,96 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
   }
 
   uint16_t* srow = a.scores + (r * a.n2 + n2) * a.ld;
+
+  // ---- main loop, software-pipelined by 32-key subtile: the MFMAs of subtile
+  // j are interleaved with the relu*w epilogue of subtile j-1 (ping-pong
+  // accumulators), so the wave's VALU work co-executes with its MFMAs.
+  f32x16 acc[2][MT];
+  int pend_key0 = -1;   // first key of the subtile whose epilogue is pending (-1: none)
+
+  auto zero = [&](f32x16(&c)[MT]) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) c[mt][i] = 0.f;
+  };
+  auto finish = [&](float (&p4)[4], int key0) {
+    float p = (p4[0] + p4[1]) + (p4[2] + p4[3]);
+    p += __shfl_xor(p, 32);
+    const int s2 = key0 + (lane & 31);
+    if (lane < 32 && s2 < L_row) srow[s2] = from_f32<IO>(p);
+  };
+  // one subtile: MFMAs into `cur` from the LDS rows at `bp`; epilogue of `prev` interleaved
+  auto step = [&](f32x16(&cur)[MT], f32x16(&prev)[MT], const uint16_t* bp, bool has_prev, int prev_key0) {
+    constexpr int KC = KK < 8 ? KK : 8;
+    constexpr int EPK = (MT * 16 + KK - 1) / KK;   // epilogue elements per k-step
+    float p4[4] = {0.f, 0.f, 0.f, 0.f};
+    zero(cur);
+#pragma unroll
+    for (int k0 = 0; k0 < KK; k0 += KC) {
+      uint4 bf[KC];
+#pragma unroll
+      for (int j = 0; j < KC; ++j) bf[j] = *reinterpret_cast<const uint4*>(bp + (k0 + j) * 16);
+#pragma unroll
+      for (int j = 0; j < KC; ++j) {
+        const int kk = k0 + j;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          uint4 af;
+          if constexpr (QREG) {
+            af = qf[mt][kk];
+          } else {
+            const int m = mt * 32 + (lane & 31);
+            af = (row_ok && m < G) ? ldg16(qrow + (int64_t)m * D + kk * 16 + (lane >> 5) * 8)
+                                   : make_uint4(0, 0, 0, 0);
+          }
+          cur[mt] = Mfma<IO>::m32(af, bf[j], cur[mt]);
+        }
+        if (has_prev) {
+#pragma unroll
+          for (int q = 0; q < EPK; ++q) {
+            const int e = kk * EPK + q;
+            if (e < MT * 16) p4[e & 3] += fmaxf(prev[e >> 4][e & 15], 0.f) * wv[e >> 4][e & 15];
+          }
+        }
+      }
+    }
+    if (has_prev) finish(p4, prev_key0);
+  };
+  auto drain = [&](f32x16(&prev)[MT], int key0) {
+    float p4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int e = 0; e < MT * 16; ++e) p4[e & 3] += fmaxf(prev[e >> 4][e & 15], 0.f) * wv[e >> 4][e & 15];
+    finish(p4, key0);
+  };
+
   stash(0);
   __syncthreads();
   for (int t = 0; t < ntiles; ++t) {
     const int buf = t & 1;
     if (t + 1 < ntiles) fetch(t + 1);
+    const uint16_t* bp0 = &kt[buf][(lane & 31) * T::PITCH + (lane >> 5) * 8];
     if (t * T::BN < L_row) {  // wave-uniform: this row sees part of the tile
-      f32x16 acc[NSUB][MT];
+      if constexpr (NSUB % 2 == 0) {
 #pragma unroll
-      for (int sub = 0; sub < NSUB; ++sub)
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) acc[sub][mt][i] = 0.f;
-#pragma unroll
-      for (int sub = 0; sub < NSUB; ++sub) {
-        const uint16_t* bp = &kt[buf][(sub * 32 + (lane & 31)) * T::PITCH + (lane >> 5) * 8];
-        constexpr int KC = KK < 8 ? KK : 8;   // fragments issued ahead of their MFMAs
-#pragma unroll
-        for (int k0 = 0; k0 < KK; k0 += KC) {
-          uint4 bf[KC];
-#pragma unroll
-          for (int j = 0; j < KC; ++j) bf[j] = *reinterpret_cast<const uint4*>(bp + (k0 + j) * 16);
-#pragma unroll
-          for (int j = 0; j < KC; ++j) {
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-              uint4 af;
-              if constexpr (QREG) {
-                af = qf[mt][k0 + j];
-              } else {
-                const int m = mt * 32 + (lane & 31);
-                af = (row_ok && m < G) ? ldg16(qrow + (int64_t)m * D + (k0 + j) * 16 + (lane >> 5) * 8)
-                                       : make_uint4(0, 0, 0, 0);
-              }
-              acc[sub][mt] = Mfma<IO>::m32(af, bf[j], acc[sub][mt]);
-            }
-          }
+        for (int sub = 0; sub < NSUB; sub += 2) {
+          step(acc[0], acc[1], bp0 + sub * 32 * T::PITCH, sub > 0 || pend_key0 >= 0,
+               sub > 0 ? t * T::BN + (sub - 1) * 32 : pend_key0);
+          step(acc[1], acc[0], bp0 + (sub + 1) * 32 * T::PITCH, true, t * T::BN + sub * 32);
         }
+        pend_key0 = t * T::BN + (NSUB - 1) * 32;
+      } else {
+        step(acc[0], acc[1], bp0, false, 0);
+        drain(acc[0], t * T::BN);
       }
-#pragma unroll
-      for (int sub = 0; sub < NSUB; ++sub) {
-        float p4[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) p4[i & 3] += fmaxf(acc[sub][mt][i], 0.f) * wv[mt][i];
-        float p = (p4[0] + p4[1]) + (p4[2] + p4[3]);
-        p += __shfl_xor(p, 32);
-        const int s2 = t * T::BN + sub * 32 + (lane & 31);
-        if (lane < 32 && s2 < L_row) srow[s2] = from_f32<IO>(p);
-      }
+    } else if (pend_key0 >= 0) {
+      drain(acc[1], pend_key0);
+      pend_key0 = -1;
     }
     if (t + 1 < ntiles) stash(buf ^ 1);
     __syncthreads();
   }
+  if (pend_key0 >= 0) drain(acc[1], pend_key0);
 }
 
 template <int IO, int D>
