@@ -100,6 +100,16 @@ __device__ __forceinline__ int m16_row(int r, int lane) { return (lane >> 4) * 4
 
 // ------------------------------------------------------------------ misc
 __device__ __forceinline__ uint4 ldg16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+
+// Work-group barrier that orders LDS accesses only. __syncthreads() is a
+// release/acquire fence on all address spaces, which makes every wave drain its
+// outstanding global loads (vmcnt 0) at the barrier and so cancels any global
+// prefetch issued before it; here only LDS traffic is waited for.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 __device__ __forceinline__ void stg16(void* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
 
 __device__ __forceinline__ int batch_of_row(const int32_t* row_start, int batch, int r) {

@@ -14,19 +14,25 @@
 //  * the row's Q fragments stay in VGPRs for the whole key sweep (MT <= 2, MT*D <= 512),
 //    otherwise they are re-read from L2 per key tile;
 //  * a work-group = NW waves = NW consecutive query rows of one (batch, n2);
-//    they share each 64-key K tile, staged global -> VGPR -> LDS with a
-//    one-tile register prefetch and two LDS buffers (one barrier per tile);
-//    LDS rows are padded by 16 B so the 16-byte B-fragment reads are
-//    conflict-free;
+//    they share each K tile (64 keys for D <= 128), which is copied global ->
+//    LDS by direct-to-LDS loads (no VGPR round trip) two tiles ahead into a
+//    ring of three LDS buffers; one LDS-only barrier per tile, so the loads in
+//    flight are never drained by it;
+//  * K rows are stored unpadded with their 16-byte chunks permuted (chunk c of
+//    key row k sits at c ^ (k & 7)), which keeps the 16-byte B-fragment reads
+//    of 8 consecutive keys on distinct LDS banks;
 //  * per tile a wave issues its B-fragment reads ahead of the MFMAs and keeps
 //    one accumulator set per 32-key subtile, so the epilogue of one subtile can
 //    overlap the MFMAs of the next;
 //  * the epilogue is fused: relu(acc) * w[head] summed over the 16 heads a lane
 //    holds and the MT tiles (four independent partial sums), then one
-//    cross-lane add (lanes l and l^32) gives the per-key score; fully causal-
-//    masked tiles are never loaded or computed;
+//    cross-lane add (lanes l and l^32, v_permlane32_swap) gives the per-key
+//    score; the scores of a tile are written by one store at the start of the
+//    next tile; fully causal-masked tiles are never loaded or computed;
 //  * row blocks are issued heaviest-first (largest s1 first) to flatten the
 //    causal triangle's tail.
+#include <type_traits>
+
 #include "dsa_common.hpp"
 
 namespace dsa {
@@ -39,14 +45,49 @@ namespace {
 #ifndef DSA_LI_BN
 #define DSA_LI_BN 64
 #endif
+#ifndef DSA_LI_NBUF
+#define DSA_LI_NBUF 3
+#endif
 constexpr int NW = DSA_LI_NW;  // waves (= query rows) per work-group
 
 template <int D> struct LiTile {
-  static constexpr int BN = D <= 128 ? DSA_LI_BN : 32;  // keys per LDS tile
-  static constexpr int PITCH = D + 8;                  // uint16 elements per LDS key row
-  static constexpr int CHUNKS = BN * D / 8;            // 16-byte chunks per tile
-  static constexpr int CPT = (CHUNKS + NW * 64 - 1) / (NW * 64);   // chunks per thread
+  static constexpr int BN = D == 96 ? 128 : (D <= 128 ? DSA_LI_BN : 32);  // keys per LDS tile
+  static constexpr int CPR = D / 8;                  // 16-byte chunks per key row
+  static constexpr int SWZ = CPR % 8 == 0 ? 7 : 3;   // chunk permutation mask (c ^ (k & SWZ)); stays in the row
+  static constexpr int SLOTS = BN * CPR;             // 16-byte slots per tile
+  static constexpr int IPW = SLOTS / (NW * 64);      // direct-to-LDS loads per wave per tile
+  static_assert(IPW >= 1 && IPW * NW * 64 == SLOTS, "tile must split evenly over the waves");
+  static constexpr int NBUF = DSA_LI_NBUF;           // LDS ring: tile t being read, the rest in flight
 };
+
+// 16-byte direct-to-LDS load: lane l writes LDS [lds_base + 16 l, +16). Issued
+// as inline asm so the compiler does not track it: its wait insertion assumes
+// every LDS read may alias an outstanding direct-to-LDS load and would drain
+// the prefetched tiles (vmcnt 0) before each B-fragment read. The kernel orders
+// these loads itself with wait_vmcnt and the LDS barrier.
+__device__ __forceinline__ void lds_dma16_untracked(const void* gptr, void* lds_base) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds_base;
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gptr), "s"(m0) : "memory");
+}
+
+// x[l] + x[l ^ 32] on every lane, with one v_permlane32_swap (VALU, no LDS).
+// After swapping the upper half of `a` with the lower half of `b` (both x),
+// a[l] + b[l] = x[l mod 32] + x[l mod 32 + 32]. Written as inline asm with two
+// distinct in/out registers: the compiler folds the builtin's two results of
+// permlane32_swap(x, x) into one and returns 2 x[l]. The s_nop 1 gives the two
+// wait states the swap needs after the VALU writes of its operands.
+__device__ __forceinline__ float add_half_swap(float x) {
+  float a = x, b = x;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return a + b;
+}
+
+// s_waitcnt vmcnt(N) (gfx9 encoding; expcnt and lgkmcnt left unconstrained).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
 
 __device__ __forceinline__ float load_w(const void* w, int wdt, int64_t i) {
   if (wdt == DSA_DTYPE_F32) return reinterpret_cast<const float*>(w)[i];
@@ -73,10 +114,12 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
   constexpr int KK = D / 16;                 // MFMA k-steps
   constexpr int NSUB = T::BN / 32;           // 32-key subtiles per tile
   constexpr bool QREG = MT <= 2 && MT * D <= 512;   // Q fragments resident in VGPRs
-  __shared__ __attribute__((aligned(16))) uint16_t kt[2][T::BN * T::PITCH];
+  __shared__ __attribute__((aligned(16))) uint16_t kt[T::NBUF][T::BN * D];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // wave index in an SGPR: every per-row bound below is then wave-uniform and
+  // the row/tile conditions compile to scalar branches instead of exec masks
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int b = blockIdx.z;
   const int n2 = blockIdx.y;
   const int rb = gridDim.x - 1 - blockIdx.x;  // heaviest row block first
@@ -101,30 +144,28 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
                           ((int64_t)a.key_start[b] * a.n2 + n2) * D;
   const int64_t kstride = (int64_t)a.n2 * D;
 
-  // ---- K tile staging (started first so its latency overlaps the Q / w loads)
+  // ---- K tile staging (started first so its latency overlaps the Q / w loads).
+  // Direct-to-LDS load j of wave w fills the 64 slots [64 i, 64 i + 64) of a
+  // tile, i = w * IPW + j; slot s holds chunk (s % CPR) ^ (k & SWZ) of key row
+  // k = s / CPR. Every lane always issues its loads (keys past L_blk re-read the
+  // last visible key, whose columns are never stored), so each wave has exactly
+  // IPW loads per tile in flight and one partial vmcnt wait retires a tile.
   const int ntiles = (L_blk + T::BN - 1) / T::BN;
-  uint4 pre[T::CPT];
-  auto fetch = [&](int tile) {
+  auto dma = [&](int tile) {
+    uint16_t* buf = kt[tile % T::NBUF];
 #pragma unroll
-    for (int c = 0; c < T::CPT; ++c) {
-      const int ch = threadIdx.x + c * NW * 64;
-      const int key = ch / (D / 8), off = (ch % (D / 8)) * 8;
-      const int s2 = tile * T::BN + key;
-      pre[c] = (ch < T::CHUNKS && s2 < L_blk) ? ldg16(kbase + (int64_t)s2 * kstride + off)
-                                              : make_uint4(0, 0, 0, 0);
+    for (int j = 0; j < T::IPW; ++j) {
+      const int i = wave * T::IPW + j;
+      const int slot = i * 64 + lane;
+      const int k = slot / T::CPR;
+      const int c = (slot % T::CPR) ^ (k & T::SWZ);
+      int s2 = tile * T::BN + k;
+      s2 = s2 < L_blk ? s2 : L_blk - 1;
+      lds_dma16_untracked(kbase + (int64_t)s2 * kstride + c * 8, buf + i * 512);
     }
   };
-  auto stash = [&](int buf) {
 #pragma unroll
-    for (int c = 0; c < T::CPT; ++c) {
-      const int ch = threadIdx.x + c * NW * 64;
-      if (ch < T::CHUNKS) {
-        const int key = ch / (D / 8), off = (ch % (D / 8)) * 8;
-        *reinterpret_cast<uint4*>(&kt[buf][key * T::PITCH + off]) = pre[c];
-      }
-    }
-  };
-  fetch(0);
+  for (int j = 0; j < T::NBUF - 1; ++j) dma(j);
 
   // ---- per-row operands: Q fragments (A) and head weights
   uint4 qf[QREG ? MT : 1][QREG ? KK : 1];
@@ -173,14 +214,46 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) c[mt][i] = 0.f;
   };
-  auto finish = [&](float (&p4)[4], int key0) {
-    float p = (p4[0] + p4[1]) + (p4[2] + p4[3]);
-    p += __shfl_xor(p, 32);
-    const int s2 = key0 + (lane & 31);
-    if (lane < 32 && s2 < L_row) srow[s2] = from_f32<IO>(p);
+  // Scores of a subtile wait in a register slot and are written at the start of
+  // the next tile, before its K loads are issued, so the stores never hold up
+  // the partial vmcnt wait for the tile in flight. Slots pair up: lanes 0-31
+  // store slot 2m, lanes 32-63 slot 2m+1 (64 consecutive keys, one store).
+  constexpr int NSLOT = NSUB;
+  float pv[NSLOT];
+  int pk[NSLOT];
+#pragma unroll
+  for (int i = 0; i < NSLOT; ++i) pk[i] = -1;
+  auto flush = [&]() {
+#pragma unroll
+    for (int m = 0; m < NSLOT; m += 2) {
+      const bool hi = lane >= 32;
+      const int k0 = (hi && m + 1 < NSLOT) ? pk[m + 1] : (hi ? -1 : pk[m]);
+      const float v = (hi && m + 1 < NSLOT) ? pv[m + 1] : pv[m];
+      const int s2 = k0 + (lane & 31);
+      if (k0 >= 0 && s2 < L_row) srow[s2] = from_f32<IO>(v);
+    }
+#pragma unroll
+    for (int i = 0; i < NSLOT; ++i) pk[i] = -1;
   };
+  auto finish = [&](float (&p4)[4], int key0, int slot) {
+    const float p = (p4[0] + p4[1]) + (p4[2] + p4[3]);
+    // lanes l and l^32 hold the two halves of the head sum of the same key
+    pv[slot] = add_half_swap(p);
+    pk[slot] = key0;
+  };
+  // per-lane chunk offsets of the B-fragment reads (rows are 8-aligned per subtile,
+  // so a row's permutation key is lane & SWZ): chunk 2 kk + h sits at
+  // GS * (kk / JN) + ((2 (kk % JN) + h) ^ (lane & SWZ)), h = lane >> 5
+  constexpr int GS = T::SWZ + 1, JN = GS / 2;
+  int coff[JN];
+#pragma unroll
+  for (int j = 0; j < JN; ++j) coff[j] = 8 * ((2 * j + (lane >> 5)) ^ (lane & T::SWZ));
   // one subtile: MFMAs into `cur` from the LDS rows at `bp`; epilogue of `prev` interleaved
-  auto step = [&](f32x16(&cur)[MT], f32x16(&prev)[MT], const uint16_t* bp, bool has_prev, int prev_key0) {
+  // `hp` (std::true_type / std::false_type): whether `prev` holds a pending subtile; a
+  // compile-time flag so each variant is one straight-line block for the scheduler.
+  auto step = [&](auto hp, f32x16(&cur)[MT], f32x16(&prev)[MT], const uint16_t* bp, int prev_key0,
+                  int slot) {
+    constexpr bool has_prev = decltype(hp)::value;
     constexpr int KC = KK < 8 ? KK : 8;
     constexpr int EPK = (MT * 16 + KK - 1) / KK;   // epilogue elements per k-step
     float p4[4] = {0.f, 0.f, 0.f, 0.f};
@@ -189,7 +262,10 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
     for (int k0 = 0; k0 < KK; k0 += KC) {
       uint4 bf[KC];
 #pragma unroll
-      for (int j = 0; j < KC; ++j) bf[j] = *reinterpret_cast<const uint4*>(bp + (k0 + j) * 16);
+      for (int j = 0; j < KC; ++j) {
+        const int kk = k0 + j;   // logical chunk 2 kk + (lane >> 5) of this lane's key row
+        bf[j] = *reinterpret_cast<const uint4*>(bp + 8 * GS * (kk / JN) + coff[kk % JN]);
+      }
 #pragma unroll
       for (int j = 0; j < KC; ++j) {
         const int kk = k0 + j;
@@ -205,7 +281,7 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
           }
           cur[mt] = Mfma<IO>::m32(af, bf[j], cur[mt]);
         }
-        if (has_prev) {
+        if constexpr (has_prev) {
 #pragma unroll
           for (int q = 0; q < EPK; ++q) {
             const int e = kk * EPK + q;
@@ -214,42 +290,53 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
         }
       }
     }
-    if (has_prev) finish(p4, prev_key0);
+    if constexpr (has_prev) finish(p4, prev_key0, slot);
   };
-  auto drain = [&](f32x16(&prev)[MT], int key0) {
+  auto drain = [&](f32x16(&prev)[MT], int key0, int slot) {
     float p4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int e = 0; e < MT * 16; ++e) p4[e & 3] += fmaxf(prev[e >> 4][e & 15], 0.f) * wv[e >> 4][e & 15];
-    finish(p4, key0);
+    finish(p4, key0, slot);
   };
 
-  stash(0);
-  __syncthreads();
+  // Tile t is read from LDS buffer t % 3 while tile t+1 has landed (or is
+  // landing) in the next buffer and tile t+2 is being loaded into the third.
+  wait_vmcnt<0>();
+  lds_barrier();
   for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < ntiles) fetch(t + 1);
-    const uint16_t* bp0 = &kt[buf][(lane & 31) * T::PITCH + (lane >> 5) * 8];
+    flush();            // scores of tile t-1
+    dma(t + T::NBUF - 1);   // its buffer held tile t-1, released by the last barrier
+    const uint16_t* bp0 = &kt[t % T::NBUF][(lane & 31) * D];
     if (t * T::BN < L_row) {  // wave-uniform: this row sees part of the tile
       if constexpr (NSUB % 2 == 0) {
+        if (pend_key0 >= 0)
+          step(std::true_type{}, acc[0], acc[1], bp0, pend_key0, 0);
+        else
+          step(std::false_type{}, acc[0], acc[1], bp0, 0, 0);
+        step(std::true_type{}, acc[1], acc[0], bp0 + 32 * D, t * T::BN, 1);
 #pragma unroll
-        for (int sub = 0; sub < NSUB; sub += 2) {
-          step(acc[0], acc[1], bp0 + sub * 32 * T::PITCH, sub > 0 || pend_key0 >= 0,
-               sub > 0 ? t * T::BN + (sub - 1) * 32 : pend_key0);
-          step(acc[1], acc[0], bp0 + (sub + 1) * 32 * T::PITCH, true, t * T::BN + sub * 32);
+        for (int sub = 2; sub < NSUB; sub += 2) {
+          step(std::true_type{}, acc[0], acc[1], bp0 + sub * 32 * D, t * T::BN + (sub - 1) * 32, sub);
+          step(std::true_type{}, acc[1], acc[0], bp0 + (sub + 1) * 32 * D, t * T::BN + sub * 32, sub + 1);
         }
         pend_key0 = t * T::BN + (NSUB - 1) * 32;
       } else {
-        step(acc[0], acc[1], bp0, false, 0);
-        drain(acc[0], t * T::BN);
+        step(std::false_type{}, acc[0], acc[1], bp0, 0, 0);
+        drain(acc[0], t * T::BN, 0);
       }
     } else if (pend_key0 >= 0) {
-      drain(acc[1], pend_key0);
+      drain(acc[1], pend_key0, 0);
       pend_key0 = -1;
     }
-    if (t + 1 < ntiles) stash(buf ^ 1);
-    __syncthreads();
+    wait_vmcnt<T::IPW * (T::NBUF - 2)>();   // this wave's part of tile t+1 has landed
+    lds_barrier();
   }
-  if (pend_key0 >= 0) drain(acc[1], pend_key0);
+  flush();
+  if (pend_key0 >= 0) {
+    drain(acc[1], pend_key0, 0);
+    flush();
+  }
+  wait_vmcnt<0>();   // no direct-to-LDS load may outlive the work-group's LDS
 }
 
 template <int IO, int D>
