@@ -60,35 +60,6 @@ template <int D> struct LiTile {
   static constexpr int NBUF = DSA_LI_NBUF;           // LDS ring: tile t being read, the rest in flight
 };
 
-// 16-byte direct-to-LDS load: lane l writes LDS [lds_base + 16 l, +16). Issued
-// as inline asm so the compiler does not track it: its wait insertion assumes
-// every LDS read may alias an outstanding direct-to-LDS load and would drain
-// the prefetched tiles (vmcnt 0) before each B-fragment read. The kernel orders
-// these loads itself with wait_vmcnt and the LDS barrier.
-__device__ __forceinline__ void lds_dma16_untracked(const void* gptr, void* lds_base) {
-  const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds_base;
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gptr), "s"(m0) : "memory");
-}
-
-// x[l] + x[l ^ 32] on every lane, with one v_permlane32_swap (VALU, no LDS).
-// After swapping the upper half of `a` with the lower half of `b` (both x),
-// a[l] + b[l] = x[l mod 32] + x[l mod 32 + 32]. Written as inline asm with two
-// distinct in/out registers: the compiler folds the builtin's two results of
-// permlane32_swap(x, x) into one and returns 2 x[l]. The s_nop 1 gives the two
-// wait states the swap needs after the VALU writes of its operands.
-__device__ __forceinline__ float add_half_swap(float x) {
-  float a = x, b = x;
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-  return a + b;
-}
-
-// s_waitcnt vmcnt(N) (gfx9 encoding; expcnt and lgkmcnt left unconstrained).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
 __device__ __forceinline__ float load_w(const void* w, int wdt, int64_t i) {
   if (wdt == DSA_DTYPE_F32) return reinterpret_cast<const float*>(w)[i];
   uint16_t h = reinterpret_cast<const uint16_t*>(w)[i];

@@ -16,14 +16,19 @@
 //     KV split) covering all (up to 128) heads, so every gathered KV row is
 //     fetched once per row:
 //       * tokens are processed in tiles of 32; a tile's [D | Dr] rows are
-//         gathered with direct-to-LDS 16-byte loads (no VGPR staging) into one
-//         of two LDS buffers while the previous tile is being computed;
+//         gathered with direct-to-LDS 16-byte loads (no VGPR staging) into a
+//         ring of three LDS buffers, two tiles ahead of the one being computed;
+//         the token ids travel the same ordered path (a 4-slot LDS ring filled
+//         four tiles ahead), the loads are spread over the S^T MFMA chain and
+//         the per-tile barriers are LDS-only, so nothing drains the gathers in
+//         flight and one partial vmcnt wait per tile retires the oldest tile;
 //       * S^T = K Q^T on v_mfma_f32_32x32x16 with tokens as M and 32 heads per
 //         wave as N (Q^T resident in VGPRs): a lane then holds 16 tokens of one
 //         head, so the softmax row max is in-lane plus one lane swap;
 //       * online softmax in fp32 with lazy rescaling: the exponent reference
-//         m_used only moves when a tile's max exceeds it by more than 8 ln 2,
-//         so O is rarely rescaled; the true max is tracked for softmax_max;
+//         m_used only moves when a tile's max exceeds it by more than TAU = 40
+//         (natural-log units), so O is rarely rescaled; the true max is tracked
+//         for softmax_max;
 //       * P (io dtype) goes to LDS as [head][token]; each wave then owns a
 //         D/4-column slice of O[128 heads, D] and accumulates P V on
 //         v_mfma_f32_32x32x16, the V^T operand read with ds_read_b64_tr_b16
@@ -61,7 +66,8 @@ __device__ __forceinline__ RowInfo row_info(const SfaArgs& a, int r) {
 // ---------------------------------------------------------------- workspace
 struct Ws {
   int32_t* counts;   // [rows]
-  int32_t* tokens;   // [rows, cap]
+  int32_t* tokens;   // [rows, tstride]
+  int tstride;       // token-list row stride: cap rounded up to a whole 32-token tile
   uint16_t* zero;    // one zero KV row: 512 + Dr elements
   float* part_o;     // [rows, splits, N1, D]   (splits > 1)
   float* part_s;     // [rows, splits, N1, 3]   m_used, m_true, l
@@ -74,10 +80,11 @@ __host__ __device__ inline Ws ws_layout(void* base, int rows, int cap, int n1, i
   char* p = reinterpret_cast<char*>(base);
   size_t off = 0;
   Ws w;
+  w.tstride = (cap + 31) & ~31;
   w.counts = reinterpret_cast<int32_t*>(p + off);
   off += align256((size_t)rows * 4);
   w.tokens = reinterpret_cast<int32_t*>(p + off);
-  off += align256((size_t)rows * cap * 4);
+  off += align256((size_t)rows * w.tstride * 4);
   w.zero = reinterpret_cast<uint16_t*>(p + off);
   off += align256((size_t)(512 + DR) * 2);
   w.part_o = reinterpret_cast<float*>(p + off);
@@ -144,7 +151,7 @@ __global__ __launch_bounds__(TOK_TPB) void sfa_tokens_kernel(SfaArgs a, int cap,
     tot += wsum[w];
   }
   int pos = off + v - my;
-  int32_t* out = ws.tokens + (int64_t)r * cap;
+  int32_t* out = ws.tokens + (int64_t)r * ws.tstride;
   for (int i = i0; i < i1; ++i) {
     const int id = ids[i];
     if (id < 0) continue;
@@ -170,6 +177,7 @@ __global__ __launch_bounds__(TOK_TPB) void sfa_tokens_kernel(SfaArgs a, int cap,
 constexpr int NWV = 4;      // waves per work-group (one per SIMD)
 constexpr int HB = 128;     // heads per work-group (N1 <= 128, padded)
 constexpr int BN = 32;      // tokens per tile
+constexpr int NBUF = 3;     // gather ring: tile t read, t+1 and t+2 in flight
 constexpr int PP = BN + 8;  // P tile pitch (elements)
 constexpr int QRP = DR + 8; // Q-rope LDS pitch (elements): 144-byte rows, conflict-free 16-byte reads
 constexpr float LOG2E = 1.4426950408889634f;
@@ -188,6 +196,7 @@ template <int D> struct Cfg {
   static constexpr int DW = D / NWV;            // O columns per wave
   static constexpr int NT = DW / 32;            // 32-wide N tiles per wave
   static constexpr int LANES_ROW = D / 8;       // lanes that load one nope row
+  static constexpr int GPW = 8 + 1 + 1;         // direct-to-LDS loads per wave per tile (8 rows, rope, ids)
 };
 
 // Start of token t's nope row inside a buffer: rows are ROW bytes apart and
@@ -209,45 +218,37 @@ __device__ __forceinline__ uint2 ds_read_tr(const void* lds_ptr) {
   return __builtin_bit_cast(uint2, v);
 }
 
-__device__ __forceinline__ void lds_dma16(const void* gptr, void* lds_base) {
-  __builtin_amdgcn_global_load_lds(gptr, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
-}
-
-// Token indices of one tile for this wave: 8 wave-uniform nope rows (scalar
-// loads) and one per-lane rope row (lane -> token wave*8 + lane%8). Loaded one
-// tile ahead so issuing the gather never waits on them.
+// Token rows of one tile for this wave (tokens 8w..8w+7): wave-uniform rows for
+// the nope gathers and, per lane, the row of token lane % 8 for the rope gather.
 struct TileIdx {
   int nope[8];
   int rope;
 };
 
-__device__ __forceinline__ TileIdx load_idx(const int32_t* toks, int nvalid, int wave_u, int lane) {
-  TileIdx ix;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int t = wave_u * 8 + i;
-    ix.nope[i] = __builtin_amdgcn_readfirstlane(toks[t < nvalid ? t : 0]);  // tail slots re-read a valid row
+// One of the GPW - 1 gather loads of a tile for wave w: part j < 8 copies the
+// nope row of token 8w + j (one instruction, D/8 lanes), part 8 the rope chunks
+// of the wave's 8 tokens (lane -> token lane%8, chunk lane/8).
+template <int D>
+__device__ __forceinline__ void gather_part(int j, const uint16_t* kb, const uint16_t* krb,
+                                            const uint16_t* zero, const TileIdx& ix, uint8_t* nope,
+                                            uint8_t* rope, int wave_u, int lane) {
+  using C = Cfg<D>;
+  if (j < 8) {
+    const int phys = ix.nope[j];   // wave-uniform: the row base goes in an SGPR pair
+    const uint16_t* src = phys >= 0 ? kb + (int64_t)phys * D : zero;
+    if (lane < C::LANES_ROW) lds_dma16_sbase_untracked(src, lane * 16, nope + nope_off<D>(wave_u * 8 + j));
+  } else {
+    const uint16_t* src = ix.rope >= 0 ? krb + (int64_t)ix.rope * DR : zero + 512;
+    lds_dma16_untracked(src + (lane >> 3) * 8, rope + wave_u * 1024);
   }
-  const int t = wave_u * 8 + (lane & 7);
-  ix.rope = toks[t < nvalid ? t : 0];
-  return ix;
 }
 
-// Issue the gather of one tile: wave w loads tokens 8w..8w+7 (one nope row per
-// instruction, D/8 lanes) and their rope chunks (one instruction for the 8 tokens).
 template <int D>
 __device__ __forceinline__ void gather_tile(const uint16_t* kb, const uint16_t* krb,
                                             const uint16_t* zero, const TileIdx& ix, uint8_t* nope,
                                             uint8_t* rope, int wave_u, int lane) {
-  using C = Cfg<D>;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int phys = ix.nope[i];
-    const uint16_t* src = phys >= 0 ? kb + (int64_t)phys * D : zero;
-    if (lane < C::LANES_ROW) lds_dma16(src + lane * 8, nope + nope_off<D>(wave_u * 8 + i));
-  }
-  const uint16_t* src = ix.rope >= 0 ? krb + (int64_t)ix.rope * DR : zero + 512;
-  lds_dma16(src + (lane >> 3) * 8, rope + wave_u * 1024);
+  for (int j = 0; j < 9; ++j) gather_part<D>(j, kb, krb, zero, ix, nope, rope, wave_u, lane);
 }
 
 // o *= f on an accumulator element kept in an AGPR (VALU cannot read AGPRs):
@@ -260,17 +261,14 @@ __device__ __forceinline__ float agpr_scale(float o, float f) {
   return o;
 }
 
-__device__ __forceinline__ void wait_all() { __builtin_amdgcn_s_waitcnt(0); }  // vm, lgkm, exp counters 0
-
 template <int IO, int D>
 __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, int splits, Ws ws) {
   using C = Cfg<D>;
-  __shared__ __attribute__((aligned(16))) uint8_t nope0[C::NOPE];
-  __shared__ __attribute__((aligned(16))) uint8_t nope1[C::NOPE];
-  __shared__ __attribute__((aligned(16))) uint8_t rope0[C::ROPE];
-  __shared__ __attribute__((aligned(16))) uint8_t rope1[C::ROPE];
+  __shared__ __attribute__((aligned(16))) uint8_t nope_buf[NBUF][C::NOPE];
+  __shared__ __attribute__((aligned(16))) uint8_t rope_buf[NBUF][C::ROPE];
   __shared__ __attribute__((aligned(16))) uint16_t pt[HB * PP];
   __shared__ __attribute__((aligned(16))) uint16_t qrs[HB * QRP];   // Q rope of all heads
+  __shared__ __attribute__((aligned(16))) int32_t s_ids[4][BN];   // token-id ring (tiles t+2 .. t+4)
   __shared__ float s_alpha[HB];
   __shared__ float s_l[HB];
   __shared__ int s_flag[2];
@@ -284,7 +282,7 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   const int t_beg = sp * per;
   const int t_end = (t_beg + per < ntok_all ? t_beg + per : ntok_all);
   const int ntok = t_end > t_beg ? t_end - t_beg : 0;
-  const int32_t* toks = ws.tokens + (int64_t)r * cap + t_beg;
+  const int32_t* toks = ws.tokens + (int64_t)r * ws.tstride + t_beg;
   uint16_t* out = reinterpret_cast<uint16_t*>(a.out);
   const int n1 = a.n1;
 
@@ -312,11 +310,38 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   const int ntiles = (ntok + BN - 1) / BN;
 
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  // ---- start the first gather, then load Q^T (B operand of S^T) for this wave's 32 heads
-  TileIdx ix_next = load_idx(toks, ntok < BN ? ntok : BN, wave_u, lane);
-  gather_tile<D>(kb, krb, ws.zero, ix_next, nope0, rope0, wave_u, lane);
-  if (ntiles > 1) ix_next = load_idx(toks + BN, ntok - BN < BN ? ntok - BN : BN, wave_u, lane);
-
+  // Token ids travel the same ordered path as the gathers: wave w copies ids
+  // 8w..8w+7 of tile t (2 lanes x 16 B, direct-to-LDS) into ring slot t % 4, four
+  // tiles ahead, just before the gathers of tile t-2; the loop-top vmcnt wait
+  // that retires a tile's gathers then also covers the ids read after the
+  // barrier. (Scalar loads would share lgkmcnt with the LDS reads and every LDS
+  // wait would drain them.) Tiles past the end re-read the last tile, so every
+  // wave issues exactly GPW loads per tile.
+  auto clamp_tile = [&](int t) { return t < ntiles ? t : ntiles - 1; };
+  auto ids_dma = [&](int t) {
+    if (lane < 2)
+      lds_dma16_sbase_untracked(toks + clamp_tile(t) * BN + wave_u * 8, lane * 16, &s_ids[t & 3][wave_u * 8]);
+  };
+  // ids of tile t from the ring; slots past the token list take the tile's first token
+  auto tile_idx = [&](int t) {
+    const int tb = clamp_tile(t) * BN;
+    const int nvalid = ntok - tb < BN ? ntok - tb : BN;
+    const int k = wave_u * 8 + (lane & 7);
+    int v = s_ids[t & 3][k];
+    v = k < nvalid ? v : s_ids[t & 3][0];
+    TileIdx ix;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ix.nope[i] = __builtin_amdgcn_readlane(v, i);
+    ix.rope = v;
+    return ix;
+  };
+  // ---- ids of tiles 0..3, the first two gathers, then Q^T (B operand of S^T) for this wave's 32 heads
+#pragma unroll
+  for (int t = 0; t < 4; ++t) ids_dma(t);
+  wait_vmcnt<0>();
+  lds_barrier();
+  gather_tile<D>(kb, krb, ws.zero, tile_idx(0), nope_buf[0], rope_buf[0], wave_u, lane);
+  gather_tile<D>(kb, krb, ws.zero, tile_idx(1), nope_buf[1], rope_buf[1], wave_u, lane);
   const int hq = wave * 32 + (lane & 31);
   const uint16_t* qn = reinterpret_cast<const uint16_t*>(a.q) + ((int64_t)r * n1 + hq) * D;
   uint4 qf[C::KSN];   // nope part in VGPRs; the rope part goes to LDS (qrs)
@@ -346,20 +371,25 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
       for (int i = 0; i < 16; ++i) o[mt][nt][i] = 0.f;
   if (threadIdx.x < 2) s_flag[threadIdx.x] = 0;
 
-  auto tile = [&](int t, const uint8_t* nope, const uint8_t* rope, uint8_t* nope_nx,
-                  uint8_t* rope_nx) {
-    wait_all();
-    __syncthreads();  // tile t resident; every wave finished tile t-1 (pt, s_alpha, other buffer free)
+  wait_vmcnt<0>();
+  for (int t = 0; t < ntiles; ++t) {
+    const uint8_t* nope = nope_buf[t % NBUF];
+    const uint8_t* rope = rope_buf[t % NBUF];
+    wait_vmcnt<C::GPW>();   // this wave's gathers of tile t (and ids of tile t+2) landed; tile t+1 may be in flight
+    lds_barrier();          // tile t resident; every wave finished tile t-1 (pt, s_alpha, its buffer free)
     const int tb = t * BN;
     const int nvalid = ntok - tb < BN ? ntok - tb : BN;
     if (threadIdx.x == 0) s_flag[(t + 1) & 1] = 0;
-    if (t + 1 < ntiles) {
-      gather_tile<D>(kb, krb, ws.zero, ix_next, nope_nx, rope_nx, wave_u, lane);
-      if (t + 2 < ntiles) {
-        const int tb2 = tb + 2 * BN;
-        ix_next = load_idx(toks + tb2, ntok - tb2 < BN ? ntok - tb2 : BN, wave_u, lane);
-      }
-    }
+    // the GPW loads of tile t+2 (gathers, then the ids of tile t+4) are spread
+    // over the S^T MFMA chain: issued back to back they stall the wave while the
+    // CU's vector-memory path drains
+    const TileIdx ix = tile_idx(t + 2);
+    uint8_t* gnope = nope_buf[(t + 2) % NBUF];
+    uint8_t* grope = rope_buf[(t + 2) % NBUF];
+    auto issue_load = [&](int j) {
+      if (j < C::GPW - 1) gather_part<D>(j, kb, krb, ws.zero, ix, gnope, grope, wave_u, lane);
+      else ids_dma(t + 4);   // slot (t+4)%4 held the ids of tile t, read two iterations ago
+    };
     // ---- S^T[32 tokens, 32 heads] for this wave
     f32x16 s = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     const int tr = lane & 31, kg = lane >> 5;
@@ -370,15 +400,23 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
       return ks < C::KSN ? *reinterpret_cast<const uint4*>(arow + ks * 32)
                          : *reinterpret_cast<const uint4*>(rope + rope_off(tr, (ks - C::KSN) * 2 + kg));
     };
+    // the Q-rope B fragments (LDS) are fetched with the first operands, so the
+    // rope k-steps at the end of the chain do not wait on LDS
+    uint4 qr[(C::KS - C::KSN)];
+#pragma unroll
+    for (int j = 0; j < C::KS - C::KSN; ++j)
+      qr[j] = *reinterpret_cast<const uint4*>(qrs + hq * QRP + j * 16 + kg * 8);
     uint4 af[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) af[j] = a_frag(j);
 #pragma unroll
     for (int ks = 0; ks < C::KS; ++ks) {
-      const uint4 bq = ks < C::KSN ? qf[ks]
-                                   : *reinterpret_cast<const uint4*>(qrs + hq * QRP + (ks - C::KSN) * 16 + kg * 8);
+      const uint4 bq = ks < C::KSN ? qf[ks] : qr[ks - C::KSN];
       s = Mfma<IO>::m32(af[ks & 3], bq, s);
       if (ks + 4 < C::KS) af[ks & 3] = a_frag(ks + 4);
+#pragma unroll
+      for (int j = 0; j < C::GPW; ++j)
+        if (j * C::KS / C::GPW == ks) issue_load(j);
       __builtin_amdgcn_sched_barrier(0);
     }
     // ---- online softmax for head hq over this tile (lane holds 16 tokens)
@@ -397,7 +435,7 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
         mx = fmaxf(mx, s[i]);
       }
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx = max_half_swap(mx);
     m_true = fmaxf(m_true, mx);
     float alpha = 1.f;
     if (mx > m_used + TAU) {
@@ -421,7 +459,7 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
     l_part = l_part * alpha + psum;
     if (lane < 32) s_alpha[hq] = alpha;
     if (alpha != 1.f) s_flag[t & 1] = 1;
-    __syncthreads();  // P, alpha and the flag of tile t complete
+    lds_barrier();  // P, alpha and the flag of tile t complete
     // ---- O[128 heads, this wave's D/4 columns] = alpha * O + P V
     if (s_flag[t & 1]) {
 #pragma unroll
@@ -434,30 +472,34 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
         }
     }
     const int g16 = lane >> 4, c16 = lane & 15;
+    // every operand of the tile's PV product (P fragments and transposed V reads
+    // for both 16-token steps) is requested first; the 2 x 4 x NT MFMAs then only
+    // wait for the reads they consume, in issue order
+    constexpr int KQ = BN / 16;
+    uint4 pa[KQ][4], vb[KQ][C::NT];
 #pragma unroll
-    for (int kq = 0; kq < BN / 16; ++kq) {
-      uint4 pa[4];
+    for (int kq = 0; kq < KQ; ++kq) {
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
-        pa[mt] = *reinterpret_cast<const uint4*>(pt + (mt * 32 + (lane & 31)) * PP + kq * 16 + kg * 8);
+        pa[kq][mt] = *reinterpret_cast<const uint4*>(pt + (mt * 32 + (lane & 31)) * PP + kq * 16 + kg * 8);
 #pragma unroll
       for (int nt = 0; nt < C::NT; ++nt) {
         const int col = wave * C::DW + nt * 32 + (g16 & 1) * 16 + 4 * (c16 & 3);
         const int tok0 = kq * 16 + (g16 >> 1) * 8 + (c16 >> 2);
         const uint2 lo = ds_read_tr(nope + nope_off<D>(tok0) + col * 2);
         const uint2 hi = ds_read_tr(nope + nope_off<D>(tok0 + 4) + col * 2);
-        const uint4 vb = make_uint4(lo.x, lo.y, hi.x, hi.y);
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) o[mt][nt] = Mfma<IO>::m32(pa[mt], vb, o[mt][nt]);
-        __builtin_amdgcn_sched_barrier(0);
+        vb[kq][nt] = make_uint4(lo.x, lo.y, hi.x, hi.y);
       }
     }
-  };
-
-  for (int t = 0; t < ntiles; t += 2) {
-    tile(t, nope0, rope0, nope1, rope1);
-    if (t + 1 < ntiles) tile(t + 1, nope1, rope1, nope0, rope0);
+#pragma unroll
+    for (int kq = 0; kq < KQ; ++kq)
+#pragma unroll
+      for (int nt = 0; nt < C::NT; ++nt)
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) o[mt][nt] = Mfma<IO>::m32(pa[kq][mt], vb[kq][nt], o[mt][nt]);
+    __builtin_amdgcn_sched_barrier(0);
   }
+  wait_vmcnt<0>();   // the ring's last (unused) gathers must land before the LDS is released
 
   // ---- epilogue
   const float l_tot = l_part + __shfl_xor(l_part, 32);
