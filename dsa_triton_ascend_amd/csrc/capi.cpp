@@ -129,6 +129,7 @@ int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key, cons
     return fail(DSA_ERR_INVALID, "dsa_sfa_fwd: sm_max and sm_sum must both be given or both NULL");
   if ((int64_t)sparse_count * sparse_block_size > (1 << 20))
     return fail(DSA_ERR_UNSUPPORTED, "dsa_sfa_fwd: sparse_count*sparse_block_size > 2^20 tokens");
+  if (kv_splits > 16) return fail(DSA_ERR_UNSUPPORTED, "dsa_sfa_fwd: kv_splits=%d > 16", kv_splits);
   const size_t need = sfa_workspace_bytes(total_rows, n1, d, sparse_count, sparse_block_size, kv_splits);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
     return fail(DSA_ERR_INVALID, "dsa_sfa_fwd: workspace of %zu bytes required, %zu given", need,

@@ -34,16 +34,19 @@
 //         v_mfma_f32_32x32x16, the V^T operand read with ds_read_b64_tr_b16
 //         straight from the gathered rows (value = key);
 //       * O stays in registers; the epilogue divides by the row sum (or, with
-//         several KV splits, writes unnormalised partials for the combine).
-//  3. sfa_combine_kernel -- merges KV-split partials (log-sum-exp weights).
+//         several KV splits, writes unnormalised partials).
+//  3. sfa_merge_kernel -- merges KV-split partials (log-sum-exp weights).
 // Unlike the reference (sparse_flash_attention_triton.py:509-525) the fp32
 // accumulator never round-trips through HBM for unsplit rows.
+#include <climits>
+
 #include "dsa_common.hpp"
 
 namespace dsa {
 namespace {
 
 constexpr int DR = 64;
+constexpr float LOG2E = 1.4426950408889634f;
 
 struct RowInfo {
   int b, s1, aq, ak, threshold;
@@ -100,12 +103,53 @@ __host__ __device__ inline Ws ws_layout(void* base, int rows, int cap, int n1, i
 
 // ---------------------------------------------------------------- kernel 1
 constexpr int TOK_TPB = 256;
+constexpr int TOK_PER = 8;                       // ids per thread per pass
+constexpr int TOK_CHUNK = TOK_TPB * TOK_PER;     // ids per pass
 
+__device__ __forceinline__ int block_min_i(int v, int* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o));
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  int m = red[0];
+#pragma unroll
+  for (int w = 1; w < TOK_TPB / 64; ++w) m = min(m, red[w]);
+  return m;
+}
+
+// exclusive block scan of v; *tot receives the block total
+__device__ __forceinline__ int block_excl_scan_i(int v, int* red, int* tot) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int n = __shfl_up(x, o);
+    if (lane >= o) x += n;
+  }
+  __syncthreads();
+  if (lane == 63) red[wave] = x;
+  __syncthreads();
+  int off = 0, t = 0;
+#pragma unroll
+  for (int w = 0; w < TOK_TPB / 64; ++w) {
+    off += w < wave ? red[w] : 0;
+    t += red[w];
+  }
+  *tot = t;
+  return off + x - v;
+}
+
+// One work-group per packed query row. Pass c covers ids [c*2048, c*2048+2048):
+// thread t holds ids 8t..8t+7 of the pass in registers (one load each, issued
+// together), the first -1 is found with a block min, per-thread token counts
+// are scanned to output positions, and every page-table lookup of the thread is
+// issued before its stores.
 __global__ __launch_bounds__(TOK_TPB) void sfa_tokens_kernel(SfaArgs a, int cap, Ws ws) {
-  __shared__ int s_first_neg;
-  __shared__ int wsum[TOK_TPB / 64];
+  __shared__ int red[TOK_TPB / 64];
   const int r = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x;
   if (r == 0)
     for (int i = tid; i < 512 + DR; i += TOK_TPB) ws.zero[i] = 0;
   const RowInfo ri = row_info(a, r);
@@ -117,60 +161,132 @@ __global__ __launch_bounds__(TOK_TPB) void sfa_tokens_kernel(SfaArgs a, int cap,
   const int64_t ceil_blocks = ((int64_t)ri.threshold + bs - 1) / bs;
   const int nscan0 = (int)((int64_t)a.topk < ceil_blocks ? a.topk : ceil_blocks);
   const int32_t* ids = a.sidx + (int64_t)r * a.topk;
-  if (tid == 0) s_first_neg = nscan0;
-  __syncthreads();
-  for (int i = tid; i < nscan0; i += TOK_TPB)
-    if (ids[i] == -1) atomicMin(&s_first_neg, i);
-  __syncthreads();
-  const int nscan = s_first_neg;
   const int end_lim = ri.ak < ri.threshold ? ri.ak : ri.threshold;
-  // each thread owns a contiguous run of entries so the block scan keeps order
-  const int per = (nscan + TOK_TPB - 1) / TOK_TPB;
-  const int i0 = tid * per, i1 = (i0 + per < nscan ? i0 + per : nscan);
-  int my = 0;
-  for (int i = i0; i < i1; ++i) {
-    const int id = ids[i];
-    if (id < 0) continue;  // only -1 is defined (stops the scan); other negatives are skipped
-    const int64_t begin = (int64_t)id * bs;
-    if (begin >= ri.threshold) continue;
-    const int64_t e = begin + bs < end_lim ? begin + bs : end_lim;
-    if (e > begin) my += (int)(e - begin);
-  }
-  int v = my;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    int n = __shfl_up(v, o);
-    if (lane >= o) v += n;
-  }
-  if (lane == 63) wsum[wave] = v;
-  __syncthreads();
-  int off = 0, tot = 0;
-#pragma unroll
-  for (int w = 0; w < TOK_TPB / 64; ++w) {
-    off += w < wave ? wsum[w] : 0;
-    tot += wsum[w];
-  }
-  int pos = off + v - my;
   int32_t* out = ws.tokens + (int64_t)r * ws.tstride;
-  for (int i = i0; i < i1; ++i) {
-    const int id = ids[i];
-    if (id < 0) continue;
-    const int64_t begin = (int64_t)id * bs;
-    if (begin >= ri.threshold) continue;
-    const int64_t e = begin + bs < end_lim ? begin + bs : end_lim;
-    for (int64_t t = begin; t < e; ++t) {
-      int64_t p;
-      if (a.block_table) {
-        const int64_t bi = t / a.page_bs;
-        const int blk = bi < a.max_blocks ? a.block_table[(int64_t)ri.b * a.max_blocks + bi] : -1;
-        p = blk < 0 ? -1 : (int64_t)blk * a.page_bs + t % a.page_bs;
-      } else {
-        p = t < a.s2 ? (int64_t)a.key_start[ri.b] + t : -1;
+  auto phys_row = [&](int64_t t) -> int32_t {
+    int64_t p;
+    if (a.block_table) {
+      const int64_t bi = t / a.page_bs;
+      const int blk = bi < a.max_blocks ? a.block_table[(int64_t)ri.b * a.max_blocks + bi] : -1;
+      p = blk < 0 ? -1 : (int64_t)blk * a.page_bs + t % a.page_bs;
+    } else {
+      p = t < a.s2 ? (int64_t)a.key_start[ri.b] + t : -1;
+    }
+    return (p >= 0 && p < a.key_rows) ? (int32_t)p : -1;
+  };
+  int base = 0;   // tokens written by earlier passes
+  for (int c0 = 0; c0 < nscan0; c0 += TOK_CHUNK) {
+    const int g0 = c0 + tid * TOK_PER;
+    int v[TOK_PER];
+#pragma unroll
+    for (int j = 0; j < TOK_PER; ++j) v[j] = g0 + j < nscan0 ? ids[g0 + j] : -2;  // -2: past the scan
+    int fneg = INT_MAX;
+#pragma unroll
+    for (int j = TOK_PER - 1; j >= 0; --j) fneg = v[j] == -1 ? g0 + j : fneg;
+    fneg = block_min_i(fneg, red);   // the scan stops at the first -1 (only -1 is defined to stop it)
+    int cnt[TOK_PER], my = 0;
+#pragma unroll
+    for (int j = 0; j < TOK_PER; ++j) {
+      int n = 0;
+      if (g0 + j < fneg && v[j] >= 0) {   // other negative ids are skipped
+        const int64_t begin = (int64_t)v[j] * bs;
+        if (begin < ri.threshold) {
+          const int64_t e = begin + bs < end_lim ? begin + bs : end_lim;
+          n = e > begin ? (int)(e - begin) : 0;
+        }
       }
-      out[pos++] = (p >= 0 && p < a.key_rows) ? (int32_t)p : -1;
+      cnt[j] = n;
+      my += n;
+    }
+    int tot;
+    int pos = base + block_excl_scan_i(my, red, &tot);
+    if (bs == 1) {
+      int32_t pr[TOK_PER];
+#pragma unroll
+      for (int j = 0; j < TOK_PER; ++j) pr[j] = cnt[j] ? phys_row(v[j]) : 0;
+#pragma unroll
+      for (int j = 0; j < TOK_PER; ++j)
+        if (cnt[j]) out[pos++] = pr[j];
+    } else {
+#pragma unroll 1
+      for (int j = 0; j < TOK_PER; ++j)
+        for (int k = 0; k < cnt[j]; ++k) out[pos++] = phys_row((int64_t)v[j] * bs + k);
+    }
+    base += tot;
+    if (fneg != INT_MAX) break;
+  }
+  if (tid == 0) ws.counts[r] = base;
+}
+
+// ---------------------------------------------------------------- kernel 3
+// Merge of the KV-split partials. One work-group per (row, 4 heads); thread t
+// owns columns 8(t%64)..+8 of head 4 blockIdx.y + t/64 and issues the loads of
+// every split before using any, so the launch streams the partials at memory
+// bandwidth. Per head: M = max m_used and m_true over the splits with l > 0,
+// w_s = 2^((m_s - M) log2 e), L = sum l_s w_s, out = sum_s w_s O_s / L;
+// softmax_max / sum as for an unsplit row.
+constexpr int MERGE_MAX_SPLITS = 16;
+
+template <int IO>
+__global__ __launch_bounds__(256) void sfa_merge_kernel(SfaArgs a, int splits, Ws ws) {
+  const int r = blockIdx.x;
+  const int n1 = a.n1, D = a.d;
+  const int h = blockIdx.y * 4 + (threadIdx.x >> 6);
+  const int c = (threadIdx.x & 63) * 8;
+  if (h >= n1) return;
+  const float* ps = ws.part_s + (int64_t)r * splits * n1 * 3;
+  float M = -INFINITY, mt = -INFINITY;
+  for (int sp = 0; sp < splits; ++sp) {
+    const float* q = ps + ((int64_t)sp * n1 + h) * 3;
+    if (q[2] > 0.f) {
+      M = fmaxf(M, q[0]);
+      mt = fmaxf(mt, q[1]);
     }
   }
-  if (tid == 0) ws.counts[r] = tot;
+  float w[MERGE_MAX_SPLITS];
+  float L = 0.f;
+#pragma unroll
+  for (int sp = 0; sp < MERGE_MAX_SPLITS; ++sp) {
+    w[sp] = 0.f;
+    if (sp < splits) {
+      const float* q = ps + ((int64_t)sp * n1 + h) * 3;
+      if (q[2] > 0.f) {
+        w[sp] = exp2f((q[0] - M) * LOG2E);
+        L += q[2] * w[sp];
+      }
+    }
+  }
+  if (c < D) {
+    float4 v[MERGE_MAX_SPLITS][2];
+#pragma unroll
+    for (int sp = 0; sp < MERGE_MAX_SPLITS; ++sp)
+      if (w[sp] != 0.f) {   // empty splits (l = 0) have weight 0 and no partial O
+        const float4* src = reinterpret_cast<const float4*>(ws.part_o + (((int64_t)r * splits + sp) * n1 + h) * D + c);
+        v[sp][0] = src[0];
+        v[sp][1] = src[1];
+      }
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int sp = 0; sp < MERGE_MAX_SPLITS; ++sp)
+      if (w[sp] != 0.f) {
+        acc[0] += v[sp][0].x * w[sp];
+        acc[1] += v[sp][0].y * w[sp];
+        acc[2] += v[sp][0].z * w[sp];
+        acc[3] += v[sp][0].w * w[sp];
+        acc[4] += v[sp][1].x * w[sp];
+        acc[5] += v[sp][1].y * w[sp];
+        acc[6] += v[sp][1].z * w[sp];
+        acc[7] += v[sp][1].w * w[sp];
+      }
+    const float il = L > 0.f ? 1.f / L : 0.f;
+    uint16_t* orow = reinterpret_cast<uint16_t*>(a.out) + ((int64_t)r * n1 + h) * D + c;
+    *reinterpret_cast<uint4*>(orow) = make_uint4(pack2<IO>(acc[0] * il, acc[1] * il), pack2<IO>(acc[2] * il, acc[3] * il),
+                                                 pack2<IO>(acc[4] * il, acc[5] * il), pack2<IO>(acc[6] * il, acc[7] * il));
+  }
+  if (c == 0 && a.sm_max) {
+    a.sm_max[(int64_t)r * n1 + h] = L > 0.f ? mt : 0.f;
+    a.sm_sum[(int64_t)r * n1 + h] = L > 0.f ? L * exp2f((M - mt) * LOG2E) : 0.f;
+  }
 }
 
 // ---------------------------------------------------------------- kernel 2
@@ -180,7 +296,6 @@ constexpr int BN = 32;      // tokens per tile
 constexpr int NBUF = 3;     // gather ring: tile t read, t+1 and t+2 in flight
 constexpr int PP = BN + 8;  // P tile pitch (elements)
 constexpr int QRP = DR + 8; // Q-rope LDS pitch (elements): 144-byte rows, conflict-free 16-byte reads
-constexpr float LOG2E = 1.4426950408889634f;
 // Lazy-rescale threshold (natural units): the exponent reference m_used only
 // moves when a tile's max exceeds it by more than TAU, so P = exp(x - m_used)
 // stays below e^40 (exact in relative terms in fp32 / bf16 / fp16-free paths)
@@ -537,50 +652,13 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   }
 }
 
-// ---------------------------------------------------------------- kernel 3
-template <int IO>
-__global__ __launch_bounds__(256) void sfa_combine_kernel(SfaArgs a, int splits, Ws ws) {
-  const int r = blockIdx.x;
-  const int h = blockIdx.y;
-  const int n1 = a.n1, D = a.d;
-  const float* ps = ws.part_s + (int64_t)r * splits * n1 * 3;
-  float M = -INFINITY, mt = -INFINITY;
-  for (int s = 0; s < splits; ++s) {
-    const float* q = ps + ((int64_t)s * n1 + h) * 3;
-    if (q[2] > 0.f) {
-      M = fmaxf(M, q[0]);
-      mt = fmaxf(mt, q[1]);
-    }
-  }
-  float L = 0.f;
-  for (int s = 0; s < splits; ++s) {
-    const float* q = ps + ((int64_t)s * n1 + h) * 3;
-    if (q[2] > 0.f) L += q[2] * exp2f((q[0] - M) * LOG2E);
-  }
-  uint16_t* orow = reinterpret_cast<uint16_t*>(a.out) + ((int64_t)r * n1 + h) * D;
-  const float inv = L > 0.f ? 1.f / L : 0.f;
-  for (int d = threadIdx.x; d < D; d += 256) {
-    float acc = 0.f;
-    for (int s = 0; s < splits; ++s) {
-      const float* q = ps + ((int64_t)s * n1 + h) * 3;
-      if (q[2] > 0.f)
-        acc += ws.part_o[(((int64_t)r * splits + s) * n1 + h) * D + d] * exp2f((q[0] - M) * LOG2E);
-    }
-    orow[d] = from_f32<IO>(acc * inv);
-  }
-  if (threadIdx.x == 0 && a.sm_max) {
-    a.sm_max[(int64_t)r * n1 + h] = L > 0.f ? mt : 0.f;
-    a.sm_sum[(int64_t)r * n1 + h] = L > 0.f ? L * exp2f((M - mt) * LOG2E) : 0.f;
-  }
-}
-
 template <int IO, int D>
 hipError_t launch_attn_d(const SfaArgs& a, hipStream_t s, int cap, int splits, Ws ws) {
   hipLaunchKernelGGL((sfa_attn_kernel<IO, D>), dim3(a.total_rows, splits), dim3(NWV * 64), 0, s, a,
                      cap, splits, ws);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;
-  hipLaunchKernelGGL((sfa_combine_kernel<IO>), dim3(a.total_rows, a.n1), dim3(256), 0, s, a, splits, ws);
+  hipLaunchKernelGGL((sfa_merge_kernel<IO>), dim3(a.total_rows, (a.n1 + 3) / 4), dim3(256), 0, s, a, splits, ws);
   return hipGetLastError();
 }
 

@@ -123,6 +123,7 @@ size_t dsa_sfa_workspace_bytes(int total_rows, int n1, int d, int sparse_count,
  *   N1 <= 128, D in {128, 256, 512}, Dr = 64, sparse_block_size a power of 2 <= 128.
  *   sm_max / sm_sum may be NULL (not requested).
  *   workspace: >= dsa_sfa_workspace_bytes(...) bytes (may be NULL when that is 0).
+ *   kv_splits: KV splits per row (<= 0: the library's choice, at most 16).
  */
 int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key,
                 const void* key_rope, int io_dtype, const int32_t* sparse_indices,

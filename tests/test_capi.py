@@ -63,6 +63,9 @@ def test_invalid_arguments_return_status_without_gpu():
     bad = list(base)
     bad[27], bad[28] = None, 0
     assert lib.dsa_sfa_fwd(*bad) == _lib.DSA_ERR_INVALID and b"workspace" in lib.dsa_last_error()
+    bad = list(base)
+    bad[29] = 17
+    assert lib.dsa_sfa_fwd(*bad) == _lib.DSA_ERR_UNSUPPORTED and b"kv_splits" in lib.dsa_last_error()
     assert lib.dsa_sfa_workspace_bytes(4096, 128, 512, 2048, 1, 0) >= 4096 * 2048 * 4
 
 
