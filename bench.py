@@ -116,6 +116,36 @@ def bench_sfa(plan_kwargs, steps, warmup, torch):
     return sec, ms
 
 
+# C5 algorithmic work (four causal sequences 1024/3000/6000/8192, top-2048):
+# indexer sum_b L_b (L_b + 1) / 2 = 56,587,828 visible pairs x 64 heads x 128 x 2;
+# attention sum_b sum_s min(s + 1, 2048) = 29,445,632 (row, token) pairs x 128 heads
+# x (576 + 512) x 2.
+C5_LI_FLOP = 56587828 * 64 * 128 * 2.0
+C5_SFA_FLOP = 29445632 * 128 * (576 + 512) * 2.0
+
+
+def bench_pipeline_c5(W, reps, torch):
+    """End-to-end C5 rows/s (indexer score + top-k + SFA, one stream, no host sync)
+    and the per-stage device times."""
+    from dsa_triton_ascend_amd.pipeline import PrefillPlan
+    inp = W.tnd_pipeline_inputs(device="cuda:0", seed=42)
+    cu = inp["cu_seqlens"].tolist()
+    plan = PrefillPlan(inp["index_query"], inp["index_key"], inp["index_weights"], inp["query"],
+                       inp["key"], inp["query_rope"], inp["key_rope"], cu,
+                       sparse_count=inp["sparse_count"], scale_value=inp["scale_value"])
+    rows = int(cu[-1])
+    for _ in range(2):
+        plan.run()
+    (t_all,) = event_time([plan.run], reps, torch)
+    t_score, t_topk, t_sfa = event_time([plan.indexer.score, plan.indexer.topk, plan.attention.run], reps, torch)
+    res = {"ms": round(t_all, 4), "rows_per_s": round(rows / (t_all * 1e-3), 1), "rows": rows,
+           "li_score_ms": round(t_score, 4), "li_topk_ms": round(t_topk, 4), "sfa_ms": round(t_sfa, 4),
+           "li_tflops": round(C5_LI_FLOP / t_score / 1e9, 2), "sfa_tflops": round(C5_SFA_FLOP / t_sfa / 1e9, 2),
+           "sfa_frac_mfma": round(C5_SFA_FLOP / t_sfa / 1e9 / PEAK_BF16_TFLOPS, 4)}
+    del plan, inp
+    return res
+
+
 def pmc_pass(torch, W):
     from dsa_triton_ascend_amd.lightning_indexer import IndexerPlan
     from dsa_triton_ascend_amd.sparse_flash_attention import AttentionPlan
@@ -227,6 +257,9 @@ def main():
                                           "frac_hbm": round(kv_bytes / ms4 / 1e6 / PEAK_HBM_GBS, 4),
                                           "gathered_kv_bytes": kv_bytes}
             del sd, kw
+            torch.cuda.empty_cache()
+            log("[bench] C5 TND indexer -> SFA pipeline ...")
+            breakdown["pipeline_c5"] = bench_pipeline_c5(W, max(3, args.steps // 4), torch)
             torch.cuda.empty_cache()
         except Exception as e:  # report, keep the headline
             breakdown["sfa_error"] = repr(e)[:300]

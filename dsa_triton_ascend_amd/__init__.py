@@ -5,10 +5,15 @@ Drop-in operators with the reference's Python signatures:
 * :func:`lightning_indexer` (lightning_indexer_triton.py:466) — indexer score + stable top-k
 * :func:`sparse_flash_attention` (sparse_flash_attention_triton.py:1295) — MLA-absorb SFA forward
 
+and :class:`PrefillPlan` / :func:`dsa_prefill`, the two chained on one packed
+(TND) batch with the indexer's top-k feeding the attention in place.
+
 Both run hand-written gfx950 HIP kernels through the C ABI of
 ``libdsa_mi355x.so`` (include/dsa_mi355x.h); PyTorch tensors are only buffers.
 """
 from .lightning_indexer import LightningIndexer, lightning_indexer
+from .pipeline import PrefillPlan, dsa_prefill
 from .sparse_flash_attention import SparseFlashAttention, sparse_flash_attention
 
-__all__ = ["lightning_indexer", "LightningIndexer", "sparse_flash_attention", "SparseFlashAttention"]
+__all__ = ["lightning_indexer", "LightningIndexer", "sparse_flash_attention", "SparseFlashAttention",
+           "PrefillPlan", "dsa_prefill"]
