@@ -19,8 +19,8 @@
 //    ring of three LDS buffers; one LDS-only barrier per tile, so the loads in
 //    flight are never drained by it;
 //  * K rows are stored unpadded with their 16-byte chunks permuted (chunk c of
-//    key row k sits at c ^ (k & 7)), which keeps the 16-byte B-fragment reads
-//    of 8 consecutive keys on distinct LDS banks;
+//    key row k sits at c ^ (k & 15) for D >= 128), which keeps the 16-byte
+//    B-fragment reads of 16 consecutive keys on distinct LDS banks;
 //  * per tile a wave issues its B-fragment reads ahead of the MFMAs and keeps
 //    one accumulator set per 32-key subtile, so the epilogue of one subtile can
 //    overlap the MFMAs of the next;
@@ -53,7 +53,9 @@ constexpr int NW = DSA_LI_NW;  // waves (= query rows) per work-group
 template <int D> struct LiTile {
   static constexpr int BN = D == 96 ? 128 : (D <= 128 ? DSA_LI_BN : 32);  // keys per LDS tile
   static constexpr int CPR = D / 8;                  // 16-byte chunks per key row
-  static constexpr int SWZ = CPR % 8 == 0 ? 7 : 3;   // chunk permutation mask (c ^ (k & SWZ)); stays in the row
+  // chunk permutation mask (c ^ (k & SWZ), stays in the row): 16 consecutive key rows
+  // then cover 16 distinct 16-byte bank groups, conflict-free for 16-lane LDS reads
+  static constexpr int SWZ = CPR % 16 == 0 ? 15 : (CPR % 8 == 0 ? 7 : 3);
   static constexpr int SLOTS = BN * CPR;             // 16-byte slots per tile
   static constexpr int IPW = SLOTS / (NW * 64);      // direct-to-LDS loads per wave per tile
   static_assert(IPW >= 1 && IPW * NW * 64 == SLOTS, "tile must split evenly over the waves");
