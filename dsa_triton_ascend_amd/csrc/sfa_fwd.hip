@@ -381,12 +381,11 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   using C = Cfg<D>;
   __shared__ __attribute__((aligned(16))) uint8_t nope_buf[NBUF][C::NOPE];
   __shared__ __attribute__((aligned(16))) uint8_t rope_buf[NBUF][C::ROPE];
-  __shared__ __attribute__((aligned(16))) uint16_t pt[HB * PP];
+  __shared__ __attribute__((aligned(16))) uint16_t pt[2][HB * PP];   // P of tiles t (PV) and t+1 (softmax)
   __shared__ __attribute__((aligned(16))) uint16_t qrs[HB * QRP];   // Q rope of all heads
   __shared__ __attribute__((aligned(16))) int32_t s_ids[4][BN];   // token-id ring (tiles t+2 .. t+4)
-  __shared__ float s_alpha[HB];
+  __shared__ float s_alpha[2][HB];   // O rescale factors of tiles t and t+1
   __shared__ float s_l[HB];
-  __shared__ int s_flag[2];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = blockIdx.x;
@@ -484,30 +483,17 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
     for (int nt = 0; nt < C::NT; ++nt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) o[mt][nt][i] = 0.f;
-  if (threadIdx.x < 2) s_flag[threadIdx.x] = 0;
 
-  wait_vmcnt<0>();
-  for (int t = 0; t < ntiles; ++t) {
-    const uint8_t* nope = nope_buf[t % NBUF];
-    const uint8_t* rope = rope_buf[t % NBUF];
-    wait_vmcnt<C::GPW>();   // this wave's gathers of tile t (and ids of tile t+2) landed; tile t+1 may be in flight
-    lds_barrier();          // tile t resident; every wave finished tile t-1 (pt, s_alpha, its buffer free)
-    const int tb = t * BN;
-    const int nvalid = ntok - tb < BN ? ntok - tb : BN;
-    if (threadIdx.x == 0) s_flag[(t + 1) & 1] = 0;
-    // the GPW loads of tile t+2 (gathers, then the ids of tile t+4) are spread
-    // over the S^T MFMA chain: issued back to back they stall the wave while the
-    // CU's vector-memory path drains
-    const TileIdx ix = tile_idx(t + 2);
-    uint8_t* gnope = nope_buf[(t + 2) % NBUF];
-    uint8_t* grope = rope_buf[(t + 2) % NBUF];
-    auto issue_load = [&](int j) {
-      if (j < C::GPW - 1) gather_part<D>(j, kb, krb, ws.zero, ix, gnope, grope, wave_u, lane);
-      else ids_dma(t + 4);   // slot (t+4)%4 held the ids of tile t, read two iterations ago
-    };
-    // ---- S^T[32 tokens, 32 heads] for this wave
-    f32x16 s = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    const int tr = lane & 31, kg = lane >> 5;
+  const int tr = lane & 31, kg = lane >> 5;
+  const int g16 = lane >> 4, c16 = lane & 15;
+  constexpr int KQ = BN / 16;
+
+  // ---- S^T[32 tokens, 32 heads] of tile u for this wave; `spread(ks)` issues the
+  // loads scheduled after k-step ks (the next tile's gathers ride on this chain)
+  auto s_tile = [&](int u, auto&& spread) __attribute__((always_inline)) -> f32x16 {
+    const uint8_t* nope = nope_buf[u % NBUF];
+    const uint8_t* rope = rope_buf[u % NBUF];
+    f32x16 sacc = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     const uint8_t* arow = nope + nope_off<D>(tr) + kg * 16;
     // operand loads run 4 k-steps ahead of the MFMA chain; the sched barrier
     // keeps that order (hoisting every load would cost ~4 VGPRs per k-step)
@@ -527,76 +513,72 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
 #pragma unroll
     for (int ks = 0; ks < C::KS; ++ks) {
       const uint4 bq = ks < C::KSN ? qf[ks] : qr[ks - C::KSN];
-      s = Mfma<IO>::m32(af[ks & 3], bq, s);
+      sacc = Mfma<IO>::m32(af[ks & 3], bq, sacc);
       if (ks + 4 < C::KS) af[ks & 3] = a_frag(ks + 4);
-#pragma unroll
-      for (int j = 0; j < C::GPW; ++j)
-        if (j * C::KS / C::GPW == ks) issue_load(j);
+      spread(ks);
       __builtin_amdgcn_sched_barrier(0);
     }
-    // ---- online softmax for head hq over this tile (lane holds 16 tokens)
-    float mx = -INFINITY;
-    if (nvalid == BN) {
+    return sacc;
+  };
+
+  // ---- scores of tile u scaled; slots past the token list (partial last tile) masked
+  auto scale_tile = [&](int u, f32x16& sv) __attribute__((always_inline)) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        s[i] *= a.scale;
-        mx = fmaxf(mx, s[i]);
-      }
-    } else {  // partial last tile: mask the slots past the token list
+    for (int i = 0; i < 16; ++i) sv[i] *= a.scale;
+    const int nvalid = ntok - u * BN;
+    if (nvalid < BN) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int tk = (i >> 2) * 8 + kg * 4 + (i & 3);
-        s[i] = tk < nvalid ? s[i] * a.scale : -INFINITY;
-        mx = fmaxf(mx, s[i]);
+        sv[i] = tk < nvalid ? sv[i] : -INFINITY;
       }
     }
-    mx = max_half_swap(mx);
+  };
+
+  // ---- online softmax of tile u for head hq (lane holds 16 scaled scores): P (io
+  // dtype) to pt[u & 1], the O rescale factor to s_alpha[u & 1]. Branch-free, so
+  // the scheduler can place it among the PV MFMAs it is issued with.
+  auto softmax_tile = [&](int u, const f32x16& sv) __attribute__((always_inline)) {
+    float mx = sv[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sv[i]);
+    mx = max_half_swap(mx);   // every tile holds at least one valid token: mx is finite
     m_true = fmaxf(m_true, mx);
-    float alpha = 1.f;
-    if (mx > m_used + TAU) {
-      // first tile: O and l are still zero, nothing to rescale (alpha stays 1)
-      if (m_used != -INFINITY) alpha = __builtin_amdgcn_exp2f((m_used - mx) * LOG2E);
-      m_used = mx;
-    }
+    // lazy rescaling: the reference maximum moves only when the tile max exceeds it
+    // by more than TAU; alpha is exactly 1 otherwise, and 1 on the first tile (O
+    // and l are still zero)
+    const float m_new = mx > m_used + TAU ? mx : m_used;
+    const float alpha = m_used == -INFINITY ? 1.f : __builtin_amdgcn_exp2f((m_used - m_new) * LOG2E);
+    m_used = m_new;
     const float mb = m_used * LOG2E;
     float psum = 0.f;
-    uint16_t* prow = pt + hq * PP + kg * 4;
+    uint16_t* prow = pt[u & 1] + hq * PP + kg * 4;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       float p[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[g * 4 + j], LOG2E, -mb));
+        p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[g * 4 + j], LOG2E, -mb));
         psum += p[j];
       }
       *reinterpret_cast<uint2*>(prow + g * 8) = make_uint2(pack2<IO>(p[0], p[1]), pack2<IO>(p[2], p[3]));
     }
     l_part = l_part * alpha + psum;
-    if (lane < 32) s_alpha[hq] = alpha;
-    if (alpha != 1.f) s_flag[t & 1] = 1;
-    lds_barrier();  // P, alpha and the flag of tile t complete
-    // ---- O[128 heads, this wave's D/4 columns] = alpha * O + P V
-    if (s_flag[t & 1]) {
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float al = s_alpha[mt * 32 + m32_row(i, lane)];
-#pragma unroll
-          for (int nt = 0; nt < C::NT; ++nt) o[mt][nt][i] = agpr_scale(o[mt][nt][i], al);
-        }
-    }
-    const int g16 = lane >> 4, c16 = lane & 15;
-    // every operand of the tile's PV product (P fragments and transposed V reads
-    // for both 16-token steps) is requested first; the 2 x 4 x NT MFMAs then only
-    // wait for the reads they consume, in issue order
-    constexpr int KQ = BN / 16;
+    s_alpha[u & 1][hq] = alpha;   // both lane halves hold the same head and value
+  };
+
+  // ---- O[128 heads, this wave's D/4 columns] += P V for tile u. Every operand (P
+  // fragments of pt[u & 1] and transposed V reads for both 16-token steps) is
+  // requested first; `between()` runs after the requests and before the MFMAs.
+  auto pv_tile = [&](int u, auto&& between) __attribute__((always_inline)) {
+    const uint8_t* nope = nope_buf[u % NBUF];
+    const uint16_t* ptu = pt[u & 1];
     uint4 pa[KQ][4], vb[KQ][C::NT];
 #pragma unroll
     for (int kq = 0; kq < KQ; ++kq) {
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
-        pa[kq][mt] = *reinterpret_cast<const uint4*>(pt + (mt * 32 + (lane & 31)) * PP + kq * 16 + kg * 8);
+        pa[kq][mt] = *reinterpret_cast<const uint4*>(ptu + (mt * 32 + (lane & 31)) * PP + kq * 16 + kg * 8);
 #pragma unroll
       for (int nt = 0; nt < C::NT; ++nt) {
         const int col = wave * C::DW + nt * 32 + (g16 & 1) * 16 + 4 * (c16 & 3);
@@ -606,14 +588,66 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
         vb[kq][nt] = make_uint4(lo.x, lo.y, hi.x, hi.y);
       }
     }
+    between();
 #pragma unroll
     for (int kq = 0; kq < KQ; ++kq)
 #pragma unroll
       for (int nt = 0; nt < C::NT; ++nt)
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) o[mt][nt] = Mfma<IO>::m32(pa[kq][mt], vb[kq][nt], o[mt][nt]);
+  };
+
+  // ---- software pipeline over tiles. Iteration t: (barrier) rescale O for tile t,
+  // S^T of tile t+1 with the loads of tile t+2 spread over it, then the PV MFMAs of
+  // tile t with the softmax of tile t+1 placed between their operand reads and
+  // the MFMAs, so the VALU softmax runs while the matrix core works. Buffers:
+  // tile t (PV) and t+1 (S^T) are read, t+2 is loaded into the third; P and the
+  // rescale factors are double-buffered by tile parity.
+  wait_vmcnt<0>();
+  lds_barrier();   // tile 0 (and Q rope) visible
+  {
+    f32x16 s0 = s_tile(0, [&](int) {});
+    scale_tile(0, s0);
+    softmax_tile(0, s0);
+  }
+  // barrier at the top of iteration t, then rescale O by alpha(t) when any head's
+  // factor differs from 1 (rare: lazy rescaling)
+  auto tile_top = [&](int t) __attribute__((always_inline)) {
+    wait_vmcnt<1>();   // this wave's gathers of tile t+1 landed (the ids copy after them may be in flight)
+    lds_barrier();     // P and alpha of tile t visible; tile t+1 resident; PV of tile t-1 done everywhere
+    const float a0 = s_alpha[t & 1][lane], a1 = s_alpha[t & 1][lane + 64];
+    if (__builtin_amdgcn_ballot_w64(a0 != 1.f || a1 != 1.f)) {
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float al = s_alpha[t & 1][mt * 32 + m32_row(i, lane)];
+#pragma unroll
+          for (int nt = 0; nt < C::NT; ++nt) o[mt][nt][i] = agpr_scale(o[mt][nt][i], al);
+        }
+    }
+  };
+  // The last tile is peeled off the loop so the PV code is never duplicated
+  // across the two arms of a branch (the merge would copy all of O).
+  for (int t = 0; t + 1 < ntiles; ++t) {
+    tile_top(t);
+    const TileIdx ix = tile_idx(t + 2);
+    uint8_t* gnope = nope_buf[(t + 2) % NBUF];   // held tile t-1, whose PV finished before the barrier
+    uint8_t* grope = rope_buf[(t + 2) % NBUF];
+    f32x16 s1 = s_tile(t + 1, [&](int ks) {
+#pragma unroll
+      for (int j = 0; j < C::GPW; ++j)
+        if (j * C::KS / C::GPW == ks) {
+          if (j < C::GPW - 1) gather_part<D>(j, kb, krb, ws.zero, ix, gnope, grope, wave_u, lane);
+          else ids_dma(t + 4);   // slot (t+4)%4 held the ids of tile t, read two iterations ago
+        }
+    });
+    scale_tile(t + 1, s1);
+    pv_tile(t, [&]() { softmax_tile(t + 1, s1); });
     __builtin_amdgcn_sched_barrier(0);
   }
+  tile_top(ntiles - 1);
+  pv_tile(ntiles - 1, [&]() {});
   wait_vmcnt<0>();   // the ring's last (unused) gathers must land before the LDS is released
 
   // ---- epilogue
