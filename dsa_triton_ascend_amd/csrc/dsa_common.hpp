@@ -124,10 +124,7 @@ __device__ __forceinline__ void lds_dma16_untracked(const void* gptr, void* lds_
 // Same with a wave-uniform base address (SGPR pair) and a per-lane 32-bit byte
 // offset: lane l reads sbase + voff[l] and writes LDS [lds_base + 16 l, +16).
 __device__ __forceinline__ void lds_dma16_sbase_untracked(const void* sbase, uint32_t voff, void* lds_base) {
-  // lds_base is wave-uniform; readfirstlane keeps it in an SGPR when the
-  // compiler would otherwise hand the "s" operand a VGPR copy
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
-      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds_base);
+  const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds_base;
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "s"(m0) : "memory");
 }
 

@@ -4,7 +4,8 @@
 // layouts of sparse_flash_attention_triton.py:1353-1450.
 //
 // Kernels:
-//  1. sfa_tokens_kernel -- one work-group per packed query row: applies the
+//  1. sfa_tokens_kernel (sfa_tokens1_kernel when sparse_block_size == 1: one
+//     wave per row) -- one work-group per packed query row: applies the
 //     row-skip rules and the golden's gatherKV scan (first
 //     min(count, ceil(threshold/bs)) ids, stop at the first -1, expand id to
 //     [id*bs, min(id*bs+bs, act_k, threshold))) and writes the row's token list
@@ -33,8 +34,8 @@
 //         D/4-column slice of O[128 heads, D] and accumulates P V on
 //         v_mfma_f32_32x32x16, the V^T operand read with ds_read_b64_tr_b16
 //         straight from the gathered rows (value = key);
-//       * O stays in registers; the epilogue divides by the row sum (or, with
-//         several KV splits, writes unnormalised partials).
+//       * O stays in registers; the epilogue divides by the row sum (with
+//         several KV splits the normalised partial goes out in the io dtype).
 //  3. sfa_merge_kernel -- merges KV-split partials (log-sum-exp weights).
 // Unlike the reference (sparse_flash_attention_triton.py:509-525) the fp32
 // accumulator never round-trips through HBM for unsplit rows.
@@ -72,7 +73,7 @@ struct Ws {
   int32_t* tokens;   // [rows, tstride]
   int tstride;       // token-list row stride: cap rounded up to a whole 32-token tile
   uint16_t* zero;    // one zero KV row: 512 + Dr elements
-  float* part_o;     // [rows, splits, N1, D]   (splits > 1)
+  uint16_t* part_o;  // [rows, splits, N1, D]   O_s / l_s in the io dtype (splits > 1)
   float* part_s;     // [rows, splits, N1, 3]   m_used, m_true, l
 };
 
@@ -90,10 +91,10 @@ __host__ __device__ inline Ws ws_layout(void* base, int rows, int cap, int n1, i
   off += align256((size_t)rows * w.tstride * 4);
   w.zero = reinterpret_cast<uint16_t*>(p + off);
   off += align256((size_t)(512 + DR) * 2);
-  w.part_o = reinterpret_cast<float*>(p + off);
+  w.part_o = reinterpret_cast<uint16_t*>(p + off);
   w.part_s = nullptr;
   if (splits > 1) {
-    off += align256((size_t)rows * splits * n1 * d * 4);
+    off += align256((size_t)rows * splits * n1 * d * 2);
     w.part_s = reinterpret_cast<float*>(p + off);
     off += align256((size_t)rows * splits * n1 * 3 * 4);
   }
@@ -163,12 +164,16 @@ __global__ __launch_bounds__(TOK_TPB) void sfa_tokens_kernel(SfaArgs a, int cap,
   const int32_t* ids = a.sidx + (int64_t)r * a.topk;
   const int end_lim = ri.ak < ri.threshold ? ri.ak : ri.threshold;
   int32_t* out = ws.tokens + (int64_t)r * ws.tstride;
+  // page of token t: shift and mask for power-of-two page sizes (32-bit division otherwise)
+  const bool pow2 = a.block_table && (a.page_bs & (a.page_bs - 1)) == 0;
+  const int pshift = pow2 ? __builtin_ctz((unsigned)a.page_bs) : 0;
   auto phys_row = [&](int64_t t) -> int32_t {
     int64_t p;
     if (a.block_table) {
-      const int64_t bi = t / a.page_bs;
+      const int bi = pow2 ? (int)(t >> pshift) : (int)((uint64_t)t / (unsigned)a.page_bs);
+      const int within = (int)(t - (int64_t)bi * a.page_bs);
       const int blk = bi < a.max_blocks ? a.block_table[(int64_t)ri.b * a.max_blocks + bi] : -1;
-      p = blk < 0 ? -1 : (int64_t)blk * a.page_bs + t % a.page_bs;
+      p = blk < 0 ? -1 : (int64_t)blk * a.page_bs + within;
     } else {
       p = t < a.s2 ? (int64_t)a.key_start[ri.b] + t : -1;
     }
@@ -218,13 +223,107 @@ __global__ __launch_bounds__(TOK_TPB) void sfa_tokens_kernel(SfaArgs a, int cap,
   if (tid == 0) ws.counts[r] = base;
 }
 
+// sparse_block_size == 1 (every id is one token): one wave per packed query row,
+// TOK1_ROWS rows per work-group, no block-level synchronisation. Pass c covers ids
+// [c*2048, c*2048+2048): lane l loads the 16-byte groups i*64 + l (i < 8) of the
+// pass, i.e. ids 4(i*64 + l) .. +3; the first -1 (wave min) ends the scan. Ids are
+// kept in id order: a valid id's output slot is the number of valid ids before it,
+// counted with one ballot + mbcnt per (group row i, position j in the group).
+constexpr int TOK1_ROWS = 4;
+
+__global__ __launch_bounds__(64 * TOK1_ROWS) void sfa_tokens1_kernel(SfaArgs a, int cap, Ws ws) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * TOK1_ROWS + (threadIdx.x >> 6);
+  if (blockIdx.x == 0)
+    for (int i = threadIdx.x; i < 512 + DR; i += 64 * TOK1_ROWS) ws.zero[i] = 0;
+  if (r >= a.total_rows) return;
+  const RowInfo ri = row_info(a, r);
+  if (!ri.active) {
+    if (lane == 0) ws.counts[r] = 0;
+    return;
+  }
+  const int nscan0 = a.topk < ri.threshold ? a.topk : ri.threshold;
+  const int32_t* ids = a.sidx + (int64_t)r * a.topk;
+  const int end_lim = ri.ak < ri.threshold ? ri.ak : ri.threshold;
+  int32_t* out = ws.tokens + (int64_t)r * ws.tstride;
+  const bool vec = (a.topk & 3) == 0;   // 16-byte aligned rows
+  // page of token t: shift and mask for power-of-two page sizes (32-bit division otherwise)
+  const bool pow2 = a.block_table && (a.page_bs & (a.page_bs - 1)) == 0;
+  const int pshift = pow2 ? __builtin_ctz((unsigned)a.page_bs) : 0;
+  auto phys_row = [&](int t) -> int32_t {
+    int64_t p;
+    if (a.block_table) {
+      const int bi = pow2 ? t >> pshift : (int)((unsigned)t / (unsigned)a.page_bs);
+      const int within = t - bi * a.page_bs;
+      const int blk = bi < a.max_blocks ? a.block_table[(int64_t)ri.b * a.max_blocks + bi] : -1;
+      p = blk < 0 ? -1 : (int64_t)blk * a.page_bs + within;
+    } else {
+      p = t < a.s2 ? (int64_t)a.key_start[ri.b] + t : -1;
+    }
+    return (p >= 0 && p < a.key_rows) ? (int32_t)p : -1;
+  };
+  const uint32_t lo_mask = lane < 32 ? (1u << lane) - 1u : 0xFFFFFFFFu;
+  const uint32_t hi_mask = lane < 32 ? 0u : (lane == 32 ? 0u : (1u << (lane - 32)) - 1u);
+  auto below = [&](uint64_t m) {   // set bits of m in lanes below this one
+    return __builtin_popcount((uint32_t)m & lo_mask) + __builtin_popcount((uint32_t)(m >> 32) & hi_mask);
+  };
+  int base = 0;   // tokens written by earlier passes
+  for (int c0 = 0; c0 < nscan0; c0 += 2048) {
+    int v[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int g = c0 + (i * 64 + lane) * 4;
+      if (vec && g + 3 < nscan0) {
+        const int4 x = *reinterpret_cast<const int4*>(ids + g);
+        v[i][0] = x.x; v[i][1] = x.y; v[i][2] = x.z; v[i][3] = x.w;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[i][j] = g + j < nscan0 ? ids[g + j] : -2;   // -2: past the scan
+      }
+    }
+    int fneg = INT_MAX;
+#pragma unroll
+    for (int i = 7; i >= 0; --i)
+#pragma unroll
+      for (int j = 3; j >= 0; --j) fneg = v[i][j] == -1 ? c0 + (i * 64 + lane) * 4 + j : fneg;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) fneg = min(fneg, __shfl_xor(fneg, o));   // only -1 stops the scan
+    bool ok[8][4];
+    int32_t pr[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int pos = c0 + (i * 64 + lane) * 4 + j;
+        ok[i][j] = pos < fneg && v[i][j] >= 0 && v[i][j] < end_lim;   // other negative ids are skipped
+        pr[i][j] = ok[i][j] ? phys_row(v[i][j]) : 0;                  // every lookup issued before the stores
+      }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      int off = base, mine = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint64_t m = __ballot(ok[i][j]);
+        off += below(m);
+        base += __popcll(m);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (ok[i][j]) out[off + mine++] = pr[i][j];
+    }
+    if (fneg != INT_MAX) break;
+  }
+  if (lane == 0) ws.counts[r] = base;
+}
+
 // ---------------------------------------------------------------- kernel 3
 // Merge of the KV-split partials. One work-group per (row, 4 heads); thread t
-// owns columns 8(t%64)..+8 of head 4 blockIdx.y + t/64 and issues the loads of
-// every split before using any, so the launch streams the partials at memory
-// bandwidth. Per head: M = max m_used and m_true over the splits with l > 0,
-// w_s = 2^((m_s - M) log2 e), L = sum l_s w_s, out = sum_s w_s O_s / L;
-// softmax_max / sum as for an unsplit row.
+// owns columns 8(t%64)..+8 of head 4 blockIdx.y + t/64. Each split s left its
+// normalised output O_s / l_s (io dtype; zeros for an empty split) and
+// (m_used_s, m_true_s, l_s); every load is issued before any is used, so the
+// launch streams the partials at memory bandwidth. Per head: M = max m_used_s
+// over the splits with l_s > 0, w_s = l_s 2^((m_used_s - M) log2 e),
+// out = sum_s w_s (O_s / l_s) / sum_s w_s; softmax_max / sum as for an unsplit row.
 constexpr int MERGE_MAX_SPLITS = 16;
 
 template <int IO>
@@ -234,49 +333,47 @@ __global__ __launch_bounds__(256) void sfa_merge_kernel(SfaArgs a, int splits, W
   const int h = blockIdx.y * 4 + (threadIdx.x >> 6);
   const int c = (threadIdx.x & 63) * 8;
   if (h >= n1) return;
+  uint4 v[MERGE_MAX_SPLITS];
+  if (c < D) {
+#pragma unroll
+    for (int sp = 0; sp < MERGE_MAX_SPLITS; ++sp)
+      if (sp < splits) v[sp] = ldg16(ws.part_o + (((int64_t)r * splits + sp) * n1 + h) * D + c);
+  }
   const float* ps = ws.part_s + (int64_t)r * splits * n1 * 3;
+  float mu[MERGE_MAX_SPLITS], ls[MERGE_MAX_SPLITS];
   float M = -INFINITY, mt = -INFINITY;
-  for (int sp = 0; sp < splits; ++sp) {
-    const float* q = ps + ((int64_t)sp * n1 + h) * 3;
-    if (q[2] > 0.f) {
-      M = fmaxf(M, q[0]);
-      mt = fmaxf(mt, q[1]);
+#pragma unroll
+  for (int sp = 0; sp < MERGE_MAX_SPLITS; ++sp) {
+    mu[sp] = -INFINITY;
+    ls[sp] = 0.f;
+    if (sp < splits) {
+      const float* q = ps + ((int64_t)sp * n1 + h) * 3;
+      mu[sp] = q[0];
+      ls[sp] = q[2];
+      if (ls[sp] > 0.f) {
+        M = fmaxf(M, mu[sp]);
+        mt = fmaxf(mt, q[1]);
+      }
     }
   }
   float w[MERGE_MAX_SPLITS];
   float L = 0.f;
 #pragma unroll
   for (int sp = 0; sp < MERGE_MAX_SPLITS; ++sp) {
-    w[sp] = 0.f;
-    if (sp < splits) {
-      const float* q = ps + ((int64_t)sp * n1 + h) * 3;
-      if (q[2] > 0.f) {
-        w[sp] = exp2f((q[0] - M) * LOG2E);
-        L += q[2] * w[sp];
-      }
-    }
+    w[sp] = sp < splits && ls[sp] > 0.f ? ls[sp] * exp2f((mu[sp] - M) * LOG2E) : 0.f;
+    L += w[sp];
   }
   if (c < D) {
-    float4 v[MERGE_MAX_SPLITS][2];
-#pragma unroll
-    for (int sp = 0; sp < MERGE_MAX_SPLITS; ++sp)
-      if (w[sp] != 0.f) {   // empty splits (l = 0) have weight 0 and no partial O
-        const float4* src = reinterpret_cast<const float4*>(ws.part_o + (((int64_t)r * splits + sp) * n1 + h) * D + c);
-        v[sp][0] = src[0];
-        v[sp][1] = src[1];
-      }
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int sp = 0; sp < MERGE_MAX_SPLITS; ++sp)
-      if (w[sp] != 0.f) {
-        acc[0] += v[sp][0].x * w[sp];
-        acc[1] += v[sp][0].y * w[sp];
-        acc[2] += v[sp][0].z * w[sp];
-        acc[3] += v[sp][0].w * w[sp];
-        acc[4] += v[sp][1].x * w[sp];
-        acc[5] += v[sp][1].y * w[sp];
-        acc[6] += v[sp][1].z * w[sp];
-        acc[7] += v[sp][1].w * w[sp];
+      if (sp < splits) {
+        const uint32_t u[4] = {v[sp].x, v[sp].y, v[sp].z, v[sp].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc[2 * j] += w[sp] * to_f32<IO>((uint16_t)(u[j] & 0xFFFFu));
+          acc[2 * j + 1] += w[sp] * to_f32<IO>((uint16_t)(u[j] >> 16));
+        }
       }
     const float il = L > 0.f ? 1.f / L : 0.f;
     uint16_t* orow = reinterpret_cast<uint16_t*>(a.out) + ((int64_t)r * n1 + h) * D + c;
@@ -385,7 +482,7 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   __shared__ __attribute__((aligned(16))) uint16_t qrs[HB * QRP];   // Q rope of all heads
   __shared__ __attribute__((aligned(16))) int32_t s_ids[4][BN];   // token-id ring (tiles t+2 .. t+4)
   __shared__ float s_alpha[2][HB];   // O rescale factors of tiles t and t+1
-  __shared__ float s_l[HB];
+  __shared__ float s_l[HB];   // 1 / row sum, per head
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = blockIdx.x;
@@ -408,13 +505,15 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
           a.sm_max[(int64_t)r * n1 + h] = 0.f;
           a.sm_sum[(int64_t)r * n1 + h] = 0.f;
         }
-    } else {
+    } else {   // empty split: l = 0 and a zero partial (the merge reads every split)
       float* ps = ws.part_s + ((int64_t)r * splits + sp) * n1 * 3;
       for (int h = threadIdx.x; h < n1; h += NWV * 64) {
         ps[h * 3 + 0] = -INFINITY;
         ps[h * 3 + 1] = -INFINITY;
         ps[h * 3 + 2] = 0.f;
       }
+      uint4* po = reinterpret_cast<uint4*>(ws.part_o + ((int64_t)r * splits + sp) * n1 * D);
+      for (int i = threadIdx.x; i < n1 * D / 8; i += NWV * 64) po[i] = make_uint4(0, 0, 0, 0);
     }
     return;
   }
@@ -449,25 +548,27 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
     ix.rope = v;
     return ix;
   };
-  // ---- ids of tiles 0..3, the first two gathers, then Q^T (B operand of S^T) for this wave's 32 heads
-#pragma unroll
-  for (int t = 0; t < 4; ++t) ids_dma(t);
-  wait_vmcnt<0>();
-  lds_barrier();
-  gather_tile<D>(kb, krb, ws.zero, tile_idx(0), nope_buf[0], rope_buf[0], wave_u, lane);
-  gather_tile<D>(kb, krb, ws.zero, tile_idx(1), nope_buf[1], rope_buf[1], wave_u, lane);
+  // ---- Q^T (B operand of S^T) for this wave's 32 heads and the Q rope of all
+  // heads, then the ids of tiles 0..3 (their latencies overlap), then the first
+  // two gathers
   const int hq = wave * 32 + (lane & 31);
   const uint16_t* qn = reinterpret_cast<const uint16_t*>(a.q) + ((int64_t)r * n1 + hq) * D;
   uint4 qf[C::KSN];   // nope part in VGPRs; the rope part goes to LDS (qrs)
 #pragma unroll
   for (int ks = 0; ks < C::KSN; ++ks)
     qf[ks] = hq < n1 ? ldg16(qn + ks * 16 + (lane >> 5) * 8) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+  for (int t = 0; t < 4; ++t) ids_dma(t);
   for (int c = threadIdx.x; c < HB * (DR / 8); c += NWV * 64) {
     const int h = c / (DR / 8), e = (c % (DR / 8)) * 8;
     *reinterpret_cast<uint4*>(qrs + h * QRP + e) =
         h < n1 ? ldg16(reinterpret_cast<const uint16_t*>(a.qr) + ((int64_t)r * n1 + h) * DR + e)
                : make_uint4(0, 0, 0, 0);
   }
+  wait_vmcnt<0>();
+  lds_barrier();
+  gather_tile<D>(kb, krb, ws.zero, tile_idx(0), nope_buf[0], rope_buf[0], wave_u, lane);
+  gather_tile<D>(kb, krb, ws.zero, tile_idx(1), nope_buf[1], rope_buf[1], wave_u, lane);
 
   float m_used = -INFINITY, m_true = -INFINITY, l_part = 0.f;
   {
@@ -653,7 +754,7 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   // ---- epilogue
   const float l_tot = l_part + __shfl_xor(l_part, 32);
   __syncthreads();  // all PV reads of s_alpha / pt done before s_l is written
-  if (lane < 32) s_l[hq] = l_tot;
+  if (lane < 32) s_l[hq] = 1.f / l_tot;   // l > 0: a row or split holds at least one token
   if (splits == 1) {
     if (lane < 32 && hq < n1 && a.sm_max) {
       a.sm_max[(int64_t)r * n1 + hq] = m_true;
@@ -672,16 +773,13 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
     for (int i = 0; i < 16; ++i) {
       const int h = mt * 32 + m32_row(i, lane);
       if (h >= n1) continue;
-      if (splits == 1) {
-        const float inv = 1.f / s_l[h];
-        uint16_t* orow = out + ((int64_t)r * n1 + h) * D + wave * C::DW + (lane & 31);
+      // unsplit: the output row; split: this split's normalised partial
+      const float inv = s_l[h];
+      uint16_t* orow = (splits == 1 ? out + ((int64_t)r * n1 + h) * D
+                                    : ws.part_o + (((int64_t)r * splits + sp) * n1 + h) * D) +
+                       wave * C::DW + (lane & 31);
 #pragma unroll
-        for (int nt = 0; nt < C::NT; ++nt) orow[nt * 32] = from_f32<IO>(o[mt][nt][i] * inv);
-      } else {
-        float* prow = ws.part_o + (((int64_t)r * splits + sp) * n1 + h) * D + wave * C::DW + (lane & 31);
-#pragma unroll
-        for (int nt = 0; nt < C::NT; ++nt) prow[nt * 32] = o[mt][nt][i];
-      }
+      for (int nt = 0; nt < C::NT; ++nt) orow[nt * 32] = from_f32<IO>(o[mt][nt][i] * inv);
     }
   }
 }
@@ -733,7 +831,13 @@ hipError_t launch_sfa_fwd(const SfaArgs& a, hipStream_t s) {
   const int cap = a.topk * a.sbs;
   const int splits = sfa_splits(a.total_rows, cap, a.kv_splits);
   dsa::Ws ws = dsa::ws_layout(a.ws, a.total_rows, cap, a.n1, a.d, splits, nullptr);
-  hipLaunchKernelGGL(dsa::sfa_tokens_kernel, dim3(a.total_rows), dim3(dsa::TOK_TPB), 0, s, a, cap, ws);
+  // one wave per row pays off once there are enough rows to fill the GPU; a few
+  // rows (decode) are spread over a whole work-group each
+  if (a.sbs == 1 && a.total_rows >= 1024)
+    hipLaunchKernelGGL(dsa::sfa_tokens1_kernel, dim3((a.total_rows + dsa::TOK1_ROWS - 1) / dsa::TOK1_ROWS),
+                       dim3(64 * dsa::TOK1_ROWS), 0, s, a, cap, ws);
+  else
+    hipLaunchKernelGGL(dsa::sfa_tokens_kernel, dim3(a.total_rows), dim3(dsa::TOK_TPB), 0, s, a, cap, ws);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   return a.io == dsa::IO_BF16 ? dsa::launch_attn<dsa::IO_BF16>(a, s, cap, splits, ws)
