@@ -10,10 +10,10 @@
 //   1. Thread t owns the contiguous index range [32t, 32t+32) of the row; the
 //      16-bit scores are mapped to order-preserving keys u (ord16) and kept in
 //      VGPRs (rows longer than 8192 entries are streamed from memory instead).
-//   2. L > k: the k-th largest key T is found by a 16-step binary search over
-//      the key bits, each step a block-wide count of u >= candidate (wave
-//      reductions + one LDS exchange; no atomics, so no contention on the few
-//      crowded high-score bins).
+//   2. L > k: the k-th largest key T is found with two 256-bin LDS histograms:
+//      one over the high byte of the keys picks the bin holding the k-th largest
+//      (a scan from the top bin), one over the low byte of the keys in that bin
+//      picks T; the same scans give the number of keys above T.
 //   3. Order-preserving compaction: entries with u > T and the first
 //      k - count(u > T) entries with u == T (in index order) are written, in
 //      index order, as keys (u << 16 | index) into LDS; per-thread positions come
@@ -31,6 +31,9 @@ namespace {
 constexpr int TPB = 256;
 constexpr int RPT = 32;                 // row entries per thread held in VGPRs
 constexpr int ROW_CACHED = TPB * RPT;   // 8192
+// Histogram bins are split into HSUB counters picked by lane % HSUB: scores cluster
+// in few high-byte bins, and same-address LDS atomics of one instruction serialise.
+constexpr int HSUB = 8;
 
 __device__ __forceinline__ int visible_len(int s1, int aq, int ak, int S2, int mode) {
   int L;
@@ -155,6 +158,8 @@ __global__ __launch_bounds__(TPB) void li_topk_kernel(LiTopkArgs a) {
   __shared__ __attribute__((aligned(16))) uint32_t sbuf[E * TPB];
   __shared__ uint16_t cnt[16 * TPB];
   __shared__ uint32_t red[TPB / 64];
+  __shared__ uint32_t hist[256 * HSUB];
+  __shared__ uint32_t pick[2];
 
   const int sr = blockIdx.x;
   const int r = sr / a.n2;
@@ -184,26 +189,41 @@ __global__ __launch_bounds__(TPB) void li_topk_kernel(LiTopkArgs a) {
   uint32_t T = 0;  // keys > T are all taken; keys == T up to `need`
   uint32_t need = 0xFFFFFFFFu;
   if (L > k) {
-#pragma unroll 1
-    for (int bit = 15; bit >= 0; --bit) {
-      const uint32_t cand = T | (1u << bit);
-      uint32_t c = 0;
+    // 256-bin histogram over (u >> shift) of the keys whose high byte is `match`
+    // (every key for the first pass), then a scan from the top bin: the bin that
+    // holds the `want`-th largest and the count of keys in higher bins
+    auto select_byte = [&](int shift, int match, uint32_t want, uint32_t& above) -> int {
+#pragma unroll
+      for (int i = 0; i < HSUB; ++i) hist[i * TPB + t] = 0;
+      __syncthreads();
+      const int sub = t & (HSUB - 1);
 #pragma unroll 1
       for (int ch = 0; ch < nchunks; ++ch) {
         if (nchunks > 1) load_keys(row, L, ch * ROW_CACHED, u);
 #pragma unroll
-        for (int e = 0; e < RPT; ++e) c += u[e] >= cand ? 1u : 0u;
+        for (int e = 0; e < RPT; ++e)
+          if (u[e] != 0u && (match < 0 || (int)(u[e] >> 8) == match))
+            atomicAdd(&hist[((u[e] >> shift) & 255u) * HSUB + sub], 1u);
       }
-      if (block_sum(c, red) >= (uint32_t)k) T = cand;
-    }
-    uint32_t g = 0;
-#pragma unroll 1
-    for (int ch = 0; ch < nchunks; ++ch) {
-      if (nchunks > 1) load_keys(row, L, ch * ROW_CACHED, u);
+      __syncthreads();
+      uint32_t h = 0;   // thread t: bin 255 - t, so the scan runs from the top
 #pragma unroll
-      for (int e = 0; e < RPT; ++e) g += u[e] > T ? 1u : 0u;
-    }
-    need = (uint32_t)k - block_sum(g, red);
+      for (int i = 0; i < HSUB; ++i) h += hist[(255 - t) * HSUB + i];
+      uint32_t tot;
+      const uint32_t before = block_excl_scan(h, red, &tot);
+      if (before < want && before + h >= want) {
+        pick[0] = 255 - t;
+        pick[1] = before;
+      }
+      __syncthreads();
+      above = pick[1];
+      return (int)pick[0];
+    };
+    uint32_t above_hi, above_lo;
+    const int hb = select_byte(8, -1, (uint32_t)k, above_hi);
+    const int lb = select_byte(0, hb, (uint32_t)k - above_hi, above_lo);
+    T = ((uint32_t)hb << 8) | (uint32_t)lb;
+    need = (uint32_t)k - (above_hi + above_lo);   // keys == T to take, in index order
   }
   // positions: selected-before = greater-before + min(ties-before, need)
   uint32_t run_g = 0, run_e = 0;  // totals of previous chunks
