@@ -208,3 +208,46 @@ def test_c3_prefill_sampled(dev):
     s = [r[1] for r in rows]
     compare(out[:, s], smax[:, :, s], ssum[:, :, s], o[0][:, s], o[1][:, :, s], o[2][:, :, s],
             what="C3 prefill (sampled rows)")
+
+
+def test_pa_many_rows_token_list(dev):
+    """PA_BSND with 1,088 query rows, so the one-wave-per-row token-list kernel runs with a
+    block table: shuffled pages, a missing (-1) page, a -1 in the middle of a row (the scan
+    stops there), -1 tail padding and rows shorter than the count."""
+    B = 1088
+    inp = W.sfa_decode_inputs(B=B, N1=8, len_lo=40, len_hi=400, block_size=32, sparse_count=48,
+                              device="cpu", seed=11)
+    si = inp.sparse_indices.clone()
+    si[5, 0, 0, 7] = -1           # stop mid-row
+    si[1024, 0, 0, 20:] = -1      # tail padding
+    bt = inp.block_table.clone()
+    bt[9, 1] = -1                 # a missing page reads as zeros
+    out, smax, ssum = sparse_flash_attention(inp.query.to(dev), inp.key.to(dev), inp.key.to(dev),
+                                             si.to(dev), scale_value=inp.scale_value, block_table=bt.to(dev),
+                                             actual_seq_lengths_kv=inp.actual_seq_lengths_kv,
+                                             query_rope=inp.query_rope.to(dev), key_rope=inp.key_rope.to(dev),
+                                             layout_kv="PA_BSND", sparse_mode=3, return_softmax_lse=True,
+                                             block_size=32)
+    torch.cuda.synchronize()
+    sel = [0, 5, 9, 1023, 1024, 1087] + list(range(13, B, 97))
+    o = SFA.sparse_flash_attention(_np(inp.query[sel]), _np(inp.key), None, si[sel].numpy(),
+                                   inp.scale_value, bt[sel].numpy(), None,
+                                   [inp.actual_seq_lengths_kv[b] for b in sel], _np(inp.query_rope[sel]),
+                                   _np(inp.key_rope), 1, "BSND", "PA_BSND", 3, True,
+                                   block_size=32, io_dtype="bf16")
+    compare(out[sel], smax[sel], ssum[sel], *o, what="PA 1088 rows (token list per wave)")
+
+
+@pytest.mark.parametrize("kv_splits", [2, 5, 16])
+def test_forced_kv_splits_with_empty_splits(dev, kv_splits):
+    """Forced KV splits on short rows: splits past a row's token list are empty (they store
+    zeros and l = 0); the merge must weight them out. Also rows with no tokens at all."""
+    B, S1, S2, N1, D, count = 1, 6, 96, 16, 512, 96
+    q, k, v, qr, kr = _inputs(B, S1, S2, N1, D, "bf16", seed=21)
+    si = _ref_indices(B, S1, S2, count, 1, 3, seed=5)
+    out, smax, ssum = sparse_flash_attention(q.to(dev), k.to(dev), v.to(dev), torch.from_numpy(si).to(dev),
+                                             scale_value=0.05, query_rope=qr.to(dev), key_rope=kr.to(dev),
+                                             sparse_mode=3, return_softmax_lse=True, kv_splits=kv_splits)
+    o = SFA.sparse_flash_attention(_np(q), _np(k), None, si, 0.05, None, None, None, _np(qr), _np(kr), 1,
+                                   "BSND", "BSND", 3, True, io_dtype="bf16")
+    compare(out, smax, ssum, *o, what=f"kv_splits={kv_splits}")
