@@ -184,3 +184,27 @@ def test_c2_full_size_sampled(dev):
                      "bf16", rows=rows)
     print(f"[li parity C2] {stats}")
     assert stats.flips <= max(4, 0.01 * stats.elements), stats
+
+
+@pytest.mark.parametrize("mode", [0, 3])
+def test_rows_longer_than_register_cache(dev, mode):
+    """S2 = 12,000 > 8,192: the top-k streams a row's keys from memory in two chunks (the
+    histogram passes, the compaction and its cross-chunk offsets)."""
+    run_case(dev, 1, 16, 12000, 8, 1, 64, 512, mode, "bf16", max_rows=10 ** 9)
+
+
+def test_heavy_ties_at_the_threshold(dev):
+    """Keys repeat four distinct rows, so each score row holds only a few distinct values
+    and the k-th largest sits inside a large run of ties (taken in index order)."""
+    B, S1, S2, N1, N2, D, K = 1, 24, 700, 8, 1, 64, 100
+    q, k, w = _inputs(B, S1, S2, N1, N2, D, "bf16", seed=3)
+    k = k[:, :4].repeat(1, S2 // 4 + 1, 1, 1)[:, :S2].contiguous()
+    idx, val = lightning_indexer(q.to(dev), k.to(dev), w.to(dev), sparse_count=K, sparse_mode=0,
+                                 return_value=True)
+    torch.cuda.synchronize()
+    gi, gv = idx.cpu().numpy(), val.float().cpu().numpy()
+    Ls = np.full(B * S1 * N2, S2)
+    check_topk_properties(gi.reshape(-1, K), gv.reshape(-1, K), Ls, K)
+    stats = check_li(gi, gv, _np(q), _np(k), _np(w), np.full(B, S1), np.full(B, S2), K, 0, "bf16")
+    print(f"[li parity] heavy ties: {stats}")
+    assert stats.flips <= max(4, 0.02 * stats.elements), stats
