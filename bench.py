@@ -45,19 +45,23 @@ def timed(fn, steps, warmup, torch):
 
 
 def event_time(fns, reps, torch):
-    """Average device time (ms) of each callable, bracketed by HIP events on the
-    current stream (the stream every kernel here is launched on)."""
-    tot = [0.0] * len(fns)
-    for _ in range(reps):
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(fns) + 1)]
-        ev[0].record()
-        for i, f in enumerate(fns):
-            f()
-            ev[i + 1].record()
+    """Average device time (ms) of each callable: `reps` back-to-back calls between
+    two HIP events on the current stream (the stream every kernel here is launched
+    on). Back-to-back calls keep the GPU fed, so the host's per-call enqueue time
+    (Python + ctypes, ~10-15 us) does not show up as device time."""
+    out = []
+    for f in fns:
+        f()
         torch.cuda.synchronize()
-        for i in range(len(fns)):
-            tot[i] += ev[i].elapsed_time(ev[i + 1])
-    return [t / reps for t in tot]
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            f()
+        e1.record()
+        torch.cuda.synchronize()
+        out.append(e0.elapsed_time(e1) / reps)
+    return out
 
 
 def cpu_baseline_indexer(inp, c, torch, budget_s=20.0):

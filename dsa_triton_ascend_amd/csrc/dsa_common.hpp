@@ -147,6 +147,14 @@ __device__ __forceinline__ float max_half_swap(float x) {
   return fmaxf(a, b);
 }
 
+// v_permlane32_swap: exchanges the upper half of `a` with the lower half of `b`,
+// i.e. afterwards a[l + 32] = old b[l] and b[l] = old a[l + 32] for l < 32 (the
+// other halves keep their values). Inline asm for the same reason as above; the
+// s_nop 1 gives the wait states the swap needs after VALU writes of its operands.
+__device__ __forceinline__ void swap_halves(uint32_t& a, uint32_t& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+
 // s_waitcnt vmcnt(N) (gfx9 encoding; expcnt and lgkmcnt left unconstrained).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {

@@ -31,12 +31,17 @@
 //         (natural-log units), so O is rarely rescaled; the true max is tracked
 //         for softmax_max;
 //       * P (io dtype) goes to LDS as [head][token]; each wave then owns a
-//         D/4-column slice of O[128 heads, D] and accumulates P V on
-//         v_mfma_f32_32x32x16, the V^T operand read with ds_read_b64_tr_b16
-//         straight from the gathered rows (value = key);
-//       * O stays in registers; the epilogue divides by the row sum (with
-//         several KV splits the normalised partial goes out in the io dtype).
-//  3. sfa_merge_kernel -- merges KV-split partials (log-sum-exp weights).
+//         D/4-column slice of O[128 heads, D] and accumulates it transposed,
+//         O^T += V^T P^T, on v_mfma_f32_32x32x16, the V^T operand read with
+//         ds_read_b64_tr_b16 straight from the gathered rows (value = key), so
+//         a lane holds one head and runs of four consecutive columns;
+//       * O stays in registers; the epilogue divides by the row sum and writes
+//         16-byte rows (with several KV splits the normalised partial goes out
+//         in the io dtype).
+//  3. sfa_merge_kernel -- merges KV-split partials (log-sum-exp weights) of the
+//     rows whose tokens span several splits. With KV splits and
+//     sparse_block_size 1 (decode) each split lists its own tokens inside
+//     sfa_attn_kernel, so a decode call is two launches.
 // Unlike the reference (sparse_flash_attention_triton.py:509-525) the fp32
 // accumulator never round-trips through HBM for unsplit rows.
 #include <climits>
@@ -68,11 +73,13 @@ __device__ __forceinline__ RowInfo row_info(const SfaArgs& a, int r) {
 }
 
 // ---------------------------------------------------------------- workspace
+// The zero KV row comes first; it must be zero when the workspace is first used
+// (no launch writes anything else there, the token-list kernels rewrite zeros).
 struct Ws {
-  int32_t* counts;   // [rows]
+  uint16_t* zero;    // one zero KV row: 512 + Dr elements
+  int32_t* counts;   // [rows]   token-list length of the row
   int32_t* tokens;   // [rows, tstride]
   int tstride;       // token-list row stride: cap rounded up to a whole 32-token tile
-  uint16_t* zero;    // one zero KV row: 512 + Dr elements
   uint16_t* part_o;  // [rows, splits, N1, D]   O_s / l_s in the io dtype (splits > 1)
   float* part_s;     // [rows, splits, N1, 3]   m_used, m_true, l
 };
@@ -85,12 +92,12 @@ __host__ __device__ inline Ws ws_layout(void* base, int rows, int cap, int n1, i
   size_t off = 0;
   Ws w;
   w.tstride = (cap + 31) & ~31;
+  w.zero = reinterpret_cast<uint16_t*>(p + off);
+  off += align256((size_t)(512 + DR) * 2);
   w.counts = reinterpret_cast<int32_t*>(p + off);
   off += align256((size_t)rows * 4);
   w.tokens = reinterpret_cast<int32_t*>(p + off);
   off += align256((size_t)rows * w.tstride * 4);
-  w.zero = reinterpret_cast<uint16_t*>(p + off);
-  off += align256((size_t)(512 + DR) * 2);
   w.part_o = reinterpret_cast<uint16_t*>(p + off);
   w.part_s = nullptr;
   if (splits > 1) {
@@ -107,20 +114,43 @@ constexpr int TOK_TPB = 256;
 constexpr int TOK_PER = 8;                       // ids per thread per pass
 constexpr int TOK_CHUNK = TOK_TPB * TOK_PER;     // ids per pass
 
+// Work-group (TOK_TPB threads) reductions through LDS. LDS_ONLY barriers order
+// the LDS traffic alone, so global loads in flight (a prefetch) are not drained.
+template <bool LDS_ONLY = false>
+__device__ __forceinline__ void red_barrier() {
+  if constexpr (LDS_ONLY) lds_barrier(); else __syncthreads();
+}
+
+template <bool LDS_ONLY = false>
 __device__ __forceinline__ int block_min_i(int v, int* red) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o));
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  __syncthreads();
+  red_barrier<LDS_ONLY>();
   if (lane == 0) red[wave] = v;
-  __syncthreads();
+  red_barrier<LDS_ONLY>();
   int m = red[0];
 #pragma unroll
   for (int w = 1; w < TOK_TPB / 64; ++w) m = min(m, red[w]);
-  return m;
+  return __builtin_amdgcn_readfirstlane(m);   // uniform; read from LDS, so not provably so
+}
+
+template <bool LDS_ONLY = false>
+__device__ __forceinline__ int block_sum_i(int v, int* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  red_barrier<LDS_ONLY>();
+  if (lane == 0) red[wave] = v;
+  red_barrier<LDS_ONLY>();
+  int t = 0;
+#pragma unroll
+  for (int w = 0; w < TOK_TPB / 64; ++w) t += red[w];
+  return __builtin_amdgcn_readfirstlane(t);
 }
 
 // exclusive block scan of v; *tot receives the block total
+template <bool LDS_ONLY = false>
 __device__ __forceinline__ int block_excl_scan_i(int v, int* red, int* tot) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int x = v;
@@ -129,16 +159,16 @@ __device__ __forceinline__ int block_excl_scan_i(int v, int* red, int* tot) {
     const int n = __shfl_up(x, o);
     if (lane >= o) x += n;
   }
-  __syncthreads();
+  red_barrier<LDS_ONLY>();
   if (lane == 63) red[wave] = x;
-  __syncthreads();
+  red_barrier<LDS_ONLY>();
   int off = 0, t = 0;
 #pragma unroll
   for (int w = 0; w < TOK_TPB / 64; ++w) {
     off += w < wave ? red[w] : 0;
     t += red[w];
   }
-  *tot = t;
+  *tot = __builtin_amdgcn_readfirstlane(t);
   return off + x - v;
 }
 
@@ -316,73 +346,260 @@ __global__ __launch_bounds__(64 * TOK1_ROWS) void sfa_tokens1_kernel(SfaArgs a, 
   if (lane == 0) ws.counts[r] = base;
 }
 
-// ---------------------------------------------------------------- kernel 3
-// Merge of the KV-split partials. One work-group per (row, 4 heads); thread t
-// owns columns 8(t%64)..+8 of head 4 blockIdx.y + t/64. Each split s left its
-// normalised output O_s / l_s (io dtype; zeros for an empty split) and
-// (m_used_s, m_true_s, l_s); every load is issued before any is used, so the
-// launch streams the partials at memory bandwidth. Per head: M = max m_used_s
-// over the splits with l_s > 0, w_s = l_s 2^((m_used_s - M) log2 e),
-// out = sum_s w_s (O_s / l_s) / sum_s w_s; softmax_max / sum as for an unsplit row.
-constexpr int MERGE_MAX_SPLITS = 16;
+// ---------------------------------------------------------------- split-local token lists
+// Loads a KV split issues at the very start of the attention kernel when it lists
+// its own tokens (sparse_block_size 1): ids [8t, 8t+8) of the row's first 2048
+// (-2 past sparse_count), this thread's share of the batch count (batches
+// b = t, t + 256, ... whose rows end at or before r) and, for b = t, the batch's
+// first row and lengths (broadcast once the batch is known).
+struct TokPrefetch {
+  int v[TOK_PER];
+  int bcnt;
+  int rs0, aq, ak;
+};
 
-template <int IO>
+__device__ __forceinline__ TokPrefetch tok_prefetch(const SfaArgs& a, int r) {
+  TokPrefetch p;
+  const int32_t* ids = a.sidx + (int64_t)r * a.topk;
+  const int g0 = threadIdx.x * TOK_PER;
+  if ((a.topk & 3) == 0 && g0 + TOK_PER <= a.topk) {   // 16-byte aligned, whole
+    const int4 x0 = *reinterpret_cast<const int4*>(ids + g0);
+    const int4 x1 = *reinterpret_cast<const int4*>(ids + g0 + 4);
+    p.v[0] = x0.x; p.v[1] = x0.y; p.v[2] = x0.z; p.v[3] = x0.w;
+    p.v[4] = x1.x; p.v[5] = x1.y; p.v[6] = x1.z; p.v[7] = x1.w;
+  } else {
+#pragma unroll
+    for (int j = 0; j < TOK_PER; ++j) p.v[j] = g0 + j < a.topk ? ids[g0 + j] : -2;
+  }
+  const int b = threadIdx.x;
+  const bool own = b < a.batch;
+  p.rs0 = own ? a.row_start[b] : 0;
+  p.aq = own ? a.act_q[b] : 0;
+  p.ak = own ? a.act_k[b] : 0;
+  p.bcnt = own && a.row_start[b + 1] <= r ? 1 : 0;
+  for (int bb = b + TOK_TPB; bb < a.batch; bb += TOK_TPB) p.bcnt += a.row_start[bb + 1] <= r ? 1 : 0;
+  return p;
+}
+
+// The part of row r's token list that KV split sp (of `splits`) processes, for
+// sparse_block_size 1, built by the split's own work-group (TOK_TPB threads): the
+// golden's gatherKV scan (numpy golden :44-49 -- positions below
+// min(count, threshold), up to the first -1, ids in [0, min(act_k, threshold)))
+// numbers the row's tokens in id order; the split owns numbers
+// [sp*per, min(sp*per + per, n)), per = ceil(ceil(n / splits) / 32) * 32 (the
+// split rule of the attention kernel), and writes their physical rows to the
+// row's token list at those positions. Returns n (0 for a skipped row); the batch
+// is the count of batches ending at or before r (rows past the last batch map to
+// it). A scan longer than one 2048-id pass counts first, then numbers. Barriers
+// are LDS-only: loads issued before the call stay in flight. The split's first
+// four tiles are written to the LDS id ring s_ids, the rest to the row's token
+// list; issue_q() (the kernel's Q loads) is called right after the block-table
+// lookups are issued, once.
+template <typename IssueQ>
+__device__ int split_token_list(const SfaArgs& a, int r, int sp, int splits, const Ws& ws, int* red,
+                                const TokPrefetch& pre, int32_t (*s_ids)[32], IssueQ&& issue_q) {
+  const int tid = threadIdx.x;
+  RowInfo ri;
+  const int nb = block_sum_i<true>(pre.bcnt, red);
+  ri.b = nb < a.batch ? nb : a.batch - 1;
+  if (a.batch <= TOK_TPB) {   // the batch's thread broadcasts what it prefetched
+    if (tid == ri.b) {
+      red[4] = pre.rs0;
+      red[5] = pre.aq;
+      red[6] = pre.ak;
+    }
+    lds_barrier();
+    ri.s1 = r - __builtin_amdgcn_readfirstlane(red[4]);
+    ri.aq = __builtin_amdgcn_readfirstlane(red[5]);
+    ri.ak = __builtin_amdgcn_readfirstlane(red[6]);
+  } else {
+    ri.s1 = r - a.row_start[ri.b];
+    ri.aq = a.act_q[ri.b];
+    ri.ak = a.act_k[ri.b];
+  }
+  ri.active = ri.s1 < ri.aq;
+  if (a.sparse_mode != 0 && ri.s1 < ri.aq - ri.ak) ri.active = false;  // numpy_golden:125-126
+  ri.threshold = a.sparse_mode == 0 ? ri.ak : ri.ak - ri.aq + ri.s1 + 1;
+  if (ri.threshold <= 0) ri.active = false;                             // numpy_golden:131-132
+  bool q_issued = false;
+  if (!ri.active) {
+    issue_q();
+    return 0;
+  }
+  const int nscan0 = a.topk < ri.threshold ? a.topk : ri.threshold;
+  const int end_lim = ri.ak < ri.threshold ? ri.ak : ri.threshold;
+  const int32_t* ids = a.sidx + (int64_t)r * a.topk;
+  int32_t* out = ws.tokens + (int64_t)r * ws.tstride;
+  const bool pow2 = a.block_table && (a.page_bs & (a.page_bs - 1)) == 0;
+  const int pshift = pow2 ? __builtin_ctz((unsigned)a.page_bs) : 0;
+  auto phys_row = [&](int t) -> int32_t {
+    int64_t p;
+    if (a.block_table) {
+      const int bi = pow2 ? t >> pshift : (int)((unsigned)t / (unsigned)a.page_bs);
+      const int within = t - bi * a.page_bs;
+      const int blk = bi < a.max_blocks ? a.block_table[(int64_t)ri.b * a.max_blocks + bi] : -1;
+      p = blk < 0 ? -1 : (int64_t)blk * a.page_bs + within;
+    } else {
+      p = t < a.s2 ? (int64_t)a.key_start[ri.b] + t : -1;
+    }
+    return (p >= 0 && p < a.key_rows) ? (int32_t)p : -1;
+  };
+  // one pass: ids 8t..8t+7 of [c0, c0 + 2048) per thread (pass 0 from the
+  // prefetch), validity, the first -1
+  auto pass = [&](int c0, int (&v)[TOK_PER], bool (&ok)[TOK_PER], int& fneg) {
+    const int g0 = c0 + tid * TOK_PER;
+#pragma unroll
+    for (int j = 0; j < TOK_PER; ++j)
+      v[j] = g0 + j < nscan0 ? (c0 == 0 ? pre.v[j] : ids[g0 + j]) : -2;   // -2: past the scan
+    fneg = INT_MAX;
+#pragma unroll
+    for (int j = TOK_PER - 1; j >= 0; --j) fneg = v[j] == -1 ? g0 + j : fneg;
+    fneg = block_min_i<true>(fneg, red);   // only -1 stops the scan
+#pragma unroll
+    for (int j = 0; j < TOK_PER; ++j) ok[j] = g0 + j < fneg && v[j] >= 0 && v[j] < end_lim;
+  };
+  int v[TOK_PER];
+  bool ok[TOK_PER];
+  int fneg, n = 0;
+  const bool multi = nscan0 > TOK_CHUNK;
+  if (multi)
+    for (int c0 = 0; c0 < nscan0; c0 += TOK_CHUNK) {
+      pass(c0, v, ok, fneg);
+      int my = 0;
+#pragma unroll
+      for (int j = 0; j < TOK_PER; ++j) my += ok[j];
+      n += block_sum_i<true>(my, red);
+      if (fneg != INT_MAX) break;
+    }
+  int base = 0;
+  for (int c0 = 0; c0 < nscan0; c0 += TOK_CHUNK) {
+    pass(c0, v, ok, fneg);
+    int my = 0;
+#pragma unroll
+    for (int j = 0; j < TOK_PER; ++j) my += ok[j];
+    int tot;
+    const int pos = base + block_excl_scan_i<true>(my, red, &tot);
+    if (!multi) n = tot;
+    const int per = ((n + splits - 1) / splits + 31) / 32 * 32;
+    const int t_beg = sp * per;
+    const int t_end = t_beg + per < n ? t_beg + per : n;
+    // this thread's valid ids are numbered pos, pos+1, ... in id order
+    int32_t pr[TOK_PER];
+    bool mine[TOK_PER];
+    int q = pos;
+#pragma unroll
+    for (int j = 0; j < TOK_PER; ++j) {
+      mine[j] = ok[j] && q >= t_beg && q < t_end;
+      pr[j] = mine[j] ? phys_row(v[j]) : 0;   // every lookup issued before the stores
+      q += ok[j] ? 1 : 0;
+    }
+    if (!q_issued) {   // Q after the lookups, so waiting for these does not wait for Q
+      issue_q();
+      q_issued = true;
+    }
+    // the split's first 4 tiles go straight to the id ring (slot t: tile t; slots
+    // past the split's last tile repeat it, as the ring copies do); later tiles to
+    // the row's token list
+    const int ntl = (t_end - t_beg + 31) / 32;
+    q = pos;
+#pragma unroll
+    for (int j = 0; j < TOK_PER; ++j) {
+      if (mine[j]) {
+        const int pl = q - t_beg;
+        if (pl < 4 * 32) {
+          s_ids[pl >> 5][pl & 31] = pr[j];
+          if ((pl >> 5) == ntl - 1)
+            for (int t = ntl; t < 4; ++t) s_ids[t][pl & 31] = pr[j];
+        } else {
+          out[q] = pr[j];
+        }
+      }
+      q += ok[j] ? 1 : 0;
+    }
+    base += tot;
+    if (fneg != INT_MAX || base >= t_end) break;
+  }
+  if (!q_issued) issue_q();
+  return n;
+}
+
+// ---------------------------------------------------------------- kernel 3
+// Merge of the KV-split partials of the rows whose tokens span several splits
+// (the attention kernel writes single-split and skipped rows itself). Work-group
+// (row, blockIdx.y) covers units u = (head u / (D/8), columns 8 (u % (D/8)) ..+8),
+// 16 / MS per thread for at most MS splits, every partial load issued before any
+// is used. Split s left O_s / l_s (io dtype) and (m_used_s, m_true_s, l_s); per
+// head M = max m_used_s, w_s = l_s 2^((m_used_s - M) log2 e),
+// out = sum_s w_s (O_s / l_s) / sum_s w_s; softmax_max / sum as for an unsplit row.
+template <int IO, int D, int MS>
 __global__ __launch_bounds__(256) void sfa_merge_kernel(SfaArgs a, int splits, Ws ws) {
+  constexpr int MERGE_MAX_SPLITS = MS, MU = 16 / MS;
   const int r = blockIdx.x;
-  const int n1 = a.n1, D = a.d;
-  const int h = blockIdx.y * 4 + (threadIdx.x >> 6);
-  const int c = (threadIdx.x & 63) * 8;
-  if (h >= n1) return;
-  uint4 v[MERGE_MAX_SPLITS];
-  if (c < D) {
+  const int n1 = a.n1;
+  const int ntok_all = ws.counts[r];
+  const int per = ((ntok_all + splits - 1) / splits + 31) / 32 * 32;
+  const int nact = ntok_all > 0 ? (ntok_all + per - 1) / per : 0;
+  if (nact <= 1) return;
+  constexpr int CH = D / 8;
+  const int units = n1 * CH;
+  const float* ps = ws.part_s + (int64_t)r * splits * n1 * 3;
+  const uint16_t* po = ws.part_o + (int64_t)r * splits * n1 * D;
+  uint16_t* out = reinterpret_cast<uint16_t*>(a.out) + (int64_t)r * n1 * D;
+  const int u0 = blockIdx.y * 256 * MU + threadIdx.x;
+  uint4 v[MU][MERGE_MAX_SPLITS];
+#pragma unroll
+  for (int k = 0; k < MU; ++k) {
+    const int u = u0 + k * 256;
+    const int uc = u < units ? u : units - 1;
 #pragma unroll
     for (int sp = 0; sp < MERGE_MAX_SPLITS; ++sp)
-      if (sp < splits) v[sp] = ldg16(ws.part_o + (((int64_t)r * splits + sp) * n1 + h) * D + c);
+      if (sp < nact) v[k][sp] = ldg16(po + ((int64_t)sp * n1 + uc / CH) * D + (uc % CH) * 8);
   }
-  const float* ps = ws.part_s + (int64_t)r * splits * n1 * 3;
-  float mu[MERGE_MAX_SPLITS], ls[MERGE_MAX_SPLITS];
-  float M = -INFINITY, mt = -INFINITY;
 #pragma unroll
-  for (int sp = 0; sp < MERGE_MAX_SPLITS; ++sp) {
-    mu[sp] = -INFINITY;
-    ls[sp] = 0.f;
-    if (sp < splits) {
-      const float* q = ps + ((int64_t)sp * n1 + h) * 3;
-      mu[sp] = q[0];
-      ls[sp] = q[2];
-      if (ls[sp] > 0.f) {
+  for (int k = 0; k < MU; ++k) {
+    const int u = u0 + k * 256;
+    if (u >= units) continue;
+    const int h = u / CH;
+    float mu[MERGE_MAX_SPLITS], ls[MERGE_MAX_SPLITS];
+    float M = -INFINITY, mt = -INFINITY;
+#pragma unroll
+    for (int sp = 0; sp < MERGE_MAX_SPLITS; ++sp) {
+      mu[sp] = -INFINITY;
+      ls[sp] = 0.f;
+      if (sp < nact) {
+        const float* q = ps + ((int64_t)sp * n1 + h) * 3;
+        mu[sp] = q[0];
+        ls[sp] = q[2];
         M = fmaxf(M, mu[sp]);
         mt = fmaxf(mt, q[1]);
       }
     }
-  }
-  float w[MERGE_MAX_SPLITS];
-  float L = 0.f;
+    float w[MERGE_MAX_SPLITS];
+    float L = 0.f;
 #pragma unroll
-  for (int sp = 0; sp < MERGE_MAX_SPLITS; ++sp) {
-    w[sp] = sp < splits && ls[sp] > 0.f ? ls[sp] * exp2f((mu[sp] - M) * LOG2E) : 0.f;
-    L += w[sp];
-  }
-  if (c < D) {
+    for (int sp = 0; sp < MERGE_MAX_SPLITS; ++sp) {
+      w[sp] = sp < nact ? ls[sp] * exp2f((mu[sp] - M) * LOG2E) : 0.f;
+      L += w[sp];
+    }
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int sp = 0; sp < MERGE_MAX_SPLITS; ++sp)
-      if (sp < splits) {
-        const uint32_t u[4] = {v[sp].x, v[sp].y, v[sp].z, v[sp].w};
+      if (sp < nact) {
+        const uint32_t x[4] = {v[k][sp].x, v[k][sp].y, v[k][sp].z, v[k][sp].w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          acc[2 * j] += w[sp] * to_f32<IO>((uint16_t)(u[j] & 0xFFFFu));
-          acc[2 * j + 1] += w[sp] * to_f32<IO>((uint16_t)(u[j] >> 16));
+          acc[2 * j] += w[sp] * to_f32<IO>((uint16_t)(x[j] & 0xFFFFu));
+          acc[2 * j + 1] += w[sp] * to_f32<IO>((uint16_t)(x[j] >> 16));
         }
       }
-    const float il = L > 0.f ? 1.f / L : 0.f;
-    uint16_t* orow = reinterpret_cast<uint16_t*>(a.out) + ((int64_t)r * n1 + h) * D + c;
-    *reinterpret_cast<uint4*>(orow) = make_uint4(pack2<IO>(acc[0] * il, acc[1] * il), pack2<IO>(acc[2] * il, acc[3] * il),
-                                                 pack2<IO>(acc[4] * il, acc[5] * il), pack2<IO>(acc[6] * il, acc[7] * il));
-  }
-  if (c == 0 && a.sm_max) {
-    a.sm_max[(int64_t)r * n1 + h] = L > 0.f ? mt : 0.f;
-    a.sm_sum[(int64_t)r * n1 + h] = L > 0.f ? L * exp2f((M - mt) * LOG2E) : 0.f;
+    const float il = 1.f / L;   // L >= l of the split holding the max > 0
+    stg16(out + (int64_t)h * D + (u % CH) * 8,
+          make_uint4(pack2<IO>(acc[0] * il, acc[1] * il), pack2<IO>(acc[2] * il, acc[3] * il),
+                     pack2<IO>(acc[4] * il, acc[5] * il), pack2<IO>(acc[6] * il, acc[7] * il)));
+    if (u % CH == 0 && a.sm_max) {
+      a.sm_max[(int64_t)r * n1 + h] = mt;
+      a.sm_sum[(int64_t)r * n1 + h] = L * exp2f((M - mt) * LOG2E);
+    }
   }
 }
 
@@ -474,7 +691,7 @@ __device__ __forceinline__ float agpr_scale(float o, float f) {
 }
 
 template <int IO, int D>
-__global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, int splits, Ws ws) {
+__global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, int splits, int fuse_tok, Ws ws) {
   using C = Cfg<D>;
   __shared__ __attribute__((aligned(16))) uint8_t nope_buf[NBUF][C::NOPE];
   __shared__ __attribute__((aligned(16))) uint8_t rope_buf[NBUF][C::ROPE];
@@ -487,7 +704,41 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = blockIdx.x;
   const int sp = blockIdx.y;
-  const int ntok_all = ws.counts[r];
+  const int n1 = a.n1;
+  // a scalar load (token-list kernel ran), waited for at its first use below
+  const int ntok_pre = fuse_tok ? 0 : ws.counts[r];
+  TokPrefetch pre{};
+  if (fuse_tok) pre = tok_prefetch(a, r);   // requested first: the token list waits on them
+  // ---- Q: Q^T (B operand of S^T, nope part) for this wave's 32 heads goes to
+  // VGPRs; the Q rope of all heads is held in VGPRs (4 chunks per thread) until it
+  // is written to LDS. Head indices are clamped so every wave issues the same
+  // loads (padded heads are zeroed afterwards). Nothing here depends on the token
+  // list: these loads are in flight while the row's token count and ids are
+  // fetched (or, when the split lists its own tokens, from its block-table lookups on).
+  const int hq = wave * 32 + (lane & 31);
+  uint4 qf[C::KSN];
+  uint4 qrv[HB * (DR / 8) / (NWV * 64)];
+  auto issue_q = [&]() __attribute__((always_inline)) {
+    const uint16_t* qn = reinterpret_cast<const uint16_t*>(a.q) + ((int64_t)r * n1 + min(hq, n1 - 1)) * D;
+#pragma unroll
+    for (int ks = 0; ks < C::KSN; ++ks) qf[ks] = ldg16(qn + ks * 16 + (lane >> 5) * 8);
+#pragma unroll
+    for (int j = 0; j < HB * (DR / 8) / (NWV * 64); ++j) {
+      const int h = (threadIdx.x >> 3) + j * (NWV * 64 / 8), e = (threadIdx.x & 7) * 8;
+      qrv[j] = ldg16(reinterpret_cast<const uint16_t*>(a.qr) + ((int64_t)r * n1 + min(h, n1 - 1)) * DR + e);
+    }
+    // keeps the loads here: without it they are sunk past the branches that
+    // follow and issue only once the token count has arrived
+    asm volatile("" ::: "memory");
+  };
+  int ntok_all = ntok_pre;
+  if (fuse_tok) {   // KV-split rows with sparse_block_size 1: this split lists its own tokens
+    ntok_all = split_token_list(a, r, sp, splits, ws, reinterpret_cast<int*>(&s_alpha[0][0]), pre, s_ids,
+                                issue_q);
+    if (sp == 0 && threadIdx.x == 0) ws.counts[r] = ntok_all;   // for the merge kernel
+  } else {
+    issue_q();
+  }
   // this split's token range, in whole tiles
   const int per = ((ntok_all + splits - 1) / splits + BN - 1) / BN * BN;
   const int t_beg = sp * per;
@@ -495,28 +746,26 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   const int ntok = t_end > t_beg ? t_end - t_beg : 0;
   const int32_t* toks = ws.tokens + (int64_t)r * ws.tstride + t_beg;
   uint16_t* out = reinterpret_cast<uint16_t*>(a.out);
-  const int n1 = a.n1;
 
   if (ntok == 0) {
-    if (splits == 1) {  // skipped row: zeros (out, stats)
-      for (int i = threadIdx.x; i < n1 * D; i += NWV * 64) out[(int64_t)r * n1 * D + i] = 0;
-      if (a.sm_max)
-        for (int h = threadIdx.x; h < n1; h += NWV * 64) {
-          a.sm_max[(int64_t)r * n1 + h] = 0.f;
-          a.sm_sum[(int64_t)r * n1 + h] = 0.f;
-        }
-    } else {   // empty split: l = 0 and a zero partial (the merge reads every split)
-      float* ps = ws.part_s + ((int64_t)r * splits + sp) * n1 * 3;
-      for (int h = threadIdx.x; h < n1; h += NWV * 64) {
-        ps[h * 3 + 0] = -INFINITY;
-        ps[h * 3 + 1] = -INFINITY;
-        ps[h * 3 + 2] = 0.f;
+    wait_vmcnt<0>();   // the Q loads above are not used on this path
+    if (ntok_all == 0) {   // skipped row (every split sees it): zeros (out, stats), from split 0
+      if (sp == 0) {
+        for (int i = threadIdx.x; i < n1 * D / 8; i += NWV * 64)
+          stg16(out + (int64_t)r * n1 * D + i * 8, make_uint4(0, 0, 0, 0));
+        if (a.sm_max)
+          for (int h = threadIdx.x; h < n1; h += NWV * 64) {
+            a.sm_max[(int64_t)r * n1 + h] = 0.f;
+            a.sm_sum[(int64_t)r * n1 + h] = 0.f;
+          }
       }
-      uint4* po = reinterpret_cast<uint4*>(ws.part_o + ((int64_t)r * splits + sp) * n1 * D);
-      for (int i = threadIdx.x; i < n1 * D / 8; i += NWV * 64) po[i] = make_uint4(0, 0, 0, 0);
-    }
+    }   // else: a split past the row's tokens; the merge leaves it out
     return;
   }
+  // KV splits holding tokens (the others returned above); with one, it writes the
+  // row itself
+  const int nact = (ntok_all + per - 1) / per;
+  const bool direct = nact == 1;
 
   const uint16_t* kb = reinterpret_cast<const uint16_t*>(a.k);
   const uint16_t* krb = reinterpret_cast<const uint16_t*>(a.kr);
@@ -548,24 +797,22 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
     ix.rope = v;
     return ix;
   };
-  // ---- Q^T (B operand of S^T) for this wave's 32 heads and the Q rope of all
-  // heads, then the ids of tiles 0..3 (their latencies overlap), then the first
-  // two gathers
-  const int hq = wave * 32 + (lane & 31);
-  const uint16_t* qn = reinterpret_cast<const uint16_t*>(a.q) + ((int64_t)r * n1 + hq) * D;
-  uint4 qf[C::KSN];   // nope part in VGPRs; the rope part goes to LDS (qrs)
+  // ---- the ids of tiles 0..3 (copied from the token list, or already written to
+  // the ring by this split's own listing); once they and Q have landed, the Q
+  // rope to LDS and the first two gathers
+  if (!fuse_tok) {
 #pragma unroll
-  for (int ks = 0; ks < C::KSN; ++ks)
-    qf[ks] = hq < n1 ? ldg16(qn + ks * 16 + (lane >> 5) * 8) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-  for (int t = 0; t < 4; ++t) ids_dma(t);
-  for (int c = threadIdx.x; c < HB * (DR / 8); c += NWV * 64) {
-    const int h = c / (DR / 8), e = (c % (DR / 8)) * 8;
-    *reinterpret_cast<uint4*>(qrs + h * QRP + e) =
-        h < n1 ? ldg16(reinterpret_cast<const uint16_t*>(a.qr) + ((int64_t)r * n1 + h) * DR + e)
-               : make_uint4(0, 0, 0, 0);
+    for (int t = 0; t < 4; ++t) ids_dma(t);
   }
   wait_vmcnt<0>();
+  if (hq >= n1)
+#pragma unroll
+    for (int ks = 0; ks < C::KSN; ++ks) qf[ks] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+  for (int j = 0; j < HB * (DR / 8) / (NWV * 64); ++j) {
+    const int h = (threadIdx.x >> 3) + j * (NWV * 64 / 8), e = (threadIdx.x & 7) * 8;
+    *reinterpret_cast<uint4*>(qrs + h * QRP + e) = h < n1 ? qrv[j] : make_uint4(0, 0, 0, 0);
+  }
   lds_barrier();
   gather_tile<D>(kb, krb, ws.zero, tile_idx(0), nope_buf[0], rope_buf[0], wave_u, lane);
   gather_tile<D>(kb, krb, ws.zero, tile_idx(1), nope_buf[1], rope_buf[1], wave_u, lane);
@@ -668,7 +915,7 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
     s_alpha[u & 1][hq] = alpha;   // both lane halves hold the same head and value
   };
 
-  // ---- O[128 heads, this wave's D/4 columns] += P V for tile u. Every operand (P
+  // ---- O^T[this wave's D/4 columns, 128 heads] += V^T P^T for tile u. Every operand (P
   // fragments of pt[u & 1] and transposed V reads for both 16-token steps) is
   // requested first; `between()` runs after the requests and before the MFMAs.
   auto pv_tile = [&](int u, auto&& between) __attribute__((always_inline)) {
@@ -695,7 +942,7 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
 #pragma unroll
       for (int nt = 0; nt < C::NT; ++nt)
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) o[mt][nt] = Mfma<IO>::m32(pa[kq][mt], vb[kq][nt], o[mt][nt]);
+        for (int mt = 0; mt < 4; ++mt) o[mt][nt] = Mfma<IO>::m32(vb[kq][nt], pa[kq][mt], o[mt][nt]);
   };
 
   // ---- software pipeline over tiles. Iteration t: (barrier) rescale O for tile t,
@@ -704,8 +951,8 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   // the MFMAs, so the VALU softmax runs while the matrix core works. Buffers:
   // tile t (PV) and t+1 (S^T) are read, t+2 is loaded into the third; P and the
   // rescale factors are double-buffered by tile parity.
-  wait_vmcnt<0>();
-  lds_barrier();   // tile 0 (and Q rope) visible
+  wait_vmcnt<C::GPW - 1>();   // this wave's part of tile 0 landed; tile 1 may be in flight
+  lds_barrier();   // tile 0 visible
   {
     f32x16 s0 = s_tile(0, [&](int) {});
     scale_tile(0, s0);
@@ -714,18 +961,24 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   // barrier at the top of iteration t, then rescale O by alpha(t) when any head's
   // factor differs from 1 (rare: lazy rescaling)
   auto tile_top = [&](int t) __attribute__((always_inline)) {
-    wait_vmcnt<1>();   // this wave's gathers of tile t+1 landed (the ids copy after them may be in flight)
+    // this wave's gathers of tile t+1 landed (the ids copy after them may be in
+    // flight; at t = 0 nothing follows tile 1's gathers)
+    if (t == 0)
+      wait_vmcnt<0>();
+    else
+      wait_vmcnt<1>();
     lds_barrier();     // P and alpha of tile t visible; tile t+1 resident; PV of tile t-1 done everywhere
     const float a0 = s_alpha[t & 1][lane], a1 = s_alpha[t & 1][lane + 64];
     if (__builtin_amdgcn_ballot_w64(a0 != 1.f || a1 != 1.f)) {
+      // O^T layout: every element a lane holds in M tile mt belongs to head mt*32 + lane%32
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+      for (int mt = 0; mt < 4; ++mt) {
+        const float al = s_alpha[t & 1][mt * 32 + (lane & 31)];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float al = s_alpha[t & 1][mt * 32 + m32_row(i, lane)];
+        for (int nt = 0; nt < C::NT; ++nt)
 #pragma unroll
-          for (int nt = 0; nt < C::NT; ++nt) o[mt][nt][i] = agpr_scale(o[mt][nt][i], al);
-        }
+          for (int i = 0; i < 16; ++i) o[mt][nt][i] = agpr_scale(o[mt][nt][i], al);
+      }
     }
   };
   // The last tile is peeled off the loop so the PV code is never duplicated
@@ -755,7 +1008,7 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   const float l_tot = l_part + __shfl_xor(l_part, 32);
   __syncthreads();  // all PV reads of s_alpha / pt done before s_l is written
   if (lane < 32) s_l[hq] = 1.f / l_tot;   // l > 0: a row or split holds at least one token
-  if (splits == 1) {
+  if (direct) {
     if (lane < 32 && hq < n1 && a.sm_max) {
       a.sm_max[(int64_t)r * n1 + hq] = m_true;
       a.sm_sum[(int64_t)r * n1 + hq] = l_tot * exp2f((m_used - m_true) * LOG2E);
@@ -767,39 +1020,62 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
     ps[2] = l_tot;
   }
   __syncthreads();
+  // O^T layout: in accumulator (mt, nt) lane l holds head h = mt*32 + l%32 and, at
+  // index 4g + j, column wave*DW + nt*32 + 8g + 4(l/32) + j (g, j < 4). After scaling
+  // and packing, two lane-half swaps leave lanes l < 32 with columns [0,8) and
+  // [16,24) of the 32-column group and lanes l >= 32 with [8,16) and [24,32): two
+  // 16-byte stores per accumulator instead of sixteen 2-byte ones.
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
+    const int h = mt * 32 + (lane & 31);
+    const float inv = s_l[h];
+    // one split: the output row; several: this split's normalised partial
+    uint16_t* orow = (direct ? out + ((int64_t)r * n1 + min(h, n1 - 1)) * D
+                             : ws.part_o + (((int64_t)r * splits + sp) * n1 + min(h, n1 - 1)) * D) +
+                     wave * C::DW + (lane >> 5) * 8;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int h = mt * 32 + m32_row(i, lane);
-      if (h >= n1) continue;
-      // unsplit: the output row; split: this split's normalised partial
-      const float inv = s_l[h];
-      uint16_t* orow = (splits == 1 ? out + ((int64_t)r * n1 + h) * D
-                                    : ws.part_o + (((int64_t)r * splits + sp) * n1 + h) * D) +
-                       wave * C::DW + (lane & 31);
+    for (int nt = 0; nt < C::NT; ++nt) {
+      uint32_t d[4][2];
 #pragma unroll
-      for (int nt = 0; nt < C::NT; ++nt) orow[nt * 32] = from_f32<IO>(o[mt][nt][i] * inv);
+      for (int g = 0; g < 4; ++g) {
+        d[g][0] = pack2<IO>(o[mt][nt][4 * g] * inv, o[mt][nt][4 * g + 1] * inv);
+        d[g][1] = pack2<IO>(o[mt][nt][4 * g + 2] * inv, o[mt][nt][4 * g + 3] * inv);
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        swap_halves(d[0][j], d[1][j]);
+        swap_halves(d[2][j], d[3][j]);
+      }
+      if (h < n1) {
+        stg16(orow + nt * 32, make_uint4(d[0][0], d[0][1], d[1][0], d[1][1]));
+        stg16(orow + nt * 32 + 16, make_uint4(d[2][0], d[2][1], d[3][0], d[3][1]));
+      }
     }
   }
 }
 
 template <int IO, int D>
-hipError_t launch_attn_d(const SfaArgs& a, hipStream_t s, int cap, int splits, Ws ws) {
+hipError_t launch_attn_d(const SfaArgs& a, hipStream_t s, int cap, int splits, int fuse_tok, Ws ws) {
   hipLaunchKernelGGL((sfa_attn_kernel<IO, D>), dim3(a.total_rows, splits), dim3(NWV * 64), 0, s, a,
-                     cap, splits, ws);
+                     cap, splits, fuse_tok, ws);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;
-  hipLaunchKernelGGL((sfa_merge_kernel<IO>), dim3(a.total_rows, (a.n1 + 3) / 4), dim3(256), 0, s, a, splits, ws);
+  const int units = a.n1 * (D / 8);
+  if (splits <= 4)
+    hipLaunchKernelGGL((sfa_merge_kernel<IO, D, 4>), dim3(a.total_rows, (units + 1023) / 1024), dim3(256), 0,
+                       s, a, splits, ws);
+  else
+    hipLaunchKernelGGL((sfa_merge_kernel<IO, D, 16>), dim3(a.total_rows, (units + 255) / 256), dim3(256), 0,
+                       s, a, splits, ws);
   return hipGetLastError();
 }
 
 template <int IO>
-hipError_t launch_attn(const SfaArgs& a, hipStream_t s, int cap, int splits, Ws ws) {
+hipError_t launch_attn(const SfaArgs& a, hipStream_t s, int cap, int splits, int fuse_tok, Ws ws) {
   switch (a.d) {
-    case 128: return launch_attn_d<IO, 128>(a, s, cap, splits, ws);
-    case 256: return launch_attn_d<IO, 256>(a, s, cap, splits, ws);
-    case 512: return launch_attn_d<IO, 512>(a, s, cap, splits, ws);
+    case 128: return launch_attn_d<IO, 128>(a, s, cap, splits, fuse_tok, ws);
+    case 256: return launch_attn_d<IO, 256>(a, s, cap, splits, fuse_tok, ws);
+    case 512: return launch_attn_d<IO, 512>(a, s, cap, splits, fuse_tok, ws);
   }
   return hipErrorInvalidValue;
 }
@@ -831,15 +1107,20 @@ hipError_t launch_sfa_fwd(const SfaArgs& a, hipStream_t s) {
   const int cap = a.topk * a.sbs;
   const int splits = sfa_splits(a.total_rows, cap, a.kv_splits);
   dsa::Ws ws = dsa::ws_layout(a.ws, a.total_rows, cap, a.n1, a.d, splits, nullptr);
-  // one wave per row pays off once there are enough rows to fill the GPU; a few
-  // rows (decode) are spread over a whole work-group each
-  if (a.sbs == 1 && a.total_rows >= 1024)
-    hipLaunchKernelGGL(dsa::sfa_tokens1_kernel, dim3((a.total_rows + dsa::TOK1_ROWS - 1) / dsa::TOK1_ROWS),
-                       dim3(64 * dsa::TOK1_ROWS), 0, s, a, cap, ws);
-  else
-    hipLaunchKernelGGL(dsa::sfa_tokens_kernel, dim3(a.total_rows), dim3(dsa::TOK_TPB), 0, s, a, cap, ws);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  return a.io == dsa::IO_BF16 ? dsa::launch_attn<dsa::IO_BF16>(a, s, cap, splits, ws)
-                              : dsa::launch_attn<dsa::IO_F16>(a, s, cap, splits, ws);
+  // KV-split rows with sparse_block_size 1 (decode): each split lists its own
+  // tokens inside the attention kernel, so no token-list launch precedes it.
+  // Otherwise: one wave per row pays off once there are enough rows to fill the
+  // GPU; a few rows are spread over a whole work-group each.
+  const int fuse_tok = splits > 1 && a.sbs == 1;
+  if (!fuse_tok) {
+    if (a.sbs == 1 && a.total_rows >= 1024)
+      hipLaunchKernelGGL(dsa::sfa_tokens1_kernel, dim3((a.total_rows + dsa::TOK1_ROWS - 1) / dsa::TOK1_ROWS),
+                         dim3(64 * dsa::TOK1_ROWS), 0, s, a, cap, ws);
+    else
+      hipLaunchKernelGGL(dsa::sfa_tokens_kernel, dim3(a.total_rows), dim3(dsa::TOK_TPB), 0, s, a, cap, ws);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return a.io == dsa::IO_BF16 ? dsa::launch_attn<dsa::IO_BF16>(a, s, cap, splits, fuse_tok, ws)
+                              : dsa::launch_attn<dsa::IO_F16>(a, s, cap, splits, fuse_tok, ws);
 }

@@ -91,8 +91,8 @@ int dsa_li_topk(const uint16_t* scores, int64_t score_ld, int io_dtype,
                 int32_t* indices, uint16_t* values, void* stream);
 
 /*
- * Bytes of device workspace dsa_sfa_fwd needs for this problem
- * (0 when no split-KV partials are used). kv_splits <= 0 selects the library's choice.
+ * Bytes of device workspace dsa_sfa_fwd needs for this problem (token lists and,
+ * for KV-split rows, the split partials). kv_splits <= 0 selects the library's choice.
  */
 size_t dsa_sfa_workspace_bytes(int total_rows, int n1, int d, int sparse_count,
                                int sparse_block_size, int kv_splits);
@@ -122,8 +122,13 @@ size_t dsa_sfa_workspace_bytes(int total_rows, int n1, int d, int sparse_count,
  *     a gathered token outside [0, key_rows) reads as a zero row (never out of bounds).
  *   N1 <= 128, D in {128, 256, 512}, Dr = 64, sparse_block_size a power of 2 <= 128.
  *   sm_max / sm_sum may be NULL (not requested).
- *   workspace: >= dsa_sfa_workspace_bytes(...) bytes (may be NULL when that is 0).
- *   kv_splits: KV splits per row (<= 0: the library's choice, at most 16).
+ *   workspace: >= dsa_sfa_workspace_bytes(...) bytes, zero-filled before its first
+ *     use (e.g. hipMemset once at allocation): it starts with a zero KV row that no
+ *     call overwrites with anything but zeros, so it is zeroed once, not per call.
+ *     Calls that share a workspace must be ordered (same stream or synchronised).
+ *   kv_splits: KV splits per row (<= 0: the library's choice, at most 16). Several
+ *     splits add a merge launch; with sparse_block_size 1 the splits list their own
+ *     tokens (no token-list launch).
  */
 int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key,
                 const void* key_rope, int io_dtype, const int32_t* sparse_indices,
