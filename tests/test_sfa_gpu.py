@@ -251,3 +251,48 @@ def test_forced_kv_splits_with_empty_splits(dev, kv_splits):
     o = SFA.sparse_flash_attention(_np(q), _np(k), None, si, 0.05, None, None, None, _np(qr), _np(kr), 1,
                                    "BSND", "BSND", 3, True, io_dtype="bf16")
     compare(out, smax, ssum, *o, what=f"kv_splits={kv_splits}")
+
+
+@pytest.mark.parametrize("mode", [0, 3])
+def test_split_token_lists_long_scan(dev, mode):
+    """KV-split rows that list their own tokens when the scan spans several 2048-id
+    passes (sparse_count 5000): a -1 in the third pass stops one row, another row's
+    scan ends at its threshold, ids past act_k are skipped; default and forced splits."""
+    B, S1, S2, N1, D, count = 1, 3, 6000, 8, 128, 5000
+    q, k, v, qr, kr = _inputs(B, S1, S2, N1, D, "bf16", seed=31)
+    rng = np.random.RandomState(3)
+    si = np.stack([np.sort(rng.permutation(S2)[:count]) for _ in range(S1)]).astype(np.int32)
+    si = si.reshape(B, S1, 1, count)
+    si[0, 1, 0, 4500] = -1           # scan of row 1 stops inside the third pass
+    act_k = [5800]                   # ids in [5800, 6000) are skipped
+    for kv_splits in (0, 3, 7):
+        out, smax, ssum = sparse_flash_attention(q.to(dev), k.to(dev), v.to(dev), torch.from_numpy(si).to(dev),
+                                                 scale_value=0.06, actual_seq_lengths_kv=act_k,
+                                                 query_rope=qr.to(dev), key_rope=kr.to(dev), sparse_mode=mode,
+                                                 return_softmax_lse=True, kv_splits=kv_splits)
+        o = SFA.sparse_flash_attention(_np(q), _np(k), None, si, 0.06, None, None, act_k, _np(qr), _np(kr),
+                                       1, "BSND", "BSND", mode, True, io_dtype="bf16")
+        compare(out, smax, ssum, *o, what=f"long scan mode {mode} kv_splits={kv_splits}")
+
+
+def test_split_rows_more_than_256_batches(dev):
+    """KV-split decode rows over 300 batches (past the per-thread batch prefetch, so the
+    batch is found by count and its lengths loaded directly), with skipped batches
+    (act_q = 0) and short kv lengths; forced 2 splits."""
+    B, N1, D, count, S2 = 300, 8, 128, 64, 96
+    q, k, v, qr, kr = _inputs(B, 1, S2, N1, D, "bf16", seed=41)
+    rng = np.random.RandomState(4)
+    act_k = rng.randint(1, S2 + 1, size=B).tolist()
+    act_q = [0 if b % 37 == 5 else 1 for b in range(B)]
+    si = np.full((B, 1, 1, count), -1, dtype=np.int32)
+    for b in range(B):
+        n = min(count, act_k[b])
+        si[b, 0, 0, :n] = np.sort(rng.permutation(act_k[b])[:n])
+    out, smax, ssum = sparse_flash_attention(q.to(dev), k.to(dev), v.to(dev), torch.from_numpy(si).to(dev),
+                                             scale_value=0.08, actual_seq_lengths_query=act_q,
+                                             actual_seq_lengths_kv=act_k, query_rope=qr.to(dev),
+                                             key_rope=kr.to(dev), sparse_mode=3, return_softmax_lse=True,
+                                             kv_splits=2)
+    o = SFA.sparse_flash_attention(_np(q), _np(k), None, si, 0.08, None, act_q, act_k, _np(qr), _np(kr), 1,
+                                   "BSND", "BSND", 3, True, io_dtype="bf16")
+    compare(out, smax, ssum, *o, what="300 batches, 2 splits")
