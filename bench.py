@@ -44,6 +44,18 @@ def timed(fn, steps, warmup, torch):
     return (time.perf_counter() - t0) / steps
 
 
+def warm(fn, torch, seconds=0.2):
+    """Untimed calls for about `seconds` of GPU work, so the timed region sees the
+    steady-state clocks the card settles at under this load (the first few calls
+    after a pause run ~15% slower)."""
+    fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        fn()
+        torch.cuda.synchronize()
+
+
 def event_time(fns, reps, torch):
     """Average device time (ms) of each callable: `reps` back-to-back calls between
     two HIP events on the current stream (the stream every kernel here is launched
@@ -105,7 +117,8 @@ def bench_indexer_c2(args, torch, W, dsa):
     plan = IndexerPlan(inp.query, inp.key, inp.weights, sparse_count=c["sparse_count"],
                        sparse_mode=3, return_value=True)
     sec = timed(plan.run, args.steps, args.warmup, torch)
-    t_score, t_topk = event_time([plan.score, plan.topk], max(3, args.steps // 2), torch)
+    warm(plan.run, torch)
+    t_score, t_topk = event_time([plan.score, plan.topk], max(10, args.steps), torch)
     S = c["S1"]
     pairs = S * (S + 1) // 2
     flop = 2.0 * pairs * c["N1"] * c["D"]
@@ -115,8 +128,9 @@ def bench_indexer_c2(args, torch, W, dsa):
 def bench_sfa(plan_kwargs, steps, warmup, torch):
     from dsa_triton_ascend_amd.sparse_flash_attention import AttentionPlan
     plan = AttentionPlan(**plan_kwargs)
+    warm(plan.run, torch)
     sec = timed(plan.run, steps, warmup, torch)
-    (ms,) = event_time([plan.run], max(3, steps // 2), torch)
+    (ms,) = event_time([plan.run], steps, torch)
     return sec, ms
 
 
@@ -138,8 +152,7 @@ def bench_pipeline_c5(W, reps, torch):
                        inp["key"], inp["query_rope"], inp["key_rope"], cu,
                        sparse_count=inp["sparse_count"], scale_value=inp["scale_value"])
     rows = int(cu[-1])
-    for _ in range(2):
-        plan.run()
+    warm(plan.run, torch)
     (t_all,) = event_time([plan.run], reps, torch)
     t_score, t_topk, t_sfa = event_time([plan.indexer.score, plan.indexer.topk, plan.attention.run], reps, torch)
     res = {"ms": round(t_all, 4), "rows_per_s": round(rows / (t_all * 1e-3), 1), "rows": rows,
@@ -192,7 +205,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--quick", action="store_true", help="headline only (no breakdown, no CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--pmc-pass", action="store_true",
@@ -245,7 +258,7 @@ def main():
             log("[bench] C3 SFA prefill ...")
             si = W.sfa_prefill_inputs(device="cuda:0", seed=42)
             kw = dict(query=si.query, key=si.key, value=si.key, sparse_indices=si.sparse_indices, **si.kwargs())
-            s3, ms3 = bench_sfa(kw, steps, 1, torch)
+            s3, ms3 = bench_sfa(kw, 10, 1, torch)
             f3 = 6292480 * 128 * (576 + 512) * 2.0
             breakdown["sfa_prefill_c3"] = {"ms": round(ms3, 4), "tflops": round(f3 / ms3 / 1e9, 2),
                                            "frac_mfma": round(f3 / ms3 / 1e9 / PEAK_BF16_TFLOPS, 4),
@@ -255,7 +268,7 @@ def main():
             log("[bench] C4 SFA decode ...")
             sd = W.sfa_decode_inputs(device="cuda:0", seed=42)
             kw = dict(query=sd.query, key=sd.key, value=sd.key, sparse_indices=sd.sparse_indices, **sd.kwargs())
-            s4, ms4 = bench_sfa(kw, max(5, args.steps), 2, torch)
+            s4, ms4 = bench_sfa(kw, 50, 2, torch)
             kv_bytes = 64 * 2048 * 576 * 2
             breakdown["sfa_decode_c4"] = {"ms": round(ms4, 4), "kv_gbs": round(kv_bytes / ms4 / 1e6, 1),
                                           "frac_hbm": round(kv_bytes / ms4 / 1e6 / PEAK_HBM_GBS, 4),
