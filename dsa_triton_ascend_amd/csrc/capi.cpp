@@ -96,6 +96,8 @@ size_t dsa_sfa_workspace_bytes(int total_rows, int n1, int d, int sparse_count,
   return sfa_workspace_bytes(total_rows, n1, d, sparse_count, sparse_block_size, kv_splits);
 }
 
+size_t dsa_sfa_workspace_zero_bytes(void) { return sfa_workspace_zero_bytes(); }
+
 int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key, const void* key_rope,
                 int io_dtype, const int32_t* sparse_indices, int sparse_count,
                 int sparse_block_size, const int32_t* block_table, int max_blocks,

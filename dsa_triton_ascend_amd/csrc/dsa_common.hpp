@@ -204,3 +204,4 @@ hipError_t launch_li_score(const LiScoreArgs& a, hipStream_t s);
 hipError_t launch_li_topk(const LiTopkArgs& a, hipStream_t s);
 hipError_t launch_sfa_fwd(const SfaArgs& a, hipStream_t s);
 size_t sfa_workspace_bytes(int total_rows, int n1, int d, int topk, int sbs, int kv_splits);
+size_t sfa_workspace_zero_bytes();

@@ -392,9 +392,8 @@ __device__ __forceinline__ TokPrefetch tok_prefetch(const SfaArgs& a, int r) {
 // is the count of batches ending at or before r (rows past the last batch map to
 // it). A scan longer than one 2048-id pass counts first, then numbers. Barriers
 // are LDS-only: loads issued before the call stay in flight. The split's first
-// four tiles are written to the LDS id ring s_ids, the rest to the row's token
-// list; issue_q() (the kernel's Q loads) is called right after the block-table
-// lookups are issued, once.
+// four tiles are also written to the LDS id ring s_ids; issue_q() (the kernel's Q
+// loads) is called right after the block-table lookups are issued, once.
 template <typename IssueQ>
 __device__ int split_token_list(const SfaArgs& a, int r, int sp, int splits, const Ws& ws, int* red,
                                 const TokPrefetch& pre, int32_t (*s_ids)[32], IssueQ&& issue_q) {
@@ -497,21 +496,21 @@ __device__ int split_token_list(const SfaArgs& a, int r, int sp, int splits, con
       issue_q();
       q_issued = true;
     }
-    // the split's first 4 tiles go straight to the id ring (slot t: tile t; slots
-    // past the split's last tile repeat it, as the ring copies do); later tiles to
-    // the row's token list
+    // every position goes to the row's token list (the ring copies of the tiles
+    // past the split's end re-read its last tile from there); the split's first 4
+    // tiles also go straight to the id ring (slot t: tile t; slots past the split's
+    // last tile repeat it, as the ring copies do)
     const int ntl = (t_end - t_beg + 31) / 32;
     q = pos;
 #pragma unroll
     for (int j = 0; j < TOK_PER; ++j) {
       if (mine[j]) {
         const int pl = q - t_beg;
+        out[q] = pr[j];
         if (pl < 4 * 32) {
           s_ids[pl >> 5][pl & 31] = pr[j];
           if ((pl >> 5) == ntl - 1)
             for (int t = ntl; t < 4; ++t) s_ids[t][pl & 31] = pr[j];
-        } else {
-          out[q] = pr[j];
         }
       }
       q += ok[j] ? 1 : 0;
@@ -656,28 +655,30 @@ struct TileIdx {
 
 // One of the GPW - 1 gather loads of a tile for wave w: part j < 8 copies the
 // nope row of token 8w + j (one instruction, D/8 lanes), part 8 the rope chunks
-// of the wave's 8 tokens (lane -> token lane%8, chunk lane/8).
+// of the wave's 8 tokens (lane -> token lane%8, chunk lane/8). A physical row
+// outside [0, krows) -- -1 for a missing token -- reads the zero row, so no id
+// can address memory outside the key tensors.
 template <int D>
 __device__ __forceinline__ void gather_part(int j, const uint16_t* kb, const uint16_t* krb,
-                                            const uint16_t* zero, const TileIdx& ix, uint8_t* nope,
-                                            uint8_t* rope, int wave_u, int lane) {
+                                            const uint16_t* zero, int krows, const TileIdx& ix,
+                                            uint8_t* nope, uint8_t* rope, int wave_u, int lane) {
   using C = Cfg<D>;
   if (j < 8) {
     const int phys = ix.nope[j];   // wave-uniform: the row base goes in an SGPR pair
-    const uint16_t* src = phys >= 0 ? kb + (int64_t)phys * D : zero;
+    const uint16_t* src = (uint32_t)phys < (uint32_t)krows ? kb + (int64_t)phys * D : zero;
     if (lane < C::LANES_ROW) lds_dma16_sbase_untracked(src, lane * 16, nope + nope_off<D>(wave_u * 8 + j));
   } else {
-    const uint16_t* src = ix.rope >= 0 ? krb + (int64_t)ix.rope * DR : zero + 512;
+    const uint16_t* src = (uint32_t)ix.rope < (uint32_t)krows ? krb + (int64_t)ix.rope * DR : zero + 512;
     lds_dma16_untracked(src + (lane >> 3) * 8, rope + wave_u * 1024);
   }
 }
 
 template <int D>
 __device__ __forceinline__ void gather_tile(const uint16_t* kb, const uint16_t* krb,
-                                            const uint16_t* zero, const TileIdx& ix, uint8_t* nope,
-                                            uint8_t* rope, int wave_u, int lane) {
+                                            const uint16_t* zero, int krows, const TileIdx& ix,
+                                            uint8_t* nope, uint8_t* rope, int wave_u, int lane) {
 #pragma unroll
-  for (int j = 0; j < 9; ++j) gather_part<D>(j, kb, krb, zero, ix, nope, rope, wave_u, lane);
+  for (int j = 0; j < 9; ++j) gather_part<D>(j, kb, krb, zero, krows, ix, nope, rope, wave_u, lane);
 }
 
 // o *= f on an accumulator element kept in an AGPR (VALU cannot read AGPRs):
@@ -769,6 +770,7 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
 
   const uint16_t* kb = reinterpret_cast<const uint16_t*>(a.k);
   const uint16_t* krb = reinterpret_cast<const uint16_t*>(a.kr);
+  const int krows = a.key_rows < INT_MAX ? (int)a.key_rows : INT_MAX;   // rows the key tensors hold
   const int ntiles = (ntok + BN - 1) / BN;
 
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
@@ -814,8 +816,8 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
     *reinterpret_cast<uint4*>(qrs + h * QRP + e) = h < n1 ? qrv[j] : make_uint4(0, 0, 0, 0);
   }
   lds_barrier();
-  gather_tile<D>(kb, krb, ws.zero, tile_idx(0), nope_buf[0], rope_buf[0], wave_u, lane);
-  gather_tile<D>(kb, krb, ws.zero, tile_idx(1), nope_buf[1], rope_buf[1], wave_u, lane);
+  gather_tile<D>(kb, krb, ws.zero, krows, tile_idx(0), nope_buf[0], rope_buf[0], wave_u, lane);
+  gather_tile<D>(kb, krb, ws.zero, krows, tile_idx(1), nope_buf[1], rope_buf[1], wave_u, lane);
 
   float m_used = -INFINITY, m_true = -INFINITY, l_part = 0.f;
   {
@@ -992,7 +994,7 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
 #pragma unroll
       for (int j = 0; j < C::GPW; ++j)
         if (j * C::KS / C::GPW == ks) {
-          if (j < C::GPW - 1) gather_part<D>(j, kb, krb, ws.zero, ix, gnope, grope, wave_u, lane);
+          if (j < C::GPW - 1) gather_part<D>(j, kb, krb, ws.zero, krows, ix, gnope, grope, wave_u, lane);
           else ids_dma(t + 4);   // slot (t+4)%4 held the ids of tile t, read two iterations ago
         }
     });
@@ -1094,6 +1096,8 @@ static int sfa_splits(int total_rows, int cap, int kv_splits) {
   if (s > 16) s = 16;
   return s < 1 ? 1 : s;
 }
+
+size_t sfa_workspace_zero_bytes() { return dsa::align256((size_t)(512 + dsa::DR) * 2); }   // the zero KV row
 
 size_t sfa_workspace_bytes(int total_rows, int n1, int d, int topk, int sbs, int kv_splits) {
   const int cap = topk * sbs;

@@ -140,9 +140,10 @@ class AttentionPlan:
         self.sparse_mode, self.scale, self.kv_splits = sparse_mode, float(scale_value), int(kv_splits)
         self.ws_bytes = lib.dsa_sfa_workspace_bytes(total_rows, N1, D, count, sparse_block_size,
                                                     int(kv_splits)) if total_rows > 0 else 0
-        # zero-filled once: the workspace starts with a zero KV row that the library keeps
-        # at zero across calls (include/dsa_mi355x.h, dsa_sfa_fwd)
-        self.ws = torch.zeros(max(self.ws_bytes, 1), dtype=torch.uint8, device=dev)
+        # the workspace starts with a zero KV row that the library keeps at zero across
+        # calls; only that prefix needs clearing (include/dsa_mi355x.h, dsa_sfa_fwd)
+        self.ws = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=dev)
+        self.ws[:min(self.ws.numel(), lib.dsa_sfa_workspace_zero_bytes())].zero_()
         self.d_row_start = H.i32(row_start, dev)
         self.d_key_start = H.i32(key_start, dev)
         self.d_aq = H.i32(act_q, dev)

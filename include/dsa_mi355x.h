@@ -98,6 +98,14 @@ size_t dsa_sfa_workspace_bytes(int total_rows, int n1, int d, int sparse_count,
                                int sparse_block_size, int kv_splits);
 
 /*
+ * Bytes at the start of every dsa_sfa_fwd workspace that must be zero when the
+ * workspace is first used (the zero KV row; no call writes anything but zeros
+ * there). The rest of the workspace needs no initialisation. No counterpart in the
+ * reference (its workspace cache is internal, sparse_flash_attention_triton.py:37).
+ */
+size_t dsa_sfa_workspace_zero_bytes(void);
+
+/*
  * Sparse flash attention forward, MLA-absorb (replaces _sfa_core,
  * sparse_flash_attention_triton.py:1160-1289; semantics of
  * sparse_flash_attention_numpy.py:38-160).
@@ -122,9 +130,10 @@ size_t dsa_sfa_workspace_bytes(int total_rows, int n1, int d, int sparse_count,
  *     a gathered token outside [0, key_rows) reads as a zero row (never out of bounds).
  *   N1 <= 128, D in {128, 256, 512}, Dr = 64, sparse_block_size a power of 2 <= 128.
  *   sm_max / sm_sum may be NULL (not requested).
- *   workspace: >= dsa_sfa_workspace_bytes(...) bytes, zero-filled before its first
- *     use (e.g. hipMemset once at allocation): it starts with a zero KV row that no
- *     call overwrites with anything but zeros, so it is zeroed once, not per call.
+ *   workspace: >= dsa_sfa_workspace_bytes(...) bytes whose first
+ *     dsa_sfa_workspace_zero_bytes() bytes are zero before its first use (e.g. one
+ *     hipMemset at allocation): they hold a zero KV row that no call overwrites with
+ *     anything but zeros, so they are cleared once, not per call.
  *     Calls that share a workspace must be ordered (same stream or synchronised).
  *   kv_splits: KV splits per row (<= 0: the library's choice, at most 16). Several
  *     splits add a merge launch; with sparse_block_size 1 the splits list their own

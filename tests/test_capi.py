@@ -67,6 +67,8 @@ def test_invalid_arguments_return_status_without_gpu():
     bad[29] = 17
     assert lib.dsa_sfa_fwd(*bad) == _lib.DSA_ERR_UNSUPPORTED and b"kv_splits" in lib.dsa_last_error()
     assert lib.dsa_sfa_workspace_bytes(4096, 128, 512, 2048, 1, 0) >= 4096 * 2048 * 4
+    zb = lib.dsa_sfa_workspace_zero_bytes()
+    assert zb >= (512 + 64) * 2 and zb % 256 == 0 and zb < lib.dsa_sfa_workspace_bytes(1, 1, 128, 1, 1, 1)
 
 
 def test_python_validation_matches_reference():

@@ -296,3 +296,34 @@ def test_split_rows_more_than_256_batches(dev):
     o = SFA.sparse_flash_attention(_np(q), _np(k), None, si, 0.08, None, act_q, act_k, _np(qr), _np(kr), 1,
                                    "BSND", "BSND", 3, True, io_dtype="bf16")
     compare(out, smax, ssum, *o, what="300 batches, 2 splits")
+
+
+@pytest.mark.parametrize("fill", [0x7F, 0xFF, "random"])
+def test_workspace_contents_past_zero_prefix_are_ignored(dev, fill):
+    """Only the workspace's zero prefix is cleared; the rest may hold anything. Decode
+    rows whose KV splits list their own tokens (short splits: every tile is in the id
+    ring's first four slots) must read only token-list positions written in the same
+    call. Filled with far-out-of-range ids (0x7F7F7F7F), -1 and random bytes, then run
+    twice on the same workspace."""
+    from dsa_triton_ascend_amd.sparse_flash_attention import AttentionPlan
+    from dsa_triton_ascend_amd import _lib
+    B, S1, S2, N1, D, count = 1, 4, 2048, 8, 128, 2048
+    q, k, v, qr, kr = _inputs(B, S1, S2, N1, D, "fp16")
+    si = _ref_indices(B, S1, S2, count, 1, 3)
+    o = SFA.sparse_flash_attention(_np(q), _np(k), None, si, 0.07, None, None, None, _np(qr), _np(kr), 1,
+                                   "BSND", "BSND", 3, True, io_dtype="fp16")
+    for kv_splits in (0, 16):
+        plan = AttentionPlan(q.to(dev), k.to(dev), v.to(dev), torch.from_numpy(si).to(dev), scale_value=0.07,
+                             query_rope=qr.to(dev), key_rope=kr.to(dev), sparse_mode=3,
+                             return_softmax_lse=True, kv_splits=kv_splits)
+        zb = _lib.load().dsa_sfa_workspace_zero_bytes()
+        tail = plan.ws[zb:]
+        if fill == "random":
+            g = torch.Generator(device="cpu").manual_seed(11)
+            tail.copy_(torch.randint(0, 256, (tail.numel(),), dtype=torch.uint8, generator=g))
+        else:
+            tail.fill_(fill)
+        for rep in range(2):
+            out, smax, ssum = plan.run()
+            torch.cuda.synchronize()
+            compare(out, smax, ssum, *o, what=f"workspace fill {fill} kv_splits={kv_splits} call {rep}")
