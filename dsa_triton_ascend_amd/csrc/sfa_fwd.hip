@@ -703,7 +703,9 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   __shared__ float s_l[HB];   // 1 / row sum, per head
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int r = blockIdx.x;
+  // rows in reverse order: under causal masks the last rows of a batch hold the most
+  // tokens, so the long rows start first and short ones fill the end of the grid
+  const int r = a.total_rows - 1 - (int)blockIdx.x;
   const int sp = blockIdx.y;
   const int n1 = a.n1;
   // a scalar load (token-list kernel ran), waited for at its first use below
