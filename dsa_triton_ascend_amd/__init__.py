@@ -4,6 +4,7 @@ Drop-in operators with the reference's Python signatures:
 
 * :func:`lightning_indexer` (lightning_indexer_triton.py:466) — indexer score + stable top-k
 * :func:`sparse_flash_attention` (sparse_flash_attention_triton.py:1295) — MLA-absorb SFA forward
+* :func:`sparse_flash_attention_grad` (sparse_flash_attention_grad_triton.py:498) — its backward
 
 and :class:`PrefillPlan` / :func:`dsa_prefill`, the two chained on one packed
 (TND) batch with the indexer's top-k feeding the attention in place.
@@ -14,6 +15,7 @@ Both run hand-written gfx950 HIP kernels through the C ABI of
 from .lightning_indexer import LightningIndexer, lightning_indexer
 from .pipeline import PrefillPlan, dsa_prefill
 from .sparse_flash_attention import SparseFlashAttention, sparse_flash_attention
+from .sparse_flash_attention_grad import SparseFlashAttentionGrad, sparse_flash_attention_grad
 
 __all__ = ["lightning_indexer", "LightningIndexer", "sparse_flash_attention", "SparseFlashAttention",
-           "PrefillPlan", "dsa_prefill"]
+           "sparse_flash_attention_grad", "SparseFlashAttentionGrad", "PrefillPlan", "dsa_prefill"]

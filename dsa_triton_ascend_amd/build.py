@@ -23,12 +23,12 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
           "-Wno-unused-result", "-I", str(PKG.parent / "include")]
 
-SOURCES = ["li_score.hip", "li_topk.hip", "sfa_fwd.hip", "capi.cpp"]
+SOURCES = ["li_score.hip", "li_topk.hip", "sfa_fwd.hip", "sfa_bwd.hip", "capi.cpp"]
 
 
 # Kernels whose float code never relies on NaN propagation: lets fmaxf lower to a
 # single v_max_f32 without the IEEE-mode canonicalisation of each operand.
-NO_NANS = {"li_score.hip", "sfa_fwd.hip"}
+NO_NANS = {"li_score.hip", "sfa_fwd.hip", "sfa_bwd.hip"}
 
 
 def _compile(src: Path, obj: Path) -> None:

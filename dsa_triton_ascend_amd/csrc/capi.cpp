@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 
@@ -141,6 +142,63 @@ int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key, cons
             act_q, act_k, batch, total_rows, n1, d, dr, s2, key_rows, sparse_mode, scale, out, sm_max,
             sm_sum, workspace, workspace_bytes, kv_splits};
   return hip_status(launch_sfa_fwd(a, (hipStream_t)stream), "dsa_sfa_fwd launch");
+}
+
+size_t dsa_sfa_bwd_workspace_bytes(int total_rows, int n1, int d, int sparse_count,
+                                   int sparse_block_size, int64_t key_rows) {
+  if (total_rows < 0 || sparse_count <= 0 || sparse_block_size <= 0 || key_rows < 0 ||
+      (d != 128 && d != 256 && d != 512))
+    return 0;
+  return sfa_bwd_workspace_bytes(total_rows, n1, sparse_count, sparse_block_size, key_rows, d);
+}
+
+int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, const void* key_rope,
+                int io_dtype, const int32_t* sparse_indices, int sparse_count,
+                int sparse_block_size, const int32_t* row_start, const int32_t* key_start,
+                const int32_t* act_q, const int32_t* act_k, int batch, int total_rows, int n1,
+                int d, int dr, int s2, int64_t key_rows, int sparse_mode, float scale,
+                const void* d_out, const void* out, const float* sm_max, const float* sm_sum,
+                void* d_query, void* d_query_rope, void* d_key, void* d_key_rope, void* d_value,
+                void* workspace, size_t workspace_bytes, void* stream) {
+  if (!query || !query_rope || !key || !key_rope || !sparse_indices || !row_start || !key_start ||
+      !act_q || !act_k || !d_out || !out || !sm_max || !sm_sum || !d_query || !d_query_rope ||
+      !d_key || !d_key_rope || !d_value || !workspace)
+    return fail(DSA_ERR_INVALID, "dsa_sfa_bwd: null pointer argument");
+  if (!is16(io_dtype)) return fail(DSA_ERR_INVALID, "dsa_sfa_bwd: io_dtype must be fp16 or bf16");
+  if (sparse_mode != 0 && sparse_mode != 3)
+    return fail(DSA_ERR_INVALID, "Only sparse_mode 0 (full) / 3 (rightDownCausal) supported");
+  if (sparse_block_size < 1 || (sparse_block_size & (sparse_block_size - 1)) != 0 ||
+      sparse_block_size > 128)
+    return fail(DSA_ERR_INVALID, "sparse_block_size must be a power of 2 in [1,128]");
+  if (d != 128 && d != 256 && d != 512)
+    return fail(DSA_ERR_INVALID, "D must be one of (128, 256, 512), got %d", d);
+  if (dr != 64) return fail(DSA_ERR_INVALID, "rope dim must be 64, got %d", dr);
+  if (n1 < 1 || n1 > 128 || (n1 & (n1 - 1)) != 0)
+    return fail(DSA_ERR_INVALID, "N1 must be one of (1, 2, 4, 8, 16, 32, 64, 128), got %d", n1);
+  if (batch <= 0 || total_rows < 0 || sparse_count <= 0 || key_rows < 0)
+    return fail(DSA_ERR_INVALID, "dsa_sfa_bwd: non-positive shape");
+  if ((int64_t)sparse_count * sparse_block_size > (1 << 20))
+    return fail(DSA_ERR_UNSUPPORTED, "dsa_sfa_bwd: sparse_count*sparse_block_size > 2^20 tokens");
+  if (key_rows > INT32_MAX) return fail(DSA_ERR_UNSUPPORTED, "dsa_sfa_bwd: key_rows > 2^31-1");
+  const size_t need = sfa_bwd_workspace_bytes(total_rows, n1, sparse_count, sparse_block_size, key_rows, d);
+  if (workspace_bytes < need)
+    return fail(DSA_ERR_INVALID, "dsa_sfa_bwd: workspace of %zu bytes required, %zu given", need,
+                workspace_bytes);
+  SfaBwdArgs a{};
+  a.f = SfaArgs{query, query_rope, key, key_rope, io_dtype, sparse_indices, sparse_count,
+                sparse_block_size, nullptr, 0, 0, row_start, key_start, act_q, act_k, batch,
+                total_rows, n1, d, dr, s2, key_rows, sparse_mode, scale, nullptr, nullptr, nullptr,
+                workspace, workspace_bytes, 1};
+  a.d_out = d_out;
+  a.out = out;
+  a.sm_max = sm_max;
+  a.sm_sum = sm_sum;
+  a.dq = d_query;
+  a.dqr = d_query_rope;
+  a.dk = d_key;
+  a.dkr = d_key_rope;
+  a.dv = d_value;
+  return hip_status(launch_sfa_bwd(a, (hipStream_t)stream), "dsa_sfa_bwd launch");
 }
 
 }  // extern "C"

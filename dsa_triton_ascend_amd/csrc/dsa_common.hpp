@@ -155,6 +155,17 @@ __device__ __forceinline__ void swap_halves(uint32_t& a, uint32_t& b) {
   asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
 }
 
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16: 8 bytes per lane, transposed within groups of 16 lanes.
+// With the address pattern of tr_frag below it yields an MFMA operand whose K
+// runs down the rows of a row-major LDS array.
+__device__ __forceinline__ uint2 ds_read_tr(const void* lds_ptr) {
+  s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(const_cast<void*>(lds_ptr)));
+  return __builtin_bit_cast(uint2, v);
+}
+
 // s_waitcnt vmcnt(N) (gfx9 encoding; expcnt and lgkmcnt left unconstrained).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -205,3 +216,23 @@ hipError_t launch_li_topk(const LiTopkArgs& a, hipStream_t s);
 hipError_t launch_sfa_fwd(const SfaArgs& a, hipStream_t s);
 size_t sfa_workspace_bytes(int total_rows, int n1, int d, int topk, int sbs, int kv_splits);
 size_t sfa_workspace_zero_bytes();
+
+// Per-row token lists (physical key rows in the golden's gather order,
+// sparse_flash_attention_numpy.py:38-60) built by the forward's token-list
+// kernels into a workspace of sfa_token_ws_bytes() bytes; shared with the
+// backward pass.
+struct SfaTokenLists {
+  int32_t* counts;   // [rows]
+  int32_t* tokens;   // [rows, tstride]
+  int tstride;
+};
+size_t sfa_token_ws_bytes(int total_rows, int topk, int sbs);
+hipError_t launch_sfa_token_lists(const SfaArgs& a, void* ws, SfaTokenLists* tl, hipStream_t s);
+
+struct SfaBwdArgs {
+  SfaArgs f;   // forward arguments (q, qr, k, kr, indices, lengths, shapes, scale)
+  const void* d_out; const void* out; const float* sm_max; const float* sm_sum;
+  void* dq; void* dqr; void* dk; void* dkr; void* dv;
+};
+size_t sfa_bwd_workspace_bytes(int total_rows, int n1, int topk, int sbs, int64_t key_rows, int d);
+hipError_t launch_sfa_bwd(const SfaBwdArgs& a, hipStream_t s);

@@ -638,14 +638,6 @@ template <int D> __device__ __forceinline__ int nope_off(int t) {
 // which is what one direct-to-LDS instruction writes for 8 tokens.
 __device__ __forceinline__ int rope_off(int t, int c) { return (t >> 3) * 1024 + (c * 8 + (t & 7)) * 16; }
 
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ uint2 ds_read_tr(const void* lds_ptr) {
-  s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) s16x4*)(const_cast<void*>(lds_ptr)));
-  return __builtin_bit_cast(uint2, v);
-}
-
 // Token rows of one tile for this wave (tokens 8w..8w+7): wave-uniform rows for
 // the nope gathers and, per lane, the row of token lane % 8 for the rope gather.
 struct TileIdx {
@@ -1106,6 +1098,27 @@ size_t sfa_workspace_bytes(int total_rows, int n1, int d, int topk, int sbs, int
   size_t total = 0;
   dsa::ws_layout(nullptr, total_rows, cap, n1, d, sfa_splits(total_rows, cap, kv_splits), &total);
   return total;
+}
+
+size_t sfa_token_ws_bytes(int total_rows, int topk, int sbs) {
+  size_t total = 0;
+  dsa::ws_layout(nullptr, total_rows, topk * sbs, 1, 128, 1, &total);
+  return total;
+}
+
+hipError_t launch_sfa_token_lists(const SfaArgs& a, void* ws_base, SfaTokenLists* tl, hipStream_t s) {
+  const int cap = a.topk * a.sbs;
+  dsa::Ws ws = dsa::ws_layout(ws_base, a.total_rows, cap, a.n1, a.d, 1, nullptr);
+  tl->counts = ws.counts;
+  tl->tokens = ws.tokens;
+  tl->tstride = ws.tstride;
+  if (a.total_rows <= 0) return hipSuccess;
+  if (a.sbs == 1 && a.total_rows >= 1024)
+    hipLaunchKernelGGL(dsa::sfa_tokens1_kernel, dim3((a.total_rows + dsa::TOK1_ROWS - 1) / dsa::TOK1_ROWS),
+                       dim3(64 * dsa::TOK1_ROWS), 0, s, a, cap, ws);
+  else
+    hipLaunchKernelGGL(dsa::sfa_tokens_kernel, dim3(a.total_rows), dim3(dsa::TOK_TPB), 0, s, a, cap, ws);
+  return hipGetLastError();
 }
 
 hipError_t launch_sfa_fwd(const SfaArgs& a, hipStream_t s) {

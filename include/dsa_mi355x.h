@@ -149,6 +149,43 @@ int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key,
                 void* out, float* sm_max, float* sm_sum, void* workspace,
                 size_t workspace_bytes, int kv_splits, void* stream);
 
+/*
+ * Workspace bytes for dsa_sfa_bwd: the token lists of total_rows rows plus fp32
+ * accumulators for d_key, d_key_rope and d_value over key_rows key rows. Needs no
+ * initialisation. No counterpart in the reference (it allocates its fp32 buffers per
+ * call, sparse_flash_attention_grad_triton.py:634-642).
+ */
+size_t dsa_sfa_bwd_workspace_bytes(int total_rows, int n1, int d, int sparse_count,
+                                   int sparse_block_size, int64_t key_rows);
+
+/*
+ * Sparse flash attention backward, MLA-absorb (replaces _sfa_grad_core,
+ * sparse_flash_attention_grad_triton.py:441-495; semantics of
+ * sparse_flash_attention_grad_numpy.py:34-143).
+ *
+ * Rows, tokens, shapes and layouts as dsa_sfa_fwd (no block table). With the
+ * forward's out and its softmax stats (sm_max / sm_sum, [total_rows * N1] fp32):
+ *   P[h, t]  = exp(score[h, t] - sm_max) / sm_sum
+ *   dS[h, t] = P * (d_out[r,h,:].k[t,:D] - d_out[r,h,:].out[r,h,:]) * scale
+ *   d_query[r,h,:] = sum_t dS k[t,:D],   d_query_rope[r,h,:] = sum_t dS k_rope[t,:]
+ *   d_key[t,:]  += sum_h dS q[r,h,:],    d_key_rope[t,:] += sum_h dS q_rope[r,h,:]
+ *   d_value[t,:] += sum_h P d_out[r,h,:]   (summed over every row selecting t)
+ * d_query / d_query_rope are [total_rows, N1, D|Dr]; d_key / d_key_rope / d_value are
+ * [key_rows, D|Dr] over the whole key tensors (rows no query selects are zero); all in
+ * the io dtype, accumulated in fp32. The order of the fp32 additions into a key row is
+ * not fixed (the reference's deterministic=False contract).
+ *   workspace: >= dsa_sfa_bwd_workspace_bytes(...) bytes; calls sharing it must be
+ *   ordered on one stream.
+ */
+int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, const void* key_rope,
+                int io_dtype, const int32_t* sparse_indices, int sparse_count,
+                int sparse_block_size, const int32_t* row_start, const int32_t* key_start,
+                const int32_t* act_q, const int32_t* act_k, int batch, int total_rows, int n1,
+                int d, int dr, int s2, int64_t key_rows, int sparse_mode, float scale,
+                const void* d_out, const void* out, const float* sm_max, const float* sm_sum,
+                void* d_query, void* d_query_rope, void* d_key, void* d_key_rope, void* d_value,
+                void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

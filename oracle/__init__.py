@@ -6,6 +6,8 @@ This package restates, in numpy, the reference's host-side ground truth:
   (plus the TND converters of lightning_indexer_triton.py:287-340)
 * ``sparse_flash_attention_ref`` <- sparse_flash_attention_numpy.py:26-160
   (plus the TND / PA_BSND converters of sparse_flash_attention_triton.py:968-1051)
+* ``sparse_flash_attention_grad_ref`` <- sparse_flash_attention_grad_numpy.py:34-143
+  (plus the TND handling of sparse_flash_attention_grad_triton.py:562-674)
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
 ``bench.py`` may import it, and only as the checker / the timed CPU baseline.
@@ -28,4 +30,8 @@ PINNING = {
     "sparse_flash_attention_ref.sfa_golden_bsnd": "float64 torch.softmax attention on tiny shapes; "
                                                   "sm_max == max score, sm_sum >= 1; mode-3 leading rows zero",
     "sparse_flash_attention_ref.sfa_golden (TND/PA)": "equivalence with BSND after explicit de-packing / de-paging",
+    "sparse_flash_attention_grad_ref.sfa_grad_golden_bsnd": "float64 torch autograd of the forward attention "
+                                                            "(value a separate leaf) on tiny shapes, modes 0/3, "
+                                                            "bs 1/2/4, actual lengths, a -1 inside a scan",
+    "sparse_flash_attention_grad_ref.sparse_flash_attention_grad (TND)": "equivalence with per-batch BSND calls",
 }

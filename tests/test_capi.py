@@ -97,6 +97,46 @@ def test_python_validation_matches_reference():
         lightning_indexer(q, q[:, :, :1], torch.zeros(1, 4, 8))
 
 
+def test_grad_validation_matches_reference():
+    """The reference's guard cases (test_sfa_grad_triton.py:325-357) raise ValueError before
+    any device work; CPU tensors are refused; the C ABI rejects bad shapes."""
+    from dsa_triton_ascend_amd import sparse_flash_attention_grad
+    q = torch.zeros(1, 4, 8, 512, dtype=torch.float16)
+    k = torch.zeros(1, 128, 1, 512, dtype=torch.float16)
+    qr = torch.zeros(1, 4, 8, 64, dtype=torch.float16)
+    kr = torch.zeros(1, 128, 1, 64, dtype=torch.float16)
+    si = torch.zeros(1, 4, 1, 64, dtype=torch.int32)
+    sm = torch.zeros(1, 1, 4, 8)
+    cases = [(dict(pre_tokens=0), "pre_tokens"), (dict(next_tokens=0), "next_tokens"),
+             (dict(sparse_mode=1), "sparse_mode"), (dict(deterministic=True), "deterministic"),
+             (dict(sparse_block_size=3), "power of 2"), (dict(query_rope=None), "query_rope")]
+    for kw, msg in cases:
+        args = dict(scale_value=0.04, query_rope=qr, key_rope=kr, sparse_mode=3)
+        args.update(kw)
+        with pytest.raises(ValueError, match=msg):
+            sparse_flash_attention_grad(q, k, k, si, q, q, sm, sm, **args)
+    with pytest.raises(ValueError, match="GPU"):
+        sparse_flash_attention_grad(q, k, k, si, q, q, sm, sm, query_rope=qr, key_rope=kr)
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    base = [p, p, p, p, 1, p, 64, 1, p, p, p, p, 1, 4, 8, 512, 64, 128, 128, 3, 0.04,
+            p, p, p, p, p, p, p, p, p, p, 1 << 30, None]
+    bad = list(base)
+    bad[15] = 64
+    assert lib.dsa_sfa_bwd(*bad) == _lib.DSA_ERR_INVALID and b"D must be one of" in lib.dsa_last_error()
+    bad = list(base)
+    bad[14] = 12
+    assert lib.dsa_sfa_bwd(*bad) == _lib.DSA_ERR_INVALID and b"N1 must be one of" in lib.dsa_last_error()
+    bad = list(base)
+    bad[31] = 16
+    assert lib.dsa_sfa_bwd(*bad) == _lib.DSA_ERR_INVALID and b"workspace" in lib.dsa_last_error()
+    bad = list(base)
+    bad[21] = None
+    assert lib.dsa_sfa_bwd(*bad) == _lib.DSA_ERR_INVALID and b"null pointer" in lib.dsa_last_error()
+    need = lib.dsa_sfa_bwd_workspace_bytes(4, 8, 512, 64, 1, 128)
+    assert need >= 128 * (512 + 64 + 512) * 4 and need < (1 << 30)
+
+
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(RuntimeError, match="missing"):
         _lib.load(tmp_path / "nope.so")

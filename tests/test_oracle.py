@@ -353,3 +353,102 @@ def test_parity_checker_rejects_dropped_head():
         except AssertionError:
             failures += 1
     assert failures == 8
+
+
+# ----------------------------------------------------------------- SFA backward
+from oracle import sparse_flash_attention_grad_ref as SFG
+
+
+def _autograd_sfa_grad(q, k, qr, kr, do, si, scale, act_q, act_k, bs, mode):
+    """float64 torch autograd of the forward attention (value a separate leaf equal to
+    k_nope, so d_key is the QK path only and d_value the PV path), plus the forward's
+    exact output and softmax stats."""
+    t = lambda x: torch.tensor(np.asarray(x, np.float64), requires_grad=True)
+    tq, tk, tqr, tkr, tv = t(q), t(k), t(qr), t(kr), t(k)
+    B, S1, N1, D = q.shape
+    out = torch.zeros(B, S1, N1, D, dtype=torch.float64)
+    smax = np.zeros((B, 1, S1, N1), np.float64)
+    ssum = np.zeros((B, 1, S1, N1), np.float64)
+    loss = torch.zeros((), dtype=torch.float64)
+    for b in range(B):
+        aq, ak = int(act_q[b]), int(act_k[b])
+        for s1 in range(aq):
+            if mode != 0 and s1 < aq - ak:
+                continue
+            thr = ak if mode == 0 else ak - aq + s1 + 1
+            if thr <= 0:
+                continue
+            pos = SFA.gather_positions(si[b, s1, 0], bs, thr, ak)
+            if not pos:
+                continue
+            pos = torch.tensor(pos)
+            s = (tq[b, s1] @ tk[b, pos, 0].T + tqr[b, s1] @ tkr[b, pos, 0].T) * scale
+            p = torch.softmax(s, dim=-1)
+            o = p @ tv[b, pos, 0]
+            loss = loss + (o * torch.from_numpy(np.asarray(do[b, s1], np.float64))).sum()
+            out[b, s1] = o.detach()
+            m = s.detach().max(dim=-1).values
+            smax[b, 0, s1] = m.numpy()
+            ssum[b, 0, s1] = torch.exp(s.detach() - m[:, None]).sum(-1).numpy()
+    loss.backward()
+    g = lambda x: x.grad.numpy() if x.grad is not None else np.zeros(x.shape)
+    return out.numpy(), smax, ssum, (g(tq), g(tk), g(tv), g(tqr), g(tkr))
+
+
+@pytest.mark.parametrize("mode,bs,act", [(3, 1, None), (0, 1, None), (3, 2, ([3, 2], [9, 6])),
+                                         (0, 4, ([2, 3], [5, 12]))])
+def test_sfa_grad_golden_vs_float64_autograd(mode, bs, act):
+    """The backward golden (fed the forward's exact output and stats) equals float64
+    autograd of the forward attention: catches a dropped delta, a misplaced scale, the
+    d_key / d_value paths swapped or summed, and scatter-adds that lose duplicates."""
+    B, S1, S2, N1, D, Dr = 2, 3, 12, 4, 16, 8
+    rng = np.random.RandomState(5)
+    q, qr, do = rng.randn(B, S1, N1, D), rng.randn(B, S1, N1, Dr), rng.randn(B, S1, N1, D)
+    k, kr = rng.randn(B, S2, 1, D), rng.randn(B, S2, 1, Dr)
+    act_q, act_k = act if act else ([S1] * B, [S2] * B)
+    count = 5
+    si = np.full((B, S1, 1, count), -1, np.int32)
+    for b in range(B):
+        for s1 in range(S1):
+            nb = -(-S2 // bs)
+            n = min(count, nb)
+            si[b, s1, 0, :n] = np.sort(rng.permutation(nb)[:n])
+    si[1, 2, 0, 3] = -1       # the scan of this row stops at its fourth id
+    scale = 0.3
+    out, smax, ssum, want = _autograd_sfa_grad(q, k, qr, kr, do, si, scale, act_q, act_k, bs, mode)
+    got = SFG.sfa_grad_golden_bsnd(q, k, si, do, out, smax, ssum, qr, kr, scale, act_q, act_k,
+                                   bs, mode, io_dtype="fp32")
+    for name, gv, wv in zip(("dq", "dk", "dv", "dqr", "dkr"), got, want):
+        np.testing.assert_allclose(gv, wv, rtol=2e-5, atol=2e-5, err_msg=name)
+    # every token selected by several rows: the scatter must have summed them
+    assert np.abs(want[2]).max() > 0
+
+
+def test_sfa_grad_tnd_equals_bsnd():
+    """TND wrapper == BSND golden on explicitly de-packed inputs (stats (1,T1,N1))."""
+    rng = np.random.RandomState(6)
+    lq, lk = [3, 2], [7, 5]
+    T1, T2, N1, D, Dr = sum(lq), sum(lk), 2, 8, 4
+    q, qr, do, o = (rng.randn(T1, N1, x).astype(np.float32) for x in (D, Dr, D, D))
+    k, kr = rng.randn(T2, 1, D).astype(np.float32), rng.randn(T2, 1, Dr).astype(np.float32)
+    sm, ss = rng.randn(1, T1, N1).astype(np.float32), (rng.rand(1, T1, N1) + 1).astype(np.float32)
+    si = np.full((T1, 1, 4), -1, np.int32)
+    for t in range(T1):
+        b = 0 if t < lq[0] else 1
+        si[t, 0, :3] = np.sort(rng.permutation(lk[b])[:3])
+    cq, ck = np.cumsum(lq), np.cumsum(lk)
+    got = SFG.sparse_flash_attention_grad(q, k, None, si, do, o, sm, ss, 0.5, qr, kr, cq, ck, 1, "TND", 3,
+                                          io_dtype="fp32")
+    ref_dq, ref_dqr = np.zeros_like(q), np.zeros_like(qr)
+    ref_dk, ref_dv, ref_dkr = np.zeros_like(k), np.zeros_like(k), np.zeros_like(kr)
+    q0 = k0 = 0
+    for b in range(2):
+        sl, kl = slice(q0, q0 + lq[b]), slice(k0, k0 + lk[b])
+        r = SFG.sfa_grad_golden_bsnd(q[None, sl], k[None, kl], si[None, sl], do[None, sl], o[None, sl],
+                                     sm[:, sl][None], ss[:, sl][None], qr[None, sl], kr[None, kl], 0.5,
+                                     [lq[b]], [lk[b]], 1, 3, io_dtype="fp32")
+        ref_dq[sl], ref_dk[kl], ref_dv[kl], ref_dqr[sl], ref_dkr[kl] = (x[0] for x in r)
+        q0 += lq[b]
+        k0 += lk[b]
+    for gv, wv in zip(got, (ref_dq, ref_dk, ref_dv, ref_dqr, ref_dkr)):
+        np.testing.assert_array_equal(gv, wv)
