@@ -9,7 +9,8 @@ resident in HBM. The same JSON line carries:
   cpu_baseline  -- the numpy oracle (a port of the reference golden) on a stride
                    sample of the same rows, timed on this host;
   breakdown     -- top-k kernel, SFA prefill (config 3), SFA paged decode (config 4),
-                   the TND indexer->SFA pipeline (config 5) and the small config 1.
+                   the SFA backward at the reference's grad perf shape, and the TND
+                   indexer->SFA pipeline (config 5).
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick]
 """
@@ -163,6 +164,31 @@ def bench_pipeline_c5(W, reps, torch):
     return res
 
 
+def bench_grad(W, torch):
+    """sparse_flash_attention_grad at perf_sfa_grad_triton.py:23's shape (the reference
+    quotes 34 ms for it on Ascend 910, docs/sfa_grad_optimization_summary.md:9).
+    Algorithmic work: 512 rows x 2048 tokens x 64 heads x 2 (3 x 576 + 2 x 512) FLOP."""
+    from dsa_triton_ascend_amd import sparse_flash_attention
+    from dsa_triton_ascend_amd.sparse_flash_attention_grad import GradPlan
+    g = W.sfa_grad_inputs(device="cuda:0", seed=42, **W.GRAD_PERF)
+    out, smax, ssum = sparse_flash_attention(g.query, g.key, g.key, g.sparse_indices, **g.kwargs())
+    plan = GradPlan(g.query, g.key, g.key, g.sparse_indices, g.extra["d_out"], out, smax, ssum,
+                    scale_value=g.scale_value, query_rope=g.query_rope, key_rope=g.key_rope,
+                    sparse_mode=g.sparse_mode)
+    warm(plan.run, torch)
+    (ms,) = event_time([plan.run], 10, torch)
+    flop = GRAD_PAIRS * 64 * 2.0 * (3 * 576 + 2 * 512)
+    res = {"ms": round(ms, 4), "tflops": round(flop / ms / 1e9, 2),
+           "frac_mfma": round(flop / ms / 1e9 / PEAK_BF16_TFLOPS, 4), "algorithmic_flop": flop,
+           "shape": "BSND B=1 S1=512 S2=4096 N1=64 D=512+64 top-k 2048 causal bf16"}
+    del plan, g, out, smax, ssum
+    return res
+
+
+# every row of the grad perf shape sees >= 3585 keys, so all select 2048 tokens
+GRAD_PAIRS = 512 * 2048
+
+
 def pmc_pass(torch, W):
     from dsa_triton_ascend_amd.lightning_indexer import IndexerPlan
     from dsa_triton_ascend_amd.sparse_flash_attention import AttentionPlan
@@ -274,6 +300,9 @@ def main():
                                           "frac_hbm": round(kv_bytes / ms4 / 1e6 / PEAK_HBM_GBS, 4),
                                           "gathered_kv_bytes": kv_bytes}
             del sd, kw
+            torch.cuda.empty_cache()
+            log("[bench] SFA backward at the reference's grad perf shape ...")
+            breakdown["sfa_grad"] = bench_grad(W, torch)
             torch.cuda.empty_cache()
             log("[bench] C5 TND indexer -> SFA pipeline ...")
             breakdown["pipeline_c5"] = bench_pipeline_c5(W, max(3, args.steps // 4), torch)

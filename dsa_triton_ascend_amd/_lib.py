@@ -35,9 +35,9 @@ SIGNATURES = {
     "dsa_sfa_workspace_zero_bytes": (_SZ, []),
     "dsa_sfa_fwd": (_I, [_P, _P, _P, _P, _I, _P, _I, _I, _P, _I, _I, _P, _P, _P, _P, _I, _I, _I,
                          _I, _I, _I, _I64, _I, _F, _P, _P, _P, _P, _SZ, _I, _P]),
-    "dsa_sfa_bwd_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I, _I64]),
-    "dsa_sfa_bwd": (_I, [_P, _P, _P, _P, _I, _P, _I, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I,
-                         _I64, _I, _F, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+    "dsa_sfa_bwd_workspace_bytes": (_SZ, [_I, _P, _P, _I, _I, _I, _I, _I, _I, _I64]),
+    "dsa_sfa_bwd": (_I, [_P, _P, _P, _P, _I, _P, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I,
+                         _I, _I64, _I, _F, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
 }
 
 _lib = None

@@ -144,25 +144,28 @@ int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key, cons
   return hip_status(launch_sfa_fwd(a, (hipStream_t)stream), "dsa_sfa_fwd launch");
 }
 
-size_t dsa_sfa_bwd_workspace_bytes(int total_rows, int n1, int d, int sparse_count,
-                                   int sparse_block_size, int64_t key_rows) {
-  if (total_rows < 0 || sparse_count <= 0 || sparse_block_size <= 0 || key_rows < 0 ||
-      (d != 128 && d != 256 && d != 512))
+size_t dsa_sfa_bwd_workspace_bytes(int batch, const int32_t* host_row_start,
+                                   const int32_t* host_act_k, int s2, int total_rows, int n1, int d,
+                                   int sparse_count, int sparse_block_size, int64_t key_rows) {
+  if (batch <= 0 || !host_row_start || !host_act_k || total_rows < 0 || n1 <= 0 || sparse_count <= 0 ||
+      sparse_block_size <= 0 || key_rows < 0 || (d != 128 && d != 256 && d != 512))
     return 0;
-  return sfa_bwd_workspace_bytes(total_rows, n1, sparse_count, sparse_block_size, key_rows, d);
+  return sfa_bwd_workspace_bytes(batch, host_row_start, host_act_k, s2, total_rows, n1, d, sparse_count,
+                                 sparse_block_size, key_rows);
 }
 
 int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, const void* key_rope,
                 int io_dtype, const int32_t* sparse_indices, int sparse_count,
                 int sparse_block_size, const int32_t* row_start, const int32_t* key_start,
-                const int32_t* act_q, const int32_t* act_k, int batch, int total_rows, int n1,
-                int d, int dr, int s2, int64_t key_rows, int sparse_mode, float scale,
-                const void* d_out, const void* out, const float* sm_max, const float* sm_sum,
-                void* d_query, void* d_query_rope, void* d_key, void* d_key_rope, void* d_value,
-                void* workspace, size_t workspace_bytes, void* stream) {
+                const int32_t* act_q, const int32_t* act_k, const int32_t* host_row_start,
+                const int32_t* host_act_k, int batch, int total_rows, int n1, int d, int dr, int s2,
+                int64_t key_rows, int sparse_mode, float scale, const void* d_out, const void* out,
+                const float* sm_max, const float* sm_sum, void* d_query, void* d_query_rope,
+                void* d_key, void* d_key_rope, void* d_value, void* workspace,
+                size_t workspace_bytes, void* stream) {
   if (!query || !query_rope || !key || !key_rope || !sparse_indices || !row_start || !key_start ||
       !act_q || !act_k || !d_out || !out || !sm_max || !sm_sum || !d_query || !d_query_rope ||
-      !d_key || !d_key_rope || !d_value || !workspace)
+      !d_key || !d_key_rope || !d_value || !workspace || !host_row_start || !host_act_k)
     return fail(DSA_ERR_INVALID, "dsa_sfa_bwd: null pointer argument");
   if (!is16(io_dtype)) return fail(DSA_ERR_INVALID, "dsa_sfa_bwd: io_dtype must be fp16 or bf16");
   if (sparse_mode != 0 && sparse_mode != 3)
@@ -180,7 +183,11 @@ int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, cons
   if ((int64_t)sparse_count * sparse_block_size > (1 << 20))
     return fail(DSA_ERR_UNSUPPORTED, "dsa_sfa_bwd: sparse_count*sparse_block_size > 2^20 tokens");
   if (key_rows > INT32_MAX) return fail(DSA_ERR_UNSUPPORTED, "dsa_sfa_bwd: key_rows > 2^31-1");
-  const size_t need = sfa_bwd_workspace_bytes(total_rows, n1, sparse_count, sparse_block_size, key_rows, d);
+  if (batch > 65535) return fail(DSA_ERR_UNSUPPORTED, "dsa_sfa_bwd: batch > 65535");
+  if (host_row_start[0] != 0 || host_row_start[batch] > total_rows)
+    return fail(DSA_ERR_INVALID, "dsa_sfa_bwd: host_row_start must start at 0 and end within total_rows");
+  const size_t need = sfa_bwd_workspace_bytes(batch, host_row_start, host_act_k, s2, total_rows, n1, d,
+                                              sparse_count, sparse_block_size, key_rows);
   if (workspace_bytes < need)
     return fail(DSA_ERR_INVALID, "dsa_sfa_bwd: workspace of %zu bytes required, %zu given", need,
                 workspace_bytes);

@@ -234,5 +234,8 @@ struct SfaBwdArgs {
   const void* d_out; const void* out; const float* sm_max; const float* sm_sum;
   void* dq; void* dqr; void* dk; void* dkr; void* dv;
 };
-size_t sfa_bwd_workspace_bytes(int total_rows, int n1, int topk, int sbs, int64_t key_rows, int d);
+// h_row_start [batch + 1] and h_act_k [batch]: host copies of the row offsets and kv
+// lengths (they size the per-batch dense buffers)
+size_t sfa_bwd_workspace_bytes(int batch, const int32_t* h_row_start, const int32_t* h_act_k, int s2,
+                               int total_rows, int n1, int d, int topk, int sbs, int64_t key_rows);
 hipError_t launch_sfa_bwd(const SfaBwdArgs& a, hipStream_t s);

@@ -9,29 +9,40 @@
 //   d_key | d_key_rope    += dS^T @ [q_nope | q_rope]        (scatter over tokens)
 //   d_value               += P^T @ dO                        (scatter over tokens)
 //
+// d_key / d_value are computed as dense GEMMs instead of per-(row, token)
+// scatters: per batch, the P and dS of every (query row, head, key token) go to
+// two token-major buffers PT[token][row * N1 + head] (zero where a row does not
+// select the token), and then
+//   [d_key | d_key_rope][t, :] = sum_k dS_T[t, k] [q | q_rope][k, :]
+//   d_value[t, :]             = sum_k P_T[t, k]  d_out[k, :]
+// with k running over the batch's (row, head) pairs. At the reference's shapes a
+// key token is selected by a large share of the rows (half of them at
+// S2 = 2 * topK), so these dense products cost less than scattering
+// (D + Dr + D) fp32 atomics per selected (row, token, head block).
+//
 // Launches:
 //  1. the forward's token-list kernels (the golden's gather order, physical key
 //     rows), so both passes select exactly the same tokens;
-//  2. sfa_bwd_zero_kernel -- clears the fp32 d_key / d_key_rope / d_value
-//     accumulators in the workspace;
-//  3. sfa_bwd_kernel -- one work-group (4 waves) per (query row, block of 32
-//     heads). Q | Q rope and dO of the block sit in LDS for the whole row; the
+//  2. sfa_bwd_geo_kernel -- per-batch offsets of the dense buffers; clears the
+//     fp32 accumulators and the used part of the dense buffers;
+//  3. sfa_bwd_rows_kernel -- one work-group (4 waves) per (query row, block of
+//     32 heads). Q | Q rope and dO of the block sit in LDS for the whole row; the
 //     row's tokens are processed in tiles of 32 gathered [D | Dr] rows:
 //       * S^T = K Q^T and dP^T = K_nope dO^T on v_mfma_f32_32x32x16 (tokens as
 //         M, heads as N), their k-ranges split over the four waves and summed
 //         through LDS;
-//       * P and dS (fp32, then the io dtype) go to LDS as [head][token];
-//       * each wave then owns a quarter of the 32-column blocks of
-//         dQ (accumulated in registers over the row), of the tile's
-//         dK = dS^T [Q | Q rope] and of its dV = P^T dO; the operands whose K is
-//         the token or head index are read with ds_read_b64_tr_b16 from the
-//         row-major LDS arrays;
-//       * the dK / dV blocks are added to fp32 accumulators at the tokens'
-//         physical rows with global fp32 atomics (a key row selected by several
-//         query rows gets all their contributions; the order of the additions,
-//         and so the last bits, may differ from run to run -- the reference's
-//         contract, deterministic=False, sparse_flash_attention_grad_triton.py:550);
-//  4. sfa_bwd_finish_kernel -- converts the accumulators to the io dtype.
+//       * P and dS in fp32, stored in the io dtype to the dense buffers (32
+//         consecutive heads of one token per store group) and dS also to LDS as
+//         [head][token];
+//       * dQ[head, col] += dS K, each wave owning a quarter of the 32-column
+//         blocks, the K operand read with ds_read_b64_tr_b16 from the tile;
+//  4. sfa_bwd_gemm_kernel (twice: d_key | d_key_rope, d_value) -- 128 x BN
+//     output tiles per batch on v_mfma_f32_32x32x16, the k-range split over
+//     work-groups when the tiles alone do not fill the GPU; partial tiles are
+//     added into fp32 accumulators with global atomics (so the last bits may
+//     differ from run to run, the reference's deterministic=False contract,
+//     sparse_flash_attention_grad_triton.py:550);
+//  5. sfa_bwd_finish_kernel -- converts the accumulators to the io dtype.
 #include <climits>
 
 #include "dsa_common.hpp"
@@ -40,10 +51,12 @@ namespace dsa {
 namespace {
 
 constexpr int BDR = 64;     // rope width
-constexpr int BH = 32;      // heads per work-group
+constexpr int BH = 32;      // heads per work-group (rows kernel)
 constexpr int BT = 32;      // tokens per tile
 constexpr int BWV = 4;      // waves per work-group
 constexpr float BLOG2E = 1.4426950408889634f;
+constexpr int GBM = 128;    // GEMM tile rows (key tokens)
+constexpr int GBK = 64;     // GEMM k-step; dense rows are padded to a multiple of it
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -51,9 +64,8 @@ template <int D> struct BCfg {
   static constexpr int DT = D + BDR;                   // [nope | rope] width
   static constexpr int QP = DT + 8;                    // Q / K row pitch: odd count of 16-byte units
   static constexpr int OP = D + 8;                     // dO row pitch
-  static constexpr int PP = BT + 8;                    // P / dS row pitch
-  static constexpr int NBQ = DT / 32;                  // 32-column blocks of dQ and dK
-  static constexpr int NBV = D / 32;                   // of dV
+  static constexpr int PP = BT + 8;                    // dS row pitch
+  static constexpr int NBQ = DT / 32;                  // 32-column blocks of dQ
   static constexpr int JQ = (NBQ + BWV - 1) / BWV;     // dQ blocks per wave, at most
   static constexpr int KS_S = DT / 16;                 // k-steps of S^T
   static constexpr int KS_P = D / 16;                  // of dP^T
@@ -72,22 +84,89 @@ __device__ __forceinline__ uint4 tr_frag(const uint16_t* X, int pitch, int c0, i
   return make_uint4(lo.x, lo.y, hi.x, hi.y);
 }
 
-struct BwdAcc {
-  float* dk;    // [key_rows, D]
-  float* dkr;   // [key_rows, Dr]
-  float* dv;    // [key_rows, D]
+struct BwdWs {
+  int64_t* boff;   // [batch + 1] dense-buffer offsets (elements)
+  float* dk;       // [key_rows, D]   fp32 accumulators
+  float* dkr;      // [key_rows, Dr]
+  float* dv;       // [key_rows, D]
+  uint16_t* dst;   // dS_T dense buffer (io dtype)
+  uint16_t* pt;    // P_T dense buffer (io dtype)
+  int64_t cap;     // elements per dense buffer
 };
 
+// Dense geometry of batch b: query rows [rs, rs + nq), key rows [ks, ks + nk)
+// (the tokens a row of the batch can select, t < min(act_k, S2)), dense rows of
+// kp = nq * N1 rounded up to GBK elements.
+struct BatchGeo {
+  int rs, nq, ks, nk, kp;
+};
+
+__host__ __device__ inline int dense_row(int nq, int n1) { return (nq * n1 + GBK - 1) / GBK * GBK; }
+
+__device__ __forceinline__ BatchGeo batch_geo(const SfaArgs& f, int b) {
+  BatchGeo g;
+  g.rs = f.row_start[b];
+  g.nq = f.row_start[b + 1] - g.rs;
+  g.ks = f.key_start[b];
+  int nk = f.act_k[b] < f.s2 ? f.act_k[b] : f.s2;
+  const int64_t room = f.key_rows - g.ks;
+  nk = nk < 0 ? 0 : nk;
+  g.nk = (int64_t)nk < room ? nk : (int)(room > 0 ? room : 0);
+  g.kp = dense_row(g.nq, f.n1);
+  return g;
+}
+
+// One work-group: per-batch offsets of the dense buffers (prefix of nk * kp).
+__global__ __launch_bounds__(256) void sfa_bwd_geo_kernel(SfaArgs f, BwdWs w) {
+  __shared__ int64_t part[256];
+  const int tid = threadIdx.x;
+  const int per = (f.batch + 255) / 256;
+  const int b0 = tid * per;
+  int64_t sum = 0;
+  for (int b = b0; b < b0 + per && b < f.batch; ++b) {
+    const BatchGeo g = batch_geo(f, b);
+    sum += (int64_t)g.nk * g.kp;
+  }
+  part[tid] = sum;
+  __syncthreads();
+  if (tid == 0) {
+    int64_t run = 0;
+    for (int i = 0; i < 256; ++i) {
+      const int64_t v = part[i];
+      part[i] = run;
+      run += v;
+    }
+  }
+  __syncthreads();
+  int64_t off = part[tid];
+  for (int b = b0; b < b0 + per && b < f.batch; ++b) {
+    w.boff[b] = off;
+    const BatchGeo g = batch_geo(f, b);
+    off += (int64_t)g.nk * g.kp;
+  }
+  if (tid == 255) w.boff[f.batch] = off;
+}
+
+// Clears n4 16-byte words of p (accumulators); dense buffers: up to the used size
+__global__ void sfa_bwd_zero_kernel(uint4* p, int64_t n4, const int64_t* used_elems, int64_t cap_elems) {
+  if (used_elems) {
+    const int64_t u = *used_elems < cap_elems ? *used_elems : cap_elems;
+    const int64_t n8 = (u + 7) / 8;
+    n4 = n8 < n4 ? n8 : n4;
+  }
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = make_uint4(0, 0, 0, 0);
+}
+
 template <int IO, int D>
-__global__ __launch_bounds__(BWV * 64) void sfa_bwd_kernel(SfaBwdArgs a, SfaTokenLists tl, BwdAcc acc) {
+__global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, SfaTokenLists tl, BwdWs w) {
   using C = BCfg<D>;
   __shared__ __attribute__((aligned(16))) uint16_t Qs[BH * C::QP];    // [head][nope | rope]
   __shared__ __attribute__((aligned(16))) uint16_t Ks[BT * C::QP];    // [token][nope | rope]
   __shared__ __attribute__((aligned(16))) uint16_t dOs[BH * C::OP];   // [head][D]
-  __shared__ __attribute__((aligned(16))) uint16_t Ps[BH * C::PP];    // [head][token]
   __shared__ __attribute__((aligned(16))) uint16_t dSs[BH * C::PP];   // [head][token]
   __shared__ float part[BWV][16][64];   // S^T / dP^T k-range partials, MFMA layout
-  __shared__ int s_tok[BT];
+  __shared__ int s_tok[BT];             // the tile's token index within the batch (-1: none)
   __shared__ float s_m[BH], s_il[BH], s_dl[BH];
 
   const SfaArgs& f = a.f;
@@ -103,6 +182,13 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_kernel(SfaBwdArgs a, SfaToke
   const uint16_t* kb = reinterpret_cast<const uint16_t*>(f.k);
   const uint16_t* krb = reinterpret_cast<const uint16_t*>(f.kr);
   const uint4 z4 = make_uint4(0, 0, 0, 0);
+  // dense-buffer row base of this (row, head block): token t of the batch at
+  // dbase + t * kp; writes only when the batch's block fits the buffers
+  const int b = batch_of_row(f.row_start, f.batch, r);
+  const BatchGeo g = batch_geo(f, b);
+  const int rl = r - g.rs;
+  const bool dense_ok = rl >= 0 && rl < g.nq && w.boff[b + 1] <= w.cap;
+  const int64_t dbase = w.boff[b] + (int64_t)rl * n1 + h0;
 
   // ---- the block's Q | Q rope and dO (rows past the heads are zero), stats
   {
@@ -130,8 +216,8 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_kernel(SfaBwdArgs a, SfaToke
     if (h < hn) {
       const int64_t hr = (int64_t)r * n1 + h0 + h;
       for (int c = part8 * 8; c < D; c += 64) {
-        const uint4 o = ldg16(ob + hr * D + c), g = ldg16(gob + hr * D + c);
-        const uint32_t ow[4] = {o.x, o.y, o.z, o.w}, gw[4] = {g.x, g.y, g.z, g.w};
+        const uint4 o = ldg16(ob + hr * D + c), gv = ldg16(gob + hr * D + c);
+        const uint32_t ow[4] = {o.x, o.y, o.z, o.w}, gw[4] = {gv.x, gv.y, gv.z, gv.w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           dl += to_f32<IO>((uint16_t)(ow[j] & 0xFFFFu)) * to_f32<IO>((uint16_t)(gw[j] & 0xFFFFu));
@@ -142,7 +228,7 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_kernel(SfaBwdArgs a, SfaToke
     dl += __shfl_xor(dl, 1);
     dl += __shfl_xor(dl, 2);
     dl += __shfl_xor(dl, 4);
-    if (part8 == 0 && h < BH) {
+    if (part8 == 0) {
       float m = 0.f, il = 0.f;
       if (h < hn) {
         const int64_t hr = (int64_t)r * n1 + h0 + h;
@@ -163,23 +249,43 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_kernel(SfaBwdArgs a, SfaToke
     for (int i = 0; i < 16; ++i) dq[jj][i] = 0.f;
   const float sl2 = f.scale * BLOG2E;
 
-  for (int t0 = 0; t0 < ntok; t0 += BT) {
-    const int nv = ntok - t0 < BT ? ntok - t0 : BT;
-    // ---- gather the tile's [nope | rope] rows; rows outside the key tensors and
-    // slots past the list are zero
-    for (int i = tid; i < BT * (C::DT / 8); i += BWV * 64) {
-      const int t = i / (C::DT / 8), c = (i % (C::DT / 8)) * 8;
-      const int p = t < nv ? toks[t0 + t] : -1;
+  // ---- gathers of a tile's [nope | rope] rows into registers (rows outside the key
+  // tensors and slots past the list are zero); the next tile's are in flight while
+  // the current one is computed
+  constexpr int KCH = BT * (C::DT / 8) / (BWV * 64);   // 16-byte chunks per thread
+  static_assert(KCH * BWV * 64 == BT * (C::DT / 8), "tile splits evenly");
+  uint4 kreg[KCH];
+  int ptok = -1;
+  auto gather = [&](int t0) {
+    const int nvt = ntok - t0 < BT ? ntok - t0 : BT;
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      const int idx = tid + BWV * 64 * i;
+      const int t = idx / (C::DT / 8), c = (idx % (C::DT / 8)) * 8;
+      const int p = t < nvt ? toks[t0 + t] : -1;
       uint4 v = z4;
       if ((uint32_t)p < (uint32_t)krows)
         v = c < D ? ldg16(kb + (int64_t)p * D + c) : ldg16(krb + (int64_t)p * BDR + (c - D));
-      *reinterpret_cast<uint4*>(&Ks[t * C::QP + c]) = v;
+      kreg[i] = v;
     }
     if (tid < BT) {
-      const int p = tid < nv ? toks[t0 + tid] : -1;
-      s_tok[tid] = (uint32_t)p < (uint32_t)krows ? p : -1;
+      const int p = tid < nvt ? toks[t0 + tid] : -1;
+      const int tb = p - g.ks;   // token index within the batch
+      ptok = dense_ok && (uint32_t)p < (uint32_t)krows && tb >= 0 && tb < g.nk ? tb : -1;
     }
+  };
+  if (ntok > 0) gather(0);
+
+  for (int t0 = 0; t0 < ntok; t0 += BT) {
+    const int nv = ntok - t0 < BT ? ntok - t0 : BT;
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      const int idx = tid + BWV * 64 * i;
+      *reinterpret_cast<uint4*>(&Ks[(idx / (C::DT / 8)) * C::QP + (idx % (C::DT / 8)) * 8]) = kreg[i];
+    }
+    if (tid < BT) s_tok[tid] = ptok;
     __syncthreads();
+    if (t0 + BT < ntok) gather(t0 + BT);
 
     // ---- S^T (waves 0, 1: halves of the [nope | rope] k-range) and dP^T (waves 2,
     // 3: halves of the nope range), tokens as M, heads as N
@@ -189,16 +295,17 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_kernel(SfaBwdArgs a, SfaToke
       const int ks0 = (wave & 1) * nks;
       const uint16_t* arow = Ks + (lane & 31) * C::QP + (lane >> 5) * 8 + ks0 * 16;
       const uint16_t* brow = (is_s ? Qs + (lane & 31) * C::QP : dOs + (lane & 31) * C::OP) + (lane >> 5) * 8 + ks0 * 16;
-      f32x16 s = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      f32x16 sacc = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
       for (int ks = 0; ks < nks; ++ks)
-        s = Mfma<IO>::m32(*reinterpret_cast<const uint4*>(arow + ks * 16),
-                          *reinterpret_cast<const uint4*>(brow + ks * 16), s);
+        sacc = Mfma<IO>::m32(*reinterpret_cast<const uint4*>(arow + ks * 16),
+                             *reinterpret_cast<const uint4*>(brow + ks * 16), sacc);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) part[wave][i][lane] = s[i];
+      for (int i = 0; i < 16; ++i) part[wave][i][lane] = sacc[i];
     }
     __syncthreads();
 
-    // ---- P and dS of the tile (fp32, stored in the io dtype as [head][token])
+    // ---- P and dS of the tile (fp32 -> io dtype): dS to LDS as [head][token] for
+    // dQ, both to the dense buffers (a store group = 32 heads of one token)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int i = wave * 4 + j;
@@ -210,8 +317,14 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_kernel(SfaBwdArgs a, SfaToke
         p = __builtin_amdgcn_exp2f(sv * sl2 - s_m[h]) * s_il[h];
         ds = p * (dp - s_dl[h]) * f.scale;
       }
-      Ps[h * C::PP + tk] = from_f32<IO>(p);
-      dSs[h * C::PP + tk] = from_f32<IO>(ds);
+      const uint16_t ds16 = from_f32<IO>(ds);
+      dSs[h * C::PP + tk] = ds16;
+      const int tb = s_tok[tk];
+      if (tb >= 0 && h < hn) {
+        const int64_t di = dbase + (int64_t)tb * g.kp + h;
+        w.dst[di] = ds16;
+        w.pt[di] = from_f32<IO>(p);
+      }
     }
     __syncthreads();
 
@@ -227,43 +340,7 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_kernel(SfaBwdArgs a, SfaToke
         }
       }
     }
-    // ---- dK[token, col] = dS^T Q and dV[token, col] = P^T dO, added at the
-    // tokens' key rows (fp32 atomics, coalesced along the 32 columns of a block)
-#pragma unroll
-    for (int jj = 0; jj < C::JQ; ++jj) {
-      const int j = wave + BWV * jj;
-      if (j < C::NBQ) {
-        f32x16 c = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kq = 0; kq < BH / 16; ++kq)
-          c = Mfma<IO>::m32(tr_frag(dSs, C::PP, 0, kq * 16, lane), tr_frag(Qs, C::QP, 32 * j, kq * 16, lane), c);
-        const int col = 32 * j + (lane & 31);
-        float* dst = col < D ? acc.dk + col : acc.dkr + (col - D);
-        const int ld = col < D ? D : BDR;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int p = s_tok[m32_row(i, lane)];
-          if (p >= 0) unsafeAtomicAdd(dst + (int64_t)p * ld, c[i]);
-        }
-      }
-    }
-#pragma unroll
-    for (int jj = 0; jj < (C::NBV + BWV - 1) / BWV; ++jj) {
-      const int j = wave + BWV * jj;
-      if (j < C::NBV) {
-        f32x16 c = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kq = 0; kq < BH / 16; ++kq)
-          c = Mfma<IO>::m32(tr_frag(Ps, C::PP, 0, kq * 16, lane), tr_frag(dOs, C::OP, 32 * j, kq * 16, lane), c);
-        float* dst = acc.dv + 32 * j + (lane & 31);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int p = s_tok[m32_row(i, lane)];
-          if (p >= 0) unsafeAtomicAdd(dst + (int64_t)p * D, c[i]);
-        }
-      }
-    }
-    __syncthreads();   // the next tile overwrites Ks, Ps, dSs and s_tok
+    __syncthreads();   // the next tile overwrites Ks, dSs and s_tok
   }
 
   // ---- d_query | d_query_rope of the block's heads (zeros for rows without tokens)
@@ -288,9 +365,148 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_kernel(SfaBwdArgs a, SfaToke
   }
 }
 
-__global__ void sfa_bwd_zero_kernel(float4* p, int64_t n4) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x)
-    p[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+// ---- dense GEMM per batch: C[t, n] = sum_k A[t, k] B[k, n] over the batch's
+// (row, head) pairs k. A: the dense dS_T (KV = false: d_key | d_key_rope, B = q |
+// q_rope) or P_T (KV = true: d_value, B = d_out) buffer; 128 x BN tiles, BN = 64 NB,
+// four waves as 2 (rows) x 2 (columns), each 64 x 32 NB. xt = m-tile * n-tiles +
+// n-tile, blockIdx.y = batch, blockIdx.z = k-split. Results are added to the fp32
+// accumulators (rows t < nk of the batch).
+template <int IO, int D, bool KV, int NB>
+__device__ __forceinline__ void gemm_tile(const SfaBwdArgs& a, const BwdWs& w, int ksplit, int xt,
+                                          uint16_t (*As)[GBM * (GBK + 8)], uint16_t* Bs0) {
+  constexpr int N = KV ? D : D + BDR;
+  constexpr int BN = 64 * NB;
+  constexpr int NT = N / BN;
+  static_assert(N % BN == 0, "n-tiles cover the columns");
+  constexpr int AP = GBK + 8;    // A tile pitch (elements)
+  constexpr int BP = BN + 8;     // B tile pitch
+  constexpr int ACH = GBM * GBK / 8 / 256;   // 16-byte A chunks per thread per k-step
+  constexpr int BCH = GBK * BN / 8 / 256;    // B chunks
+  static_assert(ACH * 256 * 8 == GBM * GBK && BCH * 256 * 8 == GBK * BN, "tiles split evenly");
+  uint16_t* Bs[2] = {Bs0, Bs0 + GBK * BP};
+
+  const SfaArgs& f = a.f;
+  const int b = blockIdx.y;
+  const BatchGeo g = batch_geo(f, b);
+  const int mt = xt / NT, nt = xt % NT;
+  const int m0 = mt * GBM;
+  if (m0 >= g.nk || w.boff[b + 1] > w.cap) return;
+  const int kper = ((g.kp + ksplit - 1) / ksplit + GBK - 1) / GBK * GBK;
+  const int kbeg = blockIdx.z * kper;
+  const int kend = kbeg + kper < g.kp ? kbeg + kper : g.kp;
+  if (kbeg >= kend) return;
+  const int kreal = g.nq * f.n1;   // k past this is padding (zero A, no B row)
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  const uint16_t* abuf = (KV ? w.pt : w.dst) + w.boff[b];
+  const uint16_t* bq = reinterpret_cast<const uint16_t*>(KV ? a.d_out : a.f.q);
+  const uint16_t* bqr = reinterpret_cast<const uint16_t*>(a.f.qr);
+  const int64_t brow0 = (int64_t)g.rs * f.n1;   // B row of k = 0
+  const uint4 z4 = make_uint4(0, 0, 0, 0);
+
+  uint4 ra[ACH], rb[BCH];
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      const int c = tid + 256 * i;
+      const int m = c / (GBK / 8), kk = (c % (GBK / 8)) * 8;
+      const int t = m0 + m;
+      ra[i] = t < g.nk ? ldg16(abuf + (int64_t)t * g.kp + k0 + kk) : z4;
+    }
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) {
+      const int c = tid + 256 * i;
+      const int kk = c / (BN / 8), n = nt * BN + (c % (BN / 8)) * 8;
+      const int k = k0 + kk;
+      uint4 v = z4;
+      if (k < kreal) {
+        const int64_t row = brow0 + k;
+        v = (KV || n < D) ? ldg16(bq + row * D + n) : ldg16(bqr + row * BDR + (n - D));
+      }
+      rb[i] = v;
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      const int c = tid + 256 * i;
+      *reinterpret_cast<uint4*>(&As[buf][(c / (GBK / 8)) * AP + (c % (GBK / 8)) * 8]) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) {
+      const int c = tid + 256 * i;
+      *reinterpret_cast<uint4*>(&Bs[buf][(c / (BN / 8)) * BP + (c % (BN / 8)) * 8]) = rb[i];
+    }
+  };
+
+  f32x16 acc[2][NB];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  load(kbeg);
+  store(0);
+  __syncthreads();
+  int buf = 0;
+  for (int k0 = kbeg; k0 < kend; k0 += GBK) {
+    const bool more = k0 + GBK < kend;
+    if (more) load(k0 + GBK);   // in flight while this step's MFMAs run
+#pragma unroll
+    for (int s = 0; s < GBK / 16; ++s) {
+      uint4 af[2], bfr[NB];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        af[i] = *reinterpret_cast<const uint4*>(&As[buf][(64 * wm + 32 * i + (lane & 31)) * AP + s * 16 + (lane >> 5) * 8]);
+#pragma unroll
+      for (int j = 0; j < NB; ++j) bfr[j] = tr_frag(Bs[buf], BP, 32 * NB * wn + 32 * j, s * 16, lane);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) acc[i][j] = Mfma<IO>::m32(af[i], bfr[j], acc[i][j]);
+    }
+    if (more) {
+      store(buf ^ 1);
+      __syncthreads();
+      buf ^= 1;
+    }
+  }
+
+  // ---- add the tile to the accumulators (rows past the batch's tokens skipped)
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int n = nt * BN + 32 * NB * wn + 32 * j + (lane & 31);
+      float* dst = KV ? w.dv + n : (n < D ? w.dk + n : w.dkr + (n - D));
+      const int ld = (KV || n < D) ? D : BDR;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int t = m0 + 64 * wm + 32 * i + m32_row(e, lane);
+        if (t < g.nk) unsafeAtomicAdd(dst + (int64_t)(g.ks + t) * ld, acc[i][j][e]);
+      }
+    }
+}
+
+// n-tile widths (in 64-column units) of the two GEMMs: d_key | d_key_rope spans
+// D + 64 columns (3, 5, 9 units), d_value D (2, 4, 8)
+template <int D> struct GemmNB;
+template <> struct GemmNB<128> { static constexpr int K = 3, V = 2; };
+template <> struct GemmNB<256> { static constexpr int K = 5, V = 4; };
+template <> struct GemmNB<512> { static constexpr int K = 3, V = 4; };
+
+// One product per launch (d_key | d_key_rope, then d_value): each instance gets only
+// the registers its tile needs.
+template <int IO, int D, bool KV>
+__global__ __launch_bounds__(256) void sfa_bwd_gemm_kernel(SfaBwdArgs a, BwdWs w, int ksplit) {
+  constexpr int NB = KV ? GemmNB<D>::V : GemmNB<D>::K;
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][GBM * (GBK + 8)];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2 * GBK * (64 * NB + 8)];
+  gemm_tile<IO, D, KV, NB>(a, w, ksplit, blockIdx.x, As, Bs);
 }
 
 // fp32 accumulator -> io dtype, 4 elements per step (every length is a multiple of 4)
@@ -302,23 +518,33 @@ __global__ void sfa_bwd_finish_kernel(const float4* src, uint2* dst, int64_t n4)
   }
 }
 
-template <int IO>
-hipError_t launch_bwd_io(const SfaBwdArgs& a, const SfaTokenLists& tl, BwdAcc acc, hipStream_t s) {
+template <int IO, int D>
+hipError_t launch_bwd_d(const SfaBwdArgs& a, const SfaTokenLists& tl, const BwdWs& w, hipStream_t s) {
   const SfaArgs& f = a.f;
   if (f.total_rows > 0) {
     const dim3 grid(f.total_rows, (f.n1 + BH - 1) / BH);
-    switch (f.d) {
-      case 128: hipLaunchKernelGGL((sfa_bwd_kernel<IO, 128>), grid, dim3(BWV * 64), 0, s, a, tl, acc); break;
-      case 256: hipLaunchKernelGGL((sfa_bwd_kernel<IO, 256>), grid, dim3(BWV * 64), 0, s, a, tl, acc); break;
-      case 512: hipLaunchKernelGGL((sfa_bwd_kernel<IO, 512>), grid, dim3(BWV * 64), 0, s, a, tl, acc); break;
-      default: return hipErrorInvalidValue;
-    }
+    hipLaunchKernelGGL((sfa_bwd_rows_kernel<IO, D>), grid, dim3(BWV * 64), 0, s, a, tl, w);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    // GEMM grid: every (m-tile, n-tile) of the largest batch; the k-range is split
+    // until about 640 work-groups are in flight
+    constexpr int NTK = (D + BDR) / (64 * GemmNB<D>::K), NTV = D / (64 * GemmNB<D>::V);
+    const int mts = (f.s2 + GBM - 1) / GBM;
+    if (mts > 0) {
+      const int64_t tiles = (int64_t)f.batch * mts * (NTK + NTV);
+      int ksplit = (int)((640 + tiles - 1) / tiles);
+      ksplit = ksplit < 1 ? 1 : (ksplit > 16 ? 16 : ksplit);
+      hipLaunchKernelGGL((sfa_bwd_gemm_kernel<IO, D, false>), dim3(mts * NTK, f.batch, ksplit), dim3(256), 0, s,
+                         a, w, ksplit);
+      hipLaunchKernelGGL((sfa_bwd_gemm_kernel<IO, D, true>), dim3(mts * NTV, f.batch, ksplit), dim3(256), 0, s,
+                         a, w, ksplit);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
   }
   const int64_t kr = f.key_rows;
   const struct { const float* src; void* dst; int64_t n; } outs[3] = {
-      {acc.dk, a.dk, kr * f.d}, {acc.dkr, a.dkr, kr * BDR}, {acc.dv, a.dv, kr * f.d}};
+      {w.dk, a.dk, kr * D}, {w.dkr, a.dkr, kr * BDR}, {w.dv, a.dv, kr * D}};
   for (const auto& o : outs) {
     if (o.n == 0) continue;
     const int64_t n4 = o.n / 4;
@@ -329,16 +555,41 @@ hipError_t launch_bwd_io(const SfaBwdArgs& a, const SfaTokenLists& tl, BwdAcc ac
   return hipGetLastError();
 }
 
+template <int IO>
+hipError_t launch_bwd_io(const SfaBwdArgs& a, const SfaTokenLists& tl, const BwdWs& w, hipStream_t s) {
+  switch (a.f.d) {
+    case 128: return launch_bwd_d<IO, 128>(a, tl, w, s);
+    case 256: return launch_bwd_d<IO, 256>(a, tl, w, s);
+    case 512: return launch_bwd_d<IO, 512>(a, tl, w, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+// Workspace: token lists | batch offsets | fp32 accumulators (d_key, d_key_rope,
+// d_value) | dS_T | P_T. Returns the offset of dS_T; the two dense buffers share
+// the rest equally.
+size_t bwd_fixed_bytes(int total_rows, int batch, int topk, int sbs, int64_t key_rows, int d) {
+  size_t off = align256(sfa_token_ws_bytes(total_rows > 0 ? total_rows : 1, topk, sbs));
+  off += align256((size_t)(batch + 1) * 8);
+  off += align256((size_t)key_rows * d * 4);
+  off += align256((size_t)key_rows * BDR * 4);
+  off += align256((size_t)key_rows * d * 4);
+  return off;
+}
+
 }  // namespace
 }  // namespace dsa
 
-size_t sfa_bwd_workspace_bytes(int total_rows, int n1, int topk, int sbs, int64_t key_rows, int d) {
-  (void)n1;
-  size_t off = dsa::align256(sfa_token_ws_bytes(total_rows > 0 ? total_rows : 1, topk, sbs));
-  off += dsa::align256((size_t)key_rows * d * 4);
-  off += dsa::align256((size_t)key_rows * dsa::BDR * 4);
-  off += dsa::align256((size_t)key_rows * d * 4);
-  return off;
+size_t sfa_bwd_workspace_bytes(int batch, const int32_t* h_row_start, const int32_t* h_act_k, int s2,
+                               int total_rows, int n1, int d, int topk, int sbs, int64_t key_rows) {
+  int64_t dense = 0;
+  for (int b = 0; b < batch; ++b) {
+    const int nq = h_row_start[b + 1] - h_row_start[b];
+    int nk = h_act_k[b] < s2 ? h_act_k[b] : s2;
+    nk = nk < 0 ? 0 : nk;
+    dense += (int64_t)nk * dsa::dense_row(nq, n1);
+  }
+  return dsa::bwd_fixed_bytes(total_rows, batch, topk, sbs, key_rows, d) + 2 * dsa::align256((size_t)dense * 2);
 }
 
 hipError_t launch_sfa_bwd(const SfaBwdArgs& a, hipStream_t s) {
@@ -348,22 +599,34 @@ hipError_t launch_sfa_bwd(const SfaBwdArgs& a, hipStream_t s) {
   hipError_t e = launch_sfa_token_lists(f, base, &tl, s);
   if (e != hipSuccess) return e;
   size_t off = dsa::align256(sfa_token_ws_bytes(f.total_rows > 0 ? f.total_rows : 1, f.topk, f.sbs));
-  dsa::BwdAcc acc;
-  acc.dk = reinterpret_cast<float*>(base + off);
+  dsa::BwdWs w;
+  w.boff = reinterpret_cast<int64_t*>(base + off);
+  off += dsa::align256((size_t)(f.batch + 1) * 8);
+  char* acc0 = base + off;
+  w.dk = reinterpret_cast<float*>(base + off);
   off += dsa::align256((size_t)f.key_rows * f.d * 4);
-  acc.dkr = reinterpret_cast<float*>(base + off);
+  w.dkr = reinterpret_cast<float*>(base + off);
   off += dsa::align256((size_t)f.key_rows * dsa::BDR * 4);
-  acc.dv = reinterpret_cast<float*>(base + off);
+  w.dv = reinterpret_cast<float*>(base + off);
   off += dsa::align256((size_t)f.key_rows * f.d * 4);
-  // the three accumulators are contiguous up to the 256-byte padding: clear the span
-  const int64_t n4 = (int64_t)((off - (reinterpret_cast<char*>(acc.dk) - base)) / 16);
-  if (n4 > 0) {
-    const int blocks = (int)((n4 + 255) / 256 < 4096 ? (n4 + 255) / 256 : 4096);
-    hipLaunchKernelGGL(dsa::sfa_bwd_zero_kernel, dim3(blocks), dim3(256), 0, s,
-                       reinterpret_cast<float4*>(acc.dk), n4);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-  }
-  return f.io == dsa::IO_BF16 ? dsa::launch_bwd_io<dsa::IO_BF16>(a, tl, acc, s)
-                              : dsa::launch_bwd_io<dsa::IO_F16>(a, tl, acc, s);
+  const size_t acc_bytes = (size_t)(base + off - acc0);
+  // the two dense buffers split what is left (256-byte aligned halves)
+  const size_t rest = f.ws_bytes > off ? f.ws_bytes - off : 0;
+  const size_t half = rest / 2 / 256 * 256;
+  w.dst = reinterpret_cast<uint16_t*>(base + off);
+  w.pt = reinterpret_cast<uint16_t*>(base + off + half);
+  w.cap = (int64_t)(half / 2);
+
+  hipLaunchKernelGGL(dsa::sfa_bwd_geo_kernel, dim3(1), dim3(256), 0, s, f, w);
+  const int zb = 2048;
+  hipLaunchKernelGGL(dsa::sfa_bwd_zero_kernel, dim3(zb), dim3(256), 0, s, reinterpret_cast<uint4*>(acc0),
+                     (int64_t)(acc_bytes / 16), (const int64_t*)nullptr, (int64_t)0);
+  hipLaunchKernelGGL(dsa::sfa_bwd_zero_kernel, dim3(zb), dim3(256), 0, s, reinterpret_cast<uint4*>(w.dst),
+                     (int64_t)(half / 16), (const int64_t*)(w.boff + f.batch), w.cap);
+  hipLaunchKernelGGL(dsa::sfa_bwd_zero_kernel, dim3(zb), dim3(256), 0, s, reinterpret_cast<uint4*>(w.pt),
+                     (int64_t)(half / 16), (const int64_t*)(w.boff + f.batch), w.cap);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return f.io == dsa::IO_BF16 ? dsa::launch_bwd_io<dsa::IO_BF16>(a, tl, w, s)
+                              : dsa::launch_bwd_io<dsa::IO_F16>(a, tl, w, s);
 }

@@ -12,6 +12,8 @@ kernels through packed-row offsets instead of the reference's de-packing copies
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _host as H
@@ -122,8 +124,15 @@ class GradPlan:
         self.count, self.sbs = count, sparse_block_size
         self.B, self.total_rows, self.N1, self.D, self.Dr, self.S2 = B, total_rows, N1, D, Dr, S2
         self.sparse_mode, self.scale = sparse_mode, float(scale_value)
-        self.ws_bytes = lib.dsa_sfa_bwd_workspace_bytes(total_rows, N1, D, count, sparse_block_size,
+        # host copies of the row offsets and kv lengths size the per-batch dense buffers
+        self.h_row_start = (ctypes.c_int32 * len(row_start))(*row_start)
+        self.h_act_k = (ctypes.c_int32 * len(act_k))(*act_k)
+        self.ws_bytes = lib.dsa_sfa_bwd_workspace_bytes(B, ctypes.cast(self.h_row_start, ctypes.c_void_p),
+                                                        ctypes.cast(self.h_act_k, ctypes.c_void_p), S2,
+                                                        total_rows, N1, D, count, sparse_block_size,
                                                         self.key_rows)
+        if self.ws_bytes == 0:
+            raise ValueError("dsa_sfa_bwd_workspace_bytes rejected the shapes")
         self.ws = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=dev)
         self.d_row_start = H.i32(row_start, dev)
         self.d_key_start = H.i32(key_start if key_start else [0], dev)
@@ -134,7 +143,8 @@ class GradPlan:
         _lib.check(self.lib.dsa_sfa_bwd(
             self.q.data_ptr(), self.qr.data_ptr(), self.kk.data_ptr(), self.kr.data_ptr(), self.io,
             self.si.data_ptr(), self.count, self.sbs, self.d_row_start.data_ptr(),
-            self.d_key_start.data_ptr(), self.d_aq.data_ptr(), self.d_ak.data_ptr(), self.B,
+            self.d_key_start.data_ptr(), self.d_aq.data_ptr(), self.d_ak.data_ptr(),
+            ctypes.cast(self.h_row_start, ctypes.c_void_p), ctypes.cast(self.h_act_k, ctypes.c_void_p), self.B,
             self.total_rows, self.N1, self.D, self.Dr, self.S2, self.key_rows, self.sparse_mode,
             self.scale, self.do.data_ptr(), self.o.data_ptr(), self.sm_max.data_ptr(),
             self.sm_sum.data_ptr(), self.dq.data_ptr(), self.dqr.data_ptr(), self.dk.data_ptr(),

@@ -5,6 +5,7 @@ C2  lightning_indexer BSND 1x8192, N1=64, D=128, k=2048, causal (DeepSeek-V3.2 p
 C3  sparse_flash_attention BSND 1x4096, N1=128, D=512+64, top-k 2048, causal, LSE on
 C4  sparse_flash_attention PA_BSND decode, block 128, B=64, kv lengths U[4096, 32768]
 C5  TND pipeline: lengths {1024, 3000, 6000, 8192}, indexer (64 heads) feeding SFA (128 heads)
+GRAD_PERF  sparse_flash_attention_grad BSND 1x512 over 4096 keys, N1=64, D=512+64, top-k 2048
 
 All shapes are parameters so tests can run scaled-down versions. Tensors are
 drawn with a ``torch.Generator`` (on the CPU for tests, on the device for the
@@ -166,6 +167,19 @@ def sfa_decode_inputs(B=64, N1=128, D=512, Dr=64, block_size=128, len_lo=4096, l
     return SFAInputs(q, kc, kc, si.to(device), qr, krc, 1.0 / math.sqrt(D + Dr), 1, 3,
                      "BSND", "PA_BSND", bt.to(device), None, lens.to(torch.int32).tolist(), block_size,
                      extra=dict(lens=lens))
+
+
+# The reference's SFA backward perf shape (perf_sfa_grad_triton.py:23): B=1, S1=512,
+# S2=4096, N1=64, top-k 2048, D=512 (+64 rope), causal, bf16.
+GRAD_PERF = dict(B=1, S1=512, S2=4096, N1=64, D=512, sparse_count=2048)
+
+
+def sfa_grad_inputs(B=1, S1=512, S2=4096, N1=64, D=512, Dr=64, sparse_count=2048, sparse_mode=3,
+                    dtype=torch.bfloat16, device="cpu", seed=42):
+    """Forward inputs plus a seeded d_out for the backward (value = key)."""
+    fwd = sfa_prefill_inputs(B, S1, S2, N1, D, Dr, sparse_count, 1, sparse_mode, dtype, device, seed)
+    fwd.extra["d_out"] = _randn((B, S1, N1, D), _gen(device, seed + 7), device, dtype)
+    return fwd
 
 
 C5_LENGTHS = (1024, 3000, 6000, 8192)

@@ -150,13 +150,17 @@ int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key,
                 size_t workspace_bytes, int kv_splits, void* stream);
 
 /*
- * Workspace bytes for dsa_sfa_bwd: the token lists of total_rows rows plus fp32
- * accumulators for d_key, d_key_rope and d_value over key_rows key rows. Needs no
- * initialisation. No counterpart in the reference (it allocates its fp32 buffers per
+ * Workspace bytes for dsa_sfa_bwd: the token lists of total_rows rows, fp32
+ * accumulators for d_key, d_key_rope and d_value over key_rows key rows, and two
+ * dense io-dtype buffers of sum_b min(act_k[b], s2) * ceil64(rows_b * N1) elements
+ * (rows_b = host_row_start[b+1] - host_row_start[b]). host_row_start [batch + 1] and
+ * host_act_k [batch] are host copies of the row offsets and kv lengths. Needs no
+ * initialisation. No counterpart in the reference (it allocates its buffers per
  * call, sparse_flash_attention_grad_triton.py:634-642).
  */
-size_t dsa_sfa_bwd_workspace_bytes(int total_rows, int n1, int d, int sparse_count,
-                                   int sparse_block_size, int64_t key_rows);
+size_t dsa_sfa_bwd_workspace_bytes(int batch, const int32_t* host_row_start,
+                                   const int32_t* host_act_k, int s2, int total_rows, int n1, int d,
+                                   int sparse_count, int sparse_block_size, int64_t key_rows);
 
 /*
  * Sparse flash attention backward, MLA-absorb (replaces _sfa_grad_core,
@@ -173,18 +177,21 @@ size_t dsa_sfa_bwd_workspace_bytes(int total_rows, int n1, int d, int sparse_cou
  * d_query / d_query_rope are [total_rows, N1, D|Dr]; d_key / d_key_rope / d_value are
  * [key_rows, D|Dr] over the whole key tensors (rows no query selects are zero); all in
  * the io dtype, accumulated in fp32. The order of the fp32 additions into a key row is
- * not fixed (the reference's deterministic=False contract).
+ * not fixed (the reference's deterministic=False contract). Key token t of batch b is
+ * key row key_start[b] + t for t < min(act_k[b], s2).
+ *   host_row_start / host_act_k: host copies of row_start / act_k (same values).
  *   workspace: >= dsa_sfa_bwd_workspace_bytes(...) bytes; calls sharing it must be
  *   ordered on one stream.
  */
 int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, const void* key_rope,
                 int io_dtype, const int32_t* sparse_indices, int sparse_count,
                 int sparse_block_size, const int32_t* row_start, const int32_t* key_start,
-                const int32_t* act_q, const int32_t* act_k, int batch, int total_rows, int n1,
-                int d, int dr, int s2, int64_t key_rows, int sparse_mode, float scale,
-                const void* d_out, const void* out, const float* sm_max, const float* sm_sum,
-                void* d_query, void* d_query_rope, void* d_key, void* d_key_rope, void* d_value,
-                void* workspace, size_t workspace_bytes, void* stream);
+                const int32_t* act_q, const int32_t* act_k, const int32_t* host_row_start,
+                const int32_t* host_act_k, int batch, int total_rows, int n1, int d, int dr, int s2,
+                int64_t key_rows, int sparse_mode, float scale, const void* d_out, const void* out,
+                const float* sm_max, const float* sm_sum, void* d_query, void* d_query_rope,
+                void* d_key, void* d_key_rope, void* d_value, void* workspace,
+                size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

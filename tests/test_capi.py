@@ -119,22 +119,29 @@ def test_grad_validation_matches_reference():
         sparse_flash_attention_grad(q, k, k, si, q, q, sm, sm, query_rope=qr, key_rope=kr)
     lib = _lib.load()
     p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
-    base = [p, p, p, p, 1, p, 64, 1, p, p, p, p, 1, 4, 8, 512, 64, 128, 128, 3, 0.04,
+    hrs = (ctypes.c_int32 * 2)(0, 4)
+    hak = (ctypes.c_int32 * 1)(128)
+    hp = lambda x: ctypes.cast(x, ctypes.c_void_p)
+    base = [p, p, p, p, 1, p, 64, 1, p, p, p, p, hp(hrs), hp(hak), 1, 4, 8, 512, 64, 128, 128, 3, 0.04,
             p, p, p, p, p, p, p, p, p, p, 1 << 30, None]
     bad = list(base)
-    bad[15] = 64
+    bad[17] = 64
     assert lib.dsa_sfa_bwd(*bad) == _lib.DSA_ERR_INVALID and b"D must be one of" in lib.dsa_last_error()
     bad = list(base)
-    bad[14] = 12
+    bad[16] = 12
     assert lib.dsa_sfa_bwd(*bad) == _lib.DSA_ERR_INVALID and b"N1 must be one of" in lib.dsa_last_error()
     bad = list(base)
-    bad[31] = 16
+    bad[33] = 16
     assert lib.dsa_sfa_bwd(*bad) == _lib.DSA_ERR_INVALID and b"workspace" in lib.dsa_last_error()
     bad = list(base)
-    bad[21] = None
+    bad[23] = None
     assert lib.dsa_sfa_bwd(*bad) == _lib.DSA_ERR_INVALID and b"null pointer" in lib.dsa_last_error()
-    need = lib.dsa_sfa_bwd_workspace_bytes(4, 8, 512, 64, 1, 128)
-    assert need >= 128 * (512 + 64 + 512) * 4 and need < (1 << 30)
+    bad = list(base)
+    bad[12] = None
+    assert lib.dsa_sfa_bwd(*bad) == _lib.DSA_ERR_INVALID and b"null pointer" in lib.dsa_last_error()
+    need = lib.dsa_sfa_bwd_workspace_bytes(1, hp(hrs), hp(hak), 128, 4, 8, 512, 64, 1, 128)
+    # accumulators (128 key rows x (512 + 64 + 512) fp32) + two dense 128 x 64 buffers
+    assert need >= 128 * (512 + 64 + 512) * 4 + 2 * 128 * 64 * 2 and need < (1 << 30)
 
 
 def test_missing_library_fails_loudly(tmp_path):
