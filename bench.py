@@ -212,6 +212,14 @@ def pmc_pass(torch, W):
                       **si.kwargs()).run()
         torch.cuda.synchronize()
         del si
+    from dsa_triton_ascend_amd import sparse_flash_attention
+    from dsa_triton_ascend_amd.sparse_flash_attention_grad import GradPlan
+    g = W.sfa_grad_inputs(device="cuda:0", seed=42, **W.GRAD_PERF)
+    out, smax, ssum = sparse_flash_attention(g.query, g.key, g.key, g.sparse_indices, **g.kwargs())
+    GradPlan(g.query, g.key, g.key, g.sparse_indices, g.extra["d_out"], out, smax, ssum,
+             scale_value=g.scale_value, query_rope=g.query_rope, key_rope=g.key_rope,
+             sparse_mode=g.sparse_mode).run()
+    torch.cuda.synchronize()
     log("[pmc-pass] done")
 
 
