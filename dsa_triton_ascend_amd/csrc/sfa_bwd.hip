@@ -37,8 +37,8 @@
 //       * dQ[head, col] += dS K, each wave owning a quarter of the 32-column
 //         blocks, the K operand read with ds_read_b64_tr_b16 from the tile;
 //  4. sfa_bwd_gemm_kernel (twice: d_key | d_key_rope, d_value) -- 128 x BN
-//     output tiles per batch on v_mfma_f32_32x32x16, the k-range split over
-//     work-groups when the tiles alone do not fill the GPU; partial tiles are
+//     output tiles per batch on v_mfma_f32_32x32x16 (two work-groups per CU),
+//     the k-range split over work-groups when the tiles alone do not fill the GPU; partial tiles are
 //     added into fp32 accumulators with global atomics (so the last bits may
 //     differ from run to run, the reference's deterministic=False contract,
 //     sparse_flash_attention_grad_triton.py:550);
@@ -167,6 +167,7 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
   __shared__ __attribute__((aligned(16))) uint16_t dSs[BH * C::PP];   // [head][token]
   __shared__ float part[BWV][16][64];   // S^T / dP^T k-range partials, MFMA layout
   __shared__ int s_tok[BT];             // the tile's token index within the batch (-1: none)
+  __shared__ int s_idr[4][BT];          // token-id ring: the ids of tile t in slot t % 4
   __shared__ float s_m[BH], s_il[BH], s_dl[BH];
 
   const SfaArgs& f = a.f;
@@ -250,42 +251,57 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
   const float sl2 = f.scale * BLOG2E;
 
   // ---- gathers of a tile's [nope | rope] rows into registers (rows outside the key
-  // tensors and slots past the list are zero); the next tile's are in flight while
-  // the current one is computed
+  // tensors and slots past the list are zero), two register sets: the next two
+  // tiles' rows are in flight while one is computed
   constexpr int KCH = BT * (C::DT / 8) / (BWV * 64);   // 16-byte chunks per thread
   static_assert(KCH * BWV * 64 == BT * (C::DT / 8), "tile splits evenly");
-  uint4 kreg[KCH];
-  int ptok = -1;
-  auto gather = [&](int t0) {
+  uint4 ka[KCH], kbr[KCH];
+  int pa = -1, pb = -1;
+  auto gather = [&](int t0, uint4 (&kreg)[KCH], int& ptok) __attribute__((always_inline)) {
     const int nvt = ntok - t0 < BT ? ntok - t0 : BT;
+    const int* ids = s_idr[(t0 / BT) & 3];
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
       const int idx = tid + BWV * 64 * i;
       const int t = idx / (C::DT / 8), c = (idx % (C::DT / 8)) * 8;
-      const int p = t < nvt ? toks[t0 + t] : -1;
+      const int p = t < nvt ? ids[t] : -1;
       uint4 v = z4;
       if ((uint32_t)p < (uint32_t)krows)
         v = c < D ? ldg16(kb + (int64_t)p * D + c) : ldg16(krb + (int64_t)p * BDR + (c - D));
       kreg[i] = v;
     }
     if (tid < BT) {
-      const int p = tid < nvt ? toks[t0 + tid] : -1;
+      const int p = tid < nvt ? ids[tid] : -1;
       const int tb = p - g.ks;   // token index within the batch
       ptok = dense_ok && (uint32_t)p < (uint32_t)krows && tb >= 0 && tb < g.nk ? tb : -1;
     }
   };
-  if (ntok > 0) gather(0);
-
-  for (int t0 = 0; t0 < ntok; t0 += BT) {
+  // The token ids reach the gathers through the LDS ring s_idr: threads < 32 load
+  // the ids of tile t+4 during tile t (before that tile's row loads, so waiting
+  // for them never waits for rows) and publish them at the start of tile t+1;
+  // the rows of tile t+2 are gathered during tile t from the ids published at
+  // tile t-1. No gather waits on a global id load.
+  int idreg = -1;
+  auto load_ids = [&](int t0) __attribute__((always_inline)) {
+    if (tid < BT) idreg = t0 + tid < ntok ? toks[t0 + tid] : -1;
+  };
+  // one tile: its rows from the register set `kreg` to LDS, then that set is
+  // refilled with the rows two tiles ahead. Barriers order LDS only (lds_barrier):
+  // a full __syncthreads() would also wait for the gathers in flight.
+  auto tile = [&](int t0, uint4 (&kreg)[KCH], int& ptok) __attribute__((always_inline)) {
     const int nv = ntok - t0 < BT ? ntok - t0 : BT;
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
       const int idx = tid + BWV * 64 * i;
       *reinterpret_cast<uint4*>(&Ks[(idx / (C::DT / 8)) * C::QP + (idx % (C::DT / 8)) * 8]) = kreg[i];
     }
-    if (tid < BT) s_tok[tid] = ptok;
-    __syncthreads();
-    if (t0 + BT < ntok) gather(t0 + BT);
+    if (tid < BT) {
+      s_tok[tid] = ptok;
+      s_idr[(t0 / BT + 3) & 3][tid] = idreg;   // ids of tile t+3, loaded during tile t-1
+    }
+    lds_barrier();
+    load_ids(t0 + 4 * BT);
+    if (t0 + 2 * BT < ntok) gather(t0 + 2 * BT, kreg, ptok);
 
     // ---- S^T (waves 0, 1: halves of the [nope | rope] k-range) and dP^T (waves 2,
     // 3: halves of the nope range), tokens as M, heads as N
@@ -302,7 +318,7 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
 #pragma unroll
       for (int i = 0; i < 16; ++i) part[wave][i][lane] = sacc[i];
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- P and dS of the tile (fp32 -> io dtype): dS to LDS as [head][token] for
     // dQ, both to the dense buffers (a store group = 32 heads of one token)
@@ -326,7 +342,7 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
         w.pt[di] = from_f32<IO>(p);
       }
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- dQ[head, col] += dS[head, token] K[token, col]   (this wave's column blocks)
 #pragma unroll
@@ -340,7 +356,17 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
         }
       }
     }
-    __syncthreads();   // the next tile overwrites Ks, dSs and s_tok
+    lds_barrier();   // the next tile overwrites Ks, dSs and s_tok
+  };
+  // prologue: the ids of tiles 0-2 straight to the ring, tile 3's into idreg
+  if (tid < 3 * BT) s_idr[tid / BT][tid % BT] = tid < ntok ? toks[tid] : -1;
+  load_ids(3 * BT);
+  lds_barrier();
+  if (ntok > 0) gather(0, ka, pa);
+  if (ntok > BT) gather(BT, kbr, pb);
+  for (int t0 = 0; t0 < ntok; t0 += 2 * BT) {
+    tile(t0, ka, pa);
+    if (t0 + BT < ntok) tile(t0 + BT, kbr, pb);
   }
 
   // ---- d_query | d_query_rope of the block's heads (zeros for rows without tokens)
@@ -373,7 +399,7 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
 // accumulators (rows t < nk of the batch).
 template <int IO, int D, bool KV, int NB>
 __device__ __forceinline__ void gemm_tile(const SfaBwdArgs& a, const BwdWs& w, int ksplit, int xt,
-                                          uint16_t (*As)[GBM * (GBK + 8)], uint16_t* Bs0) {
+                                          uint16_t* As, uint16_t* Bs) {
   constexpr int N = KV ? D : D + BDR;
   constexpr int BN = 64 * NB;
   constexpr int NT = N / BN;
@@ -383,14 +409,16 @@ __device__ __forceinline__ void gemm_tile(const SfaBwdArgs& a, const BwdWs& w, i
   constexpr int ACH = GBM * GBK / 8 / 256;   // 16-byte A chunks per thread per k-step
   constexpr int BCH = GBK * BN / 8 / 256;    // B chunks
   static_assert(ACH * 256 * 8 == GBM * GBK && BCH * 256 * 8 == GBK * BN, "tiles split evenly");
-  uint16_t* Bs[2] = {Bs0, Bs0 + GBK * BP};
-
   const SfaArgs& f = a.f;
   const int b = blockIdx.y;
   const BatchGeo g = batch_geo(f, b);
-  const int mt = xt / NT, nt = xt % NT;
+  // xt -> (m-tile, n-tile): the NT tiles of an m-tile get x values 8 apart, so with
+  // round-robin dispatch over the 8 XCDs they run on one XCD and share its L2 copy
+  // of the A rows
+  const int grp = xt / (8 * NT), rem = xt % (8 * NT);
+  const int nt = rem / 8, mt = grp * 8 + rem % 8;
   const int m0 = mt * GBM;
-  if (m0 >= g.nk || w.boff[b + 1] > w.cap) return;
+  if (nt >= NT || m0 >= g.nk || w.boff[b + 1] > w.cap) return;
   const int kper = ((g.kp + ksplit - 1) / ksplit + GBK - 1) / GBK * GBK;
   const int kbeg = blockIdx.z * kper;
   const int kend = kbeg + kper < g.kp ? kbeg + kper : g.kp;
@@ -428,16 +456,16 @@ __device__ __forceinline__ void gemm_tile(const SfaBwdArgs& a, const BwdWs& w, i
       rb[i] = v;
     }
   };
-  auto store = [&](int buf) {
+  auto store = [&]() {
 #pragma unroll
     for (int i = 0; i < ACH; ++i) {
       const int c = tid + 256 * i;
-      *reinterpret_cast<uint4*>(&As[buf][(c / (GBK / 8)) * AP + (c % (GBK / 8)) * 8]) = ra[i];
+      *reinterpret_cast<uint4*>(&As[(c / (GBK / 8)) * AP + (c % (GBK / 8)) * 8]) = ra[i];
     }
 #pragma unroll
     for (int i = 0; i < BCH; ++i) {
       const int c = tid + 256 * i;
-      *reinterpret_cast<uint4*>(&Bs[buf][(c / (BN / 8)) * BP + (c % (BN / 8)) * 8]) = rb[i];
+      *reinterpret_cast<uint4*>(&Bs[(c / (BN / 8)) * BP + (c % (BN / 8)) * 8]) = rb[i];
     }
   };
 
@@ -449,30 +477,26 @@ __device__ __forceinline__ void gemm_tile(const SfaBwdArgs& a, const BwdWs& w, i
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
+  // one LDS stage, the next k-step in registers: two work-groups share a CU, so one
+  // computes while the other waits on its loads; barriers order LDS only
   load(kbeg);
-  store(0);
-  __syncthreads();
-  int buf = 0;
   for (int k0 = kbeg; k0 < kend; k0 += GBK) {
-    const bool more = k0 + GBK < kend;
-    if (more) load(k0 + GBK);   // in flight while this step's MFMAs run
+    lds_barrier();   // the previous step's LDS reads are done
+    store();
+    lds_barrier();
+    if (k0 + GBK < kend) load(k0 + GBK);   // in flight while this step's MFMAs run
 #pragma unroll
     for (int s = 0; s < GBK / 16; ++s) {
       uint4 af[2], bfr[NB];
 #pragma unroll
       for (int i = 0; i < 2; ++i)
-        af[i] = *reinterpret_cast<const uint4*>(&As[buf][(64 * wm + 32 * i + (lane & 31)) * AP + s * 16 + (lane >> 5) * 8]);
+        af[i] = *reinterpret_cast<const uint4*>(&As[(64 * wm + 32 * i + (lane & 31)) * AP + s * 16 + (lane >> 5) * 8]);
 #pragma unroll
-      for (int j = 0; j < NB; ++j) bfr[j] = tr_frag(Bs[buf], BP, 32 * NB * wn + 32 * j, s * 16, lane);
+      for (int j = 0; j < NB; ++j) bfr[j] = tr_frag(Bs, BP, 32 * NB * wn + 32 * j, s * 16, lane);
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < NB; ++j) acc[i][j] = Mfma<IO>::m32(af[i], bfr[j], acc[i][j]);
-    }
-    if (more) {
-      store(buf ^ 1);
-      __syncthreads();
-      buf ^= 1;
     }
   }
 
@@ -493,19 +517,20 @@ __device__ __forceinline__ void gemm_tile(const SfaBwdArgs& a, const BwdWs& w, i
 }
 
 // n-tile widths (in 64-column units) of the two GEMMs: d_key | d_key_rope spans
-// D + 64 columns (3, 5, 9 units), d_value D (2, 4, 8)
+// D + 64 columns (3, 5, 9 units), d_value D (2, 4, 8); at most 3 units so the
+// accumulators leave room for two work-groups per CU
 template <int D> struct GemmNB;
 template <> struct GemmNB<128> { static constexpr int K = 3, V = 2; };
-template <> struct GemmNB<256> { static constexpr int K = 5, V = 4; };
-template <> struct GemmNB<512> { static constexpr int K = 3, V = 4; };
+template <> struct GemmNB<256> { static constexpr int K = 1, V = 2; };
+template <> struct GemmNB<512> { static constexpr int K = 3, V = 2; };
 
 // One product per launch (d_key | d_key_rope, then d_value): each instance gets only
 // the registers its tile needs.
 template <int IO, int D, bool KV>
-__global__ __launch_bounds__(256) void sfa_bwd_gemm_kernel(SfaBwdArgs a, BwdWs w, int ksplit) {
+__global__ __launch_bounds__(256, 2) void sfa_bwd_gemm_kernel(SfaBwdArgs a, BwdWs w, int ksplit) {
   constexpr int NB = KV ? GemmNB<D>::V : GemmNB<D>::K;
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][GBM * (GBK + 8)];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[2 * GBK * (64 * NB + 8)];
+  __shared__ __attribute__((aligned(16))) uint16_t As[GBM * (GBK + 8)];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[GBK * (64 * NB + 8)];
   gemm_tile<IO, D, KV, NB>(a, w, ksplit, blockIdx.x, As, Bs);
 }
 
@@ -526,18 +551,22 @@ hipError_t launch_bwd_d(const SfaBwdArgs& a, const SfaTokenLists& tl, const BwdW
     hipLaunchKernelGGL((sfa_bwd_rows_kernel<IO, D>), grid, dim3(BWV * 64), 0, s, a, tl, w);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    // GEMM grid: every (m-tile, n-tile) of the largest batch; the k-range is split
-    // until about 640 work-groups are in flight
+    // GEMM grid: every (m-tile, n-tile) of the largest batch; the k-range is split so
+    // each product fills about one round of two work-groups per CU
     constexpr int NTK = (D + BDR) / (64 * GemmNB<D>::K), NTV = D / (64 * GemmNB<D>::V);
     const int mts = (f.s2 + GBM - 1) / GBM;
     if (mts > 0) {
-      const int64_t tiles = (int64_t)f.batch * mts * (NTK + NTV);
-      int ksplit = (int)((640 + tiles - 1) / tiles);
-      ksplit = ksplit < 1 ? 1 : (ksplit > 16 ? 16 : ksplit);
-      hipLaunchKernelGGL((sfa_bwd_gemm_kernel<IO, D, false>), dim3(mts * NTK, f.batch, ksplit), dim3(256), 0, s,
-                         a, w, ksplit);
-      hipLaunchKernelGGL((sfa_bwd_gemm_kernel<IO, D, true>), dim3(mts * NTV, f.batch, ksplit), dim3(256), 0, s,
-                         a, w, ksplit);
+      const int mts8 = (mts + 7) / 8 * 8;   // x covers whole groups of 8 m-tiles
+      auto splits = [&](int nt) {
+        const int64_t tiles = (int64_t)f.batch * mts * nt;
+        const int64_t k = 512 / tiles;
+        return (int)(k < 1 ? 1 : (k > 16 ? 16 : k));
+      };
+      const int kk = splits(NTK), kv = splits(NTV);
+      hipLaunchKernelGGL((sfa_bwd_gemm_kernel<IO, D, false>), dim3(mts8 * NTK, f.batch, kk), dim3(256), 0, s,
+                         a, w, kk);
+      hipLaunchKernelGGL((sfa_bwd_gemm_kernel<IO, D, true>), dim3(mts8 * NTV, f.batch, kv), dim3(256), 0, s,
+                         a, w, kv);
       e = hipGetLastError();
       if (e != hipSuccess) return e;
     }
