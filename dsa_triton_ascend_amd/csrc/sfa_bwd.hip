@@ -37,8 +37,9 @@
 //       * dQ[head, col] += dS K, each wave owning a quarter of the 32-column
 //         blocks, the K operand read with ds_read_b64_tr_b16 from the tile;
 //  4. sfa_bwd_gemm_kernel (twice: d_key | d_key_rope, d_value) -- 128 x BN
-//     output tiles per batch on v_mfma_f32_32x32x16 (two work-groups per CU),
-//     the k-range split over work-groups when the tiles alone do not fill the GPU; partial tiles are
+//     output tiles per batch on v_mfma_f32_32x32x16, operands streamed with
+//     direct-to-LDS loads through a 3-stage LDS ring two k-steps ahead, the k-range
+//     split over work-groups when the tiles alone do not fill the GPU; partial tiles are
 //     added into fp32 accumulators with global atomics (so the last bits may
 //     differ from run to run, the reference's deterministic=False contract,
 //     sparse_flash_attention_grad_triton.py:550);
@@ -397,18 +398,21 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
 // four waves as 2 (rows) x 2 (columns), each 64 x 32 NB. xt = m-tile * n-tiles +
 // n-tile, blockIdx.y = batch, blockIdx.z = k-split. Results are added to the fp32
 // accumulators (rows t < nk of the batch).
-template <int IO, int D, bool KV, int NB>
+template <int IO, int D, bool KV, int NB, int NST>
 __device__ __forceinline__ void gemm_tile(const SfaBwdArgs& a, const BwdWs& w, int ksplit, int xt,
-                                          uint16_t* As, uint16_t* Bs) {
+                                          uint8_t* lds) {
   constexpr int N = KV ? D : D + BDR;
   constexpr int BN = 64 * NB;
   constexpr int NT = N / BN;
   static_assert(N % BN == 0, "n-tiles cover the columns");
-  constexpr int AP = GBK + 8;    // A tile pitch (elements)
-  constexpr int BP = BN + 8;     // B tile pitch
-  constexpr int ACH = GBM * GBK / 8 / 256;   // 16-byte A chunks per thread per k-step
-  constexpr int BCH = GBK * BN / 8 / 256;    // B chunks
-  static_assert(ACH * 256 * 8 == GBM * GBK && BCH * 256 * 8 == GBK * BN, "tiles split evenly");
+  constexpr int AP = GBK + 8;          // A tile pitch (elements): 8 data chunks + 1 pad chunk per row
+  constexpr int BP = BN + 8;           // B tile pitch: 8 NB data chunks + 1 pad chunk
+  constexpr int ACR = AP / 8, BCR = BP / 8;            // 16-byte chunk slots per row
+  constexpr int NIA = GBM * ACR / 64, NIB = GBK * BCR / 64;   // 64-slot load instructions per k-step
+  static_assert(NIA * 64 == GBM * ACR && NIB * 64 == GBK * BCR, "slots fill whole instructions");
+  constexpr int NI = NIA + NIB;
+  constexpr int NMIN = NI / BWV;       // loads per wave per k-step, at least
+  constexpr int ABYTES = GBM * AP * 2, STAGE = ABYTES + GBK * BP * 2;
   const SfaArgs& f = a.f;
   const int b = blockIdx.y;
   const BatchGeo g = batch_geo(f, b);
@@ -423,7 +427,8 @@ __device__ __forceinline__ void gemm_tile(const SfaBwdArgs& a, const BwdWs& w, i
   const int kbeg = blockIdx.z * kper;
   const int kend = kbeg + kper < g.kp ? kbeg + kper : g.kp;
   if (kbeg >= kend) return;
-  const int kreal = g.nq * f.n1;   // k past this is padding (zero A, no B row)
+  const int nsteps = (kend - kbeg) / GBK;
+  const int kreal = g.nq * f.n1;   // k past this is padding: zero A columns, B rows clamped
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -432,40 +437,36 @@ __device__ __forceinline__ void gemm_tile(const SfaBwdArgs& a, const BwdWs& w, i
   const uint16_t* bq = reinterpret_cast<const uint16_t*>(KV ? a.d_out : a.f.q);
   const uint16_t* bqr = reinterpret_cast<const uint16_t*>(a.f.qr);
   const int64_t brow0 = (int64_t)g.rs * f.n1;   // B row of k = 0
-  const uint4 z4 = make_uint4(0, 0, 0, 0);
 
-  uint4 ra[ACH], rb[BCH];
-  auto load = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < ACH; ++i) {
-      const int c = tid + 256 * i;
-      const int m = c / (GBK / 8), kk = (c % (GBK / 8)) * 8;
-      const int t = m0 + m;
-      ra[i] = t < g.nk ? ldg16(abuf + (int64_t)t * g.kp + k0 + kk) : z4;
-    }
-#pragma unroll
-    for (int i = 0; i < BCH; ++i) {
-      const int c = tid + 256 * i;
-      const int kk = c / (BN / 8), n = nt * BN + (c % (BN / 8)) * 8;
-      const int k = k0 + kk;
-      uint4 v = z4;
-      if (k < kreal) {
-        const int64_t row = brow0 + k;
-        v = (KV || n < D) ? ldg16(bq + row * D + n) : ldg16(bqr + row * BDR + (n - D));
+  // ---- k-step s goes global -> LDS stage s % NST with direct-to-LDS 16-byte loads:
+  // instruction q of the step fills slots [64 q, 64 q + 64) of the tile (A slots
+  // first, then B), slot = row * chunks-per-row + chunk; the pad chunk of a row
+  // re-reads its chunk 0. Every address is in bounds: A rows past the batch's tokens
+  // read its last token (their outputs are discarded), B rows past the batch's
+  // (row, head) pairs read its last pair (they meet zero A columns). Instructions
+  // are dealt round-robin to the waves; steps past the range re-load the last one,
+  // so each wave issues the same loads every step.
+  auto issue = [&](int step) __attribute__((always_inline)) {
+    const int st = step < nsteps ? step : nsteps - 1;
+    const int k0 = kbeg + st * GBK;
+    uint8_t* stage = lds + (step % NST) * STAGE;
+    for (int q = wave; q < NI; q += BWV) {
+      const int slot = (q < NIA ? q : q - NIA) * 64 + lane;
+      const void* src;
+      if (q < NIA) {
+        const int row = slot / ACR, ch = slot % ACR;
+        int t = m0 + row;
+        t = t < g.nk ? t : g.nk - 1;
+        src = abuf + (int64_t)t * g.kp + k0 + (ch < 8 ? ch : 0) * 8;
+      } else {
+        const int row = slot / BCR, ch = slot % BCR;
+        int k = k0 + row;
+        k = k < kreal ? k : kreal - 1;
+        const int n = nt * BN + (ch < 8 * NB ? ch : 0) * 8;
+        const int64_t r = brow0 + k;
+        src = (KV || n < D) ? (const void*)(bq + r * D + n) : (const void*)(bqr + r * BDR + (n - D));
       }
-      rb[i] = v;
-    }
-  };
-  auto store = [&]() {
-#pragma unroll
-    for (int i = 0; i < ACH; ++i) {
-      const int c = tid + 256 * i;
-      *reinterpret_cast<uint4*>(&As[(c / (GBK / 8)) * AP + (c % (GBK / 8)) * 8]) = ra[i];
-    }
-#pragma unroll
-    for (int i = 0; i < BCH; ++i) {
-      const int c = tid + 256 * i;
-      *reinterpret_cast<uint4*>(&Bs[(c / (BN / 8)) * BP + (c % (BN / 8)) * 8]) = rb[i];
+      lds_dma16_untracked(src, stage + (q < NIA ? q * 1024 : ABYTES + (q - NIA) * 1024));
     }
   };
 
@@ -477,28 +478,32 @@ __device__ __forceinline__ void gemm_tile(const SfaBwdArgs& a, const BwdWs& w, i
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  // one LDS stage, the next k-step in registers: two work-groups share a CU, so one
-  // computes while the other waits on its loads; barriers order LDS only
-  load(kbeg);
-  for (int k0 = kbeg; k0 < kend; k0 += GBK) {
-    lds_barrier();   // the previous step's LDS reads are done
-    store();
-    lds_barrier();
-    if (k0 + GBK < kend) load(k0 + GBK);   // in flight while this step's MFMAs run
 #pragma unroll
-    for (int s = 0; s < GBK / 16; ++s) {
+  for (int s = 0; s < NST - 1; ++s) issue(s);
+  for (int s = 0; s < nsteps; ++s) {
+    // this wave's loads of step s have landed (the later NST - 2 steps may be in
+    // flight), then every wave's (the barrier also ends step s - 1's reads of the
+    // stage that the next issue refills)
+    wait_vmcnt<(NST - 2) * NMIN>();
+    lds_barrier();
+    issue(s + NST - 1);
+    const uint16_t* As = reinterpret_cast<const uint16_t*>(lds + (s % NST) * STAGE);
+    const uint16_t* Bs = reinterpret_cast<const uint16_t*>(lds + (s % NST) * STAGE + ABYTES);
+#pragma unroll
+    for (int ks = 0; ks < GBK / 16; ++ks) {
       uint4 af[2], bfr[NB];
 #pragma unroll
       for (int i = 0; i < 2; ++i)
-        af[i] = *reinterpret_cast<const uint4*>(&As[(64 * wm + 32 * i + (lane & 31)) * AP + s * 16 + (lane >> 5) * 8]);
+        af[i] = *reinterpret_cast<const uint4*>(&As[(64 * wm + 32 * i + (lane & 31)) * AP + ks * 16 + (lane >> 5) * 8]);
 #pragma unroll
-      for (int j = 0; j < NB; ++j) bfr[j] = tr_frag(Bs, BP, 32 * NB * wn + 32 * j, s * 16, lane);
+      for (int j = 0; j < NB; ++j) bfr[j] = tr_frag(Bs, BP, 32 * NB * wn + 32 * j, ks * 16, lane);
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < NB; ++j) acc[i][j] = Mfma<IO>::m32(af[i], bfr[j], acc[i][j]);
     }
   }
+  wait_vmcnt<0>();   // the trailing re-loads land before the work-group's LDS is released
 
   // ---- add the tile to the accumulators (rows past the batch's tokens skipped)
 #pragma unroll
@@ -517,21 +522,26 @@ __device__ __forceinline__ void gemm_tile(const SfaBwdArgs& a, const BwdWs& w, i
 }
 
 // n-tile widths (in 64-column units) of the two GEMMs: d_key | d_key_rope spans
-// D + 64 columns (3, 5, 9 units), d_value D (2, 4, 8); at most 3 units so the
-// accumulators leave room for two work-groups per CU
+// D + 64 columns (3, 5, 9 units), d_value D (2, 4, 8)
 template <int D> struct GemmNB;
 template <> struct GemmNB<128> { static constexpr int K = 3, V = 2; };
-template <> struct GemmNB<256> { static constexpr int K = 1, V = 2; };
-template <> struct GemmNB<512> { static constexpr int K = 3, V = 2; };
+template <> struct GemmNB<256> { static constexpr int K = 5, V = 4; };
+template <> struct GemmNB<512> { static constexpr int K = 3, V = 4; };
+
+// LDS ring depth: three stages (loads two k-steps ahead) when they fit
+template <int NB> struct GemmStages {
+  static constexpr int STAGE = GBM * (GBK + 8) * 2 + GBK * (64 * NB + 8) * 2;
+  static constexpr int NST = 3 * STAGE <= 160 * 1024 ? 3 : 2;
+};
 
 // One product per launch (d_key | d_key_rope, then d_value): each instance gets only
 // the registers its tile needs.
 template <int IO, int D, bool KV>
-__global__ __launch_bounds__(256, 2) void sfa_bwd_gemm_kernel(SfaBwdArgs a, BwdWs w, int ksplit) {
+__global__ __launch_bounds__(256) void sfa_bwd_gemm_kernel(SfaBwdArgs a, BwdWs w, int ksplit) {
   constexpr int NB = KV ? GemmNB<D>::V : GemmNB<D>::K;
-  __shared__ __attribute__((aligned(16))) uint16_t As[GBM * (GBK + 8)];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[GBK * (64 * NB + 8)];
-  gemm_tile<IO, D, KV, NB>(a, w, ksplit, blockIdx.x, As, Bs);
+  using S = GemmStages<NB>;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[S::NST * S::STAGE];
+  gemm_tile<IO, D, KV, NB, S::NST>(a, w, ksplit, blockIdx.x, lds);
 }
 
 // fp32 accumulator -> io dtype, 4 elements per step (every length is a multiple of 4)
@@ -552,14 +562,14 @@ hipError_t launch_bwd_d(const SfaBwdArgs& a, const SfaTokenLists& tl, const BwdW
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     // GEMM grid: every (m-tile, n-tile) of the largest batch; the k-range is split so
-    // each product fills about one round of two work-groups per CU
+    // each product fills about one round of one work-group per CU
     constexpr int NTK = (D + BDR) / (64 * GemmNB<D>::K), NTV = D / (64 * GemmNB<D>::V);
     const int mts = (f.s2 + GBM - 1) / GBM;
     if (mts > 0) {
       const int mts8 = (mts + 7) / 8 * 8;   // x covers whole groups of 8 m-tiles
       auto splits = [&](int nt) {
         const int64_t tiles = (int64_t)f.batch * mts * nt;
-        const int64_t k = 512 / tiles;
+        const int64_t k = 256 / tiles;
         return (int)(k < 1 ? 1 : (k > 16 ? 16 : k));
       };
       const int kk = splits(NTK), kv = splits(NTV);
