@@ -70,6 +70,43 @@ int dsa_li_score(const void* query, const void* key, const void* weights, int io
   return hip_status(launch_li_score(a, (hipStream_t)stream), "dsa_li_score launch");
 }
 
+int dsa_li_score_paged(const void* query, const void* key_cache, const void* weights, int io_dtype,
+                       int w_dtype, const int32_t* row_start, const int32_t* block_table,
+                       int max_blocks, int page_block_size, int64_t key_rows, const int32_t* act_q,
+                       const int32_t* act_k, int batch, int total_rows, int n1, int n2, int d,
+                       int max_rows_per_batch, int max_kv, int sparse_mode, uint16_t* scores,
+                       int64_t score_ld, void* stream) {
+  if (!query || !key_cache || !weights || !row_start || !block_table || !act_q || !act_k || !scores)
+    return fail(DSA_ERR_INVALID, "dsa_li_score_paged: null pointer argument");
+  if (max_blocks <= 0 || page_block_size <= 0 || key_rows <= 0)
+    return fail(DSA_ERR_INVALID, "dsa_li_score_paged: max_blocks, page_block_size and key_rows must be positive");
+  if (max_blocks > LI_MAX_BLOCKS)
+    return fail(DSA_ERR_UNSUPPORTED, "dsa_li_score_paged: max_blocks=%d > %d", max_blocks, LI_MAX_BLOCKS);
+  const int64_t s2 = (int64_t)max_blocks * page_block_size;
+  if (s2 > 65536) return fail(DSA_ERR_UNSUPPORTED, "dsa_li_score_paged: max_blocks*block_size > 65536");
+  if (!is16(io_dtype)) return fail(DSA_ERR_INVALID, "dsa_li_score_paged: io_dtype must be fp16 or bf16");
+  if (!is16(w_dtype) && w_dtype != DSA_DTYPE_F32)
+    return fail(DSA_ERR_INVALID, "dsa_li_score_paged: weights dtype must be fp16, bf16 or fp32");
+  if (batch <= 0 || total_rows < 0 || n1 <= 0 || n2 <= 0 || max_rows_per_batch < 0)
+    return fail(DSA_ERR_INVALID, "dsa_li_score_paged: non-positive shape");
+  if (n1 % n2 != 0) return fail(DSA_ERR_INVALID, "N1(%d) must be divisible by N2(%d)", n1, n2);
+  if (n1 / n2 > 128) return fail(DSA_ERR_UNSUPPORTED, "dsa_li_score_paged: group size N1/N2=%d > 128", n1 / n2);
+  if (!li_score_supported_d(d))
+    return fail(DSA_ERR_UNSUPPORTED, "dsa_li_score_paged: D=%d not in {64, 96, 128, 256, 512}", d);
+  if (sparse_mode != 0 && sparse_mode != 3)
+    return fail(DSA_ERR_INVALID, "dsa_li_score_paged: sparse_mode must be 0 or 3");
+  if (score_ld < s2) return fail(DSA_ERR_INVALID, "dsa_li_score_paged: score_ld < max_blocks*block_size");
+  if (batch > 65535 || n2 > 65535) return fail(DSA_ERR_UNSUPPORTED, "dsa_li_score_paged: batch or N2 > 65535");
+  LiScoreArgs a{query, key_cache, weights, io_dtype, w_dtype, row_start, act_q, act_q, act_k,
+                batch, total_rows, n1, n2, d, (int)s2, max_rows_per_batch, max_kv, sparse_mode,
+                scores, score_ld};
+  a.block_table = block_table;
+  a.max_blocks = max_blocks;
+  a.page_bs = page_block_size;
+  a.key_rows = key_rows;
+  return hip_status(launch_li_score(a, (hipStream_t)stream), "dsa_li_score_paged launch");
+}
+
 int dsa_li_topk(const uint16_t* scores, int64_t score_ld, int io_dtype, const int32_t* row_start,
                 const int32_t* act_q, const int32_t* act_k, int batch, int total_rows, int n2,
                 int s2, int sparse_mode, int sparse_count, int32_t* indices, uint16_t* values,

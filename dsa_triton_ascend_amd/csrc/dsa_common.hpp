@@ -195,7 +195,11 @@ struct LiScoreArgs {
   const int32_t* row_start; const int32_t* key_start; const int32_t* act_q; const int32_t* act_k;
   int batch, total_rows, n1, n2, d, s2, max_rows_per_batch, max_kv, sparse_mode;
   uint16_t* scores; int64_t ld;
+  // PA_BSND keys (block_table != nullptr): token t of batch b is row
+  // block_table[b * max_blocks + t / page_bs] * page_bs + t % page_bs of `k`
+  const int32_t* block_table = nullptr; int max_blocks = 0; int page_bs = 0; int64_t key_rows = 0;
 };
+constexpr int LI_MAX_BLOCKS = 4096;   // block-table row held in LDS by the paged score kernel
 struct LiTopkArgs {
   const uint16_t* scores; int64_t ld; int io;
   const int32_t* row_start; const int32_t* act_q; const int32_t* act_k;

@@ -81,13 +81,14 @@ __device__ __forceinline__ int visible_len(int s1, int aq, int ak, int S2, int m
   return L < 0 ? 0 : L;
 }
 
-template <int IO, int D, int MT>
+template <int IO, int D, int MT, bool PAGED>
 __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
   using T = LiTile<D>;
   constexpr int KK = D / 16;                 // MFMA k-steps
   constexpr int NSUB = T::BN / 32;           // 32-key subtiles per tile
   constexpr bool QREG = MT <= 2 && MT * D <= 512;   // Q fragments resident in VGPRs
   __shared__ __attribute__((aligned(16))) uint16_t kt[T::NBUF][T::BN * D];
+  __shared__ int bt_s[PAGED ? LI_MAX_BLOCKS : 1];   // PA_BSND: the batch's block-table row
 
   const int lane = threadIdx.x & 63;
   // wave index in an SGPR: every per-row bound below is then wave-uniform and
@@ -114,8 +115,29 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
 
   const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.q) + (r * a.n1 + (int64_t)n2 * G) * D;
   const uint16_t* kbase = reinterpret_cast<const uint16_t*>(a.k) +
-                          ((int64_t)a.key_start[b] * a.n2 + n2) * D;
+                          ((PAGED ? 0 : (int64_t)a.key_start[b]) * a.n2 + n2) * D;
   const int64_t kstride = (int64_t)a.n2 * D;
+  // PA_BSND: the block-table entries of the visible keys go to LDS first (one
+  // round trip before the first K loads); key t then reads physical row
+  // bt[t / page] * page + t % page, and a -1 block (or one past the cache) reads
+  // row 0 and its score is written as 0 -- a zero key row, as the reference's
+  // de-paging produces (sparse_flash_attention_triton.py:1012-1033)
+  const int page = PAGED ? a.page_bs : 1;
+  const int pshift = PAGED && (page & (page - 1)) == 0 ? __builtin_ctz((unsigned)page) : -1;
+  auto block_of = [&](int t) { return pshift >= 0 ? t >> pshift : t / page; };
+  auto phys_row = [&](int t, bool& ok) -> int64_t {
+    const int bi = block_of(t);
+    const int blk = bt_s[bi];
+    const int64_t p = (int64_t)blk * page + (t - bi * page);
+    ok = blk >= 0 && p < a.key_rows;
+    return ok ? p : 0;
+  };
+  if constexpr (PAGED) {
+    const int nb = block_of(L_blk - 1) + 1;
+    for (int i = threadIdx.x; i < nb; i += NW * 64)
+      bt_s[i] = i < a.max_blocks ? a.block_table[(int64_t)b * a.max_blocks + i] : -1;
+    __syncthreads();
+  }
 
   // ---- K tile staging (started first so its latency overlaps the Q / w loads).
   // Direct-to-LDS load j of wave w fills the 64 slots [64 i, 64 i + 64) of a
@@ -134,7 +156,12 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
       const int c = (slot % T::CPR) ^ (k & T::SWZ);
       int s2 = tile * T::BN + k;
       s2 = s2 < L_blk ? s2 : L_blk - 1;
-      lds_dma16_untracked(kbase + (int64_t)s2 * kstride + c * 8, buf + i * 512);
+      int64_t row = s2;
+      if constexpr (PAGED) {
+        bool ok;
+        row = phys_row(s2, ok);
+      }
+      lds_dma16_untracked(kbase + row * kstride + c * 8, buf + i * 512);
     }
   };
 #pragma unroll
@@ -201,9 +228,16 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
     for (int m = 0; m < NSLOT; m += 2) {
       const bool hi = lane >= 32;
       const int k0 = (hi && m + 1 < NSLOT) ? pk[m + 1] : (hi ? -1 : pk[m]);
-      const float v = (hi && m + 1 < NSLOT) ? pv[m + 1] : pv[m];
+      float v = (hi && m + 1 < NSLOT) ? pv[m + 1] : pv[m];
       const int s2 = k0 + (lane & 31);
-      if (k0 >= 0 && s2 < L_row) srow[s2] = from_f32<IO>(v);
+      if (k0 >= 0 && s2 < L_row) {
+        if constexpr (PAGED) {
+          bool ok;
+          phys_row(s2, ok);
+          v = ok ? v : 0.f;
+        }
+        srow[s2] = from_f32<IO>(v);
+      }
     }
 #pragma unroll
     for (int i = 0; i < NSLOT; ++i) pk[i] = -1;
@@ -312,14 +346,22 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
   wait_vmcnt<0>();   // no direct-to-LDS load may outlive the work-group's LDS
 }
 
+template <int IO, int D, bool PAGED>
+void launch_mt(const LiScoreArgs& a, hipStream_t s, int MT, dim3 grid, dim3 block) {
+  switch (MT) {
+    case 1: hipLaunchKernelGGL((li_score_kernel<IO, D, 1, PAGED>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((li_score_kernel<IO, D, 2, PAGED>), grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL((li_score_kernel<IO, D, 4, PAGED>), grid, block, 0, s, a); break;
+  }
+}
+
 template <int IO, int D>
 hipError_t launch_d(const LiScoreArgs& a, hipStream_t s, int MT) {
   dim3 grid((a.max_rows_per_batch + NW - 1) / NW, a.n2, a.batch), block(NW * 64);
-  switch (MT) {
-    case 1: hipLaunchKernelGGL((li_score_kernel<IO, D, 1>), grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL((li_score_kernel<IO, D, 2>), grid, block, 0, s, a); break;
-    default: hipLaunchKernelGGL((li_score_kernel<IO, D, 4>), grid, block, 0, s, a); break;
-  }
+  if (a.block_table)
+    launch_mt<IO, D, true>(a, s, MT, grid, block);
+  else
+    launch_mt<IO, D, false>(a, s, MT, grid, block);
   return hipGetLastError();
 }
 

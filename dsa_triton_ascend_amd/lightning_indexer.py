@@ -35,11 +35,14 @@ class IndexerPlan:
     def __init__(self, query, key, weights, actual_seq_lengths_query=None,
                  actual_seq_lengths_key=None, block_table=None, layout_query="BSND",
                  layout_key="BSND", sparse_count=2048, sparse_mode=3, return_value=False):
-        if block_table is not None:
+        is_pa = layout_key == "PA_BSND"
+        if block_table is not None and not is_pa:
             raise ValueError("PA_BSND / block_table not supported in triton lightning_indexer")
-        if layout_query not in ("BSND", "TND") or layout_key not in ("BSND", "TND"):
+        if is_pa and block_table is None:
+            raise ValueError("PA_BSND requires block_table")
+        if layout_query not in ("BSND", "TND") or layout_key not in ("BSND", "TND", "PA_BSND"):
             raise ValueError(f"unsupported layout {layout_query}/{layout_key}")
-        dev = H.require_device(query, key, weights)
+        dev = H.require_device(query, key, weights, block_table)
         self.lib = _lib.load()
         self.io = H.dtype_code(query.dtype, "query")
         if key.dtype != query.dtype:
@@ -53,7 +56,9 @@ class IndexerPlan:
             row_start = H.prefix(act_q)
             if row_start[-1] > T1:
                 raise ValueError("actual_seq_lengths_query exceeds the packed query length")
-            if layout_key == "TND":
+            if is_pa:
+                act_k = None   # per batch, not cumulative: set below
+            elif layout_key == "TND":
                 if sum(act_k) > key.shape[0]:
                     raise ValueError("actual_seq_lengths_key exceeds the packed key length")
                 N2 = key.shape[1]
@@ -66,13 +71,27 @@ class IndexerPlan:
             out_lead = (T1,)
         else:
             B, S1, N1, D = query.shape
-            _, S2, N2, _ = key.shape
             act_q = H.host_lengths(actual_seq_lengths_query, B, S1)
-            act_k = H.host_lengths(actual_seq_lengths_key, B, S2)
+            if not is_pa:
+                _, S2, N2, _ = key.shape
+                act_k = H.host_lengths(actual_seq_lengths_key, B, S2)
+                key_start = [b * S2 for b in range(B)]
             row_start = [b * S1 for b in range(B + 1)]
-            key_start = [b * S2 for b in range(B)]
             total_rows = B * S1
             out_lead = (B, S1)
+        self.d_bt, self.max_blocks, self.page_bs, self.key_rows = None, 0, 0, 0
+        if is_pa:
+            # key cache [num_blocks, page, N2, D]; kv lengths per batch (as the SFA
+            # forward's PA_BSND); S2 = max_blocks * page
+            _, page, N2, _ = key.shape
+            if block_table.dim() != 2 or block_table.shape[0] != B:
+                raise ValueError("block_table must be [batch, max_blocks]")
+            self.max_blocks, self.page_bs = int(block_table.shape[1]), int(page)
+            S2 = self.max_blocks * self.page_bs
+            act_k = H.host_lengths(actual_seq_lengths_key, B, S2)
+            key_start = [0] * B
+            self.key_rows = key.shape[0] * page
+            self.d_bt = block_table.to(torch.int32).contiguous()
         if key.shape[-1] != D:
             raise ValueError("query and key head dims differ")
         if N1 % N2 != 0:
@@ -96,6 +115,14 @@ class IndexerPlan:
 
     def score(self):
         if self.total_rows == 0:
+            return
+        if self.d_bt is not None:
+            _lib.check(self.lib.dsa_li_score_paged(
+                self.q.data_ptr(), self.kk.data_ptr(), self.w.data_ptr(), self.io, self.wdt,
+                self.d_row_start.data_ptr(), self.d_bt.data_ptr(), self.max_blocks, self.page_bs,
+                self.key_rows, self.d_aq.data_ptr(), self.d_ak.data_ptr(), self.B, self.total_rows,
+                self.N1, self.N2, self.D, self.max_rows, self.max_kv, self.sparse_mode,
+                self.scores.data_ptr(), self.ld, H.stream_ptr(self.dev)), "dsa_li_score_paged")
             return
         _lib.check(self.lib.dsa_li_score(
             self.q.data_ptr(), self.kk.data_ptr(), self.w.data_ptr(), self.io, self.wdt,
@@ -128,8 +155,11 @@ def lightning_indexer(query, key, weights, actual_seq_lengths_query=None,
     Args mirror lightning_indexer_triton.py:466-497: query [B,S1,N1,D] (BSND) or
     [T1,N1,D] (TND) fp16/bf16; key [B,S2,N2,D] / [T2,N2,D]; weights [B,S1,N1] /
     [T1,N1] fp16/bf16/fp32; actual_seq_lengths_* per-batch (BSND) or cumulative
-    (TND); block_table must be None; pre_tokens / next_tokens are ignored (as in
-    the reference). Returns (indices, values)."""
+    (TND); pre_tokens / next_tokens are ignored (as in the reference). Returns
+    (indices, values). Beyond the reference (which raises on any block_table,
+    :501-502): ``layout_key="PA_BSND"`` with ``block_table`` [B, max_blocks] reads the
+    keys from a paged cache [num_blocks, block_size, N2, D] with per-batch kv lengths;
+    any other layout with a block_table raises as the reference does."""
     return IndexerPlan(query, key, weights, actual_seq_lengths_query, actual_seq_lengths_key,
                        block_table, layout_query, layout_key, sparse_count, sparse_mode,
                        return_value).run()

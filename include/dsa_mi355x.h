@@ -14,6 +14,10 @@
  *                        _expand_block_indices :1036-1051)
  *   dsa_sfa_workspace_bytes <- the workspace sizing of _sfa_core :1218-1250
  *                     (the caller allocates; the library keeps no cache)
+ *   dsa_sfa_bwd    <- _sfa_grad_core                   sparse_flash_attention_grad_triton.py:441-495
+ *                     (+ _sfa_grad_kernel :157-415)
+ *   dsa_li_score_paged: dsa_li_score over a paged key cache (an extension; the
+ *                     reference's indexer rejects block_table)
  *
  * Conventions
  *  - Every pointer is device memory unless stated; the caller owns every buffer.
@@ -74,6 +78,25 @@ int dsa_li_score(const void* query, const void* key, const void* weights, int io
                  const int32_t* act_q, const int32_t* act_k, int batch, int total_rows, int n1,
                  int n2, int d, int s2, int max_rows_per_batch, int max_kv, int sparse_mode,
                  uint16_t* scores, int64_t score_ld, void* stream);
+
+/*
+ * dsa_li_score with the keys in a paged cache (PA_BSND). No counterpart in the
+ * reference: lightning_indexer_triton rejects block_table (:501-502); the
+ * semantics are those of dsa_li_score on the keys de-paged the way the reference
+ * de-pages the SFA cache (_pa_to_bsnd, sparse_flash_attention_triton.py:1012-1033).
+ *   key_cache [num_blocks, page_block_size, N2, D]; key_rows = num_blocks * page_block_size;
+ *   block_table [batch, max_blocks] int32: token t of batch b is cache row
+ *     block_table[b*max_blocks + t/page_block_size]*page_block_size + t%page_block_size;
+ *     a -1 block (or one past the cache) is a zero key row: its scores are 0.
+ *   S2 = max_blocks * page_block_size (<= 65536, max_blocks <= 4096); score_ld >= S2.
+ * Everything else as dsa_li_score (act_k[b] keys visible; no key_start).
+ */
+int dsa_li_score_paged(const void* query, const void* key_cache, const void* weights, int io_dtype,
+                       int w_dtype, const int32_t* row_start, const int32_t* block_table,
+                       int max_blocks, int page_block_size, int64_t key_rows, const int32_t* act_q,
+                       const int32_t* act_k, int batch, int total_rows, int n1, int n2, int d,
+                       int max_rows_per_batch, int max_kv, int sparse_mode, uint16_t* scores,
+                       int64_t score_ld, void* stream);
 
 /*
  * Stable top-k over the quantised score rows (replaces _stable_topk,

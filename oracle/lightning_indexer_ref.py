@@ -151,16 +151,33 @@ def lightning_indexer(query, key, weights, actual_seq_lengths_query=None,
                       layout_key="BSND", sparse_count=2048, sparse_mode=3,
                       return_value=False, value_dtype="bf16", rows=None):
     """Oracle twin of ``lightning_indexer_triton`` (lightning_indexer_triton.py:466-554)
-    on numpy arrays. ``value_dtype`` is the query dtype ("bf16" / "fp16")."""
-    if block_table is not None:
+    on numpy arrays. ``value_dtype`` is the query dtype ("bf16" / "fp16").
+
+    ``layout_key="PA_BSND"`` (no counterpart in the reference, which rejects a block
+    table, :501-502): the paged key cache is de-paged the way the reference de-pages
+    the SFA cache (``pa_to_bsnd``, sparse_flash_attention_triton.py:1012-1033: a -1
+    block is a zero key row) and the kv lengths are per batch; then the BSND golden."""
+    is_pa = layout_key == "PA_BSND"
+    if block_table is not None and not is_pa:
         raise ValueError("PA_BSND / block_table not supported in lightning_indexer")
     is_tnd = layout_query == "TND"
+    if is_pa:
+        from .sparse_flash_attention_ref import pa_to_bsnd
+        bt = np.asarray(block_table)
+        k = pa_to_bsnd(np.asarray(key, np.float32), bt, bt.shape[1] * key.shape[1])
+        B = bt.shape[0]
+        act_k = (np.full(B, k.shape[1], np.int32) if actual_seq_lengths_key is None
+                 else np.asarray(actual_seq_lengths_key, np.int32))
     if is_tnd:
         act_q = tnd_cumsum_to_per_batch(actual_seq_lengths_query)
-        act_k = tnd_cumsum_to_per_batch(actual_seq_lengths_key)
         q = tnd_to_bsnd(np.asarray(query, np.float32), act_q)
         w = tnd_to_bsnd(np.asarray(weights, np.float32), act_q)
-        k = tnd_to_bsnd(np.asarray(key, np.float32), act_k) if layout_key == "TND" else np.asarray(key, np.float32)
+        if not is_pa:
+            act_k = tnd_cumsum_to_per_batch(actual_seq_lengths_key)
+            k = tnd_to_bsnd(np.asarray(key, np.float32), act_k) if layout_key == "TND" else np.asarray(key, np.float32)
+    elif is_pa:
+        q, w = np.asarray(query, np.float32), np.asarray(weights, np.float32)
+        act_q = np.full(q.shape[0], q.shape[1], np.int32) if actual_seq_lengths_query is None else np.asarray(actual_seq_lengths_query, np.int32)
     else:
         q, k, w = (np.asarray(x, np.float32) for x in (query, key, weights))
         B = q.shape[0]

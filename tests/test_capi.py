@@ -75,6 +75,8 @@ def test_python_validation_matches_reference():
     q = torch.zeros(1, 4, 8, 128, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="block_table"):
         lightning_indexer(q, q[:, :, :1], torch.zeros(1, 4, 8), block_table=torch.zeros(1, 1))
+    with pytest.raises(ValueError, match="requires block_table"):
+        lightning_indexer(q, q[:, :, :1], torch.zeros(1, 4, 8), layout_key="PA_BSND")
     k = torch.zeros(1, 16, 1, 512, dtype=torch.bfloat16)
     qs = torch.zeros(1, 4, 8, 512, dtype=torch.bfloat16)
     qr = torch.zeros(1, 4, 8, 64, dtype=torch.bfloat16)

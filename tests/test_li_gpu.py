@@ -208,3 +208,80 @@ def test_heavy_ties_at_the_threshold(dev):
     stats = check_li(gi, gv, _np(q), _np(k), _np(w), np.full(B, S1), np.full(B, S2), K, 0, "bf16")
     print(f"[li parity] heavy ties: {stats}")
     assert stats.flips <= max(4, 0.02 * stats.elements), stats
+
+
+def _paged(rng, B, lens, page, N2, D, dtype, missing=None, spare=3):
+    """Random paged key cache for per-batch kv lengths: a block table [B, max_blocks] over a
+    shuffled pool (-1 past each batch's blocks and at `missing` = (b, i)), the cache
+    [pool, page, N2, D] and the same keys de-paged by hand [B, max_blocks * page, N2, D]."""
+    nb = [(l + page - 1) // page for l in lens]
+    max_blocks = max(nb) + 1
+    pool = sum(nb) + spare
+    perm = rng.permutation(pool)
+    bt = np.full((B, max_blocks), -1, np.int32)
+    off = 0
+    for b in range(B):
+        bt[b, :nb[b]] = perm[off:off + nb[b]]
+        off += nb[b]
+    if missing is not None:
+        bt[missing] = -1
+    cache = torch.from_numpy(rng.randn(pool, page, N2, D).astype(np.float32)).to(DT[dtype])
+    c = cache.float().numpy()
+    dense = np.zeros((B, max_blocks * page, N2, D), np.float32)
+    for b in range(B):
+        for i in range(max_blocks):
+            if bt[b, i] >= 0:
+                dense[b, i * page:(i + 1) * page] = c[bt[b, i]]
+    return torch.from_numpy(bt), cache, dense
+
+
+@pytest.mark.parametrize("mode", [0, 3])
+@pytest.mark.parametrize("page", [16, 48, 64])
+def test_pa_bsnd_keys(dev, mode, page):
+    """Keys from a paged cache (an extension: the reference rejects block_table). Parity
+    with the golden on the keys de-paged by hand; a missing (-1) block inside a batch's
+    range is a zero key row (score 0); non-power-of-two pages."""
+    rng = np.random.RandomState(12)
+    B, S1, N1, N2, D, K, dtype = 3, 4, 32, 1, 128, 64, "bf16"
+    lens = [200, 77, 511]
+    bt, cache, dense = _paged(rng, B, lens, page, N2, D, dtype, missing=(0, 1))
+    q = torch.from_numpy(rng.randn(B, S1, N1, D).astype(np.float32)).to(DT[dtype])
+    w = torch.from_numpy(rng.randn(B, S1, N1).astype(np.float32)).to(DT[dtype])
+    idx, val = lightning_indexer(q.to(dev), cache.to(dev), w.to(dev), actual_seq_lengths_key=lens,
+                                 block_table=bt.to(dev), layout_key="PA_BSND", sparse_count=K,
+                                 sparse_mode=mode, return_value=True)
+    torch.cuda.synchronize()
+    gi, gv = idx.cpu().numpy(), val.float().cpu().numpy()
+    S2 = dense.shape[1]
+    aq, ak = np.full(B, S1), np.asarray(lens)
+    Ls = np.concatenate([_visible(S1, S2, aq[b], ak[b], mode) for b in range(B)])
+    check_topk_properties(gi.reshape(-1, K), gv.reshape(-1, K), Ls, K)
+    stats = check_li(gi, gv, _np(q), dense, _np(w), aq, ak, K, mode, dtype)
+    assert stats.flips <= max(4, 0.02 * stats.elements), stats
+    # the oracle's own de-paging agrees with the hand-built one
+    o_idx, _ = LI.lightning_indexer(_np(q), cache.float().numpy(), _np(w), None, lens, bt.numpy(), "BSND",
+                                    "PA_BSND", K, mode, True, value_dtype=dtype)
+    assert (o_idx == gi).mean() > 0.97
+
+
+def test_pa_bsnd_decode_shape(dev):
+    """Decode-time indexing: one query row per batch, 64 heads, kv lengths in the
+    thousands over 128-token pages (the SFA decode cache layout), TND queries."""
+    rng = np.random.RandomState(13)
+    B, N1, D, K, dtype, page = 8, 64, 128, 2048, "bf16", 128
+    lens = rng.randint(2500, 9000, size=B).tolist()
+    bt, cache, dense = _paged(rng, B, lens, page, 1, D, dtype)
+    q = torch.from_numpy(rng.randn(B, N1, D).astype(np.float32)).to(DT[dtype])
+    w = torch.from_numpy(rng.randn(B, N1).astype(np.float32) / 8).to(DT[dtype])
+    cq = list(range(1, B + 1))
+    idx, val = lightning_indexer(q.to(dev), cache.to(dev), w.to(dev), actual_seq_lengths_query=cq,
+                                 actual_seq_lengths_key=lens, block_table=bt.to(dev), layout_query="TND",
+                                 layout_key="PA_BSND", sparse_count=K, sparse_mode=3, return_value=True)
+    torch.cuda.synchronize()
+    gi, gv = idx.cpu().numpy().reshape(B, 1, 1, K), val.float().cpu().numpy().reshape(B, 1, 1, K)
+    S2 = dense.shape[1]
+    Ls = np.array([min(l, S2) for l in lens])
+    check_topk_properties(gi.reshape(-1, K), gv.reshape(-1, K), Ls, K)
+    stats = check_li(gi, gv, _np(q).reshape(B, 1, N1, D), dense, _np(w).reshape(B, 1, N1), np.ones(B, int),
+                     np.asarray(lens), K, 3, dtype)
+    assert stats.flips <= max(4, 0.02 * stats.elements), stats

@@ -452,3 +452,28 @@ def test_sfa_grad_tnd_equals_bsnd():
         k0 += lk[b]
     for gv, wv in zip(got, (ref_dq, ref_dk, ref_dv, ref_dqr, ref_dkr)):
         np.testing.assert_array_equal(gv, wv)
+
+
+def test_li_pa_bsnd_equals_depaged_bsnd():
+    """Paged keys (random block table, one -1 block) == the BSND golden on the de-paged
+    keys built by hand: the -1 block's keys are zero rows (score 0, still selectable)."""
+    rng = np.random.RandomState(8)
+    B, S1, N1, D, page, mb = 2, 3, 8, 32, 4, 5
+    q = round_bf16(rng.randn(B, S1, N1, D).astype(np.float32))
+    w = rng.randn(B, S1, N1).astype(np.float32)
+    nblk = 9
+    cache = round_bf16(rng.randn(nblk, page, 1, D).astype(np.float32))
+    bt = np.array([[3, 0, 7, -1, 5], [8, 1, 2, 4, 6]], np.int32)
+    act_k = [18, 20]
+    dense = np.zeros((B, mb * page, 1, D), np.float32)
+    for b in range(B):
+        for i in range(mb):
+            if bt[b, i] >= 0:
+                dense[b, i * page:(i + 1) * page] = cache[bt[b, i]]
+    for mode in (0, 3):
+        got = LI.lightning_indexer(q, cache, w, None, act_k, bt, "BSND", "PA_BSND", 6, mode, True)
+        want = LI.lightning_indexer(q, dense, w, None, act_k, None, "BSND", "BSND", 6, mode, True)
+        np.testing.assert_array_equal(got[0], want[0])
+        np.testing.assert_array_equal(got[1], want[1])
+    with pytest.raises(ValueError):
+        LI.lightning_indexer(q, dense, w, block_table=bt)
