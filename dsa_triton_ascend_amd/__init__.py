@@ -5,6 +5,8 @@ Drop-in operators with the reference's Python signatures:
 * :func:`lightning_indexer` (lightning_indexer_triton.py:466) — indexer score + stable top-k
 * :func:`sparse_flash_attention` (sparse_flash_attention_triton.py:1295) — MLA-absorb SFA forward
 * :func:`sparse_flash_attention_grad` (sparse_flash_attention_grad_triton.py:498) — its backward
+* :func:`sparse_lightning_indexer_grad_kl_loss` (sparse_lightning_indexer_grad_kl_loss_triton.py:496)
+  — the indexer's KL training loss and its gradients
 
 and :class:`PrefillPlan` / :func:`dsa_prefill`, the two chained on one packed
 (TND) batch with the indexer's top-k feeding the attention in place.
@@ -16,6 +18,8 @@ from .lightning_indexer import LightningIndexer, lightning_indexer
 from .pipeline import PrefillPlan, dsa_prefill
 from .sparse_flash_attention import SparseFlashAttention, sparse_flash_attention
 from .sparse_flash_attention_grad import SparseFlashAttentionGrad, sparse_flash_attention_grad
+from .sli_grad_kl_loss import SparseLightningIndexerGradKLLoss, sparse_lightning_indexer_grad_kl_loss
 
 __all__ = ["lightning_indexer", "LightningIndexer", "sparse_flash_attention", "SparseFlashAttention",
-           "sparse_flash_attention_grad", "SparseFlashAttentionGrad", "PrefillPlan", "dsa_prefill"]
+           "sparse_flash_attention_grad", "SparseFlashAttentionGrad", "sparse_lightning_indexer_grad_kl_loss",
+           "SparseLightningIndexerGradKLLoss", "PrefillPlan", "dsa_prefill"]

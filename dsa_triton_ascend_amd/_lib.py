@@ -37,6 +37,9 @@ SIGNATURES = {
                          _I, _I, _I, _I64, _I, _F, _P, _P, _P, _P, _SZ, _I, _P]),
     "dsa_li_score_paged": (_I, [_P, _P, _P, _I, _I, _P, _P, _I, _I, _I64, _P, _P, _I, _I, _I, _I, _I, _I, _I,
                                 _I, _P, _I64, _P]),
+    "dsa_sli_grad_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
+    "dsa_sli_grad_kl_loss": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I,
+                                  _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _SZ, _P]),
     "dsa_sfa_bwd_workspace_bytes": (_SZ, [_I, _P, _P, _I, _I, _I, _I, _I, _I, _I64]),
     "dsa_sfa_bwd": (_I, [_P, _P, _P, _P, _I, _P, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I,
                          _I, _I64, _I, _F, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),

@@ -23,7 +23,7 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
           "-Wno-unused-result", "-I", str(PKG.parent / "include")]
 
-SOURCES = ["li_score.hip", "li_topk.hip", "sfa_fwd.hip", "sfa_bwd.hip", "capi.cpp"]
+SOURCES = ["li_score.hip", "li_topk.hip", "sfa_fwd.hip", "sfa_bwd.hip", "sli_grad.hip", "capi.cpp"]
 
 
 # Kernels whose float code never relies on NaN propagation: lets fmaxf lower to a

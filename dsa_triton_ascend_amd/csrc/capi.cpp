@@ -6,6 +6,7 @@
 // instead of reaching a kernel; the Python layer raises the same conditions first.
 #include <hip/hip_runtime.h>
 
+#include <climits>
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
@@ -243,6 +244,49 @@ int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, cons
   a.dkr = d_key_rope;
   a.dv = d_value;
   return hip_status(launch_sfa_bwd(a, (hipStream_t)stream), "dsa_sfa_bwd launch");
+}
+
+size_t dsa_sli_grad_workspace_bytes(int batch, int s1, int s2, int sparse_count, int d_idx) {
+  if (batch <= 0 || s1 < 0 || s2 <= 0 || sparse_count <= 0 || d_idx <= 0) return 0;
+  return sli_grad_workspace_bytes(batch * s1, sparse_count, (int64_t)batch * s2, d_idx);
+}
+
+int dsa_sli_grad_kl_loss(const void* query, const void* key, const void* query_rope, const void* key_rope,
+                         const void* query_index, const void* key_index, const void* weights, int io_dtype,
+                         int w_dtype, const int32_t* sparse_indices, int sparse_count, const float* sm_max,
+                         const float* sm_sum, const int32_t* act_q, const int32_t* act_k, int batch, int s1,
+                         int s2, int n1, int d, int dr, int nidx1, int d_idx, float scale,
+                         void* d_query_index, void* d_key_index, void* d_weights, float* loss,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+  if (!query || !key || !query_index || !key_index || !weights || !sparse_indices || !sm_max || !sm_sum ||
+      !act_q || !act_k || !d_query_index || !d_key_index || !d_weights || !loss || !workspace ||
+      (dr > 0 && (!query_rope || !key_rope)))
+    return fail(DSA_ERR_INVALID, "dsa_sli_grad_kl_loss: null pointer argument");
+  if (!is16(io_dtype)) return fail(DSA_ERR_INVALID, "dsa_sli_grad_kl_loss: io_dtype must be fp16 or bf16");
+  if (!is16(w_dtype) && w_dtype != DSA_DTYPE_F32)
+    return fail(DSA_ERR_INVALID, "dsa_sli_grad_kl_loss: weights dtype must be fp16, bf16 or fp32");
+  if (batch <= 0 || s1 < 0 || s2 <= 0 || n1 <= 0 || sparse_count <= 0)
+    return fail(DSA_ERR_INVALID, "dsa_sli_grad_kl_loss: non-positive shape");
+  if (n1 > 128) return fail(DSA_ERR_UNSUPPORTED, "dsa_sli_grad_kl_loss: N1=%d > 128", n1);
+  if (dr != 0 && dr != 64) return fail(DSA_ERR_INVALID, "rope dim must be 64 (or 0 without rope), got %d", dr);
+  if (!sli_grad_supported(d, dr, nidx1, d_idx, sparse_count))
+    return fail(DSA_ERR_UNSUPPORTED,
+                "dsa_sli_grad_kl_loss: D=%d (+%d), Nidx1=%d, D_idx=%d, topK=%d outside D in {128,256,512}, "
+                "D_idx in {128,256,512}, Nidx1 <= 128 with ceil8(Nidx1)*D_idx <= 32768, topK <= 2048",
+                d, dr, nidx1, d_idx, sparse_count);
+  if (batch > 65535 || (int64_t)batch * s1 > INT32_MAX)
+    return fail(DSA_ERR_UNSUPPORTED, "dsa_sli_grad_kl_loss: too many rows");
+  const size_t need = sli_grad_workspace_bytes(batch * s1, sparse_count, (int64_t)batch * s2, d_idx);
+  if (workspace_bytes < need)
+    return fail(DSA_ERR_INVALID, "dsa_sli_grad_kl_loss: workspace of %zu bytes required, %zu given", need,
+                workspace_bytes);
+  if (batch * s1 == 0) return DSA_OK;
+  return hip_status(launch_sli_grad(query, key, query_rope ? query_rope : query, key_rope ? key_rope : key,
+                                    query_index, key_index, weights, io_dtype, w_dtype, sparse_indices,
+                                    sparse_count, sm_max, sm_sum, act_q, act_k, batch, s1, s2, n1, d, dr,
+                                    nidx1, d_idx, scale, d_query_index, d_key_index, d_weights, loss,
+                                    workspace, (hipStream_t)stream),
+                    "dsa_sli_grad_kl_loss launch");
 }
 
 }  // extern "C"

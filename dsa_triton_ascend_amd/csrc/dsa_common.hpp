@@ -243,3 +243,13 @@ struct SfaBwdArgs {
 size_t sfa_bwd_workspace_bytes(int batch, const int32_t* h_row_start, const int32_t* h_act_k, int s2,
                                int total_rows, int n1, int d, int topk, int sbs, int64_t key_rows);
 hipError_t launch_sfa_bwd(const SfaBwdArgs& a, hipStream_t s);
+
+// sparse lightning-indexer grad KL loss (BSND)
+size_t sli_grad_workspace_bytes(int rows, int topk, int64_t key_rows, int didx);
+bool sli_grad_supported(int d, int dr, int nidx1, int didx, int topk);
+hipError_t launch_sli_grad(const void* q, const void* k, const void* qr, const void* kr, const void* qi,
+                           const void* ki, const void* w, int io, int wdt, const int32_t* sidx, int topk,
+                           const float* sm_max, const float* sm_sum, const int32_t* act_q,
+                           const int32_t* act_k, int batch, int s1, int s2, int n1, int d, int dr,
+                           int nidx1, int didx, float scale, void* dqi, void* dki, void* dw, float* loss,
+                           void* ws, hipStream_t s);

@@ -1,0 +1,456 @@
+// Sparse lightning-indexer grad KL loss for gfx950.
+//
+// Semantics: sli_grad_kl_loss_numpy.py:17-180 with the row bounds of
+// sparse_lightning_indexer_grad_kl_loss_triton.py:63-69 (BSND, N2 = Nidx2 = 1).
+// Per query row r = (b, s1 < act_q), the first n = min(topK, max(act_k - act_q +
+// s1 + 1, 0)) slots of sparse_indices[r], each id clipped to [0, S2 - 1]:
+//   teacher p[k] = (1/N1) sum_h exp(score[h,k] - sm_max[h]) / (sm_sum[h] + 1e-8)
+//   student I[k] = sum_g w[g] relu(qi[g] . ki[k]),  sI = softmax(I) (+1e-8)
+//   dI = sI - p;  loss = sum_rows sum_k p~ (log p~ - log sI~)  (x~ = max(x, 1e-8))
+//   dW[g] = sum_k relu[g,k] dI[k];  ds[g,k] = dI[k] w[g] [relu > 0]
+//   dQI[g] = sum_k ds[g,k] ki[k];   dKI[id_k] += sum_g ds[g,k] qi[g]  (per slot)
+//
+// Launches:
+//  1. sli_zero_kernel -- clears the teacher sums and the fp32 dKI accumulator;
+//  2. sli_teacher_kernel -- one work-group per (row, 32-head block): Q | Q rope of
+//     the block in LDS, tiles of 32 gathered [D | Dr] key rows, S^T on
+//     v_mfma_f32_32x32x16 (k-range split over the 4 waves, summed through LDS),
+//     the block's probabilities summed over its heads and added to p[r, k];
+//  3. sli_student_kernel -- one work-group per row: qi in LDS, two passes over
+//     tiles of 32 gathered ki rows in fp32 VALU (I, then softmax / dI / loss, then
+//     dW, dQI in registers and dKI added per slot with fp32 atomics);
+//  4. sli_finish_kernel -- dKI to the io dtype and the loss (sum of the row
+//     losses, in row order).
+#include <climits>
+
+#include "dsa_common.hpp"
+
+namespace dsa {
+namespace {
+
+constexpr int SBH = 32;     // heads per teacher work-group
+constexpr int SBT = 32;     // tokens per tile
+constexpr int SWV = 4;      // waves per work-group
+constexpr float SEPS = 1e-8f;
+constexpr float SLOG2E = 1.4426950408889634f;
+constexpr int SLI_MAX_TOPK = 2048;   // student keeps the row's I / dI in LDS
+constexpr int SLI_MAX_GD = 64 * 512; // Nidx1 (padded to 8) x D_idx held in LDS
+
+inline size_t salign(size_t x) { return (x + 255) & ~(size_t)255; }
+
+struct SliArgs {
+  const void* q; const void* k; const void* qr; const void* kr;
+  const void* qi; const void* ki; const void* w; int io, wdt;
+  const int32_t* sidx; int topk;
+  const float* sm_max; const float* sm_sum;
+  const int32_t* act_q; const int32_t* act_k;
+  int batch, s1, s2, n1, d, dr, nidx1, didx; float scale;
+  void* dqi; void* dki; void* dw; float* loss;
+  float* p;        // [rows, topk] teacher sums
+  float* dki_acc;  // [batch * s2, didx]
+  float* row_loss; // [rows]
+};
+
+__device__ __forceinline__ int row_slots(const SliArgs& a, int r, int& b, int& s1) {
+  b = r / a.s1;
+  s1 = r - b * a.s1;
+  const int aq = a.act_q[b], ak = a.act_k[b];
+  if (s1 >= aq) return 0;
+  int n = ak - aq + s1 + 1;
+  n = n < 0 ? 0 : n;
+  return n < a.topk ? n : a.topk;
+}
+
+__device__ __forceinline__ int clip_id(int id, int s2) { return id < 0 ? 0 : (id > s2 - 1 ? s2 - 1 : id); }
+
+__device__ __forceinline__ float ld_w(const void* w, int wdt, int64_t i) {
+  if (wdt == DSA_DTYPE_F32) return reinterpret_cast<const float*>(w)[i];
+  const uint16_t h = reinterpret_cast<const uint16_t*>(w)[i];
+  return wdt == DSA_DTYPE_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+}
+
+__global__ void sli_zero_kernel(float4* p, int64_t n4) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+// ---------------------------------------------------------------- teacher
+template <int IO, int DT>
+__global__ __launch_bounds__(SWV * 64) void sli_teacher_kernel(SliArgs a) {
+  constexpr int QP = DT + 8;          // row pitch: odd count of 16-byte units
+  constexpr int KS = DT / 16;         // k-steps
+  static_assert(KS % SWV == 0, "k-range splits over the waves");
+  __shared__ __attribute__((aligned(16))) uint16_t Qs[SBH * QP];
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[SBT * QP];
+  __shared__ float part[SWV][16][64];
+  __shared__ float s_m[SBH], s_il[SBH];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = blockIdx.x;
+  int b, s1;
+  const int n = row_slots(a, r, b, s1);
+  if (n == 0) return;
+  const int h0 = blockIdx.y * SBH;
+  const int hn = a.n1 - h0 < SBH ? a.n1 - h0 : SBH;
+  const int D = a.d;
+  const uint16_t* qb = reinterpret_cast<const uint16_t*>(a.q);
+  const uint16_t* qrb = reinterpret_cast<const uint16_t*>(a.qr);
+  const uint16_t* kb = reinterpret_cast<const uint16_t*>(a.k);
+  const uint16_t* krb = reinterpret_cast<const uint16_t*>(a.kr);
+  const uint4 z4 = make_uint4(0, 0, 0, 0);
+  for (int i = tid; i < SBH * (DT / 8); i += SWV * 64) {
+    const int h = i / (DT / 8), c = (i % (DT / 8)) * 8;
+    uint4 v = z4;
+    if (h < hn) {
+      const int64_t hr = (int64_t)r * a.n1 + h0 + h;
+      v = c < D ? ldg16(qb + hr * D + c) : ldg16(qrb + hr * a.dr + (c - D));
+    }
+    *reinterpret_cast<uint4*>(&Qs[h * QP + c]) = v;
+  }
+  if (tid < SBH) {
+    float m = 0.f, il = 0.f;
+    if (tid < hn) {
+      const int64_t hr = (int64_t)r * a.n1 + h0 + tid;
+      m = a.sm_max[hr];
+      il = 1.f / (a.sm_sum[hr] + SEPS);
+    }
+    s_m[tid] = m * SLOG2E;
+    s_il[tid] = il;
+  }
+  const int32_t* ids = a.sidx + (int64_t)r * a.topk;
+  const float sl2 = a.scale * SLOG2E, inv_n1 = 1.f / a.n1;
+  for (int t0 = 0; t0 < n; t0 += SBT) {
+    const int nv = n - t0 < SBT ? n - t0 : SBT;
+    for (int i = tid; i < SBT * (DT / 8); i += SWV * 64) {
+      const int t = i / (DT / 8), c = (i % (DT / 8)) * 8;
+      uint4 v = z4;
+      if (t < nv) {
+        const int64_t kr = (int64_t)b * a.s2 + clip_id(ids[t0 + t], a.s2);
+        v = c < D ? ldg16(kb + kr * D + c) : ldg16(krb + kr * a.dr + (c - D));
+      }
+      *reinterpret_cast<uint4*>(&Ks[t * QP + c]) = v;
+    }
+    __syncthreads();
+    {
+      constexpr int NKS = KS / SWV;
+      const uint16_t* arow = Ks + (lane & 31) * QP + (lane >> 5) * 8 + wave * NKS * 16;
+      const uint16_t* brow = Qs + (lane & 31) * QP + (lane >> 5) * 8 + wave * NKS * 16;
+      f32x16 s = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks)
+        s = Mfma<IO>::m32(*reinterpret_cast<const uint4*>(arow + ks * 16),
+                          *reinterpret_cast<const uint4*>(brow + ks * 16), s);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) part[wave][i][lane] = s[i];
+    }
+    __syncthreads();
+    // element (i, lane): token m32_row(i, lane), head lane % 32; the block's
+    // probabilities summed over its heads (the 32 lanes of a half-wave)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = wave * 4 + j;
+      const int tk = m32_row(i, lane), h = lane & 31;
+      const float sv = part[0][i][lane] + part[1][i][lane] + part[2][i][lane] + part[3][i][lane];
+      float pr = h < hn ? __builtin_amdgcn_exp2f(sv * sl2 - s_m[h]) * s_il[h] : 0.f;
+#pragma unroll
+      for (int o = 16; o >= 1; o >>= 1) pr += __shfl_xor(pr, o, 32);
+      if ((lane & 31) == 0 && tk < nv) unsafeAtomicAdd(a.p + (int64_t)r * a.topk + t0 + tk, pr * inv_n1);
+    }
+    __syncthreads();   // the next tile overwrites Ks and part
+  }
+}
+
+// ---------------------------------------------------------------- student
+// Thread t handles token t % 32 of a tile and heads g = t / 32 + 8 j (j < GPT).
+template <int IO, int DI, int GPT>
+__global__ __launch_bounds__(256) void sli_student_kernel(SliArgs a) {
+  constexpr int KIP = DI + 2;   // ki row pitch (elements): rows one bank apart for 4-byte reads
+  constexpr int NQ = DI / 32;   // dQI columns per thread (see the pass-2 ownership note)
+  __shared__ __attribute__((aligned(16))) uint16_t QIs[8 * GPT * DI];
+  __shared__ __attribute__((aligned(16))) uint16_t KIs[SBT * KIP];
+  __shared__ float s_i[SLI_MAX_TOPK];   // I, then dI
+  __shared__ float s_w[8 * GPT];
+  __shared__ float s_ds[8 * GPT][SBT + 1];
+  __shared__ float red[8][SBT + 1];
+  __shared__ float s_red[8];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = blockIdx.x;
+  int b, s1;
+  const int n = row_slots(a, r, b, s1);
+  const int G = a.nidx1;
+  uint16_t* dqio = reinterpret_cast<uint16_t*>(a.dqi);
+  const int64_t qrow = (int64_t)r * G;
+  if (n == 0) {   // no slot: zero gradients, zero loss
+    for (int i = tid; i < G * DI; i += 256) dqio[qrow * DI + i] = 0;
+    for (int g = tid; g < G; g += 256) {
+      if (a.wdt == DSA_DTYPE_F32) reinterpret_cast<float*>(a.dw)[qrow + g] = 0.f;
+      else reinterpret_cast<uint16_t*>(a.dw)[qrow + g] = 0;
+    }
+    if (tid == 0) a.row_loss[r] = 0.f;
+    return;
+  }
+  const uint16_t* qib = reinterpret_cast<const uint16_t*>(a.qi);
+  const uint16_t* kib = reinterpret_cast<const uint16_t*>(a.ki);
+  for (int i = tid; i < 8 * GPT * DI / 8; i += 256) {
+    const int g = i / (DI / 8), c = (i % (DI / 8)) * 8;
+    *reinterpret_cast<uint4*>(&QIs[g * DI + c]) = g < G ? ldg16(qib + (qrow + g) * DI + c) : make_uint4(0, 0, 0, 0);
+  }
+  for (int g = tid; g < 8 * GPT; g += 256) s_w[g] = g < G ? ld_w(a.w, a.wdt, qrow + g) : 0.f;
+  const int32_t* ids = a.sidx + (int64_t)r * a.topk;
+  const int tk = tid & 31, grp = tid >> 5;
+
+  auto load_tile = [&](int t0, int nv) {
+    for (int i = tid; i < SBT * (DI / 2); i += 256) {
+      const int t = i / (DI / 2), c = (i % (DI / 2)) * 2;
+      uint32_t v = 0;
+      if (t < nv) {
+        const int64_t kr = (int64_t)b * a.s2 + clip_id(ids[t0 + t], a.s2);
+        v = *reinterpret_cast<const uint32_t*>(kib + kr * DI + c);
+      }
+      *reinterpret_cast<uint32_t*>(&KIs[t * KIP + c]) = v;
+    }
+  };
+  // dot[j] = qi[grp + 8 j] . ki[tk] (fp32)
+  auto dots = [&](float (&dv)[GPT]) {
+#pragma unroll
+    for (int j = 0; j < GPT; ++j) dv[j] = 0.f;
+    const uint16_t* kr = KIs + tk * KIP;
+    for (int c = 0; c < DI; c += 2) {
+      const uint32_t kk = *reinterpret_cast<const uint32_t*>(kr + c);
+      const float k0 = to_f32<IO>((uint16_t)(kk & 0xFFFFu)), k1 = to_f32<IO>((uint16_t)(kk >> 16));
+#pragma unroll
+      for (int j = 0; j < GPT; ++j) {
+        const uint32_t qq = *reinterpret_cast<const uint32_t*>(QIs + (grp + 8 * j) * DI + c);
+        dv[j] += to_f32<IO>((uint16_t)(qq & 0xFFFFu)) * k0 + to_f32<IO>((uint16_t)(qq >> 16)) * k1;
+      }
+    }
+  };
+  __syncthreads();
+
+  // ---- pass 1: I[k]
+  for (int t0 = 0; t0 < n; t0 += SBT) {
+    const int nv = n - t0 < SBT ? n - t0 : SBT;
+    load_tile(t0, nv);
+    __syncthreads();
+    float dv[GPT];
+    dots(dv);
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < GPT; ++j) acc += s_w[grp + 8 * j] * fmaxf(dv[j], 0.f);
+    red[grp][tk] = acc;
+    __syncthreads();
+    if (tid < SBT && tid < nv) {
+      float s = 0.f;
+#pragma unroll
+      for (int gq = 0; gq < 8; ++gq) s += red[gq][tid];
+      s_i[t0 + tid] = s;
+    }
+    __syncthreads();
+  }
+  // ---- softmax of I over the n slots, dI = sI - p, the row's loss
+  auto block_sum = [&](float v) {
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    if (lane == 0) s_red[wave] = v;
+    __syncthreads();
+    const float t = s_red[0] + s_red[1] + s_red[2] + s_red[3];
+    __syncthreads();
+    return t;
+  };
+  float mx = -INFINITY;
+  for (int k = tid; k < n; k += 256) mx = fmaxf(mx, s_i[k]);
+  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if (lane == 0) s_red[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+  __syncthreads();
+  float es = 0.f;
+  for (int k = tid; k < n; k += 256) es += expf(s_i[k] - mx);
+  const float inv = 1.f / (block_sum(es) + SEPS);
+  float ls = 0.f;
+  for (int k = tid; k < n; k += 256) {
+    const float sv = expf(s_i[k] - mx) * inv;
+    const float pv = a.p[(int64_t)r * a.topk + k];
+    const float pc = fmaxf(pv, SEPS), sc = fmaxf(sv, SEPS);
+    ls += pc * (logf(pc) - logf(sc));
+    s_i[k] = sv - pv;   // dI
+  }
+  const float row_loss = block_sum(ls);
+  if (tid == 0) a.row_loss[r] = row_loss;
+
+  // ---- pass 2: dW, dQI (registers), dKI (atomics)
+  // dQI ownership: thread t holds heads g = t / 32 + 8 j (j < GPT) and columns
+  // c = (t % 32) + 32 q (q < DI / 32)
+  float dqa[GPT][NQ];
+#pragma unroll
+  for (int j = 0; j < GPT; ++j)
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) dqa[j][q] = 0.f;
+  float dwa[GPT];
+#pragma unroll
+  for (int j = 0; j < GPT; ++j) dwa[j] = 0.f;
+  float* dka = a.dki_acc;
+  for (int t0 = 0; t0 < n; t0 += SBT) {
+    const int nv = n - t0 < SBT ? n - t0 : SBT;
+    __syncthreads();   // previous tile's KIs / s_ds reads done
+    load_tile(t0, nv);
+    __syncthreads();
+    float dv[GPT];
+    dots(dv);
+    const float di = tk < nv ? s_i[t0 + tk] : 0.f;
+#pragma unroll
+    for (int j = 0; j < GPT; ++j) {
+      const int g = grp + 8 * j;
+      const float rl = fmaxf(dv[j], 0.f);
+      dwa[j] += rl * di;
+      s_ds[g][tk] = dv[j] > 0.f ? di * s_w[g] : 0.f;
+    }
+    __syncthreads();
+    // dQI[g][c] += sum_t ds[g][t] ki[t][c]
+#pragma unroll
+    for (int j = 0; j < GPT; ++j) {
+      const int g = grp + 8 * j;
+      for (int t = 0; t < nv; ++t) {
+        const float dsv = s_ds[g][t];
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) dqa[j][q] += dsv * to_f32<IO>(KIs[t * KIP + tk + 32 * q]);
+      }
+    }
+    // dKI[id_t][c] += sum_g ds[g][t] qi[g][c]: thread -> (token t = tid / 8, columns
+    // c = tid % 8 + 8 m)
+    {
+      const int t = tid >> 3, c0 = tid & 7;
+      if (t < nv) {
+        const int64_t kr = (int64_t)b * a.s2 + clip_id(ids[t0 + t], a.s2);
+        for (int c = c0; c < DI; c += 8) {
+          float v = 0.f;
+          for (int g = 0; g < G; ++g) v += s_ds[g][t] * to_f32<IO>(QIs[g * DI + c]);
+          unsafeAtomicAdd(dka + kr * DI + c, v);
+        }
+      }
+    }
+  }
+  // ---- epilogue: dQI, dW (summed over the 32 token lanes of each group)
+#pragma unroll
+  for (int j = 0; j < GPT; ++j) {
+    const int g = grp + 8 * j;
+    if (g < G)
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) dqio[(qrow + g) * DI + tk + 32 * q] = from_f32<IO>(dqa[j][q]);
+    float v = dwa[j];
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) v += __shfl_xor(v, o, 32);
+    if (tk == 0 && g < G) {
+      if (a.wdt == DSA_DTYPE_F32) reinterpret_cast<float*>(a.dw)[qrow + g] = v;
+      else if (a.wdt == DSA_DTYPE_BF16) reinterpret_cast<uint16_t*>(a.dw)[qrow + g] = f32_to_bf16_rne(v);
+      else reinterpret_cast<uint16_t*>(a.dw)[qrow + g] = f32_to_f16_rne(v);
+    }
+  }
+}
+
+// dKI accumulator -> io dtype; the loss as the row-ordered sum of the row losses
+template <int IO>
+__global__ void sli_finish_kernel(SliArgs a, int64_t n4, int rows) {
+  const float4* src = reinterpret_cast<const float4*>(a.dki_acc);
+  uint2* dst = reinterpret_cast<uint2*>(a.dki);
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x) {
+    const float4 v = src[i];
+    dst[i] = make_uint2(pack2<IO>(v.x, v.y), pack2<IO>(v.z, v.w));
+  }
+  if (blockIdx.x == 0) {
+    __shared__ float part[256];
+    float s = 0.f;
+    const int per = (rows + 255) / 256;
+    for (int i = threadIdx.x * per; i < (threadIdx.x + 1) * per && i < rows; ++i) s += a.row_loss[i];
+    part[threadIdx.x] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float t = 0.f;
+      for (int i = 0; i < 256; ++i) t += part[i];
+      a.loss[0] = t;
+    }
+  }
+}
+
+// heads per thread: the smallest of 2, 4, 8, 16 covering Nidx1 / 8 (the qi block
+// 8 GPT x DI stays within SLI_MAX_GD elements, checked by the caller)
+template <int IO, int DI>
+void launch_student(const SliArgs& a, int rows, hipStream_t s) {
+  const int gpt = (a.nidx1 + 7) / 8;
+  if (gpt <= 2)
+    hipLaunchKernelGGL((sli_student_kernel<IO, DI, 2>), dim3(rows), dim3(256), 0, s, a);
+  else if (gpt <= 4)
+    hipLaunchKernelGGL((sli_student_kernel<IO, DI, 4>), dim3(rows), dim3(256), 0, s, a);
+  else if (gpt <= 8)
+    hipLaunchKernelGGL((sli_student_kernel<IO, DI, 8>), dim3(rows), dim3(256), 0, s, a);
+  else if constexpr (8 * 16 * DI <= SLI_MAX_GD)
+    hipLaunchKernelGGL((sli_student_kernel<IO, DI, 16>), dim3(rows), dim3(256), 0, s, a);
+}
+
+template <int IO>
+hipError_t launch_sli_io(const SliArgs& a, hipStream_t s) {
+  const int rows = a.batch * a.s1;
+  const dim3 tgrid(rows, (a.n1 + SBH - 1) / SBH);
+  switch (a.d + a.dr) {
+    case 128: hipLaunchKernelGGL((sli_teacher_kernel<IO, 128>), tgrid, dim3(256), 0, s, a); break;
+    case 192: hipLaunchKernelGGL((sli_teacher_kernel<IO, 192>), tgrid, dim3(256), 0, s, a); break;
+    case 256: hipLaunchKernelGGL((sli_teacher_kernel<IO, 256>), tgrid, dim3(256), 0, s, a); break;
+    case 320: hipLaunchKernelGGL((sli_teacher_kernel<IO, 320>), tgrid, dim3(256), 0, s, a); break;
+    case 512: hipLaunchKernelGGL((sli_teacher_kernel<IO, 512>), tgrid, dim3(256), 0, s, a); break;
+    case 576: hipLaunchKernelGGL((sli_teacher_kernel<IO, 576>), tgrid, dim3(256), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  switch (a.didx) {
+    case 128: launch_student<IO, 128>(a, rows, s); break;
+    case 256: launch_student<IO, 256>(a, rows, s); break;
+    case 512: launch_student<IO, 512>(a, rows, s); break;
+    default: return hipErrorInvalidValue;
+  }
+  const int64_t n4 = (int64_t)a.batch * a.s2 * a.didx / 4;
+  const int blocks = (int)((n4 + 255) / 256 < 4096 ? ((n4 + 255) / 256 > 0 ? (n4 + 255) / 256 : 1) : 4096);
+  hipLaunchKernelGGL((sli_finish_kernel<IO>), dim3(blocks), dim3(256), 0, s, a, n4, rows);
+  return hipGetLastError();
+}
+
+}  // namespace
+}  // namespace dsa
+
+size_t sli_grad_workspace_bytes(int rows, int topk, int64_t key_rows, int didx) {
+  return dsa::salign((size_t)rows * topk * 4) + dsa::salign((size_t)key_rows * didx * 4) +
+         dsa::salign((size_t)rows * 4);
+}
+
+bool sli_grad_supported(int d, int dr, int nidx1, int didx, int topk) {
+  const int dt = d + dr;
+  const bool dt_ok = dt == 128 || dt == 192 || dt == 256 || dt == 320 || dt == 512 || dt == 576;
+  const bool di_ok = didx == 128 || didx == 256 || didx == 512;
+  const int gp = (nidx1 + 7) / 8 * 8;
+  return dt_ok && di_ok && nidx1 >= 1 && nidx1 <= 128 && topk >= 1 && topk <= dsa::SLI_MAX_TOPK &&
+         (int64_t)gp * didx <= dsa::SLI_MAX_GD;
+}
+
+hipError_t launch_sli_grad(const void* q, const void* k, const void* qr, const void* kr, const void* qi,
+                           const void* ki, const void* w, int io, int wdt, const int32_t* sidx, int topk,
+                           const float* sm_max, const float* sm_sum, const int32_t* act_q,
+                           const int32_t* act_k, int batch, int s1, int s2, int n1, int d, int dr,
+                           int nidx1, int didx, float scale, void* dqi, void* dki, void* dw, float* loss,
+                           void* ws, hipStream_t s) {
+  dsa::SliArgs a{q, k, qr, kr, qi, ki, w, io, wdt, sidx, topk, sm_max, sm_sum, act_q, act_k,
+                 batch, s1, s2, n1, d, dr, nidx1, didx, scale, dqi, dki, dw, loss,
+                 nullptr, nullptr, nullptr};
+  const int rows = batch * s1;
+  char* base = reinterpret_cast<char*>(ws);
+  a.p = reinterpret_cast<float*>(base);
+  size_t off = dsa::salign((size_t)rows * topk * 4);
+  a.dki_acc = reinterpret_cast<float*>(base + off);
+  off += dsa::salign((size_t)batch * s2 * didx * 4);
+  a.row_loss = reinterpret_cast<float*>(base + off);
+  // teacher sums and the dKI accumulator are contiguous up to the padding
+  const int64_t n4 = (int64_t)off / 16;
+  const int blocks = (int)((n4 + 255) / 256 < 4096 ? ((n4 + 255) / 256 > 0 ? (n4 + 255) / 256 : 1) : 4096);
+  hipLaunchKernelGGL(dsa::sli_zero_kernel, dim3(blocks), dim3(256), 0, s, reinterpret_cast<float4*>(base), n4);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return io == dsa::IO_BF16 ? dsa::launch_sli_io<dsa::IO_BF16>(a, s) : dsa::launch_sli_io<dsa::IO_F16>(a, s);
+}

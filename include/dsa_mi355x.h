@@ -216,6 +216,43 @@ int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, cons
                 void* d_key, void* d_key_rope, void* d_value, void* workspace,
                 size_t workspace_bytes, void* stream);
 
+/*
+ * Workspace bytes for dsa_sli_grad_kl_loss: fp32 teacher sums [batch*s1, sparse_count],
+ * an fp32 d_key_index accumulator [batch*s2, d_idx] and the row losses. Needs no
+ * initialisation. No counterpart in the reference (it allocates its buffers per call,
+ * sparse_lightning_indexer_grad_kl_loss_triton.py:375-392).
+ */
+size_t dsa_sli_grad_workspace_bytes(int batch, int s1, int s2, int sparse_count, int d_idx);
+
+/*
+ * Sparse lightning-indexer grad KL loss, BSND, sparse_mode 3 (replaces
+ * _sparse_lightning_indexer_grad_kl_loss_core,
+ * sparse_lightning_indexer_grad_kl_loss_triton.py:333-440; semantics of
+ * sli_grad_kl_loss_numpy.py:17-180 with the row bounds of the reference kernel
+ * :63-69). Per query row (b, s1 < act_q[b]) the first
+ * n = min(sparse_count, max(act_k[b] - act_q[b] + s1 + 1, 0)) ids of
+ * sparse_indices[b, s1, 0, :], each clipped to [0, s2 - 1]:
+ *   p[k]  = (1/N1) sum_h exp(score[h,k] - sm_max) / (sm_sum + 1e-8),
+ *           score = (q . k + q_rope . k_rope) * scale
+ *   I[k]  = sum_g w[g] relu(qi[g] . ki[k]),  sI = softmax(I) (1e-8 in the sum)
+ *   loss  = sum over rows and k of max(p,1e-8) (log max(p,1e-8) - log max(sI,1e-8))
+ *   d_weights[g] = sum_k relu[g,k] (sI - p)[k];  ds[g,k] = (sI - p)[k] w[g] [relu > 0]
+ *   d_query_index[g] = sum_k ds[g,k] ki[k];  d_key_index[id_k] += sum_g ds[g,k] qi[g]
+ * query [B,S1,N1,D], key [B,S2,1,D], query_rope / key_rope [..,64] (both NULL with
+ * dr = 0), query_index [B,S1,Nidx1,D_idx], key_index [B,S2,1,D_idx] (io dtype),
+ * weights [B,S1,Nidx1] (w_dtype), sm_max / sm_sum [B,1,S1,N1] fp32 (the forward's
+ * stats), act_q / act_k [B]. Outputs in the inputs' dtypes; loss: one fp32.
+ * D in {128,256,512}, D_idx in {128,256,512}, N1 <= 128, Nidx1 <= 128 with
+ * ceil8(Nidx1) * D_idx <= 32768, sparse_count <= 2048.
+ */
+int dsa_sli_grad_kl_loss(const void* query, const void* key, const void* query_rope, const void* key_rope,
+                         const void* query_index, const void* key_index, const void* weights, int io_dtype,
+                         int w_dtype, const int32_t* sparse_indices, int sparse_count, const float* sm_max,
+                         const float* sm_sum, const int32_t* act_q, const int32_t* act_k, int batch, int s1,
+                         int s2, int n1, int d, int dr, int nidx1, int d_idx, float scale,
+                         void* d_query_index, void* d_key_index, void* d_weights, float* loss,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -146,6 +146,29 @@ def test_grad_validation_matches_reference():
     assert need >= 128 * (512 + 64 + 512) * 4 + 2 * 128 * 64 * 2 and need < (1 << 30)
 
 
+def test_kl_loss_validation_matches_reference():
+    """The reference's host guards (sparse_lightning_indexer_grad_kl_loss_triton.py:510-514)
+    raise ValueError before any device work; CPU tensors are refused."""
+    from dsa_triton_ascend_amd import sparse_lightning_indexer_grad_kl_loss as kl
+    q = torch.zeros(1, 2, 8, 128, dtype=torch.float16)
+    k = torch.zeros(1, 16, 1, 128, dtype=torch.float16)
+    qi = torch.zeros(1, 2, 8, 128, dtype=torch.float16)
+    ki = torch.zeros(1, 16, 1, 128, dtype=torch.float16)
+    w = torch.zeros(1, 2, 8, dtype=torch.float16)
+    si = torch.zeros(1, 2, 1, 4, dtype=torch.int32)
+    sm = torch.zeros(1, 1, 2, 8)
+    with pytest.raises(ValueError, match="BSND"):
+        kl(q, k, qi, ki, w, si, sm, sm, layout="TND")
+    with pytest.raises(ValueError, match="sparse_mode"):
+        kl(q, k, qi, ki, w, si, sm, sm, sparse_mode=0)
+    with pytest.raises(ValueError, match="Nidx2"):
+        kl(q, k, qi, ki, w, si.reshape(1, 2, 4, 1), sm, sm)
+    with pytest.raises(ValueError, match="GPU"):
+        kl(q, k, qi, ki, w, si, sm, sm)
+    lib = _lib.load()
+    assert lib.dsa_sli_grad_workspace_bytes(1, 4, 2048, 1024, 128) >= 4 * 1024 * 4 + 2048 * 128 * 4
+
+
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(RuntimeError, match="missing"):
         _lib.load(tmp_path / "nope.so")

@@ -477,3 +477,58 @@ def test_li_pa_bsnd_equals_depaged_bsnd():
         np.testing.assert_array_equal(got[1], want[1])
     with pytest.raises(ValueError):
         LI.lightning_indexer(q, dense, w, block_table=bt)
+
+
+# ----------------------------------------------------------------- sparse LI grad KL loss
+from oracle import sli_grad_kl_loss_ref as SLI
+
+
+def test_sli_grad_kl_loss_vs_float64_autograd():
+    """Teacher p against torch.softmax over the full causal key range (averaged over
+    heads, gathered at the slots); the loss against scipy's rel_entr; dW, dQI, dKI
+    against float64 autograd of the surrogate -sum p log softmax(I) + (1 - sum p) lse(I),
+    whose gradient in I is the golden's dI = softmax(I) - p. Repeated and out-of-range
+    ids exercise the per-slot scatter and the clipping."""
+    from scipy.special import rel_entr
+    rng = np.random.RandomState(9)
+    B, S1, S2, N1, D, Dr, G, Di, K = 2, 3, 16, 4, 8, 4, 3, 8, 6
+    q, qr = rng.randn(B, S1, N1, D), rng.randn(B, S1, N1, Dr)
+    k, kr = rng.randn(B, S2, 1, D), rng.randn(B, S2, 1, Dr)
+    qi, ki, w = rng.randn(B, S1, G, Di), rng.randn(B, S2, 1, Di), np.abs(rng.randn(B, S1, G))
+    si = rng.randint(0, S2, (B, S1, 1, K))
+    si[0, 2, 0, 1] = si[0, 2, 0, 0]      # a repeated id
+    si[1, 1, 0, 0] = S2 + 3              # clipped to S2 - 1
+    scale = 0.4
+    act_q, act_k = [S1, S1], [S2, 12]
+    # full-row softmax stats over the causal range
+    sm_max = np.zeros((B, 1, S1, N1))
+    sm_sum = np.zeros((B, 1, S1, N1))
+    for b in range(B):
+        for s1 in range(S1):
+            lim = act_k[b] - act_q[b] + s1 + 1
+            sc = (q[b, s1] @ k[b, :lim, 0].T + qr[b, s1] @ kr[b, :lim, 0].T) * scale
+            sm_max[b, 0, s1] = sc.max(1)
+            sm_sum[b, 0, s1] = np.exp(sc - sc.max(1, keepdims=True)).sum(1)
+    got = SLI.sli_grad_kl_loss(q, k, qr, kr, qi, ki, w, si, sm_max, sm_sum, scale, act_q, act_k, io_dtype="fp32")
+
+    tqi, tki, tw = (torch.tensor(x, dtype=torch.float64, requires_grad=True) for x in (qi, ki, w))
+    total, loss_ref = 0.0, 0.0
+    for b in range(B):
+        for s1 in range(S1):
+            lim = act_k[b] - act_q[b] + s1 + 1
+            n = min(K, lim)
+            idx = np.clip(si[b, s1, 0, :n], 0, S2 - 1)
+            # teacher: the causal range's log-sum-exp normalises every key's probability
+            # (a slot past the causal limit still gets exp(score - lse))
+            sc = torch.tensor((q[b, s1] @ k[b, :, 0].T + qr[b, s1] @ kr[b, :, 0].T) * scale)
+            lse = torch.logsumexp(sc[:, :lim], dim=-1, keepdim=True)
+            p = torch.exp(sc - lse).mean(0)[torch.tensor(idx)]
+            ii = (torch.relu(tqi[b, s1] @ tki[b, torch.tensor(idx), 0].T) * tw[b, s1][:, None]).sum(0)
+            lsm = torch.log_softmax(ii, dim=0)
+            total = total - (p * lsm).sum() + (1 - p.sum()) * torch.logsumexp(ii, 0)
+            loss_ref += float(rel_entr(np.maximum(p.numpy(), 1e-8), np.maximum(torch.exp(lsm).detach().numpy(), 1e-8)).sum())
+    total.backward()
+    np.testing.assert_allclose(got[0], tqi.grad.numpy(), rtol=1e-4, atol=1e-5, err_msg="dQI")
+    np.testing.assert_allclose(got[1], tki.grad.numpy(), rtol=1e-4, atol=1e-5, err_msg="dKI")
+    np.testing.assert_allclose(got[2], tw.grad.numpy(), rtol=1e-4, atol=1e-5, err_msg="dW")
+    np.testing.assert_allclose(got[3][0], loss_ref, rtol=1e-4)

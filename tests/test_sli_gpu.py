@@ -1,0 +1,125 @@
+"""GPU parity: sparse_lightning_indexer_grad_kl_loss (HIP) vs the oracle
+(oracle/sli_grad_kl_loss_ref.py).
+
+Shapes from the reference's test_sli_grad_kl_loss_triton.py:16-70 (the rows the
+oracle evaluates in seconds: S1 <= 4 over S2 = 2048), fp16 and bf16, with its
+tolerances (:6, fp16 rtol = atol = 2e-3, bf16 1e-2) and its near-zero rule (:184-189:
+elements below 1e-2 in both results compare as 0). Inputs follow its generator
+(:84-101: randn -> fp16, |randn| weights, random ids in [0, S2)); the softmax stats
+are the full causal forward's (:146-170).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from dsa_triton_ascend_amd import sparse_lightning_indexer_grad_kl_loss
+from oracle import sli_grad_kl_loss_ref as SLI
+
+pytestmark = pytest.mark.gpu
+
+DT = {"bf16": torch.bfloat16, "fp16": torch.float16}
+TOLS = {"fp16": (2e-3, 2e-3), "bf16": (1e-2, 1e-2)}
+NEAR_ZERO = 1e-2
+
+
+def _close(a, b, atol, rtol, what):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    nz = (np.abs(a) < NEAR_ZERO) & (np.abs(b) < NEAR_ZERO)
+    np.testing.assert_allclose(np.where(nz, 0, a), np.where(nz, 0, b), atol=atol, rtol=rtol, err_msg=what)
+
+
+def _inputs(B, S1, S2, N1, D, G, Di, K, dtype, pattern="random", seed=42):
+    rng = np.random.RandomState(seed)
+    h = lambda *s: rng.randn(*s).astype(np.float16)
+    q, k, qr, kr = h(B, S1, N1, D), h(B, S2, 1, D), h(B, S1, N1, 64), h(B, S2, 1, 64)
+    qi, ki = h(B, S1, G, Di), h(B, S2, 1, Di)
+    w = np.abs(rng.randn(B, S1, G)).astype(np.float16)
+    si = rng.randint(0, S2, (B, S1, 1, K)).astype(np.int32)
+    if pattern == "repeated":
+        si[..., 1::2] = si[..., 0::2][..., : si[..., 1::2].shape[-1]]
+    t = lambda x: torch.from_numpy(x).to(DT[dtype])
+    return (t(q), t(k), t(qr), t(kr), t(qi), t(ki), t(w), torch.from_numpy(si))
+
+
+def _stats(q, k, qr, kr, scale, act_q, act_k):
+    """Full causal forward stats (reference test :146-170), float64 then fp32."""
+    f = lambda x: x.double().numpy()
+    q, k, qr, kr = f(q), f(k), f(qr), f(kr)
+    B, S1, N1, _ = q.shape
+    sm_max = np.zeros((B, 1, S1, N1), np.float32)
+    sm_sum = np.zeros((B, 1, S1, N1), np.float32)
+    for b in range(B):
+        for s1 in range(min(S1, act_q[b])):
+            lim = min(max(act_k[b] - act_q[b] + s1 + 1, 0), k.shape[1])
+            if lim <= 0:
+                continue
+            sc = (q[b, s1] @ k[b, :lim, 0].T + qr[b, s1] @ kr[b, :lim, 0].T) * scale
+            m = sc.max(1)
+            sm_max[b, 0, s1] = m
+            sm_sum[b, 0, s1] = np.exp(sc - m[:, None]).sum(1)
+    return torch.from_numpy(sm_max), torch.from_numpy(sm_sum)
+
+
+def run(dev, B, S1, S2, N1, D, G, Di, K, dtype, pattern="random", act_q=None, act_k=None):
+    q, k, qr, kr, qi, ki, w, si = _inputs(B, S1, S2, N1, D, G, Di, K, dtype, pattern)
+    scale = 1.0 / math.sqrt(D)
+    aq = [S1] * B if act_q is None else act_q
+    ak = [S2] * B if act_k is None else act_k
+    smax, ssum = _stats(q, k, qr, kr, scale, aq, ak)
+    g = lambda x: x.to(dev)
+    dqi, dki, dw, loss = sparse_lightning_indexer_grad_kl_loss(
+        g(q), g(k), g(qi), g(ki), g(w), g(si), g(smax), g(ssum), query_rope=g(qr), key_rope=g(kr),
+        actual_seq_qlen=act_q, actual_seq_klen=act_k, scale_value=scale)
+    torch.cuda.synchronize()
+    f = lambda x: x.float().cpu().numpy()
+    want = SLI.sli_grad_kl_loss(f(q), f(k), f(qr), f(kr), f(qi), f(ki), f(w), si.numpy(), smax.numpy(),
+                                ssum.numpy(), scale, aq, ak, io_dtype=dtype)
+    atol, rtol = TOLS[dtype]
+    what = f"B{B} S1={S1} S2={S2} N1={N1} D={D} Nidx1={G} Didx={Di} K={K} {dtype} {pattern}"
+    assert dqi.shape == qi.shape and dki.shape == ki.shape and dw.shape == w.shape and loss.shape == (1,)
+    for name, got, ref in zip(("d_query_index", "d_key_index", "d_weights", "loss"), (dqi, dki, dw, loss), want):
+        assert np.all(np.isfinite(f(got))), f"{what}: {name} not finite"
+        _close(f(got), ref, atol, rtol, f"{what}: {name}")
+
+
+CASES = [
+    (1, 1, 2048, 32, 512, 8, 128, 1024),
+    (1, 4, 2048, 64, 512, 16, 128, 1024),
+    (1, 4, 2048, 128, 512, 32, 128, 1024),
+    (1, 4, 2048, 64, 512, 64, 128, 2048),
+    (1, 4, 2048, 32, 128, 32, 128, 1024),
+    (1, 4, 2048, 64, 256, 64, 256, 1024),
+    (1, 4, 2048, 32, 256, 64, 512, 2048),
+    (1, 4, 2048, 128, 256, 64, 128, 1024),
+    (1, 4, 2048, 128, 128, 32, 512, 2048),
+]
+
+
+@pytest.fixture(scope="module")
+def dev():
+    assert torch.cuda.is_available()
+    return torch.device("cuda:0")
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("B,S1,S2,N1,D,G,Di,K", CASES)
+def test_kl_loss_matrix(dev, B, S1, S2, N1, D, G, Di, K, dtype):
+    run(dev, B, S1, S2, N1, D, G, Di, K, dtype)
+
+
+@pytest.mark.parametrize("pattern", ["random", "repeated"])
+def test_kl_loss_patterns_and_lengths(dev, pattern):
+    """Repeated ids (each slot adds to d_key_index), two batches with actual lengths:
+    rows past act_q get zero gradients, short rows use fewer slots."""
+    run(dev, 2, 4, 1024, 32, 512, 8, 128, 512, "fp16", pattern, act_q=[4, 3], act_k=[1024, 600])
+
+
+def test_kl_loss_unsupported_shape_is_refused(dev):
+    q, k, qr, kr, qi, ki, w, si = _inputs(1, 2, 256, 32, 512, 128, 512, 64, "fp16")
+    sm = torch.zeros(1, 1, 2, 32)
+    with pytest.raises(ValueError, match="outside"):
+        sparse_lightning_indexer_grad_kl_loss(q.to(dev), k.to(dev), qi.to(dev), ki.to(dev), w.to(dev), si.to(dev),
+                                              sm.to(dev), sm.to(dev) + 1, query_rope=qr.to(dev),
+                                              key_rope=kr.to(dev), scale_value=0.05)
