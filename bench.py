@@ -9,8 +9,9 @@ resident in HBM. The same JSON line carries:
   cpu_baseline  -- the numpy oracle (a port of the reference golden) on a stride
                    sample of the same rows, timed on this host;
   breakdown     -- top-k kernel, SFA prefill (config 3), SFA paged decode (config 4),
-                   the SFA backward at the reference's grad perf shape, and the TND
-                   indexer->SFA pipeline (config 5).
+                   the SFA backward at the reference's grad perf shape, the sparse LI
+                   grad KL loss at its target shape, and the TND indexer->SFA pipeline
+                   (config 5).
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick]
 """
@@ -189,6 +190,31 @@ def bench_grad(W, torch):
 GRAD_PAIRS = 512 * 2048
 
 
+def bench_kl(W, torch):
+    """sparse_lightning_indexer_grad_kl_loss at the reference's target shape
+    (test_sli_grad_kl_loss_triton.py:27: B=1, S1=512, S2=4096, N1=64, D=512 + 64 rope,
+    Nidx1=64, D_idx=128, top-k 2048; every row uses 2048 slots). Algorithmic work per
+    slot: teacher 64 x 576 x 2, student I, dQI and dKI 3 x 64 x 128 x 2 FLOP."""
+    from dsa_triton_ascend_amd import sparse_flash_attention
+    from dsa_triton_ascend_amd.sli_grad_kl_loss import KLLossPlan
+    g = W.sfa_grad_inputs(device="cuda:0", seed=42, **W.GRAD_PERF)
+    gen = torch.Generator(device="cuda:0").manual_seed(5)
+    qi = torch.randn(1, 512, 64, 128, device="cuda:0", generator=gen).to(torch.bfloat16)
+    ki = torch.randn(1, 4096, 1, 128, device="cuda:0", generator=gen).to(torch.bfloat16)
+    w = torch.rand(1, 512, 64, device="cuda:0", generator=gen).to(torch.bfloat16)
+    _, smax, ssum = sparse_flash_attention(g.query, g.key, g.key, g.sparse_indices, **g.kwargs())
+    plan = KLLossPlan(g.query, g.key, qi, ki, w, g.sparse_indices, smax, ssum, query_rope=g.query_rope,
+                      key_rope=g.key_rope, scale_value=g.scale_value)
+    warm(plan.run, torch)
+    (ms,) = event_time([plan.run], 10, torch)
+    flop = 512 * 2048 * 2.0 * (64 * 576 + 3 * 64 * 128)
+    res = {"ms": round(ms, 4), "tflops": round(flop / ms / 1e9, 2),
+           "frac_mfma": round(flop / ms / 1e9 / PEAK_BF16_TFLOPS, 4), "algorithmic_flop": flop,
+           "shape": "BSND B=1 S1=512 S2=4096 N1=64 D=512+64 Nidx1=64 D_idx=128 top-k 2048 bf16"}
+    del plan, g, qi, ki, w
+    return res
+
+
 def pmc_pass(torch, W):
     from dsa_triton_ascend_amd.lightning_indexer import IndexerPlan
     from dsa_triton_ascend_amd.sparse_flash_attention import AttentionPlan
@@ -311,6 +337,9 @@ def main():
             torch.cuda.empty_cache()
             log("[bench] SFA backward at the reference's grad perf shape ...")
             breakdown["sfa_grad"] = bench_grad(W, torch)
+            torch.cuda.empty_cache()
+            log("[bench] sparse LI grad KL loss at the reference's target shape ...")
+            breakdown["sli_grad_kl_loss"] = bench_kl(W, torch)
             torch.cuda.empty_cache()
             log("[bench] C5 TND indexer -> SFA pipeline ...")
             breakdown["pipeline_c5"] = bench_pipeline_c5(W, max(3, args.steps // 4), torch)
