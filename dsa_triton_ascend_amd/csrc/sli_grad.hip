@@ -17,8 +17,8 @@
 //     v_mfma_f32_32x32x16 (k-range split over the 4 waves, summed through LDS),
 //     the block's probabilities summed over its heads and added to p[r, k];
 //  3. sli_student_kernel -- one work-group per row: qi in LDS, two passes over
-//     tiles of 32 gathered ki rows in fp32 VALU (I, then softmax / dI / loss, then
-//     dW, dQI in registers and dKI added per slot with fp32 atomics);
+//     tiles of 32 gathered ki rows on 32x32x16 MFMAs (I, then softmax / dI / loss,
+//     then dW, dQI in registers and dKI added per slot with fp32 atomics);
 //  4. sli_finish_kernel -- dKI to the io dtype and the loss (sum of the row
 //     losses, in row order).
 #include <climits>
@@ -34,7 +34,7 @@ constexpr int SWV = 4;      // waves per work-group
 constexpr float SEPS = 1e-8f;
 constexpr float SLOG2E = 1.4426950408889634f;
 constexpr int SLI_MAX_TOPK = 2048;   // student keeps the row's I / dI in LDS
-constexpr int SLI_MAX_GD = 64 * 512; // Nidx1 (padded to 8) x D_idx held in LDS
+constexpr int SLI_MAX_GD = 64 * 512; // Nidx1 (padded to 32) x D_idx held in LDS
 
 inline size_t salign(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -162,90 +162,119 @@ __global__ __launch_bounds__(SWV * 64) void sli_teacher_kernel(SliArgs a) {
 }
 
 // ---------------------------------------------------------------- student
-// Thread t handles token t % 32 of a tile and heads g = t / 32 + 8 j (j < GPT).
-template <int IO, int DI, int GPT>
-__global__ __launch_bounds__(256) void sli_student_kernel(SliArgs a) {
-  constexpr int KIP = DI + 2;   // ki row pitch (elements): rows one bank apart for 4-byte reads
-  constexpr int NQ = DI / 32;   // dQI columns per thread (see the pass-2 ownership note)
-  __shared__ __attribute__((aligned(16))) uint16_t QIs[8 * GPT * DI];
-  __shared__ __attribute__((aligned(16))) uint16_t KIs[SBT * KIP];
-  __shared__ float s_i[SLI_MAX_TOPK];   // I, then dI
-  __shared__ float s_w[8 * GPT];
-  __shared__ float s_ds[8 * GPT][SBT + 1];
-  __shared__ float red[8][SBT + 1];
-  __shared__ float s_red[8];
+// MFMA operand whose K runs down the rows of a row-major 16-bit LDS array X: lane l
+// receives X[k0 + 8 (l / 32) + j][c0 + l % 32], j = 0..7 (two transposed reads).
+__device__ __forceinline__ uint4 s_tr_frag(const uint16_t* X, int pitch, int c0, int k0, int lane) {
+  const int g16 = lane >> 4, c16 = lane & 15;
+  const int col = c0 + (g16 & 1) * 16 + 4 * (c16 & 3);
+  const int k = k0 + (g16 >> 1) * 8 + (c16 >> 2);
+  const uint2 lo = ds_read_tr(X + k * pitch + col);
+  const uint2 hi = ds_read_tr(X + (k + 4) * pitch + col);
+  return make_uint4(lo.x, lo.y, hi.x, hi.y);
+}
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// One work-group (4 waves) per row; wave w < NGB owns indexer heads 32w..32w+31.
+// Per tile of 32 slots: dot^T[slot, head] = ki qi^T on 32x32x16 MFMAs (slots as M),
+// relu * w summed over the heads (half-wave shuffles, then across waves in LDS) is
+// I; in the second pass the same tiles give dW (per lane), ds = dI w [relu > 0]
+// (to LDS as [head][slot], split in two io-dtype parts), dQI[head, col] += ds ki
+// (registers) and dKI[slot, col] = ds^T qi, added at the slot's key row with fp32
+// atomics.
+template <int IO, int DI, int NGB>
+__global__ __launch_bounds__(256) void sli_student_kernel(SliArgs a) {
+  constexpr int GP = 32 * NGB;         // heads, padded to whole blocks
+  constexpr int QIP = DI + 8;          // qi / ki row pitch: odd count of 16-byte units
+  constexpr int DP = SBT + 8;          // ds row pitch
+  constexpr int KS = DI / 16;          // k-steps of the dots
+  constexpr int NCB = DI / 32;         // 32-column blocks of dQI / dKI
+  constexpr int JK = (NCB + SWV - 1) / SWV;   // dKI column blocks per wave, at most
+  __shared__ __attribute__((aligned(16))) uint16_t QIs[GP * QIP];
+  __shared__ __attribute__((aligned(16))) uint16_t KIs[SBT * QIP];
+  // ds = hi + lo, both in the io dtype (hi = ds rounded, lo = the rounding error
+  // rounded): the products use both, so ds keeps ~22 bits through the MFMAs -- the
+  // indexer softmax is sharply peaked, ds reaches |w|, and one 16-bit rounding of it
+  // alone would cost ~2^-11 relative on d_key_index
+  __shared__ __attribute__((aligned(16))) uint16_t dSs[2][GP * DP];
+  __shared__ float s_i[SLI_MAX_TOPK];   // I, then dI
+  __shared__ float s_w[GP];
+  __shared__ float red[SWV][SBT];
+  __shared__ float s_red[SWV];
+  __shared__ int s_tok[SBT];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = blockIdx.x;
   int b, s1;
   const int n = row_slots(a, r, b, s1);
   const int G = a.nidx1;
   uint16_t* dqio = reinterpret_cast<uint16_t*>(a.dqi);
   const int64_t qrow = (int64_t)r * G;
+  auto store_w = [&](int g, float v) {
+    if (a.wdt == DSA_DTYPE_F32) reinterpret_cast<float*>(a.dw)[qrow + g] = v;
+    else if (a.wdt == DSA_DTYPE_BF16) reinterpret_cast<uint16_t*>(a.dw)[qrow + g] = f32_to_bf16_rne(v);
+    else reinterpret_cast<uint16_t*>(a.dw)[qrow + g] = f32_to_f16_rne(v);
+  };
   if (n == 0) {   // no slot: zero gradients, zero loss
     for (int i = tid; i < G * DI; i += 256) dqio[qrow * DI + i] = 0;
-    for (int g = tid; g < G; g += 256) {
-      if (a.wdt == DSA_DTYPE_F32) reinterpret_cast<float*>(a.dw)[qrow + g] = 0.f;
-      else reinterpret_cast<uint16_t*>(a.dw)[qrow + g] = 0;
-    }
+    for (int g = tid; g < G; g += 256) store_w(g, 0.f);
     if (tid == 0) a.row_loss[r] = 0.f;
     return;
   }
   const uint16_t* qib = reinterpret_cast<const uint16_t*>(a.qi);
   const uint16_t* kib = reinterpret_cast<const uint16_t*>(a.ki);
-  for (int i = tid; i < 8 * GPT * DI / 8; i += 256) {
+  const uint4 z4 = make_uint4(0, 0, 0, 0);
+  for (int i = tid; i < GP * (DI / 8); i += 256) {
     const int g = i / (DI / 8), c = (i % (DI / 8)) * 8;
-    *reinterpret_cast<uint4*>(&QIs[g * DI + c]) = g < G ? ldg16(qib + (qrow + g) * DI + c) : make_uint4(0, 0, 0, 0);
+    *reinterpret_cast<uint4*>(&QIs[g * QIP + c]) = g < G ? ldg16(qib + (qrow + g) * DI + c) : z4;
   }
-  for (int g = tid; g < 8 * GPT; g += 256) s_w[g] = g < G ? ld_w(a.w, a.wdt, qrow + g) : 0.f;
+  for (int g = tid; g < GP; g += 256) s_w[g] = g < G ? ld_w(a.w, a.wdt, qrow + g) : 0.f;
   const int32_t* ids = a.sidx + (int64_t)r * a.topk;
-  const int tk = tid & 31, grp = tid >> 5;
 
   auto load_tile = [&](int t0, int nv) {
-    for (int i = tid; i < SBT * (DI / 2); i += 256) {
-      const int t = i / (DI / 2), c = (i % (DI / 2)) * 2;
-      uint32_t v = 0;
-      if (t < nv) {
-        const int64_t kr = (int64_t)b * a.s2 + clip_id(ids[t0 + t], a.s2);
-        v = *reinterpret_cast<const uint32_t*>(kib + kr * DI + c);
-      }
-      *reinterpret_cast<uint32_t*>(&KIs[t * KIP + c]) = v;
+    for (int i = tid; i < SBT * (DI / 8); i += 256) {
+      const int t = i / (DI / 8), c = (i % (DI / 8)) * 8;
+      uint4 v = z4;
+      if (t < nv) v = ldg16(kib + ((int64_t)b * a.s2 + clip_id(ids[t0 + t], a.s2)) * DI + c);
+      *reinterpret_cast<uint4*>(&KIs[t * QIP + c]) = v;
     }
+    if (tid < SBT) s_tok[tid] = tid < nv ? b * a.s2 + clip_id(ids[t0 + tid], a.s2) : -1;
   };
-  // dot[j] = qi[grp + 8 j] . ki[tk] (fp32)
-  auto dots = [&](float (&dv)[GPT]) {
+  // dot^T of this wave's head block over the tile: element e -> slot m32_row(e, lane),
+  // head 32 wave + lane % 32
+  auto dots = [&]() -> f32x16 {
+    f32x16 acc = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const uint16_t* arow = KIs + (lane & 31) * QIP + (lane >> 5) * 8;
+    const uint16_t* brow = QIs + (32 * wave + (lane & 31)) * QIP + (lane >> 5) * 8;
 #pragma unroll
-    for (int j = 0; j < GPT; ++j) dv[j] = 0.f;
-    const uint16_t* kr = KIs + tk * KIP;
-    for (int c = 0; c < DI; c += 2) {
-      const uint32_t kk = *reinterpret_cast<const uint32_t*>(kr + c);
-      const float k0 = to_f32<IO>((uint16_t)(kk & 0xFFFFu)), k1 = to_f32<IO>((uint16_t)(kk >> 16));
-#pragma unroll
-      for (int j = 0; j < GPT; ++j) {
-        const uint32_t qq = *reinterpret_cast<const uint32_t*>(QIs + (grp + 8 * j) * DI + c);
-        dv[j] += to_f32<IO>((uint16_t)(qq & 0xFFFFu)) * k0 + to_f32<IO>((uint16_t)(qq >> 16)) * k1;
-      }
-    }
+    for (int ks = 0; ks < KS; ++ks)
+      acc = Mfma<IO>::m32(*reinterpret_cast<const uint4*>(arow + ks * 16),
+                          *reinterpret_cast<const uint4*>(brow + ks * 16), acc);
+    return acc;
   };
   __syncthreads();
 
-  // ---- pass 1: I[k]
+  // ---- pass 1: I per slot
   for (int t0 = 0; t0 < n; t0 += SBT) {
     const int nv = n - t0 < SBT ? n - t0 : SBT;
     load_tile(t0, nv);
     __syncthreads();
-    float dv[GPT];
-    dots(dv);
-    float acc = 0.f;
+    if (wave < NGB) {
+      const f32x16 acc = dots();
+      const float wg = s_w[32 * wave + (lane & 31)];
 #pragma unroll
-    for (int j = 0; j < GPT; ++j) acc += s_w[grp + 8 * j] * fmaxf(dv[j], 0.f);
-    red[grp][tk] = acc;
+      for (int e = 0; e < 16; ++e) {
+        float v = wg * fmaxf(acc[e], 0.f);
+#pragma unroll
+        for (int o = 16; o >= 1; o >>= 1) v += __shfl_xor(v, o, 32);
+        if ((lane & 31) == 0) red[wave][m32_row(e, lane)] = v;
+      }
+    }
     __syncthreads();
-    if (tid < SBT && tid < nv) {
-      float s = 0.f;
+    if (tid < nv) {
+      float sv = 0.f;
 #pragma unroll
-      for (int gq = 0; gq < 8; ++gq) s += red[gq][tid];
-      s_i[t0 + tid] = s;
+      for (int w = 0; w < NGB; ++w) sv += red[w][tid];
+      s_i[t0 + tid] = sv;
     }
     __syncthreads();
   }
@@ -279,73 +308,82 @@ __global__ __launch_bounds__(256) void sli_student_kernel(SliArgs a) {
   const float row_loss = block_sum(ls);
   if (tid == 0) a.row_loss[r] = row_loss;
 
-  // ---- pass 2: dW, dQI (registers), dKI (atomics)
-  // dQI ownership: thread t holds heads g = t / 32 + 8 j (j < GPT) and columns
-  // c = (t % 32) + 32 q (q < DI / 32)
-  float dqa[GPT][NQ];
+  // ---- pass 2
+  f32x16 dq[NCB];
 #pragma unroll
-  for (int j = 0; j < GPT; ++j)
+  for (int j = 0; j < NCB; ++j)
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) dqa[j][q] = 0.f;
-  float dwa[GPT];
-#pragma unroll
-  for (int j = 0; j < GPT; ++j) dwa[j] = 0.f;
-  float* dka = a.dki_acc;
+    for (int e = 0; e < 16; ++e) dq[j][e] = 0.f;
+  float dwl = 0.f;
   for (int t0 = 0; t0 < n; t0 += SBT) {
     const int nv = n - t0 < SBT ? n - t0 : SBT;
-    __syncthreads();   // previous tile's KIs / s_ds reads done
     load_tile(t0, nv);
     __syncthreads();
-    float dv[GPT];
-    dots(dv);
-    const float di = tk < nv ? s_i[t0 + tk] : 0.f;
+    if (wave < NGB) {
+      const f32x16 acc = dots();
+      const int g = 32 * wave + (lane & 31);
+      const float wg = s_w[g];
 #pragma unroll
-    for (int j = 0; j < GPT; ++j) {
-      const int g = grp + 8 * j;
-      const float rl = fmaxf(dv[j], 0.f);
-      dwa[j] += rl * di;
-      s_ds[g][tk] = dv[j] > 0.f ? di * s_w[g] : 0.f;
-    }
-    __syncthreads();
-    // dQI[g][c] += sum_t ds[g][t] ki[t][c]
-#pragma unroll
-    for (int j = 0; j < GPT; ++j) {
-      const int g = grp + 8 * j;
-      for (int t = 0; t < nv; ++t) {
-        const float dsv = s_ds[g][t];
-#pragma unroll
-        for (int q = 0; q < NQ; ++q) dqa[j][q] += dsv * to_f32<IO>(KIs[t * KIP + tk + 32 * q]);
+      for (int e = 0; e < 16; ++e) {
+        const int tk = m32_row(e, lane);
+        const float di = tk < nv ? s_i[t0 + tk] : 0.f;
+        dwl += fmaxf(acc[e], 0.f) * di;
+        const float ds = acc[e] > 0.f ? di * wg : 0.f;
+        const uint16_t hi = from_f32<IO>(ds);
+        dSs[0][g * DP + tk] = hi;
+        dSs[1][g * DP + tk] = from_f32<IO>(ds - to_f32<IO>(hi));
       }
     }
-    // dKI[id_t][c] += sum_g ds[g][t] qi[g][c]: thread -> (token t = tid / 8, columns
-    // c = tid % 8 + 8 m)
-    {
-      const int t = tid >> 3, c0 = tid & 7;
-      if (t < nv) {
-        const int64_t kr = (int64_t)b * a.s2 + clip_id(ids[t0 + t], a.s2);
-        for (int c = c0; c < DI; c += 8) {
-          float v = 0.f;
-          for (int g = 0; g < G; ++g) v += s_ds[g][t] * to_f32<IO>(QIs[g * DI + c]);
-          unsafeAtomicAdd(dka + kr * DI + c, v);
+    __syncthreads();
+    // dQI[head, col] += ds[head, slot] ki[slot, col]   (this wave's head block)
+    if (wave < NGB) {
+#pragma unroll
+      for (int kq = 0; kq < SBT / 16; ++kq) {
+        const int off = (32 * wave + (lane & 31)) * DP + kq * 16 + (lane >> 5) * 8;
+        const uint4 ah = *reinterpret_cast<const uint4*>(dSs[0] + off);
+        const uint4 al = *reinterpret_cast<const uint4*>(dSs[1] + off);
+#pragma unroll
+        for (int j = 0; j < NCB; ++j) {
+          const uint4 bv = s_tr_frag(KIs, QIP, 32 * j, kq * 16, lane);
+          dq[j] = Mfma<IO>::m32(ah, bv, dq[j]);
+          dq[j] = Mfma<IO>::m32(al, bv, dq[j]);
         }
       }
     }
-  }
-  // ---- epilogue: dQI, dW (summed over the 32 token lanes of each group)
+    // dKI[slot, col] = ds^T qi over the heads, this wave's column blocks
 #pragma unroll
-  for (int j = 0; j < GPT; ++j) {
-    const int g = grp + 8 * j;
-    if (g < G)
+    for (int jj = 0; jj < JK; ++jj) {
+      const int j = wave + SWV * jj;
+      if (j < NCB) {
+        f32x16 c = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int q = 0; q < NQ; ++q) dqio[(qrow + g) * DI + tk + 32 * q] = from_f32<IO>(dqa[j][q]);
-    float v = dwa[j];
+        for (int kq = 0; kq < GP / 16; ++kq) {
+          const uint4 bv = s_tr_frag(QIs, QIP, 32 * j, kq * 16, lane);
+          c = Mfma<IO>::m32(s_tr_frag(dSs[0], DP, 0, kq * 16, lane), bv, c);
+          c = Mfma<IO>::m32(s_tr_frag(dSs[1], DP, 0, kq * 16, lane), bv, c);
+        }
+        float* dst = a.dki_acc + 32 * j + (lane & 31);
 #pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) v += __shfl_xor(v, o, 32);
-    if (tk == 0 && g < G) {
-      if (a.wdt == DSA_DTYPE_F32) reinterpret_cast<float*>(a.dw)[qrow + g] = v;
-      else if (a.wdt == DSA_DTYPE_BF16) reinterpret_cast<uint16_t*>(a.dw)[qrow + g] = f32_to_bf16_rne(v);
-      else reinterpret_cast<uint16_t*>(a.dw)[qrow + g] = f32_to_f16_rne(v);
+        for (int e = 0; e < 16; ++e) {
+          const int kr = s_tok[m32_row(e, lane)];
+          if (kr >= 0) unsafeAtomicAdd(dst + (int64_t)kr * DI, c[e]);
+        }
+      }
     }
+    __syncthreads();   // the next tile overwrites KIs, dSs and s_tok
+  }
+  // ---- epilogue: dQI (element e -> head 32 wave + m32_row(e, lane), column 32 j + lane % 32), dW
+  if (wave < NGB) {
+#pragma unroll
+    for (int j = 0; j < NCB; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int g = 32 * wave + m32_row(e, lane);
+        if (g < G) dqio[(qrow + g) * DI + 32 * j + (lane & 31)] = from_f32<IO>(dq[j][e]);
+      }
+    const float v = dwl + __shfl_xor(dwl, 32);   // the two slot halves of head lane % 32
+    const int g = 32 * wave + lane;
+    if (lane < 32 && g < G) store_w(g, v);
   }
 }
 
@@ -373,19 +411,17 @@ __global__ void sli_finish_kernel(SliArgs a, int64_t n4, int rows) {
   }
 }
 
-// heads per thread: the smallest of 2, 4, 8, 16 covering Nidx1 / 8 (the qi block
-// 8 GPT x DI stays within SLI_MAX_GD elements, checked by the caller)
+// head blocks: the smallest of 1, 2, 4 covering Nidx1 / 32 (the qi block
+// 32 NGB x DI stays within SLI_MAX_GD elements, checked by the caller)
 template <int IO, int DI>
 void launch_student(const SliArgs& a, int rows, hipStream_t s) {
-  const int gpt = (a.nidx1 + 7) / 8;
-  if (gpt <= 2)
+  const int ngb = (a.nidx1 + 31) / 32;
+  if (ngb <= 1)
+    hipLaunchKernelGGL((sli_student_kernel<IO, DI, 1>), dim3(rows), dim3(256), 0, s, a);
+  else if (ngb <= 2)
     hipLaunchKernelGGL((sli_student_kernel<IO, DI, 2>), dim3(rows), dim3(256), 0, s, a);
-  else if (gpt <= 4)
+  else if constexpr (128 * DI <= SLI_MAX_GD)
     hipLaunchKernelGGL((sli_student_kernel<IO, DI, 4>), dim3(rows), dim3(256), 0, s, a);
-  else if (gpt <= 8)
-    hipLaunchKernelGGL((sli_student_kernel<IO, DI, 8>), dim3(rows), dim3(256), 0, s, a);
-  else if constexpr (8 * 16 * DI <= SLI_MAX_GD)
-    hipLaunchKernelGGL((sli_student_kernel<IO, DI, 16>), dim3(rows), dim3(256), 0, s, a);
 }
 
 template <int IO>
@@ -425,7 +461,7 @@ bool sli_grad_supported(int d, int dr, int nidx1, int didx, int topk) {
   const int dt = d + dr;
   const bool dt_ok = dt == 128 || dt == 192 || dt == 256 || dt == 320 || dt == 512 || dt == 576;
   const bool di_ok = didx == 128 || didx == 256 || didx == 512;
-  const int gp = (nidx1 + 7) / 8 * 8;
+  const int gp = (nidx1 + 31) / 32 * 32;
   return dt_ok && di_ok && nidx1 >= 1 && nidx1 <= 128 && topk >= 1 && topk <= dsa::SLI_MAX_TOPK &&
          (int64_t)gp * didx <= dsa::SLI_MAX_GD;
 }
