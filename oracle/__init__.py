@@ -34,4 +34,11 @@ PINNING = {
                                                             "(value a separate leaf) on tiny shapes, modes 0/3, "
                                                             "bs 1/2/4, actual lengths, a -1 inside a scan",
     "sparse_flash_attention_grad_ref.sparse_flash_attention_grad (TND)": "equivalence with per-batch BSND calls",
+    "lightning_indexer_ref.lightning_indexer (PA_BSND)": "equivalence with BSND on the de-paged key cache",
+    "sli_grad_kl_loss_ref.sli_grad_kl_loss": "float64 torch autograd of the KL loss on tiny shapes; the teacher "
+                                             "built from exp(score - lse) over full keys; scipy rel_entr for the loss",
+    "dense_loss_ref.dense_softmax_lse": "log(sum) + max equals scipy logsumexp over the visible keys; "
+                                        "invisible rows keep (-inf, 0)",
+    "dense_loss_ref.dense_loss_backward": "equals the sparse KL loss with every visible key as a slot (N2 = 1); "
+                                          "with N2 = N1 the loss matches a per-head torch softmax teacher",
 }

@@ -532,3 +532,68 @@ def test_sli_grad_kl_loss_vs_float64_autograd():
     np.testing.assert_allclose(got[1], tki.grad.numpy(), rtol=1e-4, atol=1e-5, err_msg="dKI")
     np.testing.assert_allclose(got[2], tw.grad.numpy(), rtol=1e-4, atol=1e-5, err_msg="dW")
     np.testing.assert_allclose(got[3][0], loss_ref, rtol=1e-4)
+
+
+# ----------------------------------------------------------------- dense indexer loss
+from oracle import dense_loss_ref as DLO
+
+
+def test_dense_lse_vs_scipy_logsumexp():
+    from scipy.special import logsumexp
+    rng = np.random.RandomState(10)
+    B, S1, S2, G, Di = 2, 4, 9, 3, 8
+    qi, ki, w = rng.randn(B, S1, G, Di), rng.randn(B, S2, 1, Di), np.abs(rng.randn(B, S1, G))
+    act_q, act_k = [4, 3], [9, 5]
+    mx, sm = DLO.dense_softmax_lse(qi, ki, w, act_q, act_k)
+    for b in range(B):
+        for s1 in range(S1):
+            n = min(max(act_k[b] - act_q[b] + s1 + 1, 0), act_k[b], S2) if s1 < act_q[b] else 0
+            if n == 0:
+                assert mx[b, 0, s1] == -np.inf and sm[b, 0, s1] == 0
+                continue
+            ii = (np.maximum(qi[b, s1] @ ki[b, :n, 0].T, 0) * w[b, s1][:, None]).sum(0)
+            np.testing.assert_allclose(np.log(sm[b, 0, s1]) + mx[b, 0, s1], logsumexp(ii), rtol=1e-5)
+
+
+def test_dense_loss_equals_sparse_loss_over_all_visible_keys():
+    """With one KV head (N2 = 1) the dense loss is the sparse one whose slots are all the
+    visible keys in order (the two differ only by the 1e-8 placement in the indexer
+    softmax); with N2 = N1 the teacher of each head reads its own key head, checked
+    against per-head torch softmax over the causal range."""
+    rng = np.random.RandomState(11)
+    B, S1, S2, N1, D, G, Di = 1, 3, 10, 4, 8, 2, 8
+    q, qr, k, kr = rng.randn(B, S1, N1, D), rng.randn(B, S1, N1, 4), rng.randn(B, S2, 1, D), rng.randn(B, S2, 1, 4)
+    qi, ki, w = rng.randn(B, S1, G, Di), rng.randn(B, S2, 1, Di), np.abs(rng.randn(B, S1, G))
+    scale = 0.3
+    sm_max, sm_sum = np.zeros((B, 1, S1, N1)), np.zeros((B, 1, S1, N1))
+    for s1 in range(S1):
+        lim = S2 - S1 + s1 + 1
+        sc = (q[0, s1] @ k[0, :lim, 0].T + qr[0, s1] @ kr[0, :lim, 0].T) * scale
+        sm_max[0, 0, s1] = sc.max(1)
+        sm_sum[0, 0, s1] = np.exp(sc - sc.max(1, keepdims=True)).sum(1)
+    mxi, smi = DLO.dense_softmax_lse(qi, ki, w)
+    got = DLO.dense_loss_backward(q, k, qr, kr, qi, ki, w, sm_max, sm_sum, mxi, smi, scale, io_dtype="fp32")
+    si = np.tile(np.arange(S2, dtype=np.int32), (B, S1, 1, 1))
+    want = SLI.sli_grad_kl_loss(q, k, qr, kr, qi, ki, w, si, sm_max, sm_sum, scale, io_dtype="fp32")
+    for gv, wv in zip(got, want):
+        np.testing.assert_allclose(gv, wv, rtol=1e-5, atol=1e-7)
+    # grouped heads: N2 = N1, stats [B, N2, S1, 1]
+    k2, kr2 = rng.randn(B, S2, N1, D), rng.randn(B, S2, N1, 4)
+    sm2, ss2 = np.zeros((B, N1, S1, 1)), np.zeros((B, N1, S1, 1))
+    p_ref = []
+    for s1 in range(S1):
+        lim = S2 - S1 + s1 + 1
+        sc = np.stack([(q[0, s1, h] @ k2[0, :lim, h].T + qr[0, s1, h] @ kr2[0, :lim, h].T) * scale for h in range(N1)])
+        sm2[0, :, s1, 0] = sc.max(1)
+        ss2[0, :, s1, 0] = np.exp(sc - sc.max(1, keepdims=True)).sum(1)
+        p_ref.append(torch.softmax(torch.tensor(sc), -1).mean(0).numpy())
+    got2 = DLO.dense_loss_backward(q, k2, qr, kr2, qi, ki, w, sm2, ss2, mxi, smi, scale, io_dtype="fp32")
+    # the teacher enters the loss: recompute it from p_ref and the student of the same rows
+    loss = 0.0
+    for s1 in range(S1):
+        n = S2 - S1 + s1 + 1
+        ii = (np.maximum(qi[0, s1] @ ki[0, :n, 0].T, 0) * w[0, s1][:, None]).sum(0)
+        st = np.exp(ii - mxi[0, 0, s1]) / smi[0, 0, s1]
+        p = np.maximum(p_ref[s1], 1e-8)
+        loss += float(np.sum(p * (np.log(p) - np.log(np.maximum(st, 1e-8)))))
+    np.testing.assert_allclose(got2[3][0], loss, rtol=1e-5)
