@@ -215,6 +215,39 @@ def bench_kl(W, torch):
     return res
 
 
+def bench_dense(torch):
+    """Dense indexer loss at the reference's perf shape (perf_dense_loss_backward_triton.py:18:
+    B=1, S1=512, S2=4096, N1=N2=64, D=128 + 64 rope, Nidx1=64, D_idx=128, fp16): the
+    softmax LSE, then the loss backward with those stats. Every row s1 sees
+    4096 - 512 + s1 + 1 keys; algorithmic work per key: LSE 64 x 128 x 2, loss teacher
+    64 x 192 x 2 plus student I, dQI and dKI 3 x 64 x 128 x 2 FLOP."""
+    from dsa_triton_ascend_amd.dense_loss import DenseLossPlan, dense_lightning_indexer_softmax_lse
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(11)
+    r = lambda *s: torch.randn(*s, device=dev, generator=gen).to(torch.float16)
+    B, S1, S2, N1, D, Nidx1, Didx = 1, 512, 4096, 64, 128, 64, 128
+    q, k, qr, kr = r(B, S1, N1, D), r(B, S2, N1, D), r(B, S1, N1, 64), r(B, S2, N1, 64)
+    qi, ki = r(B, S1, Nidx1, Didx), r(B, S2, 1, Didx)
+    w = torch.rand(B, S1, Nidx1, device=dev, generator=gen).to(torch.float16)
+    smax = torch.zeros(B, N1, S1, 1, device=dev)
+    ssum = torch.full((B, N1, S1, 1), 64.0, device=dev)
+    lse = lambda: dense_lightning_indexer_softmax_lse(qi, ki, w)
+    mxi, smi = lse()
+    plan = DenseLossPlan(q, k, qi, ki, w, smax, ssum, mxi, smi, 1.0 / 192 ** 0.5, qr, kr)
+    warm(plan.run, torch)
+    warm(lse, torch)
+    ms_lse, ms = event_time([lse, plan.run], 10, torch)
+    keys = sum(S2 - S1 + s1 + 1 for s1 in range(S1))
+    f_lse = keys * 64 * 128 * 2.0
+    f_loss = keys * 2.0 * (64 * 192 + 3 * 64 * 128)
+    res = {"lse_ms": round(ms_lse, 4), "lse_tflops": round(f_lse / ms_lse / 1e9, 2),
+           "loss_ms": round(ms, 4), "loss_tflops": round(f_loss / ms / 1e9, 2),
+           "frac_mfma": round(f_loss / ms / 1e9 / PEAK_BF16_TFLOPS, 4), "algorithmic_flop": f_loss,
+           "shape": "BSND B=1 S1=512 S2=4096 N1=N2=64 D=128+64 Nidx1=64 D_idx=128 fp16"}
+    del plan, q, k, qr, kr, qi, ki, w
+    return res
+
+
 def pmc_pass(torch, W):
     from dsa_triton_ascend_amd.lightning_indexer import IndexerPlan
     from dsa_triton_ascend_amd.sparse_flash_attention import AttentionPlan
@@ -340,6 +373,7 @@ def main():
             torch.cuda.empty_cache()
             log("[bench] sparse LI grad KL loss at the reference's target shape ...")
             breakdown["sli_grad_kl_loss"] = bench_kl(W, torch)
+            breakdown["dense_li_loss"] = bench_dense(torch)
             torch.cuda.empty_cache()
             log("[bench] C5 TND indexer -> SFA pipeline ...")
             breakdown["pipeline_c5"] = bench_pipeline_c5(W, max(3, args.steps // 4), torch)

@@ -19,7 +19,15 @@ from .pipeline import PrefillPlan, dsa_prefill
 from .sparse_flash_attention import SparseFlashAttention, sparse_flash_attention
 from .sparse_flash_attention_grad import SparseFlashAttentionGrad, sparse_flash_attention_grad
 from .sli_grad_kl_loss import SparseLightningIndexerGradKLLoss, sparse_lightning_indexer_grad_kl_loss
+from .dense_loss import (DenseLightningIndexerGradKLLoss, DenseLightningIndexerSoftmaxLse, DenseLossBackward,
+                         dense_lightning_indexer_grad_kl_loss, dense_lightning_indexer_softmax_lse,
+                         dense_loss_backward, npu_dense_lightning_indexer_grad_kl_loss,
+                         npu_dense_lightning_indexer_softmax_lse)
 
 __all__ = ["lightning_indexer", "LightningIndexer", "sparse_flash_attention", "SparseFlashAttention",
            "sparse_flash_attention_grad", "SparseFlashAttentionGrad", "sparse_lightning_indexer_grad_kl_loss",
-           "SparseLightningIndexerGradKLLoss", "PrefillPlan", "dsa_prefill"]
+           "SparseLightningIndexerGradKLLoss", "dense_lightning_indexer_softmax_lse",
+           "npu_dense_lightning_indexer_softmax_lse", "dense_loss_backward",
+           "dense_lightning_indexer_grad_kl_loss", "npu_dense_lightning_indexer_grad_kl_loss",
+           "DenseLightningIndexerSoftmaxLse", "DenseLossBackward", "DenseLightningIndexerGradKLLoss",
+           "PrefillPlan", "dsa_prefill"]

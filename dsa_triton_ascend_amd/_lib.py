@@ -40,6 +40,10 @@ SIGNATURES = {
     "dsa_sli_grad_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
     "dsa_sli_grad_kl_loss": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I,
                                   _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _SZ, _P]),
+    "dsa_dense_li_softmax_lse": (_I, [_P, _P, _P, _I, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P]),
+    "dsa_dense_li_grad_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
+    "dsa_dense_li_grad_kl_loss": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I,
+                                       _I, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _SZ, _P]),
     "dsa_sfa_bwd_workspace_bytes": (_SZ, [_I, _P, _P, _I, _I, _I, _I, _I, _I, _I64]),
     "dsa_sfa_bwd": (_I, [_P, _P, _P, _P, _I, _P, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I,
                          _I, _I64, _I, _F, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),

@@ -289,4 +289,71 @@ int dsa_sli_grad_kl_loss(const void* query, const void* key, const void* query_r
                     "dsa_sli_grad_kl_loss launch");
 }
 
+size_t dsa_dense_li_grad_workspace_bytes(int batch, int s1, int s2, int d_idx) {
+  if (batch <= 0 || s1 < 0 || s2 <= 0 || d_idx <= 0) return 0;
+  return sli_grad_workspace_bytes(batch * s1, s2, (int64_t)batch * s2, d_idx);
+}
+
+int dsa_dense_li_softmax_lse(const void* query_index, const void* key_index, const void* weights, int io_dtype,
+                             int w_dtype, const int32_t* act_q, const int32_t* act_k, int batch, int s1, int s2,
+                             int nidx1, int d_idx, float* softmax_max_index, float* softmax_sum_index,
+                             void* stream) {
+  if (!query_index || !key_index || !weights || !act_q || !act_k || !softmax_max_index || !softmax_sum_index)
+    return fail(DSA_ERR_INVALID, "dsa_dense_li_softmax_lse: null pointer argument");
+  if (!is16(io_dtype)) return fail(DSA_ERR_INVALID, "dsa_dense_li_softmax_lse: io_dtype must be fp16 or bf16");
+  if (!is16(w_dtype) && w_dtype != DSA_DTYPE_F32)
+    return fail(DSA_ERR_INVALID, "dsa_dense_li_softmax_lse: weights dtype must be fp16, bf16 or fp32");
+  if (batch <= 0 || s1 < 0 || s2 <= 0) return fail(DSA_ERR_INVALID, "dsa_dense_li_softmax_lse: non-positive shape");
+  if (!dense_li_grad_supported(1, 1, 128, 0, nidx1, d_idx, s2))
+    return fail(DSA_ERR_UNSUPPORTED,
+                "dsa_dense_li_softmax_lse: Nidx1=%d, D_idx=%d, S2=%d outside D_idx in {128,256,512}, Nidx1 <= 128 "
+                "with ceil32(Nidx1)*D_idx <= 32768, S2 <= 4096", nidx1, d_idx, s2);
+  if (batch > 65535 || (int64_t)batch * s1 > INT32_MAX)
+    return fail(DSA_ERR_UNSUPPORTED, "dsa_dense_li_softmax_lse: too many rows");
+  if (batch * s1 == 0) return DSA_OK;
+  return hip_status(launch_dense_li_lse(query_index, key_index, weights, io_dtype, w_dtype, act_q, act_k, batch,
+                                        s1, s2, nidx1, d_idx, softmax_max_index, softmax_sum_index,
+                                        (hipStream_t)stream),
+                    "dsa_dense_li_softmax_lse launch");
+}
+
+int dsa_dense_li_grad_kl_loss(const void* query, const void* key, const void* query_rope, const void* key_rope,
+                              const void* query_index, const void* key_index, const void* weights, int io_dtype,
+                              int w_dtype, const float* sm_max, const float* sm_sum, const float* max_index,
+                              const float* sum_index, const int32_t* act_q, const int32_t* act_k, int batch,
+                              int s1, int s2, int n1, int n2, int d, int dr, int nidx1, int d_idx, float scale,
+                              void* d_query_index, void* d_key_index, void* d_weights, float* loss,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  if (!query || !key || !query_index || !key_index || !weights || !sm_max || !sm_sum || !act_q || !act_k ||
+      !d_query_index || !d_key_index || !d_weights || !loss || !workspace ||
+      (dr > 0 && (!query_rope || !key_rope)) || (!max_index != !sum_index))
+    return fail(DSA_ERR_INVALID, "dsa_dense_li_grad_kl_loss: null pointer argument");
+  if (!is16(io_dtype)) return fail(DSA_ERR_INVALID, "dsa_dense_li_grad_kl_loss: io_dtype must be fp16 or bf16");
+  if (!is16(w_dtype) && w_dtype != DSA_DTYPE_F32)
+    return fail(DSA_ERR_INVALID, "dsa_dense_li_grad_kl_loss: weights dtype must be fp16, bf16 or fp32");
+  if (batch <= 0 || s1 < 0 || s2 <= 0 || n1 <= 0 || n2 <= 0)
+    return fail(DSA_ERR_INVALID, "dsa_dense_li_grad_kl_loss: non-positive shape");
+  if (n1 % n2 != 0) return fail(DSA_ERR_INVALID, "dsa_dense_li_grad_kl_loss: N1=%d not divisible by N2=%d", n1, n2);
+  if (n1 > 128) return fail(DSA_ERR_UNSUPPORTED, "dsa_dense_li_grad_kl_loss: N1=%d > 128", n1);
+  if (dr != 0 && dr != 64) return fail(DSA_ERR_INVALID, "rope dim must be 64 (or 0 without rope), got %d", dr);
+  if (!dense_li_grad_supported(n1, n2, d, dr, nidx1, d_idx, s2))
+    return fail(DSA_ERR_UNSUPPORTED,
+                "dsa_dense_li_grad_kl_loss: D=%d (+%d), N1=%d, N2=%d, Nidx1=%d, D_idx=%d, S2=%d outside D, D_idx in "
+                "{128,256,512}, Nidx1 <= 128 with ceil32(Nidx1)*D_idx <= 32768, S2 <= 4096, "
+                "ceil8(N1/N2)*(D+Dr) <= 24576 for N2 > 1", d, dr, n1, n2, nidx1, d_idx, s2);
+  if (batch > 65535 || (int64_t)batch * s1 > INT32_MAX)
+    return fail(DSA_ERR_UNSUPPORTED, "dsa_dense_li_grad_kl_loss: too many rows");
+  const size_t need = sli_grad_workspace_bytes(batch * s1, s2, (int64_t)batch * s2, d_idx);
+  if (workspace_bytes < need)
+    return fail(DSA_ERR_INVALID, "dsa_dense_li_grad_kl_loss: workspace of %zu bytes required, %zu given", need,
+                workspace_bytes);
+  if (batch * s1 == 0) return DSA_OK;
+  return hip_status(launch_dense_li_grad(query, key, query_rope ? query_rope : query, key_rope ? key_rope : key,
+                                         query_index, key_index, weights, io_dtype, w_dtype, sm_max, sm_sum,
+                                         max_index, sum_index, act_q, act_k, batch, s1, s2, n1, n2, d, dr, nidx1,
+                                         d_idx, scale, d_query_index, d_key_index, d_weights, loss, workspace,
+                                         (hipStream_t)stream),
+                    "dsa_dense_li_grad_kl_loss launch");
+}
+
 }  // extern "C"

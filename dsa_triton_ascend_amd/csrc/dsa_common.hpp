@@ -253,3 +253,15 @@ hipError_t launch_sli_grad(const void* q, const void* k, const void* qr, const v
                            const int32_t* act_k, int batch, int s1, int s2, int n1, int d, int dr,
                            int nidx1, int didx, float scale, void* dqi, void* dki, void* dw, float* loss,
                            void* ws, hipStream_t s);
+// dense lightning-indexer loss (BSND): every visible key is a slot; workspace as the
+// sparse loss with topk = s2
+bool dense_li_grad_supported(int n1, int n2, int d, int dr, int nidx1, int didx, int s2);
+hipError_t launch_dense_li_lse(const void* qi, const void* ki, const void* w, int io, int wdt,
+                               const int32_t* act_q, const int32_t* act_k, int batch, int s1, int s2,
+                               int nidx1, int didx, float* out_max, float* out_sum, hipStream_t s);
+hipError_t launch_dense_li_grad(const void* q, const void* k, const void* qr, const void* kr, const void* qi,
+                                const void* ki, const void* w, int io, int wdt, const float* sm_max,
+                                const float* sm_sum, const float* max_index, const float* sum_index,
+                                const int32_t* act_q, const int32_t* act_k, int batch, int s1, int s2, int n1,
+                                int n2, int d, int dr, int nidx1, int didx, float scale, void* dqi, void* dki,
+                                void* dw, float* loss, void* ws, hipStream_t s);

@@ -33,7 +33,9 @@ constexpr int SBT = 32;     // tokens per tile
 constexpr int SWV = 4;      // waves per work-group
 constexpr float SEPS = 1e-8f;
 constexpr float SLOG2E = 1.4426950408889634f;
-constexpr int SLI_MAX_TOPK = 2048;   // student keeps the row's I / dI in LDS
+constexpr int SLI_MAX_TOPK = 2048;   // sparse slots per row
+constexpr int SLI_MAX_SLOTS = 4096;  // student keeps the row's I / dI in LDS (dense: S2)
+constexpr int SLI_GQA_MAX_Q = 24576; // GQA teacher: G x (D + Dr) fp32 query elements in LDS
 constexpr int SLI_MAX_GD = 64 * 512; // Nidx1 (padded to 32) x D_idx held in LDS
 
 inline size_t salign(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -49,7 +51,12 @@ struct SliArgs {
   float* p;        // [rows, topk] teacher sums
   float* dki_acc;  // [batch * s2, didx]
   float* row_loss; // [rows]
+  // dense mode (sidx == nullptr: slot t is key t, up to S2 slots per row)
+  int n2;                              // key heads of the teacher, stats [B, N2, S1, N1 / N2]
+  const float* imax; const float* isum; // given indexer softmax stats [rows], or nullptr
+  float* lse_max; float* lse_sum;       // set: the student only writes the stats
 };
+
 
 __device__ __forceinline__ int row_slots(const SliArgs& a, int r, int& b, int& s1) {
   b = r / a.s1;
@@ -62,6 +69,9 @@ __device__ __forceinline__ int row_slots(const SliArgs& a, int r, int& b, int& s
 }
 
 __device__ __forceinline__ int clip_id(int id, int s2) { return id < 0 ? 0 : (id > s2 - 1 ? s2 - 1 : id); }
+__device__ __forceinline__ int slot_key(const SliArgs& a, const int32_t* ids, int t) {
+  return ids ? clip_id(ids[t], a.s2) : t;
+}
 
 __device__ __forceinline__ float ld_w(const void* w, int wdt, int64_t i) {
   if (wdt == DSA_DTYPE_F32) return reinterpret_cast<const float*>(w)[i];
@@ -118,7 +128,7 @@ __global__ __launch_bounds__(SWV * 64) void sli_teacher_kernel(SliArgs a) {
     s_m[tid] = m * SLOG2E;
     s_il[tid] = il;
   }
-  const int32_t* ids = a.sidx + (int64_t)r * a.topk;
+  const int32_t* ids = a.sidx ? a.sidx + (int64_t)r * a.topk : nullptr;
   const float sl2 = a.scale * SLOG2E, inv_n1 = 1.f / a.n1;
   for (int t0 = 0; t0 < n; t0 += SBT) {
     const int nv = n - t0 < SBT ? n - t0 : SBT;
@@ -126,7 +136,7 @@ __global__ __launch_bounds__(SWV * 64) void sli_teacher_kernel(SliArgs a) {
       const int t = i / (DT / 8), c = (i % (DT / 8)) * 8;
       uint4 v = z4;
       if (t < nv) {
-        const int64_t kr = (int64_t)b * a.s2 + clip_id(ids[t0 + t], a.s2);
+        const int64_t kr = (int64_t)b * a.s2 + slot_key(a, ids, t0 + t);
         v = c < D ? ldg16(kb + kr * D + c) : ldg16(krb + kr * a.dr + (c - D));
       }
       *reinterpret_cast<uint4*>(&Ks[t * QP + c]) = v;
@@ -158,6 +168,75 @@ __global__ __launch_bounds__(SWV * 64) void sli_teacher_kernel(SliArgs a) {
       if ((lane & 31) == 0 && tk < nv) unsafeAtomicAdd(a.p + (int64_t)r * a.topk + t0 + tk, pr * inv_n1);
     }
     __syncthreads();   // the next tile overwrites Ks and part
+  }
+}
+
+// Dense teacher over grouped key heads (N2 > 1): work-group (row, key head), one
+// thread per visible key; the G = N1 / N2 query heads of the key head sit in LDS as
+// fp32 (pre-scaled by scale log2 e); each thread reads its key row once per chunk of
+// GC heads and adds (1/N1) sum_g exp(score_g - max_g) / (sum_g + eps) at slot t.
+template <int IO, int GC>
+__global__ __launch_bounds__(256) void sli_teacher_gqa_kernel(SliArgs a) {
+  constexpr int QF = GC == 1 ? 576 : SLI_GQA_MAX_Q;   // one head: D + Dr <= 576
+  __shared__ float Qf[QF];
+  __shared__ float s_m[QF / 128], s_il[QF / 128];
+  const int tid = threadIdx.x;
+  const int r = blockIdx.x, kvh = blockIdx.y;
+  int b, s1;
+  const int n = row_slots(a, r, b, s1);
+  if (n == 0) return;
+  const int G = a.n1 / a.n2, GP = (G + GC - 1) / GC * GC, D = a.d, DT = a.d + a.dr;
+  const uint16_t* qb = reinterpret_cast<const uint16_t*>(a.q);
+  const uint16_t* qrb = reinterpret_cast<const uint16_t*>(a.qr);
+  const uint16_t* kb = reinterpret_cast<const uint16_t*>(a.k);
+  const uint16_t* krb = reinterpret_cast<const uint16_t*>(a.kr);
+  const float sl2 = a.scale * SLOG2E;
+  for (int i = tid; i < GP * DT; i += 256) {
+    const int g = i / DT, c = i - g * DT;
+    float v = 0.f;
+    if (g < G) {
+      const int64_t hr = (int64_t)r * a.n1 + kvh * G + g;
+      v = to_f32<IO>(c < D ? qb[hr * D + c] : qrb[hr * a.dr + (c - D)]);
+    }
+    Qf[i] = v * sl2;
+  }
+  for (int g = tid; g < GP; g += 256) {
+    float m = 0.f, il = 0.f;
+    if (g < G) {
+      const int64_t si = (((int64_t)b * a.n2 + kvh) * a.s1 + s1) * G + g;
+      m = a.sm_max[si];
+      il = 1.f / (a.sm_sum[si] + SEPS);
+    }
+    s_m[g] = m * SLOG2E;
+    s_il[g] = il;
+  }
+  __syncthreads();
+  const float inv_n1 = 1.f / a.n1;
+  for (int t = tid; t < n; t += 256) {
+    const int64_t kr = ((int64_t)b * a.s2 + t) * a.n2 + kvh;
+    float pr = 0.f;
+    for (int g0 = 0; g0 < GP; g0 += GC) {
+      float acc[GC];
+#pragma unroll
+      for (int j = 0; j < GC; ++j) acc[j] = 0.f;
+      auto part = [&](const uint16_t* src, int len, int qoff) {
+        for (int c = 0; c < len; c += 8) {
+          const uint4 kv = ldg16(src + c);
+          const uint32_t w4[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float kf = to_f32<IO>((uint16_t)(w4[e >> 1] >> (16 * (e & 1))));
+#pragma unroll
+            for (int j = 0; j < GC; ++j) acc[j] += kf * Qf[(g0 + j) * DT + qoff + c + e];
+          }
+        }
+      };
+      part(kb + kr * D, D, 0);
+      if (a.dr > 0) part(krb + kr * a.dr, a.dr, D);
+#pragma unroll
+      for (int j = 0; j < GC; ++j) pr += __builtin_amdgcn_exp2f(acc[j] - s_m[g0 + j]) * s_il[g0 + j];
+    }
+    unsafeAtomicAdd(a.p + (int64_t)r * a.topk + t, pr * inv_n1);
   }
 }
 
@@ -195,7 +274,7 @@ __global__ __launch_bounds__(256) void sli_student_kernel(SliArgs a) {
   // indexer softmax is sharply peaked, ds reaches |w|, and one 16-bit rounding of it
   // alone would cost ~2^-11 relative on d_key_index
   __shared__ __attribute__((aligned(16))) uint16_t dSs[2][GP * DP];
-  __shared__ float s_i[SLI_MAX_TOPK];   // I, then dI
+  __shared__ float s_i[SLI_MAX_SLOTS];  // I, then dI
   __shared__ float s_w[GP];
   __shared__ float red[SWV][SBT];
   __shared__ float s_red[SWV];
@@ -214,7 +293,13 @@ __global__ __launch_bounds__(256) void sli_student_kernel(SliArgs a) {
     else if (a.wdt == DSA_DTYPE_BF16) reinterpret_cast<uint16_t*>(a.dw)[qrow + g] = f32_to_bf16_rne(v);
     else reinterpret_cast<uint16_t*>(a.dw)[qrow + g] = f32_to_f16_rne(v);
   };
-  if (n == 0) {   // no slot: zero gradients, zero loss
+  const bool lse_only = a.lse_max != nullptr;
+  if (lse_only && n == 0) {
+    if (tid == 0) { a.lse_max[r] = -INFINITY; a.lse_sum[r] = 0.f; }
+    return;
+  }
+  // no slot, or (dense, given stats) an empty indexer softmax: zero gradients, zero loss
+  if (n == 0 || (a.isum && !(a.isum[r] > 0.f))) {
     for (int i = tid; i < G * DI; i += 256) dqio[qrow * DI + i] = 0;
     for (int g = tid; g < G; g += 256) store_w(g, 0.f);
     if (tid == 0) a.row_loss[r] = 0.f;
@@ -228,16 +313,16 @@ __global__ __launch_bounds__(256) void sli_student_kernel(SliArgs a) {
     *reinterpret_cast<uint4*>(&QIs[g * QIP + c]) = g < G ? ldg16(qib + (qrow + g) * DI + c) : z4;
   }
   for (int g = tid; g < GP; g += 256) s_w[g] = g < G ? ld_w(a.w, a.wdt, qrow + g) : 0.f;
-  const int32_t* ids = a.sidx + (int64_t)r * a.topk;
+  const int32_t* ids = a.sidx ? a.sidx + (int64_t)r * a.topk : nullptr;
 
   auto load_tile = [&](int t0, int nv) {
     for (int i = tid; i < SBT * (DI / 8); i += 256) {
       const int t = i / (DI / 8), c = (i % (DI / 8)) * 8;
       uint4 v = z4;
-      if (t < nv) v = ldg16(kib + ((int64_t)b * a.s2 + clip_id(ids[t0 + t], a.s2)) * DI + c);
+      if (t < nv) v = ldg16(kib + ((int64_t)b * a.s2 + slot_key(a, ids, t0 + t)) * DI + c);
       *reinterpret_cast<uint4*>(&KIs[t * QIP + c]) = v;
     }
-    if (tid < SBT) s_tok[tid] = tid < nv ? b * a.s2 + clip_id(ids[t0 + tid], a.s2) : -1;
+    if (tid < SBT) s_tok[tid] = tid < nv ? b * a.s2 + slot_key(a, ids, t0 + tid) : -1;
   };
   // dot^T of this wave's head block over the tile: element e -> slot m32_row(e, lane),
   // head 32 wave + lane % 32
@@ -287,16 +372,29 @@ __global__ __launch_bounds__(256) void sli_student_kernel(SliArgs a) {
     __syncthreads();
     return t;
   };
-  float mx = -INFINITY;
-  for (int k = tid; k < n; k += 256) mx = fmaxf(mx, s_i[k]);
-  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-  if (lane == 0) s_red[wave] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-  __syncthreads();
-  float es = 0.f;
-  for (int k = tid; k < n; k += 256) es += expf(s_i[k] - mx);
-  const float inv = 1.f / (block_sum(es) + SEPS);
+  // sparse: sI = e / (sum e + eps); dense: sI = e / max(sum e, eps), with the given
+  // stats when the caller has them
+  float mx, inv;
+  if (a.isum) {
+    mx = a.imax[r];
+    inv = 1.f / fmaxf(a.isum[r], SEPS);
+  } else {
+    mx = -INFINITY;
+    for (int k = tid; k < n; k += 256) mx = fmaxf(mx, s_i[k]);
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if (lane == 0) s_red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    __syncthreads();
+    float es = 0.f;
+    for (int k = tid; k < n; k += 256) es += expf(s_i[k] - mx);
+    es = block_sum(es);
+    if (lse_only) {
+      if (tid == 0) { a.lse_max[r] = mx; a.lse_sum[r] = es; }
+      return;
+    }
+    inv = ids ? 1.f / (es + SEPS) : 1.f / fmaxf(es, SEPS);
+  }
   float ls = 0.f;
   for (int k = tid; k < n; k += 256) {
     const float sv = expf(s_i[k] - mx) * inv;
@@ -427,8 +525,21 @@ void launch_student(const SliArgs& a, int rows, hipStream_t s) {
 template <int IO>
 hipError_t launch_sli_io(const SliArgs& a, hipStream_t s) {
   const int rows = a.batch * a.s1;
+  if (a.lse_max) {   // stats only: the student's first pass
+    switch (a.didx) {
+      case 128: launch_student<IO, 128>(a, rows, s); break;
+      case 256: launch_student<IO, 256>(a, rows, s); break;
+      case 512: launch_student<IO, 512>(a, rows, s); break;
+      default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+  }
   const dim3 tgrid(rows, (a.n1 + SBH - 1) / SBH);
-  switch (a.d + a.dr) {
+  if (a.n2 > 1) {
+    const dim3 ggrid(rows, a.n2);
+    if (a.n1 == a.n2) hipLaunchKernelGGL((sli_teacher_gqa_kernel<IO, 1>), ggrid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((sli_teacher_gqa_kernel<IO, 8>), ggrid, dim3(256), 0, s, a);
+  } else switch (a.d + a.dr) {
     case 128: hipLaunchKernelGGL((sli_teacher_kernel<IO, 128>), tgrid, dim3(256), 0, s, a); break;
     case 192: hipLaunchKernelGGL((sli_teacher_kernel<IO, 192>), tgrid, dim3(256), 0, s, a); break;
     case 256: hipLaunchKernelGGL((sli_teacher_kernel<IO, 256>), tgrid, dim3(256), 0, s, a); break;
@@ -466,6 +577,55 @@ bool sli_grad_supported(int d, int dr, int nidx1, int didx, int topk) {
          (int64_t)gp * didx <= dsa::SLI_MAX_GD;
 }
 
+namespace {
+// workspace: teacher sums [rows, topk] | dKI accumulator [batch s2, didx] | row losses
+hipError_t run_sli(dsa::SliArgs a, void* ws, hipStream_t s) {
+  const int rows = a.batch * a.s1;
+  char* base = reinterpret_cast<char*>(ws);
+  a.p = reinterpret_cast<float*>(base);
+  size_t off = dsa::salign((size_t)rows * a.topk * 4);
+  a.dki_acc = reinterpret_cast<float*>(base + off);
+  off += dsa::salign((size_t)a.batch * a.s2 * a.didx * 4);
+  a.row_loss = reinterpret_cast<float*>(base + off);
+  // teacher sums and the dKI accumulator are contiguous up to the padding
+  const int64_t n4 = (int64_t)off / 16;
+  const int blocks = (int)((n4 + 255) / 256 < 4096 ? ((n4 + 255) / 256 > 0 ? (n4 + 255) / 256 : 1) : 4096);
+  hipLaunchKernelGGL(dsa::sli_zero_kernel, dim3(blocks), dim3(256), 0, s, reinterpret_cast<float4*>(base), n4);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return a.io == dsa::IO_BF16 ? dsa::launch_sli_io<dsa::IO_BF16>(a, s) : dsa::launch_sli_io<dsa::IO_F16>(a, s);
+}
+}  // namespace
+
+bool dense_li_grad_supported(int n1, int n2, int d, int dr, int nidx1, int didx, int s2) {
+  if (n2 < 1 || n1 % n2 != 0 || s2 < 1 || s2 > dsa::SLI_MAX_SLOTS) return false;
+  if (!sli_grad_supported(d, dr, nidx1, didx, 1)) return false;
+  const int g = n1 / n2, gp = g == 1 ? 1 : (g + 7) / 8 * 8;
+  return n2 == 1 || (int64_t)gp * (d + dr) <= dsa::SLI_GQA_MAX_Q;
+}
+
+hipError_t launch_dense_li_lse(const void* qi, const void* ki, const void* w, int io, int wdt,
+                               const int32_t* act_q, const int32_t* act_k, int batch, int s1, int s2,
+                               int nidx1, int didx, float* out_max, float* out_sum, hipStream_t s) {
+  dsa::SliArgs a{};
+  a.qi = qi; a.ki = ki; a.w = w; a.io = io; a.wdt = wdt; a.topk = s2;
+  a.act_q = act_q; a.act_k = act_k; a.batch = batch; a.s1 = s1; a.s2 = s2; a.n1 = 1; a.n2 = 1;
+  a.nidx1 = nidx1; a.didx = didx; a.lse_max = out_max; a.lse_sum = out_sum;
+  return io == dsa::IO_BF16 ? dsa::launch_sli_io<dsa::IO_BF16>(a, s) : dsa::launch_sli_io<dsa::IO_F16>(a, s);
+}
+
+hipError_t launch_dense_li_grad(const void* q, const void* k, const void* qr, const void* kr, const void* qi,
+                                const void* ki, const void* w, int io, int wdt, const float* sm_max,
+                                const float* sm_sum, const float* max_index, const float* sum_index,
+                                const int32_t* act_q, const int32_t* act_k, int batch, int s1, int s2, int n1,
+                                int n2, int d, int dr, int nidx1, int didx, float scale, void* dqi, void* dki,
+                                void* dw, float* loss, void* ws, hipStream_t s) {
+  dsa::SliArgs a{q, k, qr, kr, qi, ki, w, io, wdt, nullptr, s2, sm_max, sm_sum, act_q, act_k,
+                 batch, s1, s2, n1, d, dr, nidx1, didx, scale, dqi, dki, dw, loss,
+                 nullptr, nullptr, nullptr, n2, max_index, sum_index, nullptr, nullptr};
+  return run_sli(a, ws, s);
+}
+
 hipError_t launch_sli_grad(const void* q, const void* k, const void* qr, const void* kr, const void* qi,
                            const void* ki, const void* w, int io, int wdt, const int32_t* sidx, int topk,
                            const float* sm_max, const float* sm_sum, const int32_t* act_q,
@@ -475,18 +635,6 @@ hipError_t launch_sli_grad(const void* q, const void* k, const void* qr, const v
   dsa::SliArgs a{q, k, qr, kr, qi, ki, w, io, wdt, sidx, topk, sm_max, sm_sum, act_q, act_k,
                  batch, s1, s2, n1, d, dr, nidx1, didx, scale, dqi, dki, dw, loss,
                  nullptr, nullptr, nullptr};
-  const int rows = batch * s1;
-  char* base = reinterpret_cast<char*>(ws);
-  a.p = reinterpret_cast<float*>(base);
-  size_t off = dsa::salign((size_t)rows * topk * 4);
-  a.dki_acc = reinterpret_cast<float*>(base + off);
-  off += dsa::salign((size_t)batch * s2 * didx * 4);
-  a.row_loss = reinterpret_cast<float*>(base + off);
-  // teacher sums and the dKI accumulator are contiguous up to the padding
-  const int64_t n4 = (int64_t)off / 16;
-  const int blocks = (int)((n4 + 255) / 256 < 4096 ? ((n4 + 255) / 256 > 0 ? (n4 + 255) / 256 : 1) : 4096);
-  hipLaunchKernelGGL(dsa::sli_zero_kernel, dim3(blocks), dim3(256), 0, s, reinterpret_cast<float4*>(base), n4);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  return io == dsa::IO_BF16 ? dsa::launch_sli_io<dsa::IO_BF16>(a, s) : dsa::launch_sli_io<dsa::IO_F16>(a, s);
+  a.n2 = 1;
+  return run_sli(a, ws, s);
 }

@@ -243,7 +243,7 @@ size_t dsa_sli_grad_workspace_bytes(int batch, int s1, int s2, int sparse_count,
  * weights [B,S1,Nidx1] (w_dtype), sm_max / sm_sum [B,1,S1,N1] fp32 (the forward's
  * stats), act_q / act_k [B]. Outputs in the inputs' dtypes; loss: one fp32.
  * D in {128,256,512}, D_idx in {128,256,512}, N1 <= 128, Nidx1 <= 128 with
- * ceil8(Nidx1) * D_idx <= 32768, sparse_count <= 2048.
+ * ceil32(Nidx1) * D_idx <= 32768, sparse_count <= 2048.
  */
 int dsa_sli_grad_kl_loss(const void* query, const void* key, const void* query_rope, const void* key_rope,
                          const void* query_index, const void* key_index, const void* weights, int io_dtype,
@@ -252,6 +252,49 @@ int dsa_sli_grad_kl_loss(const void* query, const void* key, const void* query_r
                          int s2, int n1, int d, int dr, int nidx1, int d_idx, float scale,
                          void* d_query_index, void* d_key_index, void* d_weights, float* loss,
                          void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Dense lightning-indexer softmax LSE, BSND, sparse_mode 3 (replaces
+ * _dense_index_stats_core, dense_loss_backward_triton.py:354-378, behind
+ * npu_dense_lightning_indexer_softmax_lse_triton :776-806). Per query row
+ * (b, s1 < act_q[b]) over keys t < min(max(act_k[b] - act_q[b] + s1 + 1, 0), s2):
+ * softmax_max_index = max_t I[t], softmax_sum_index = sum_t exp(I[t] - max),
+ * I[t] = sum_g w[g] relu(qi[g] . ki[t]); other rows get (-inf, 0). Outputs [B*S1] fp32
+ * (the reference's [B,1,S1]). D_idx in {128,256,512}, Nidx1 <= 128 with
+ * ceil32(Nidx1) * D_idx <= 32768, s2 <= 4096. Needs no workspace.
+ */
+int dsa_dense_li_softmax_lse(const void* query_index, const void* key_index, const void* weights, int io_dtype,
+                             int w_dtype, const int32_t* act_q, const int32_t* act_k, int batch, int s1, int s2,
+                             int nidx1, int d_idx, float* softmax_max_index, float* softmax_sum_index,
+                             void* stream);
+
+/* Workspace bytes for dsa_dense_li_grad_kl_loss (the sparse loss's layout with s2 slots
+ * per row); no initialisation needed. No counterpart in the reference (it allocates
+ * per call, dense_loss_backward_triton.py:393-605). */
+size_t dsa_dense_li_grad_workspace_bytes(int batch, int s1, int s2, int d_idx);
+
+/*
+ * Dense lightning-indexer grad KL loss, BSND, sparse_mode 3 (replaces
+ * _dense_loss_backward_core / _dense_loss_backward_with_index_core,
+ * dense_loss_backward_triton.py:393-605, behind dense_loss_backward_triton :709-774).
+ * dsa_sli_grad_kl_loss with every visible key t < min(max(act_k - act_q + s1 + 1, 0), s2)
+ * as a slot, and:
+ *  - teacher over grouped key heads: key / key_rope [B,S2,N2,D(+64)], head h reads key
+ *    head h / G (G = N1 / N2) and sm_max / sm_sum [B,N2,S1,G] at (b, h / G, s1, h % G);
+ *  - indexer softmax sI = exp(I - max_index) / max(sum_index, 1e-8) from the given stats
+ *    (max_index / sum_index [B*S1] fp32; a row with sum_index <= 0 gets zero gradients
+ *    and no loss), or, with both NULL, from the row's own max and sum.
+ * D in {128,256,512}, D_idx in {128,256,512}, N1 <= 128, Nidx1 <= 128 with
+ * ceil32(Nidx1) * D_idx <= 32768, s2 <= 4096, and for N2 > 1, ceil8(G) * (D + dr) <= 24576
+ * (G = 1 always fits).
+ */
+int dsa_dense_li_grad_kl_loss(const void* query, const void* key, const void* query_rope, const void* key_rope,
+                              const void* query_index, const void* key_index, const void* weights, int io_dtype,
+                              int w_dtype, const float* sm_max, const float* sm_sum, const float* max_index,
+                              const float* sum_index, const int32_t* act_q, const int32_t* act_k, int batch,
+                              int s1, int s2, int n1, int n2, int d, int dr, int nidx1, int d_idx, float scale,
+                              void* d_query_index, void* d_key_index, void* d_weights, float* loss,
+                              void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

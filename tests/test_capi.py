@@ -169,6 +169,46 @@ def test_kl_loss_validation_matches_reference():
     assert lib.dsa_sli_grad_workspace_bytes(1, 4, 2048, 1024, 128) >= 4 * 1024 * 4 + 2048 * 128 * 4
 
 
+def test_dense_loss_validation_matches_reference():
+    """The reference's dense checks (dense_loss_backward_triton.py:605-706, :745-760)
+    raise before any device work; CPU tensors are refused; out-of-range shapes return
+    DSA_ERR_UNSUPPORTED from the C ABI without touching the GPU."""
+    from dsa_triton_ascend_amd import dense_lightning_indexer_softmax_lse as lse, dense_loss_backward as dl
+    B, S1, S2 = 1, 2, 16
+    q = torch.zeros(B, S1, 4, 128, dtype=torch.float16)
+    k = torch.zeros(B, S2, 2, 128, dtype=torch.float16)
+    qi = torch.zeros(B, S1, 32, 128, dtype=torch.float16)
+    ki = torch.zeros(B, S2, 1, 128, dtype=torch.float16)
+    w = torch.zeros(B, S1, 32, dtype=torch.float16)
+    sm = torch.zeros(B, 2, S1, 2)
+    with pytest.raises(ValueError, match="BSND"):
+        lse(qi, ki, w, layout="TND")
+    with pytest.raises(ValueError, match="Nidx1"):
+        lse(qi[:, :, :8], ki, w[:, :, :8])
+    with pytest.raises(ValueError, match="GPU"):
+        lse(qi, ki, w)
+    with pytest.raises(ValueError, match=r"\[B, N2, S1, G\]"):
+        dl(q, k, qi, ki, w, sm[:, :1], sm[:, :1])
+    with pytest.raises(ValueError, match="divisible"):
+        dl(q, k[:, :, :1].expand(B, S2, 3, 128), qi, ki, w, sm, sm)
+    with pytest.raises(ValueError, match="both provided"):
+        dl(q, k, qi, ki, w, sm, sm, softmax_max_index=torch.zeros(B, 1, S1))
+    with pytest.raises(ValueError, match="Drope"):
+        dl(q, k, qi, ki, w, sm, sm, query_rope=torch.zeros(B, S1, 4, 32, dtype=torch.float16),
+           key_rope=torch.zeros(B, S2, 2, 32, dtype=torch.float16))
+    with pytest.raises(ValueError, match="GPU"):
+        dl(q, k, qi, ki, w, sm, sm)
+    lib = _lib.load()
+    assert lib.dsa_dense_li_grad_workspace_bytes(1, 4, 2048, 128) >= 4 * 2048 * 4 + 2048 * 128 * 4
+    one = ctypes.c_void_p(1)
+    assert lib.dsa_dense_li_softmax_lse(one, one, one, 1, 1, one, one, 1, 4, 8192, 32, 128, one, one,
+                                        None) == _lib.DSA_ERR_UNSUPPORTED   # S2 > 4096
+    assert lib.dsa_dense_li_grad_kl_loss(one, one, None, None, one, one, one, 1, 1, one, one, None, None, one,
+                                         one, 1, 4, 64, 6, 4, 128, 0, 32, 128, 1.0, one, one, one, one, one,
+                                         1 << 30, None) == _lib.DSA_ERR_INVALID   # N1 % N2
+    assert b"divisible" in lib.dsa_last_error()
+
+
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(RuntimeError, match="missing"):
         _lib.load(tmp_path / "nope.so")
