@@ -339,8 +339,8 @@ int dsa_dense_li_grad_kl_loss(const void* query, const void* key, const void* qu
   if (!dense_li_grad_supported(n1, n2, d, dr, nidx1, d_idx, s2))
     return fail(DSA_ERR_UNSUPPORTED,
                 "dsa_dense_li_grad_kl_loss: D=%d (+%d), N1=%d, N2=%d, Nidx1=%d, D_idx=%d, S2=%d outside D, D_idx in "
-                "{128,256,512}, Nidx1 <= 128 with ceil32(Nidx1)*D_idx <= 32768, S2 <= 4096, "
-                "ceil8(N1/N2)*(D+Dr) <= 24576 for N2 > 1", d, dr, n1, n2, nidx1, d_idx, s2);
+                "{128,256,512}, Nidx1 <= 128 with ceil32(Nidx1)*D_idx <= 32768, S2 <= 4096", d, dr, n1, n2,
+                nidx1, d_idx, s2);
   if (batch > 65535 || (int64_t)batch * s1 > INT32_MAX)
     return fail(DSA_ERR_UNSUPPORTED, "dsa_dense_li_grad_kl_loss: too many rows");
   const size_t need = sli_grad_workspace_bytes(batch * s1, s2, (int64_t)batch * s2, d_idx);

@@ -35,7 +35,6 @@ constexpr float SEPS = 1e-8f;
 constexpr float SLOG2E = 1.4426950408889634f;
 constexpr int SLI_MAX_TOPK = 2048;   // sparse slots per row
 constexpr int SLI_MAX_SLOTS = 4096;  // student keeps the row's I / dI in LDS (dense: S2)
-constexpr int SLI_GQA_MAX_Q = 24576; // GQA teacher: G x (D + Dr) fp32 query elements in LDS
 constexpr int SLI_MAX_GD = 64 * 512; // Nidx1 (padded to 32) x D_idx held in LDS
 
 inline size_t salign(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -171,72 +170,92 @@ __global__ __launch_bounds__(SWV * 64) void sli_teacher_kernel(SliArgs a) {
   }
 }
 
-// Dense teacher over grouped key heads (N2 > 1): work-group (row, key head), one
-// thread per visible key; the G = N1 / N2 query heads of the key head sit in LDS as
-// fp32 (pre-scaled by scale log2 e); each thread reads its key row once per chunk of
-// GC heads and adds (1/N1) sum_g exp(score_g - max_g) / (sum_g + eps) at slot t.
-template <int IO, int GC>
-__global__ __launch_bounds__(256) void sli_teacher_gqa_kernel(SliArgs a) {
-  constexpr int QF = GC == 1 ? 576 : SLI_GQA_MAX_Q;   // one head: D + Dr <= 576
-  __shared__ float Qf[QF];
-  __shared__ float s_m[QF / 128], s_il[QF / 128];
-  const int tid = threadIdx.x;
-  const int r = blockIdx.x, kvh = blockIdx.y;
-  int b, s1;
-  const int n = row_slots(a, r, b, s1);
-  if (n == 0) return;
-  const int G = a.n1 / a.n2, GP = (G + GC - 1) / GC * GC, D = a.d, DT = a.d + a.dr;
+// Dense teacher over grouped key heads on MFMA: work-group (32 query rows of one batch,
+// NKT x 32 keys), one wave per 32-key tile. For each attention head h (key head h / G)
+// the rows' q_h and the tiles of key head h / G sit in LDS; S^T[key, row] comes from
+// 32x32x16 MFMAs (keys as M) and exp(score - max) / (sum + eps) accumulates over the
+// heads in registers, so every p[row, key] is written once, without atomics.
+template <int IO, int DT, int NKT>
+__global__ __launch_bounds__(NKT * 64) void sli_teacher_heads_kernel(SliArgs a) {
+  constexpr int QP = DT + 8;
+  constexpr int KS = DT / 16;
+  constexpr int NT = NKT * 64;
+  __shared__ __attribute__((aligned(16))) uint16_t Qs[32 * QP];
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[NKT * 32 * QP];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nrb = (a.s1 + 31) / 32;
+  const int b = blockIdx.x / nrb, s0 = (blockIdx.x - b * nrb) * 32;
+  const int t0 = blockIdx.y * (NKT * 32);
+  const int aq = a.act_q[b], ak = a.act_k[b];
+  auto slots = [&](int s1) {
+    if (s1 >= a.s1 || s1 >= aq) return 0;
+    int n = ak - aq + s1 + 1;
+    n = n < 0 ? 0 : n;
+    return n < a.topk ? n : a.topk;
+  };
+  // n grows with s1 up to act_q - 1: the block's widest row bounds the keys it sees
+  int last = s0 + 31 < a.s1 ? s0 + 31 : a.s1 - 1;
+  last = last < aq - 1 ? last : aq - 1;
+  if (last < s0 || t0 >= slots(last)) return;
+  const int G = a.n1 / a.n2, D = a.d;
   const uint16_t* qb = reinterpret_cast<const uint16_t*>(a.q);
   const uint16_t* qrb = reinterpret_cast<const uint16_t*>(a.qr);
   const uint16_t* kb = reinterpret_cast<const uint16_t*>(a.k);
   const uint16_t* krb = reinterpret_cast<const uint16_t*>(a.kr);
+  const uint4 z4 = make_uint4(0, 0, 0, 0);
+  const int my_s1 = s0 + (lane & 31);
+  const int my_n = slots(my_s1);
+  const int64_t my_r = (int64_t)b * a.s1 + my_s1;
   const float sl2 = a.scale * SLOG2E;
-  for (int i = tid; i < GP * DT; i += 256) {
-    const int g = i / DT, c = i - g * DT;
-    float v = 0.f;
-    if (g < G) {
-      const int64_t hr = (int64_t)r * a.n1 + kvh * G + g;
-      v = to_f32<IO>(c < D ? qb[hr * D + c] : qrb[hr * a.dr + (c - D)]);
+  f32x16 pacc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) pacc[e] = 0.f;
+  for (int h = 0; h < a.n1; ++h) {
+    const int kvh = h / G, g = h - kvh * G;
+    __syncthreads();   // the previous head's MFMAs are done with Qs / Ks
+    for (int i = tid; i < 32 * (DT / 8); i += NT) {
+      const int rr = i / (DT / 8), c = (i % (DT / 8)) * 8;
+      uint4 v = z4;
+      if (s0 + rr < a.s1) {
+        const int64_t hr = ((int64_t)b * a.s1 + s0 + rr) * a.n1 + h;
+        v = c < D ? ldg16(qb + hr * D + c) : ldg16(qrb + hr * a.dr + (c - D));
+      }
+      *reinterpret_cast<uint4*>(&Qs[rr * QP + c]) = v;
     }
-    Qf[i] = v * sl2;
-  }
-  for (int g = tid; g < GP; g += 256) {
+    if (g == 0) {
+      for (int i = tid; i < NKT * 32 * (DT / 8); i += NT) {
+        const int j = i / (DT / 8), c = (i % (DT / 8)) * 8;
+        uint4 v = z4;
+        if (t0 + j < a.s2) {
+          const int64_t kr = ((int64_t)b * a.s2 + t0 + j) * a.n2 + kvh;
+          v = c < D ? ldg16(kb + kr * D + c) : ldg16(krb + kr * a.dr + (c - D));
+        }
+        *reinterpret_cast<uint4*>(&Ks[j * QP + c]) = v;
+      }
+    }
     float m = 0.f, il = 0.f;
-    if (g < G) {
-      const int64_t si = (((int64_t)b * a.n2 + kvh) * a.s1 + s1) * G + g;
-      m = a.sm_max[si];
+    if (my_n > 0) {
+      const int64_t si = (((int64_t)b * a.n2 + kvh) * a.s1 + my_s1) * G + g;
+      m = a.sm_max[si] * SLOG2E;
       il = 1.f / (a.sm_sum[si] + SEPS);
     }
-    s_m[g] = m * SLOG2E;
-    s_il[g] = il;
+    __syncthreads();
+    const uint16_t* arow = Ks + (wave * 32 + (lane & 31)) * QP + (lane >> 5) * 8;
+    const uint16_t* brow = Qs + (lane & 31) * QP + (lane >> 5) * 8;
+    f32x16 sc = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      sc = Mfma<IO>::m32(*reinterpret_cast<const uint4*>(arow + ks * 16),
+                         *reinterpret_cast<const uint4*>(brow + ks * 16), sc);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) pacc[e] += __builtin_amdgcn_exp2f(sc[e] * sl2 - m) * il;
   }
-  __syncthreads();
   const float inv_n1 = 1.f / a.n1;
-  for (int t = tid; t < n; t += 256) {
-    const int64_t kr = ((int64_t)b * a.s2 + t) * a.n2 + kvh;
-    float pr = 0.f;
-    for (int g0 = 0; g0 < GP; g0 += GC) {
-      float acc[GC];
 #pragma unroll
-      for (int j = 0; j < GC; ++j) acc[j] = 0.f;
-      auto part = [&](const uint16_t* src, int len, int qoff) {
-        for (int c = 0; c < len; c += 8) {
-          const uint4 kv = ldg16(src + c);
-          const uint32_t w4[4] = {kv.x, kv.y, kv.z, kv.w};
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float kf = to_f32<IO>((uint16_t)(w4[e >> 1] >> (16 * (e & 1))));
-#pragma unroll
-            for (int j = 0; j < GC; ++j) acc[j] += kf * Qf[(g0 + j) * DT + qoff + c + e];
-          }
-        }
-      };
-      part(kb + kr * D, D, 0);
-      if (a.dr > 0) part(krb + kr * a.dr, a.dr, D);
-#pragma unroll
-      for (int j = 0; j < GC; ++j) pr += __builtin_amdgcn_exp2f(acc[j] - s_m[g0 + j]) * s_il[g0 + j];
-    }
-    unsafeAtomicAdd(a.p + (int64_t)r * a.topk + t, pr * inv_n1);
+  for (int e = 0; e < 16; ++e) {
+    const int t = t0 + wave * 32 + m32_row(e, lane);
+    if (t < my_n) a.p[my_r * a.topk + t] = pacc[e] * inv_n1;
   }
 }
 
@@ -536,9 +555,17 @@ hipError_t launch_sli_io(const SliArgs& a, hipStream_t s) {
   }
   const dim3 tgrid(rows, (a.n1 + SBH - 1) / SBH);
   if (a.n2 > 1) {
-    const dim3 ggrid(rows, a.n2);
-    if (a.n1 == a.n2) hipLaunchKernelGGL((sli_teacher_gqa_kernel<IO, 1>), ggrid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((sli_teacher_gqa_kernel<IO, 8>), ggrid, dim3(256), 0, s, a);
+    const int nrb = (a.s1 + 31) / 32;
+    const dim3 g4(a.batch * nrb, (a.s2 + 127) / 128), g2(a.batch * nrb, (a.s2 + 63) / 64);
+    switch (a.d + a.dr) {
+      case 128: hipLaunchKernelGGL((sli_teacher_heads_kernel<IO, 128, 4>), g4, dim3(256), 0, s, a); break;
+      case 192: hipLaunchKernelGGL((sli_teacher_heads_kernel<IO, 192, 4>), g4, dim3(256), 0, s, a); break;
+      case 256: hipLaunchKernelGGL((sli_teacher_heads_kernel<IO, 256, 4>), g4, dim3(256), 0, s, a); break;
+      case 320: hipLaunchKernelGGL((sli_teacher_heads_kernel<IO, 320, 4>), g4, dim3(256), 0, s, a); break;
+      case 512: hipLaunchKernelGGL((sli_teacher_heads_kernel<IO, 512, 2>), g2, dim3(128), 0, s, a); break;
+      case 576: hipLaunchKernelGGL((sli_teacher_heads_kernel<IO, 576, 2>), g2, dim3(128), 0, s, a); break;
+      default: return hipErrorInvalidValue;
+    }
   } else switch (a.d + a.dr) {
     case 128: hipLaunchKernelGGL((sli_teacher_kernel<IO, 128>), tgrid, dim3(256), 0, s, a); break;
     case 192: hipLaunchKernelGGL((sli_teacher_kernel<IO, 192>), tgrid, dim3(256), 0, s, a); break;
@@ -599,9 +626,7 @@ hipError_t run_sli(dsa::SliArgs a, void* ws, hipStream_t s) {
 
 bool dense_li_grad_supported(int n1, int n2, int d, int dr, int nidx1, int didx, int s2) {
   if (n2 < 1 || n1 % n2 != 0 || s2 < 1 || s2 > dsa::SLI_MAX_SLOTS) return false;
-  if (!sli_grad_supported(d, dr, nidx1, didx, 1)) return false;
-  const int g = n1 / n2, gp = g == 1 ? 1 : (g + 7) / 8 * 8;
-  return n2 == 1 || (int64_t)gp * (d + dr) <= dsa::SLI_GQA_MAX_Q;
+  return sli_grad_supported(d, dr, nidx1, didx, 1);
 }
 
 hipError_t launch_dense_li_lse(const void* qi, const void* ki, const void* w, int io, int wdt,

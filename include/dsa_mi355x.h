@@ -285,8 +285,7 @@ size_t dsa_dense_li_grad_workspace_bytes(int batch, int s1, int s2, int d_idx);
  *    (max_index / sum_index [B*S1] fp32; a row with sum_index <= 0 gets zero gradients
  *    and no loss), or, with both NULL, from the row's own max and sum.
  * D in {128,256,512}, D_idx in {128,256,512}, N1 <= 128, Nidx1 <= 128 with
- * ceil32(Nidx1) * D_idx <= 32768, s2 <= 4096, and for N2 > 1, ceil8(G) * (D + dr) <= 24576
- * (G = 1 always fits).
+ * ceil32(Nidx1) * D_idx <= 32768, s2 <= 4096.
  */
 int dsa_dense_li_grad_kl_loss(const void* query, const void* key, const void* query_rope, const void* key_rope,
                               const void* query_index, const void* key_index, const void* weights, int io_dtype,
