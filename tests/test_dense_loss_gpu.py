@@ -10,7 +10,8 @@ causal attention (:180-214). Tolerances are the reference's (:62-108): atol / rt
 fraction of elements beyond the bound is below rtol). Also N2 = 1 (the MFMA
 teacher), grouped heads with G = 4, actual lengths, no rope, omitted index stats,
 a row with sum_index <= 0, and the reference's perf shape (B=1, S1=512, S2=4096,
-N1 = N2 = 64, D = 128, Nidx1 = 64, D_idx = 128) on a strided sample of rows.
+N1 = N2 = 64, D = 128, Nidx1 = 64, D_idx = 128) on a strided sample of rows, and the
+full perf-shape call against single-row calls (bit-exact per row).
 """
 import math
 
@@ -188,3 +189,29 @@ def test_dense_perf_shape_sampled_rows(dev):
         for name, gv, wv in zip(("dqi", "dki", "dw"), out[:3], want[:3]):
             _ratio_close(f"row {s1}: {name}", _np(gv), wv, 1e-2)
         np.testing.assert_allclose(_np(out[3]), want[3], rtol=1e-3, err_msg=f"row {s1}: loss")
+
+
+def test_dense_perf_shape_full_call_matches_single_rows(dev):
+    """The full perf-shape call (S1 = 512 at once: 16 row blocks, causal early exits) gives
+    every sampled row the d_query_index and d_weights of that row run alone (which the
+    test above checks against the oracle), bit for bit: a row's teacher and student do the
+    same arithmetic in either arrangement. The loss is the sum of the row losses."""
+    B, S1, S2, N1, N2, D, Nidx1, Didx = 1, 512, 4096, 64, 64, 128, 64, 128
+    q, k, qr, kr, qi, ki, w = (x.to(dev) for x in _inputs(B, S1, S2, N1, N2, D, Nidx1, Didx, "bf16", seed=4))
+    scale = 1.0 / math.sqrt(D + 64)
+    gen = torch.Generator(device=dev).manual_seed(1)
+    smx = torch.rand(B, N2, S1, 1, device=dev, generator=gen) * 4.0
+    ssm = 1.0 + torch.rand(B, N2, S1, 1, device=dev, generator=gen) * 50.0
+    mxi, smi = dense_lightning_indexer_softmax_lse(qi, ki, w)
+    full = dense_loss_backward(q, k, qi, ki, w, smx, ssm, mxi, smi, scale, query_rope=qr, key_rope=kr)
+    torch.cuda.synchronize()
+    for s1 in (0, 31, 32, 200, 511):
+        lim = S2 - S1 + s1 + 1
+        sl = slice(s1, s1 + 1)
+        one = dense_loss_backward(q[:, sl], k[:, :lim], qi[:, sl], ki[:, :lim], w[:, sl],
+                                  smx[:, :, sl].contiguous(), ssm[:, :, sl].contiguous(), mxi[:, :, sl],
+                                  smi[:, :, sl], scale, query_rope=qr[:, sl], key_rope=kr[:, :lim])
+        torch.cuda.synchronize()
+        assert torch.equal(full[0][:, sl], one[0]), f"row {s1}: d_query_index differs"
+        assert torch.equal(full[2][:, sl], one[2]), f"row {s1}: d_weights differs"
+    assert torch.isfinite(full[1]).all() and torch.isfinite(full[3]).all()
