@@ -6,8 +6,9 @@ One step = one lightning_indexer call over the whole 8192-row batch, inputs
 resident in HBM. The same JSON line carries:
   roofline      -- the indexer score kernel (dominant) against bf16 dense MFMA peak,
                    timed with HIP events on the launch stream;
-  cpu_baseline  -- the numpy oracle (a port of the reference golden) on a stride
-                   sample of the same rows, timed on this host;
+  cpu_baseline  -- the numpy oracle (a port of the reference goldens) on this host:
+                   C2 (the headline's figure) on a stride sample of rows, plus C1 and C4
+                   in full and C3 / C5 on stride samples, each beside its GPU figure;
   breakdown     -- top-k kernel, SFA prefill (config 3), SFA paged decode (config 4),
                    the SFA backward at the reference's grad perf shape, the sparse LI
                    grad KL loss at its target shape, and the TND indexer->SFA pipeline
@@ -78,37 +79,117 @@ def event_time(fns, reps, torch):
     return out
 
 
-def cpu_baseline_indexer(inp, c, torch, budget_s=20.0):
-    """Oracle (numpy port of lightning_indexer_numpy.py) on a stride sample of C2 rows."""
-    import numpy as np
-    from oracle import lightning_indexer_ref as LIO
+def cpu_host_info():
+    """Host cores this process may run on, the CPU model and numpy's BLAS threads."""
+    cores = len(os.sched_getaffinity(0))
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    blas = []
     try:
         from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+        blas = [f"{i.get('internal_api')}:{i.get('num_threads')}" for i in threadpool_info()
+                if i.get("user_api") == "blas"]
     except Exception:
-        threads = 1
-    q = inp.query.float().cpu().numpy()
-    k = inp.key.float().cpu().numpy()
-    w = inp.weights.float().cpu().numpy()
-    S = c["S1"]
-    stride = 1
-    rows = [(0, s) for s in range(0, S, stride)]
-    # calibrate on a few rows so the sample stays within the time budget
+        pass
+    return cores, model, blas
+
+
+def cpu_baselines(torch, W, gpu):
+    """The numpy oracle (a port of the reference goldens, the same per-row loops) on this
+    host, on the same seeded inputs as the GPU figures: C1 and C4 in full, C2, C3 and C5
+    on deterministic stride samples of rows spanning the causal triangle (BASELINE.md
+    section 3). Each entry gives CPU rows/s beside the GPU rows/s of the same config."""
+    import numpy as np
+    from oracle import lightning_indexer_ref as LIO
+    from oracle import sparse_flash_attention_ref as SFAO
+    f = lambda t: t.float().cpu().numpy()
+    out = {}
+
+    def entry(name, rows_done, total_rows, dt, stride, gpu_ms, what):
+        rps = rows_done / dt
+        e = {"cpu_rows_per_s": round(rps, 2), "cpu_s": round(dt, 2), "rows_sampled": rows_done,
+             "rows_total": total_rows, "stride": stride, "extrapolated_full_call_s": round(total_rows / rps, 2),
+             "sample": what}
+        if gpu_ms:
+            e["gpu_rows_per_s"] = round(total_rows / (gpu_ms * 1e-3), 1)
+        out[name] = e
+
+    # C1: the reference's own CPU shape, every row
+    inp = W.indexer_inputs(**W.C1, device="cpu", seed=42)
+    q, k, w = f(inp.query), f(inp.key), f(inp.weights)
     t0 = time.perf_counter()
-    LIO.li_golden_bsnd(q, k, w, [S], [S], c["sparse_count"], 3, True, rows=rows[-4:])
-    per_row_max = (time.perf_counter() - t0) / 4
-    n = len(rows)
-    while n > 16 and per_row_max * n / 2 > budget_s:
-        rows = rows[1::2]
-        n = len(rows)
+    LIO.li_golden_bsnd(q, k, w, [256], [256], 64, 3, True)
+    entry("C1", 256, 256, time.perf_counter() - t0, 1, gpu.get("c1_ms"), "all 256 rows")
+
+    # C2: every 2nd row, from the last (longest) one down, spanning the causal triangle
+    c = dict(W.C2)
+    inp = W.indexer_inputs(**c, device="cuda:0", seed=42)
+    q, k, w = f(inp.query), f(inp.key), f(inp.weights)
+    del inp
+    S, stride = c["S1"], 2
+    rows = [(0, s) for s in range(S - 1, -1, -stride)]
     t0 = time.perf_counter()
     LIO.li_golden_bsnd(q, k, w, [S], [S], c["sparse_count"], 3, True, rows=rows)
-    dt = time.perf_counter() - t0
-    return {"value": round(len(rows) / dt, 2), "unit": "rows/s", "cores": int(threads), "kind": "port",
-            "sample": f"{len(rows)} of {S} query rows (stride {S // len(rows)}, spanning the causal "
-                      f"triangle) of config 2 through the numpy oracle (score, bf16 quantise, "
-                      f"stable top-k per row); {dt:.1f} s; full call extrapolates to "
-                      f"{S / (len(rows) / dt):.1f} s"}
+    entry("C2", len(rows), S, time.perf_counter() - t0, stride, gpu.get("c2_ms"),
+          f"every {stride}th query row of 8192 (score, bf16 quantise, stable top-k)")
+    c2 = out["C2"]
+    del q, k, w
+
+    # C3: every 8th row of 4096
+    si = W.sfa_prefill_inputs(device="cuda:0", seed=42)
+    q, k, qr, kr, idx = f(si.query), f(si.key), f(si.query_rope), f(si.key_rope), si.sparse_indices.cpu().numpy()
+    scale = si.scale_value
+    del si
+    rows = [(0, s) for s in range(4095, -1, -8)]
+    t0 = time.perf_counter()
+    SFAO.sfa_golden_bsnd(q, k, idx, qr, kr, scale, [4096], [4096], 1, 3, "bf16", rows=rows)
+    entry("C3", len(rows), 4096, time.perf_counter() - t0, 8, gpu.get("c3_ms"),
+          "every 8th query row of 4096 (gather, scores, softmax, P@V)")
+    del q, k, qr, kr, idx
+
+    # C4: all 64 decode rows; each batch's pages de-paged on the host as the reference does
+    sd = W.sfa_decode_inputs(device="cuda:0", seed=42)
+    q, qr, kc, krc = f(sd.query), f(sd.query_rope), f(sd.key), f(sd.key_rope)
+    idx, bt = sd.sparse_indices.cpu().numpy(), sd.block_table.cpu().numpy()
+    lens, scale, bs = sd.actual_seq_lengths_kv, sd.scale_value, sd.block_size
+    del sd
+    t0 = time.perf_counter()
+    for b in range(64):
+        SFAO.sparse_flash_attention(q[b:b + 1], kc, None, idx[b:b + 1], scale, bt[b:b + 1], None, [lens[b]],
+                                    qr[b:b + 1], krc, 1, "BSND", "PA_BSND", 3, True, block_size=bs,
+                                    io_dtype="bf16")
+    entry("C4", 64, 64, time.perf_counter() - t0, 1, gpu.get("c4_ms"),
+          "all 64 rows (de-page each batch's cache, gather 2048 tokens, attention)")
+    del q, qr, kc, krc
+
+    # C5: every 16th row of each packed sequence, indexer then attention on its indices
+    inp = W.tnd_pipeline_inputs(device="cuda:0", seed=42)
+    cu = [0] + inp["cu_seqlens"].tolist()
+    iq, ik, iw = f(inp["index_query"]), f(inp["index_key"]), f(inp["index_weights"])
+    q, k, qr, kr = f(inp["query"]), f(inp["key"]), f(inp["query_rope"]), f(inp["key_rope"])
+    scale, count = inp["scale_value"], inp["sparse_count"]
+    del inp
+    n_rows = 0
+    t0 = time.perf_counter()
+    for b in range(len(cu) - 1):
+        a, e = cu[b], cu[b + 1]
+        L = e - a
+        rows = [(0, s) for s in range(L - 1, -1, -16)]
+        n_rows += len(rows)
+        ix, _ = LIO.li_golden_bsnd(iq[None, a:e], ik[None, a:e], iw[None, a:e], [L], [L], count, 3, False,
+                                   rows=rows)
+        SFAO.sfa_golden_bsnd(q[None, a:e], k[None, a:e], ix, qr[None, a:e], kr[None, a:e], scale,
+                             [L], [L], 1, 3, "bf16", rows=rows)
+    entry("C5", n_rows, cu[-1], time.perf_counter() - t0, 16, gpu.get("c5_ms"),
+          "every 16th row of each of the 4 packed sequences (indexer, top-k, then attention on its indices)")
+    return c2, out
 
 
 def bench_indexer_c2(args, torch, W, dsa):
@@ -118,13 +199,19 @@ def bench_indexer_c2(args, torch, W, dsa):
     inp = W.indexer_inputs(**c, device=dev, seed=42)
     plan = IndexerPlan(inp.query, inp.key, inp.weights, sparse_count=c["sparse_count"],
                        sparse_mode=3, return_value=True)
-    sec = timed(plan.run, args.steps, args.warmup, torch)
     warm(plan.run, torch)
+    sec = timed(plan.run, args.steps, args.warmup, torch)
     t_score, t_topk = event_time([plan.score, plan.topk], max(10, args.steps), torch)
+    # the public entry point: validation, output / score-scratch allocation and the small
+    # host-to-device length copies on every call, as a caller without a plan pays them
+    public = lambda: dsa.lightning_indexer(inp.query, inp.key, inp.weights, sparse_count=c["sparse_count"],
+                                           sparse_mode=3, return_value=True)
+    warm(public, torch)
+    sec_public = timed(public, args.steps, 2, torch)
     S = c["S1"]
     pairs = S * (S + 1) // 2
     flop = 2.0 * pairs * c["N1"] * c["D"]
-    return inp, c, sec, t_score, t_topk, flop
+    return inp, c, sec, t_score, t_topk, flop, sec_public
 
 
 def bench_sfa(plan_kwargs, steps, warmup, torch):
@@ -319,7 +406,8 @@ def main():
         return
 
     log("[bench] C2 lightning_indexer ...")
-    inp, c, sec, t_score, t_topk, flop = bench_indexer_c2(args, torch, W, dsa)
+    inp, c, sec, t_score, t_topk, flop, sec_public = bench_indexer_c2(args, torch, W, dsa)
+    del inp
     rows = c["S1"]
     achieved = flop / (t_score * 1e-3) / 1e12
     result = {
@@ -337,7 +425,10 @@ def main():
         "data": "synthetic (seeded N(0,1) bf16 inputs of the BASELINE config shapes)",
         "config": {"workload": "C2: lightning_indexer BSND B=1 S1=S2=8192 N1=64 N2=1 D=128 "
                                "sparse_count=2048 sparse_mode=3 return_value=True",
-                   "rows": rows, "indexer_tflops": round(flop / sec / 1e12, 2)},
+                   "rows": rows, "indexer_tflops": round(flop / sec / 1e12, 2),
+                   "public_call_ms": round(sec_public * 1e3, 4),
+                   "public_call_note": "lightning_indexer() itself: validation, output and score-scratch "
+                                       "allocation, length copies; value / ms_per_step time IndexerPlan.run"},
         "roofline": {"kernel": "li_score_kernel", "bound": "mfma", "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": committed_traffic("li_score_kernel"), "kernel_ms": round(t_score, 4),
@@ -345,7 +436,17 @@ def main():
     }
     breakdown = {"li_topk_kernel_ms": round(t_topk, 4),
                  "li_topk_rows_per_s": round(rows / (t_topk * 1e-3), 1)}
+    gpu_ms = {"c2_ms": sec * 1e3}
     if not args.quick:
+        log("[bench] C1 lightning_indexer ...")
+        from dsa_triton_ascend_amd.lightning_indexer import IndexerPlan
+        i1 = W.indexer_inputs(**W.C1, device="cuda:0", seed=42)
+        p1 = IndexerPlan(i1.query, i1.key, i1.weights, sparse_count=64, sparse_mode=3, return_value=True)
+        warm(p1.run, torch)
+        (gpu_ms["c1_ms"],) = event_time([p1.run], 50, torch)
+        breakdown["indexer_c1"] = {"ms": round(gpu_ms["c1_ms"], 4),
+                                   "rows_per_s": round(256 / (gpu_ms["c1_ms"] * 1e-3), 1)}
+        del p1, i1
         steps = max(3, args.steps // 4)
         try:
             log("[bench] C3 SFA prefill ...")
@@ -353,6 +454,7 @@ def main():
             kw = dict(query=si.query, key=si.key, value=si.key, sparse_indices=si.sparse_indices, **si.kwargs())
             s3, ms3 = bench_sfa(kw, 10, 1, torch)
             f3 = 6292480 * 128 * (576 + 512) * 2.0
+            gpu_ms["c3_ms"] = ms3
             breakdown["sfa_prefill_c3"] = {"ms": round(ms3, 4), "tflops": round(f3 / ms3 / 1e9, 2),
                                            "frac_mfma": round(f3 / ms3 / 1e9 / PEAK_BF16_TFLOPS, 4),
                                            "algorithmic_flop": f3}
@@ -363,6 +465,7 @@ def main():
             kw = dict(query=sd.query, key=sd.key, value=sd.key, sparse_indices=sd.sparse_indices, **sd.kwargs())
             s4, ms4 = bench_sfa(kw, 50, 2, torch)
             kv_bytes = 64 * 2048 * 576 * 2
+            gpu_ms["c4_ms"] = ms4
             breakdown["sfa_decode_c4"] = {"ms": round(ms4, 4), "kv_gbs": round(kv_bytes / ms4 / 1e6, 1),
                                           "frac_hbm": round(kv_bytes / ms4 / 1e6 / PEAK_HBM_GBS, 4),
                                           "gathered_kv_bytes": kv_bytes}
@@ -377,12 +480,22 @@ def main():
             torch.cuda.empty_cache()
             log("[bench] C5 TND indexer -> SFA pipeline ...")
             breakdown["pipeline_c5"] = bench_pipeline_c5(W, max(3, args.steps // 4), torch)
+            gpu_ms["c5_ms"] = breakdown["pipeline_c5"]["ms"]
             torch.cuda.empty_cache()
         except Exception as e:  # report, keep the headline
             breakdown["sfa_error"] = repr(e)[:300]
     if not (args.quick or args.no_cpu):
-        log("[bench] CPU baseline (oracle sample) ...")
-        result["cpu_baseline"] = cpu_baseline_indexer(inp, c, torch)
+        log("[bench] CPU baseline (numpy oracle on this host: C1, C4 in full; C2, C3, C5 sampled) ...")
+        cores, model, blas = cpu_host_info()
+        c2, per_cfg = cpu_baselines(torch, W, gpu_ms)
+        result["cpu_baseline"] = {
+            "value": c2["cpu_rows_per_s"], "unit": "rows/s", "cores": cores, "kind": "port",
+            "sample": f"C2: {c2['rows_sampled']} of 8192 query rows (every {c2['stride']}th, spanning the "
+                      f"causal triangle) through the numpy oracle (score, bf16 quantise, stable top-k); "
+                      f"{c2['cpu_s']} s; full call extrapolates to {c2['extrapolated_full_call_s']} s",
+            "cpu_model": model, "blas_threads": blas,
+            "cores_note": "len(os.sched_getaffinity(0)); numpy BLAS threads as listed",
+            "configs": per_cfg}
     else:
         result["cpu_baseline"] = None
     result["breakdown"] = breakdown

@@ -29,6 +29,19 @@ def host_lengths(x, n: int | None = None, default: int | None = None) -> list[in
     return [int(v) for v in x]
 
 
+def batch_lengths(x, n: int, default: int, name: str) -> list[int]:
+    """host_lengths(x, n, default) as exactly n per-batch lengths: the kernels read one
+    length per batch. A single value applies to every batch, as the reference's
+    broadcast `zeros[B] + lengths` does (dense_loss_backward_triton.py:37-43,
+    sparse_lightning_indexer_grad_kl_loss_triton.py:308-315); any other count raises."""
+    v = host_lengths(x, n, default)
+    if len(v) == 1 and n > 1:
+        v = v * n
+    if len(v) != n:
+        raise ValueError(f"{name} must hold {n} per-batch lengths, got {len(v)}")
+    return v
+
+
 def per_batch_from_cumsum(cu: list[int]) -> list[int]:
     """TND cumulative actual_seq_lengths -> per-batch lengths
     (lightning_indexer_triton.py:294-296)."""

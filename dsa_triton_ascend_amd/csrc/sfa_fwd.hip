@@ -27,9 +27,10 @@
 //         wave as N (Q^T resident in VGPRs): a lane then holds 16 tokens of one
 //         head, so the softmax row max is in-lane plus one lane swap;
 //       * online softmax in fp32 with lazy rescaling: the exponent reference
-//         m_used only moves when a tile's max exceeds it by more than TAU = 40
-//         (natural-log units), so O is rarely rescaled; the true max is tracked
-//         for softmax_max;
+//         m_used only moves when a tile's max exceeds it by more than TAU
+//         (natural-log units; 40 for bf16, 8 for fp16 so that P = exp(s - m_used)
+//         stays finite once packed to fp16), so O is rarely rescaled; the true
+//         max is tracked for softmax_max;
 //       * P (io dtype) goes to LDS as [head][token]; each wave then owns a
 //         D/4-column slice of O[128 heads, D] and accumulates it transposed,
 //         O^T += V^T P^T, on v_mfma_f32_32x32x16, the V^T operand read with
@@ -610,10 +611,13 @@ constexpr int NBUF = 3;     // gather ring: tile t read, t+1 and t+2 in flight
 constexpr int PP = BN + 8;  // P tile pitch (elements)
 constexpr int QRP = DR + 8; // Q-rope LDS pitch (elements): 144-byte rows, conflict-free 16-byte reads
 // Lazy-rescale threshold (natural units): the exponent reference m_used only
-// moves when a tile's max exceeds it by more than TAU, so P = exp(x - m_used)
-// stays below e^40 (exact in relative terms in fp32 / bf16 / fp16-free paths)
-// and O is practically never rescaled.
-constexpr float TAU = 40.f;
+// moves when a tile's max exceeds it by more than TAU, so every P = exp(x - m_used)
+// of a tile is at most e^TAU and O is rarely rescaled. P is packed to the io dtype
+// before the PV product, so e^TAU must be finite there: bf16 has fp32's exponent
+// range (e^40 ~ 2.4e17), fp16 overflows past 65504 ~ e^11.09, so fp16 moves the
+// reference at 8 nats (P <= e^8 ~ 2981).
+template <int IO> constexpr float lazy_tau() { return IO == IO_F16 ? 8.f : 40.f; }
+static_assert(lazy_tau<IO_F16>() < 11.0f, "fp16 P = exp(TAU) must stay below 65504");
 
 template <int D> struct Cfg {
   static constexpr int KS = (D + DR) / 16;      // 32x32x16 k-steps of S^T
@@ -891,7 +895,7 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
     // lazy rescaling: the reference maximum moves only when the tile max exceeds it
     // by more than TAU; alpha is exactly 1 otherwise, and 1 on the first tile (O
     // and l are still zero)
-    const float m_new = mx > m_used + TAU ? mx : m_used;
+    const float m_new = mx > m_used + lazy_tau<IO>() ? mx : m_used;
     const float alpha = m_used == -INFINITY ? 1.f : __builtin_amdgcn_exp2f((m_used - m_new) * LOG2E);
     m_used = m_new;
     const float mb = m_used * LOG2E;

@@ -65,6 +65,8 @@ def dense_lightning_indexer_softmax_lse(query_index, key_index, weights, actual_
     """Returns ``(softmax_max_index, softmax_sum_index)``, each (B, 1, S1) float32
     (dense_loss_backward_triton.py:776-806); rows without a visible key hold (-inf, 0)."""
     _validate_index(query_index, key_index, weights, layout, sparse_mode, pre_tokens, next_tokens)
+    aq = H.batch_lengths(actual_seq_qlen, query_index.shape[0], query_index.shape[1], "actual_seq_qlen")
+    ak = H.batch_lengths(actual_seq_klen, query_index.shape[0], key_index.shape[1], "actual_seq_klen")
     dev = H.require_device(query_index, key_index, weights)
     lib = _lib.load()
     io = H.dtype_code(query_index.dtype, "query_index")
@@ -73,8 +75,7 @@ def dense_lightning_indexer_softmax_lse(query_index, key_index, weights, actual_
     wdt = H.dtype_code(weights.dtype, "weights", allow_f32=True)
     B, S1, Nidx1, Didx = query_index.shape
     S2 = key_index.shape[1]
-    act_q = H.i32(H.host_lengths(actual_seq_qlen, B, S1), dev)
-    act_k = H.i32(H.host_lengths(actual_seq_klen, B, S2), dev)
+    act_q, act_k = H.i32(aq, dev), H.i32(ak, dev)
     qi, ki, w = query_index.contiguous(), key_index.contiguous(), weights.contiguous()
     mx = torch.empty((B, 1, S1), dtype=torch.float32, device=dev)
     sm = torch.empty((B, 1, S1), dtype=torch.float32, device=dev)
@@ -147,6 +148,8 @@ class DenseLossPlan:
                 raise TypeError("softmax_max_index and softmax_sum_index must be float32")
             self.imax = _reshape_stat(softmax_max_index, B, S1, "softmax_max_index")
             self.isum = _reshape_stat(softmax_sum_index, B, S1, "softmax_sum_index")
+        aq = H.batch_lengths(actual_seq_qlen, B, S1, "actual_seq_qlen")
+        ak = H.batch_lengths(actual_seq_klen, B, key.shape[1], "actual_seq_klen")
         dev = H.require_device(query, key, query_index, key_index, weights, softmax_max, softmax_sum,
                                query_rope, key_rope, softmax_max_index, softmax_sum_index)
         lib = _lib.load()
@@ -162,8 +165,7 @@ class DenseLossPlan:
         self.loss = torch.empty(1, dtype=torch.float32, device=dev)
         self.ws_bytes = lib.dsa_dense_li_grad_workspace_bytes(B, S1, S2, Didx)
         self.ws = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=dev)
-        self.d_aq = H.i32(H.host_lengths(actual_seq_qlen, B, S1), dev)
-        self.d_ak = H.i32(H.host_lengths(actual_seq_klen, B, S2), dev)
+        self.d_aq, self.d_ak = H.i32(aq, dev), H.i32(ak, dev)
         self.lib, self.dev = lib, dev
         self.io = H.dtype_code(query.dtype, "query")
         self.wdt = H.dtype_code(weights.dtype, "weights", allow_f32=True)

@@ -21,6 +21,40 @@ from . import _lib
 INT64_MAX = H.INT64_MAX
 
 
+def _check_shapes(query, key, query_index, key_index, weights, sparse_indices, softmax_max, softmax_sum,
+                  query_rope, key_rope):
+    """Every tensor against query [B, S1, N1, D] and key [B, S2, 1, D]: the kernels index
+    each one with B * S1 rows and S2 keys, so a mismatch would read outside it. Runs before
+    any device check, so it needs no GPU."""
+    for t, n in ((query, "query"), (key, "key"), (query_index, "query_index"), (key_index, "key_index")):
+        if t.dim() != 4:
+            raise ValueError(f"{n} must be a 4D BSND tensor, got {tuple(t.shape)}")
+    B, S1, N1, D = query.shape
+    S2 = key.shape[1]
+    if key.shape[0] != B or key.shape[3] != D:
+        raise ValueError(f"key must be [B={B}, S2, 1, D={D}], got {tuple(key.shape)}")
+    if tuple(query_index.shape[:2]) != (B, S1):
+        raise ValueError(f"query_index must be [B={B}, S1={S1}, Nidx1, D_idx], got {tuple(query_index.shape)}")
+    Nidx1, Didx = query_index.shape[2], query_index.shape[3]
+    if tuple(key_index.shape) != (B, S2, key_index.shape[2], Didx):
+        raise ValueError(f"key_index must be [B={B}, S2={S2}, 1, D_idx={Didx}], got {tuple(key_index.shape)}")
+    if tuple(weights.shape) != (B, S1, Nidx1):
+        raise ValueError(f"weights must be [B={B}, S1={S1}, Nidx1={Nidx1}], got {tuple(weights.shape)}")
+    if tuple(sparse_indices.shape[:3]) != (B, S1, 1):
+        raise ValueError(f"sparse_indices must be [B={B}, S1={S1}, 1, topK], got {tuple(sparse_indices.shape)}")
+    for t, n in ((softmax_max, "softmax_max"), (softmax_sum, "softmax_sum")):
+        if t.numel() != B * S1 * N1 or (t.dim() == 4 and tuple(t.shape) != (B, 1, S1, N1)):
+            raise ValueError(f"{n} must be [B={B}, 1, S1={S1}, N1={N1}], got {tuple(t.shape)}")
+    if (query_rope is None) != (key_rope is None):
+        raise ValueError("query_rope and key_rope must both be given or both be None")
+    if query_rope is not None:
+        Dr = query_rope.shape[-1]
+        if query_rope.dim() != 4 or tuple(query_rope.shape[:3]) != (B, S1, N1):
+            raise ValueError(f"query_rope must be [B={B}, S1={S1}, N1={N1}, Dr], got {tuple(query_rope.shape)}")
+        if key_rope.dim() != 4 or tuple(key_rope.shape) != (B, S2, 1, Dr):
+            raise ValueError(f"key_rope must be [B={B}, S2={S2}, 1, Dr={Dr}], got {tuple(key_rope.shape)}")
+
+
 class KLLossPlan:
     """Validated arguments, outputs and workspace of one call; ``run()`` launches on
     the current stream."""
@@ -36,6 +70,10 @@ class KLLossPlan:
             raise ValueError("Only sparse_mode=3 (rightDownCausal) is supported")
         if sparse_indices.dim() != 4 or sparse_indices.shape[2] != 1:
             raise ValueError("Nidx2 must be 1 (MQA constraint)")
+        _check_shapes(query, key, query_index, key_index, weights, sparse_indices, softmax_max,
+                      softmax_sum, query_rope, key_rope)
+        act_q = H.batch_lengths(actual_seq_qlen, query.shape[0], query.shape[1], "actual_seq_qlen")
+        act_k = H.batch_lengths(actual_seq_klen, query.shape[0], key.shape[1], "actual_seq_klen")
         dev = H.require_device(query, key, query_index, key_index, weights, sparse_indices,
                                softmax_max, softmax_sum, query_rope, key_rope)
         lib = _lib.load()
@@ -54,8 +92,6 @@ class KLLossPlan:
             raise ValueError("query_rope and key_rope must both be given or both be None")
         Dr = 0 if query_rope is None else query_rope.shape[-1]
         topk = int(sparse_indices.shape[-1])
-        act_q = H.host_lengths(actual_seq_qlen, B, S1)
-        act_k = H.host_lengths(actual_seq_klen, B, S2)
         self.q, self.k, self.qi, self.ki = (t.contiguous() for t in (query, key, query_index, key_index))
         self.qr = query_rope.contiguous() if query_rope is not None else None
         self.kr = key_rope.contiguous() if key_rope is not None else None

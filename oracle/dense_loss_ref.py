@@ -72,9 +72,11 @@ def dense_loss_backward(q, k, qr, kr, qi, ki, w, sm_max, sm_sum, max_index, sum_
             relu = np.maximum(qi[b, s1] @ kiv.T, 0.0)                                   # [G, n]
             ii = (w[b, s1, :, None] * relu).sum(0)
             student = np.exp(ii - float(mxi[b * S1 + s1])) / max(i_sum, EPS)
-            sc = np.einsum("hd,nhd->hn", q[b, s1], k[b, :n][:, kvh, :])                   # [N1, n]
+            # head h against key head kvh[h] (no gather copy when every head has its own key head)
+            kh = (lambda x: x if Gq == 1 else x[:, kvh, :])
+            sc = np.einsum("hd,nhd->hn", q[b, s1], kh(k[b, :n]))                          # [N1, n]
             if qr is not None:
-                sc = sc + np.einsum("hd,nhd->hn", qr[b, s1], kr[b, :n][:, kvh, :])
+                sc = sc + np.einsum("hd,nhd->hn", qr[b, s1], kh(kr[b, :n]))
             sc = sc * np.float32(scale)
             m = sm_max[b, kvh, s1, gh][:, None]
             l = sm_sum[b, kvh, s1, gh][:, None]

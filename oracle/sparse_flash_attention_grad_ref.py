@@ -63,9 +63,14 @@ def sfa_grad_golden_bsnd(q_nope, k_nope, sparse_indices, d_out, out, softmax_max
             ds = p * (dp - delta[:, None]) * scale                             # [N1, P]
             dq[b, s1] += ds @ kn_sp
             dqr[b, s1] += ds @ kr_sp
-            np.add.at(dk[b, :, 0, :], pos, ds.T @ qn[b, s1])
-            np.add.at(dkr[b, :, 0, :], pos, ds.T @ qr[b, s1])
-            np.add.at(dv[b, :, 0, :], pos, p.T @ do[b, s1])
+            if len(np.unique(pos)) == len(pos):   # distinct positions: a plain indexed add is the same sum
+                dk[b, pos, 0, :] += ds.T @ qn[b, s1]
+                dkr[b, pos, 0, :] += ds.T @ qr[b, s1]
+                dv[b, pos, 0, :] += p.T @ do[b, s1]
+            else:
+                np.add.at(dk[b, :, 0, :], pos, ds.T @ qn[b, s1])
+                np.add.at(dkr[b, :, 0, :], pos, ds.T @ qr[b, s1])
+                np.add.at(dv[b, :, 0, :], pos, p.T @ do[b, s1])
     r = lambda x: _round_io(x, io_dtype)
     return r(dq), r(dk), r(dv), r(dqr), r(dkr)
 

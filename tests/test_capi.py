@@ -169,6 +169,54 @@ def test_kl_loss_validation_matches_reference():
     assert lib.dsa_sli_grad_workspace_bytes(1, 4, 2048, 1024, 128) >= 4 * 1024 * 4 + 2048 * 128 * 4
 
 
+@pytest.mark.parametrize("bad,match", [
+    ("weights", "weights must be"), ("query_index_b", "query_index must be"),
+    ("query_index_s1", "query_index must be"), ("key_index_s2", "key_index must be"),
+    ("key_index_d", "key_index must be"), ("sparse_indices_s1", "sparse_indices must be"),
+    ("sparse_indices_b", "sparse_indices must be"), ("softmax_max", "softmax_max must be"),
+    ("softmax_sum", "softmax_sum must be"), ("query_rope", "query_rope must be"),
+    ("key_rope", "key_rope must be"), ("key_b", "key must be"), ("act_q", "actual_seq_qlen"),
+    ("act_k", "actual_seq_klen")])
+def test_kl_loss_shape_mismatch_raises_before_device(bad, match):
+    """Every tensor the KL-loss kernels index by B * S1 rows or S2 keys is checked against
+    query [B, S1, N1, D] and key [B, S2, 1, D] on the host, before the device check (CPU
+    tensors throughout: the mismatch must be what raises)."""
+    from dsa_triton_ascend_amd import sparse_lightning_indexer_grad_kl_loss as kl
+    B, S1, S2, N1, D, G, Di, K = 2, 3, 16, 8, 128, 8, 128, 4
+    z = lambda *s: torch.zeros(*s, dtype=torch.float16)
+    t = dict(q=z(B, S1, N1, D), k=z(B, S2, 1, D), qi=z(B, S1, G, Di), ki=z(B, S2, 1, Di), w=z(B, S1, G),
+             si=torch.zeros(B, S1, 1, K, dtype=torch.int32), smax=torch.zeros(B, 1, S1, N1),
+             ssum=torch.zeros(B, 1, S1, N1), qr=z(B, S1, N1, 64), kr=z(B, S2, 1, 64))
+    kw = {}
+    wrong = {"weights": ("w", z(B, S1, G + 1)), "query_index_b": ("qi", z(B + 1, S1, G, Di)),
+             "query_index_s1": ("qi", z(B, S1 + 1, G, Di)), "key_index_s2": ("ki", z(B, S2 - 1, 1, Di)),
+             "key_index_d": ("ki", z(B, S2, 1, Di * 2)), "sparse_indices_s1": ("si", t["si"][:, :2]),
+             "sparse_indices_b": ("si", t["si"][:1]), "softmax_max": ("smax", torch.zeros(B, 1, S1, N1 // 2)),
+             "softmax_sum": ("ssum", torch.zeros(B, 1, S1 + 1, N1)), "query_rope": ("qr", z(B, S1, N1 // 2, 64)),
+             "key_rope": ("kr", z(B, S2 + 1, 1, 64)), "key_b": ("k", z(B + 1, S2, 1, D))}
+    if bad in wrong:
+        name, val = wrong[bad]
+        t[name] = val
+    elif bad == "act_q":
+        kw["actual_seq_qlen"] = [3, 3, 3]
+    else:
+        kw["actual_seq_klen"] = [16, 16, 16]
+    with pytest.raises(ValueError, match=match):
+        kl(t["q"], t["k"], t["qi"], t["ki"], t["w"], t["si"], t["smax"], t["ssum"], query_rope=t["qr"],
+           key_rope=t["kr"], **kw)
+
+
+def test_batch_lengths_broadcast_and_count():
+    """One actual length applies to every batch (the reference's zeros[B] + lengths
+    broadcast); other counts are refused."""
+    from dsa_triton_ascend_amd import _host as H
+    assert H.batch_lengths(None, 3, 7, "x") == [7, 7, 7]
+    assert H.batch_lengths([5], 3, 7, "x") == [5, 5, 5]
+    assert H.batch_lengths(torch.tensor([1, 2, 3]), 3, 7, "x") == [1, 2, 3]
+    with pytest.raises(ValueError, match="3 per-batch lengths"):
+        H.batch_lengths([1, 2], 3, 7, "x")
+
+
 def test_dense_loss_validation_matches_reference():
     """The reference's dense checks (dense_loss_backward_triton.py:605-706, :745-760)
     raise before any device work; CPU tensors are refused; out-of-range shapes return

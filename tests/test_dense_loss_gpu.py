@@ -195,7 +195,8 @@ def test_dense_perf_shape_full_call_matches_single_rows(dev):
     """The full perf-shape call (S1 = 512 at once: 16 row blocks, causal early exits) gives
     every sampled row the d_query_index and d_weights of that row run alone (which the
     test above checks against the oracle), bit for bit: a row's teacher and student do the
-    same arithmetic in either arrangement. The loss is the sum of the row losses."""
+    same arithmetic in either arrangement. All four outputs of the full call (d_key_index
+    summed over every row, the loss over every row) against the oracle on all 512 rows."""
     B, S1, S2, N1, N2, D, Nidx1, Didx = 1, 512, 4096, 64, 64, 128, 64, 128
     q, k, qr, kr, qi, ki, w = (x.to(dev) for x in _inputs(B, S1, S2, N1, N2, D, Nidx1, Didx, "bf16", seed=4))
     scale = 1.0 / math.sqrt(D + 64)
@@ -215,3 +216,15 @@ def test_dense_perf_shape_full_call_matches_single_rows(dev):
         assert torch.equal(full[0][:, sl], one[0]), f"row {s1}: d_query_index differs"
         assert torch.equal(full[2][:, sl], one[2]), f"row {s1}: d_weights differs"
     assert torch.isfinite(full[1]).all() and torch.isfinite(full[3]).all()
+    # d_key_index sums every row's contribution (fp32 atomics) and the loss is the row-ordered
+    # sum of the row losses: both against the oracle over all 512 rows (the LSE stats are the
+    # GPU's, which the LSE tests check on their own)
+    want = DLO.dense_loss_backward(_np(q), _np(k), _np(qr), _np(kr), _np(qi), _np(ki), _np(w), _np(smx), _np(ssm),
+                                   _np(mxi), _np(smi), scale, io_dtype="bf16")
+    _ratio_close("full call: dki", _np(full[1]), want[1], 1e-2)
+    _ratio_close("full call: dqi", _np(full[0]), want[0], 1e-2)
+    _ratio_close("full call: dw", _np(full[2]), want[2], 1e-2)
+    np.testing.assert_allclose(_np(full[3]), want[3], rtol=1e-3, err_msg="full call: loss")
+    rel = np.linalg.norm(_np(full[1]) - want[1]) / np.linalg.norm(want[1])
+    print(f"[dense parity] perf shape d_key_index relative Frobenius error {rel:.2e}")
+    assert rel <= 1e-2

@@ -414,6 +414,7 @@ def test_sfa_grad_golden_vs_float64_autograd(mode, bs, act):
             n = min(count, nb)
             si[b, s1, 0, :n] = np.sort(rng.permutation(nb)[:n])
     si[1, 2, 0, 3] = -1       # the scan of this row stops at its fourth id
+    si[0, 2, 0, 1] = si[0, 2, 0, 0]   # a repeated id: the row gathers that position twice
     scale = 0.3
     out, smax, ssum, want = _autograd_sfa_grad(q, k, qr, kr, do, si, scale, act_q, act_k, bs, mode)
     got = SFG.sfa_grad_golden_bsnd(q, k, si, do, out, smax, ssum, qr, kr, scale, act_q, act_k,

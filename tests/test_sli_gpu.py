@@ -31,6 +31,10 @@ def _close(a, b, atol, rtol, what):
 
 
 def _inputs(B, S1, S2, N1, D, G, Di, K, dtype, pattern="random", seed=42):
+    """The reference's _make_inputs / _make_sparse_indices (test_sli_grad_kl_loss_triton.py:
+    88-131): one RandomState(42) for q, k, qr, kr, qi, ki, |w|, random ids; the causal
+    patterns redraw the ids (causal_random from a fresh RandomState(42), distinct ids in
+    each row's visible window; causal_continuous 0, 1, 2, ... up to the window)."""
     rng = np.random.RandomState(seed)
     h = lambda *s: rng.randn(*s).astype(np.float16)
     q, k, qr, kr = h(B, S1, N1, D), h(B, S2, 1, D), h(B, S1, N1, 64), h(B, S2, 1, 64)
@@ -39,12 +43,23 @@ def _inputs(B, S1, S2, N1, D, G, Di, K, dtype, pattern="random", seed=42):
     si = rng.randint(0, S2, (B, S1, 1, K)).astype(np.int32)
     if pattern == "repeated":
         si[..., 1::2] = si[..., 0::2][..., : si[..., 1::2].shape[-1]]
+    elif pattern in ("causal_random", "causal_continuous"):
+        r2 = np.random.RandomState(seed)
+        si = np.zeros((B, S1, 1, K), np.int32)
+        for b in range(B):
+            for s1 in range(S1):
+                vis = min(max(S2 - S1 + s1 + 1, 1), S2)
+                n = min(K, vis)
+                si[b, s1, 0, :n] = (r2.choice(vis, size=n, replace=False) if pattern == "causal_random"
+                                    else np.arange(n))
     t = lambda x: torch.from_numpy(x).to(DT[dtype])
     return (t(q), t(k), t(qr), t(kr), t(qi), t(ki), t(w), torch.from_numpy(si))
 
 
 def _stats(q, k, qr, kr, scale, act_q, act_k):
     """Full causal forward stats (reference test :146-170), float64 then fp32."""
+    if q.shape[1] > 16:
+        return _stats_chunked(q, k, qr, kr, scale, act_q, act_k)
     f = lambda x: x.double().numpy()
     q, k, qr, kr = f(q), f(k), f(qr), f(kr)
     B, S1, N1, _ = q.shape
@@ -62,7 +77,33 @@ def _stats(q, k, qr, kr, scale, act_q, act_k):
     return torch.from_numpy(sm_max), torch.from_numpy(sm_sum)
 
 
-def run(dev, B, S1, S2, N1, D, G, Di, K, dtype, pattern="random", act_q=None, act_k=None):
+def _stats_chunked(q, k, qr, kr, scale, act_q, act_k, chunk=32):
+    """The same stats in fp32 (as the reference computes them), 32 query rows at a time."""
+    f = lambda x: x.float().numpy()
+    q, k, qr, kr = f(q), f(k), f(qr), f(kr)
+    B, S1, N1, D = q.shape
+    S2 = k.shape[1]
+    sm_max = np.zeros((B, 1, S1, N1), np.float32)
+    sm_sum = np.zeros((B, 1, S1, N1), np.float32)
+    for b in range(B):
+        for c in range(0, min(S1, act_q[b]), chunk):
+            rows = np.arange(c, min(c + chunk, S1, act_q[b]))
+            sc = (q[b, rows].reshape(-1, D) @ k[b, :, 0].T + qr[b, rows].reshape(-1, 64) @ kr[b, :, 0].T)
+            sc = (sc * np.float32(scale)).reshape(len(rows), N1, S2)
+            lim = np.clip(act_k[b] - act_q[b] + rows + 1, 0, S2)
+            sc = np.where(np.arange(S2)[None, None, :] >= lim[:, None, None], -np.inf, sc)
+            ok = lim > 0
+            m = np.where(ok[:, None], sc.max(-1), 0)
+            sm_max[b, 0, rows] = m
+            sm_sum[b, 0, rows] = np.where(ok[:, None], np.exp(sc - m[..., None]).sum(-1), 0)
+    return torch.from_numpy(sm_max), torch.from_numpy(sm_sum)
+
+
+def run(dev, B, S1, S2, N1, D, G, Di, K, dtype, pattern="random", act_q=None, act_k=None, loose=False):
+    """One call against the oracle. ``loose``: the reference's loose group
+    (test_sli_grad_kl_loss_triton.py:191-211, shapes with S1 >= 512 or deep d_key_index
+    sums): bf16 d_query_index at (0.1, 0.1) and d_key_index not compared elementwise;
+    here d_key_index must still be within 1e-2 of the oracle in relative Frobenius norm."""
     q, k, qr, kr, qi, ki, w, si = _inputs(B, S1, S2, N1, D, G, Di, K, dtype, pattern)
     scale = 1.0 / math.sqrt(D)
     aq = [S1] * B if act_q is None else act_q
@@ -81,9 +122,18 @@ def run(dev, B, S1, S2, N1, D, G, Di, K, dtype, pattern="random", act_q=None, ac
     assert dqi.shape == qi.shape and dki.shape == ki.shape and dw.shape == w.shape and loss.shape == (1,)
     for name, got, ref in zip(("d_query_index", "d_key_index", "d_weights", "loss"), (dqi, dki, dw, loss), want):
         assert np.all(np.isfinite(f(got))), f"{what}: {name} not finite"
-        _close(f(got), ref, atol, rtol, f"{what}: {name}")
+        if loose and name == "d_key_index":
+            rel = np.linalg.norm(f(got) - ref) / max(np.linalg.norm(ref), 1e-30)
+            print(f"[kl parity] {what}: d_key_index relative Frobenius error {rel:.2e}")
+            assert rel <= 1e-2, f"{what}: d_key_index relative error {rel:.3e}"
+            continue
+        a, r = (0.1, 0.1) if (loose and dtype == "bf16" and name == "d_query_index") else (atol, rtol)
+        _close(f(got), ref, a, r, f"{what}: {name}")
 
 
+# the reference's strict group and its Triton-vs-numpy matrix (test_sli_grad_kl_loss_triton.py:
+# 17-20, 42-58) except its three Nidx1 = 128 x D_idx = 512 shapes (:47, :49, :55), which this
+# build refuses (test_kl_loss_unsupported_shape_is_refused)
 CASES = [
     (1, 1, 2048, 32, 512, 8, 128, 1024),
     (1, 4, 2048, 64, 512, 16, 128, 1024),
@@ -91,9 +141,13 @@ CASES = [
     (1, 4, 2048, 64, 512, 64, 128, 2048),
     (1, 4, 2048, 32, 128, 32, 128, 1024),
     (1, 4, 2048, 64, 256, 64, 256, 1024),
-    (1, 4, 2048, 32, 256, 64, 512, 2048),
-    (1, 4, 2048, 128, 256, 64, 128, 1024),
+    (1, 4, 2048, 32, 512, 64, 256, 2048),
+    (1, 4, 2048, 64, 128, 32, 256, 1024),
     (1, 4, 2048, 128, 128, 32, 512, 2048),
+    (1, 4, 2048, 128, 256, 64, 128, 1024),
+    (1, 4, 2048, 128, 512, 128, 128, 2048),
+    (1, 4, 2048, 32, 256, 64, 512, 2048),
+    (1, 4, 2048, 64, 512, 128, 256, 1024),
 ]
 
 
@@ -107,6 +161,22 @@ def dev():
 @pytest.mark.parametrize("B,S1,S2,N1,D,G,Di,K", CASES)
 def test_kl_loss_matrix(dev, B, S1, S2, N1, D, G, Di, K, dtype):
     run(dev, B, S1, S2, N1, D, G, Di, K, dtype)
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_kl_loss_target_shape(dev, dtype):
+    """The reference's target (performance) shape and smoke test (test_sli_grad_kl_loss_triton.py:29,
+    361-366): B=1, S1=512, S2=4096, N1=64, D=512 + 64 rope, Nidx1=64, D_idx=128, top-k 2048,
+    causal_continuous ids, every row against the oracle, the reference's loose rules."""
+    run(dev, 1, 512, 4096, 64, 512, 64, 128, 2048, dtype, pattern="causal_continuous", loose=True)
+
+
+@pytest.mark.parametrize("pattern", ["causal_random", "repeated"])
+def test_kl_loss_loose_shapes(dev, pattern):
+    """The reference's loose group shapes with S2 = 4096 (:27-33): ids drawn from each row's
+    causal window."""
+    run(dev, 1, 4, 4096, 32, 512, 64, 128, 2048, "fp16", pattern="causal_random", loose=True)
+    run(dev, 1, 4, 2048, 128, 512, 32, 128, 1024, "bf16", pattern=pattern, loose=True)
 
 
 @pytest.mark.parametrize("pattern", ["random", "repeated"])
