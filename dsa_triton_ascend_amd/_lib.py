@@ -35,6 +35,8 @@ SIGNATURES = {
     "dsa_sfa_workspace_zero_bytes": (_SZ, []),
     "dsa_sfa_fwd": (_I, [_P, _P, _P, _P, _I, _P, _I, _I, _P, _I, _I, _P, _P, _P, _P, _I, _I, _I,
                          _I, _I, _I, _I64, _I, _F, _P, _P, _P, _P, _SZ, _I, _P]),
+    "dsa_sfa_fwd_noalloc": (_I, [_P, _P, _P, _P, _I, _P, _I, _I, _P, _I, _I, _P, _P, _P, _P, _I, _I, _I,
+                                 _I, _I, _I, _I64, _I, _F, _P, _P, _P, _I, _P]),
     "dsa_li_score_paged": (_I, [_P, _P, _P, _I, _I, _P, _P, _I, _I, _I64, _P, _P, _I, _I, _I, _I, _I, _I, _I,
                                 _I, _P, _I64, _P]),
     "dsa_sli_grad_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),

@@ -137,21 +137,21 @@ size_t dsa_sfa_workspace_bytes(int total_rows, int n1, int d, int sparse_count,
 
 size_t dsa_sfa_workspace_zero_bytes(void) { return sfa_workspace_zero_bytes(); }
 
-int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key, const void* key_rope,
-                int io_dtype, const int32_t* sparse_indices, int sparse_count,
-                int sparse_block_size, const int32_t* block_table, int max_blocks,
-                int page_block_size, const int32_t* row_start, const int32_t* key_start,
-                const int32_t* act_q, const int32_t* act_k, int batch, int total_rows, int n1,
-                int d, int dr, int s2, int64_t key_rows, int sparse_mode, float scale, void* out,
-                float* sm_max,
-                float* sm_sum, void* workspace, size_t workspace_bytes, int kv_splits,
-                void* stream) {
+namespace {
+// Argument checks of dsa_sfa_fwd (the reference's conditions, sparse_flash_attention_triton.py
+// :1341-1351, :1391-1398) shared with dsa_sfa_fwd_noalloc; DSA_OK when the call may proceed.
+int check_sfa_fwd(const char* fn, const void* query, const void* query_rope, const void* key,
+                  const void* key_rope, int io_dtype, const int32_t* sparse_indices, int sparse_count,
+                  int sparse_block_size, const int32_t* block_table, int max_blocks, int page_block_size,
+                  const int32_t* row_start, const int32_t* key_start, const int32_t* act_q,
+                  const int32_t* act_k, int batch, int total_rows, int n1, int d, int dr, int64_t key_rows,
+                  int sparse_mode, void* out, float* sm_max, float* sm_sum, int kv_splits) {
   if (!query || !query_rope || !key || !key_rope || !sparse_indices || !row_start || !act_q ||
       !act_k || !out)
-    return fail(DSA_ERR_INVALID, "dsa_sfa_fwd: null pointer argument");
+    return fail(DSA_ERR_INVALID, "%s: null pointer argument", fn);
   if (!block_table && !key_start)
-    return fail(DSA_ERR_INVALID, "dsa_sfa_fwd: key_start required without block_table");
-  if (!is16(io_dtype)) return fail(DSA_ERR_INVALID, "dsa_sfa_fwd: io_dtype must be fp16 or bf16");
+    return fail(DSA_ERR_INVALID, "%s: key_start required without block_table", fn);
+  if (!is16(io_dtype)) return fail(DSA_ERR_INVALID, "%s: io_dtype must be fp16 or bf16", fn);
   if (sparse_mode != 0 && sparse_mode != 3)
     return fail(DSA_ERR_INVALID, "Only sparse_mode 0 (full) / 3 (rightDownCausal) supported");
   if (sparse_block_size < 1 || (sparse_block_size & (sparse_block_size - 1)) != 0 ||
@@ -163,14 +163,63 @@ int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key, cons
   if (n1 < 1 || n1 > 128 || (n1 & (n1 - 1)) != 0)
     return fail(DSA_ERR_INVALID, "N1 must be one of (1, 2, 4, 8, 16, 32, 64, 128), got %d", n1);
   if (batch <= 0 || total_rows < 0 || sparse_count <= 0 || key_rows < 0)
-    return fail(DSA_ERR_INVALID, "dsa_sfa_fwd: non-positive shape");
+    return fail(DSA_ERR_INVALID, "%s: non-positive shape", fn);
   if (block_table && (max_blocks <= 0 || page_block_size <= 0))
-    return fail(DSA_ERR_INVALID, "dsa_sfa_fwd: PA_BSND needs max_blocks and block_size > 0");
+    return fail(DSA_ERR_INVALID, "%s: PA_BSND needs max_blocks and block_size > 0", fn);
   if ((sm_max == nullptr) != (sm_sum == nullptr))
-    return fail(DSA_ERR_INVALID, "dsa_sfa_fwd: sm_max and sm_sum must both be given or both NULL");
+    return fail(DSA_ERR_INVALID, "%s: sm_max and sm_sum must both be given or both NULL", fn);
   if ((int64_t)sparse_count * sparse_block_size > (1 << 20))
-    return fail(DSA_ERR_UNSUPPORTED, "dsa_sfa_fwd: sparse_count*sparse_block_size > 2^20 tokens");
-  if (kv_splits > 16) return fail(DSA_ERR_UNSUPPORTED, "dsa_sfa_fwd: kv_splits=%d > 16", kv_splits);
+    return fail(DSA_ERR_UNSUPPORTED, "%s: sparse_count*sparse_block_size > 2^20 tokens", fn);
+  if (kv_splits > 16) return fail(DSA_ERR_UNSUPPORTED, "%s: kv_splits=%d > 16", fn, kv_splits);
+  return DSA_OK;
+}
+}  // namespace
+
+int dsa_sfa_fwd_noalloc(const void* query, const void* query_rope, const void* key, const void* key_rope,
+                        int io_dtype, const int32_t* sparse_indices, int sparse_count, int sparse_block_size,
+                        const int32_t* block_table, int max_blocks, int page_block_size,
+                        const int32_t* row_start, const int32_t* key_start, const int32_t* act_q,
+                        const int32_t* act_k, int batch, int total_rows, int n1, int d, int dr, int s2,
+                        int64_t key_rows, int sparse_mode, float scale, void* out, float* sm_max,
+                        float* sm_sum, int kv_splits, void* stream) {
+  const int st = check_sfa_fwd("dsa_sfa_fwd_noalloc", query, query_rope, key, key_rope, io_dtype,
+                               sparse_indices, sparse_count, sparse_block_size, block_table, max_blocks,
+                               page_block_size, row_start, key_start, act_q, act_k, batch, total_rows, n1,
+                               d, dr, key_rows, sparse_mode, out, sm_max, sm_sum, kv_splits);
+  if (st != DSA_OK) return st;
+  if (total_rows == 0) {
+    g_err[0] = 0;
+    return DSA_OK;
+  }
+  const size_t need = sfa_workspace_bytes(total_rows, n1, d, sparse_count, sparse_block_size, kv_splits);
+  if (need > DSA_SFA_NOALLOC_SCRATCH_BYTES)
+    return fail(DSA_ERR_UNSUPPORTED,
+                "dsa_sfa_fwd_noalloc: the problem needs %zu bytes of workspace, the static scratch holds %zu "
+                "(use dsa_sfa_fwd with a caller workspace)", need, (size_t)DSA_SFA_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  const hipError_t e = sfa_noalloc_workspace((hipStream_t)stream, &ws);
+  if (e != hipSuccess) return hip_status(e, "dsa_sfa_fwd_noalloc scratch set-up");
+  SfaArgs a{query, query_rope, key, key_rope, io_dtype, sparse_indices, sparse_count,
+            sparse_block_size, block_table, max_blocks, page_block_size, row_start, key_start,
+            act_q, act_k, batch, total_rows, n1, d, dr, s2, key_rows, sparse_mode, scale, out, sm_max,
+            sm_sum, ws, (size_t)DSA_SFA_NOALLOC_SCRATCH_BYTES, kv_splits};
+  return hip_status(launch_sfa_fwd(a, (hipStream_t)stream), "dsa_sfa_fwd_noalloc launch");
+}
+
+int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key, const void* key_rope,
+                int io_dtype, const int32_t* sparse_indices, int sparse_count,
+                int sparse_block_size, const int32_t* block_table, int max_blocks,
+                int page_block_size, const int32_t* row_start, const int32_t* key_start,
+                const int32_t* act_q, const int32_t* act_k, int batch, int total_rows, int n1,
+                int d, int dr, int s2, int64_t key_rows, int sparse_mode, float scale, void* out,
+                float* sm_max,
+                float* sm_sum, void* workspace, size_t workspace_bytes, int kv_splits,
+                void* stream) {
+  const int st = check_sfa_fwd("dsa_sfa_fwd", query, query_rope, key, key_rope, io_dtype, sparse_indices,
+                               sparse_count, sparse_block_size, block_table, max_blocks, page_block_size,
+                               row_start, key_start, act_q, act_k, batch, total_rows, n1, d, dr, key_rows,
+                               sparse_mode, out, sm_max, sm_sum, kv_splits);
+  if (st != DSA_OK) return st;
   const size_t need = sfa_workspace_bytes(total_rows, n1, d, sparse_count, sparse_block_size, kv_splits);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
     return fail(DSA_ERR_INVALID, "dsa_sfa_fwd: workspace of %zu bytes required, %zu given", need,

@@ -220,6 +220,9 @@ hipError_t launch_li_topk(const LiTopkArgs& a, hipStream_t s);
 hipError_t launch_sfa_fwd(const SfaArgs& a, hipStream_t s);
 size_t sfa_workspace_bytes(int total_rows, int n1, int d, int topk, int sbs, int kv_splits);
 size_t sfa_workspace_zero_bytes();
+// The library's static per-device workspace of DSA_SFA_NOALLOC_SCRATCH_BYTES (its
+// address on the current device; its zero-row prefix cleared on first use)
+hipError_t sfa_noalloc_workspace(hipStream_t s, void** ws);
 
 // Per-row token lists (physical key rows in the golden's gather order,
 // sparse_flash_attention_numpy.py:38-60) built by the forward's token-list

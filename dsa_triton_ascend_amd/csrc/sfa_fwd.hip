@@ -46,6 +46,7 @@
 // Unlike the reference (sparse_flash_attention_triton.py:509-525) the fp32
 // accumulator never round-trips through HBM for unsplit rows.
 #include <climits>
+#include <mutex>
 
 #include "dsa_common.hpp"
 
@@ -1123,6 +1124,61 @@ hipError_t launch_sfa_token_lists(const SfaArgs& a, void* ws_base, SfaTokenLists
   else
     hipLaunchKernelGGL(dsa::sfa_tokens_kernel, dim3(a.total_rows), dim3(dsa::TOK_TPB), 0, s, a, cap, ws);
   return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- no-allocation workspace
+// dsa_sfa_fwd_noalloc runs the same launches on a file-scope device array instead of a
+// caller-allocated workspace. Its name is only a host-side handle: host code uses the
+// per-device address hipGetSymbolAddress returns, never the name itself.
+namespace {
+static __device__ __align__(256) uint8_t scratch[DSA_SFA_NOALLOC_SCRATCH_BYTES];
+
+constexpr int SCRATCH_MAX_DEVICES = 64;
+struct DeviceScratch {
+  void* ptr = nullptr;   // this device's copy of `scratch`
+  bool zeroed = false;   // its zero-row prefix cleared (by a synchronised, uncaptured launch)
+};
+std::mutex g_scratch_mu;
+DeviceScratch g_scratch[SCRATCH_MAX_DEVICES];
+
+__global__ void sfa_zero_prefix_kernel(uint4* p, int n16) {
+  for (int i = threadIdx.x; i < n16; i += blockDim.x) p[i] = make_uint4(0, 0, 0, 0);
+}
+}  // namespace
+
+hipError_t sfa_noalloc_workspace(hipStream_t s, void** ws) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= SCRATCH_MAX_DEVICES) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  DeviceScratch& d = g_scratch[dev];
+  if (d.ptr == nullptr) {   // once per device, with that device current
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    d.ptr = p;
+  }
+  if (!d.zeroed) {
+    // The zero KV row at the start of the workspace must read as zeros. The clear goes
+    // on the caller's stream ahead of the call's own launches; outside stream capture it
+    // is waited for once and never repeated, under capture it is part of every captured
+    // call until an uncaptured one has run.
+    const int n16 = (int)(sfa_workspace_zero_bytes() / 16);
+    hipLaunchKernelGGL(sfa_zero_prefix_kernel, dim3(1), dim3(256), 0, s, reinterpret_cast<uint4*>(d.ptr), n16);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(s, &st);
+    if (e != hipSuccess) return e;
+    if (st == hipStreamCaptureStatusNone) {
+      e = hipStreamSynchronize(s);
+      if (e != hipSuccess) return e;
+      d.zeroed = true;
+    }
+  }
+  *ws = d.ptr;
+  return hipSuccess;
 }
 
 hipError_t launch_sfa_fwd(const SfaArgs& a, hipStream_t s) {

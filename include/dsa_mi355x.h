@@ -173,6 +173,32 @@ int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key,
                 size_t workspace_bytes, int kv_splits, void* stream);
 
 /*
+ * dsa_sfa_fwd without a caller workspace. No counterpart in the reference: for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Arguments, semantics and outputs are those
+ * of dsa_sfa_fwd (same kernels); the workspace is the library's static per-device
+ * scratch array of DSA_SFA_NOALLOC_SCRATCH_BYTES, which each GPU the library runs on
+ * holds until the process ends. A problem whose dsa_sfa_workspace_bytes(...) exceeds
+ * that size is refused with DSA_ERR_UNSUPPORTED before any device work (e.g. C4 decode,
+ * 64 rows x 2048 tokens, and C3 prefill, 4096 rows x 2048 tokens, fit). The call
+ * allocates nothing; its first call on a device looks up that device's copy of the
+ * array and clears its zero-row prefix once (synchronising the given stream unless it
+ * is capturing). Every call on one GPU shares that GPU's array: calls that overlap on
+ * one GPU (different streams, or host threads without ordering) race and must be
+ * serialised by the caller.
+ */
+#define DSA_SFA_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+
+int dsa_sfa_fwd_noalloc(const void* query, const void* query_rope, const void* key,
+                        const void* key_rope, int io_dtype, const int32_t* sparse_indices,
+                        int sparse_count, int sparse_block_size, const int32_t* block_table,
+                        int max_blocks, int page_block_size, const int32_t* row_start,
+                        const int32_t* key_start, const int32_t* act_q, const int32_t* act_k,
+                        int batch, int total_rows, int n1, int d, int dr, int s2, int64_t key_rows,
+                        int sparse_mode, float scale, void* out, float* sm_max, float* sm_sum,
+                        int kv_splits, void* stream);
+
+/*
  * Workspace bytes for dsa_sfa_bwd: the token lists of total_rows rows, fp32
  * accumulators for d_key, d_key_rope and d_value over key_rows key rows, and two
  * dense io-dtype buffers of sum_b min(act_k[b], s2) * ceil64(rows_b * N1) elements

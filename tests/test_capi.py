@@ -260,3 +260,26 @@ def test_dense_loss_validation_matches_reference():
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(RuntimeError, match="missing"):
         _lib.load(tmp_path / "nope.so")
+
+
+def test_noalloc_refuses_problems_beyond_the_scratch():
+    """dsa_sfa_fwd_noalloc validates like dsa_sfa_fwd and refuses a problem whose workspace
+    exceeds its static scratch, before any device work (no GPU needed)."""
+    lib = _lib.load()
+    one = ctypes.c_void_p(1)
+    limit = 64 << 20
+    # C5-sized prefill: 18216 rows x 2048 tokens of token lists alone exceed the scratch
+    assert lib.dsa_sfa_workspace_bytes(18216, 128, 512, 2048, 1, 0) > limit
+    args = [one, one, one, one, 1, one, 2048, 1, None, 0, 0, one, one, one, one, 4, 18216, 128, 512, 64, 8192,
+            18216, 3, 0.04, one, one, one, 0, None]
+    assert lib.dsa_sfa_fwd_noalloc(*args) == _lib.DSA_ERR_UNSUPPORTED
+    assert b"static scratch" in lib.dsa_last_error()
+    # C4 decode and C3 prefill fit
+    assert lib.dsa_sfa_workspace_bytes(64, 128, 512, 2048, 1, 0) <= limit
+    assert lib.dsa_sfa_workspace_bytes(4096, 128, 512, 2048, 1, 0) <= limit
+    bad = list(args)
+    bad[0] = None
+    assert lib.dsa_sfa_fwd_noalloc(*bad) == _lib.DSA_ERR_INVALID and b"null pointer" in lib.dsa_last_error()
+    bad = list(args)
+    bad[18] = 64
+    assert lib.dsa_sfa_fwd_noalloc(*bad) == _lib.DSA_ERR_INVALID and b"D must be" in lib.dsa_last_error()
