@@ -84,7 +84,7 @@ int dsa_li_score_paged(const void* query, const void* key_cache, const void* wei
   if (max_blocks > LI_MAX_BLOCKS)
     return fail(DSA_ERR_UNSUPPORTED, "dsa_li_score_paged: max_blocks=%d > %d", max_blocks, LI_MAX_BLOCKS);
   const int64_t s2 = (int64_t)max_blocks * page_block_size;
-  if (s2 > 65536) return fail(DSA_ERR_UNSUPPORTED, "dsa_li_score_paged: max_blocks*block_size > 65536");
+  if (s2 > INT_MAX) return fail(DSA_ERR_UNSUPPORTED, "dsa_li_score_paged: max_blocks*block_size > 2^31-1");
   if (!is16(io_dtype)) return fail(DSA_ERR_INVALID, "dsa_li_score_paged: io_dtype must be fp16 or bf16");
   if (!is16(w_dtype) && w_dtype != DSA_DTYPE_F32)
     return fail(DSA_ERR_INVALID, "dsa_li_score_paged: weights dtype must be fp16, bf16 or fp32");
@@ -118,9 +118,8 @@ int dsa_li_topk(const uint16_t* scores, int64_t score_ld, int io_dtype, const in
   if (batch <= 0 || total_rows < 0 || n2 <= 0 || s2 < 0)
     return fail(DSA_ERR_INVALID, "dsa_li_topk: non-positive shape");
   if (sparse_count <= 0) return fail(DSA_ERR_INVALID, "dsa_li_topk: sparse_count must be positive");
-  if (sparse_count > 8192)
-    return fail(DSA_ERR_UNSUPPORTED, "dsa_li_topk: sparse_count=%d > 8192", sparse_count);
-  if (s2 > 65536) return fail(DSA_ERR_UNSUPPORTED, "dsa_li_topk: S2=%d > 65536", s2);
+  if (sparse_count > LI_TOPK_MAX_K)
+    return fail(DSA_ERR_UNSUPPORTED, "dsa_li_topk: sparse_count=%d > %d", sparse_count, LI_TOPK_MAX_K);
   if (sparse_mode != 0 && sparse_mode != 3)
     return fail(DSA_ERR_INVALID, "dsa_li_topk: sparse_mode must be 0 or 3");
   if (score_ld < s2) return fail(DSA_ERR_INVALID, "dsa_li_topk: score_ld < S2");
@@ -321,7 +320,7 @@ int dsa_sli_grad_kl_loss(const void* query, const void* key, const void* query_r
   if (!sli_grad_supported(d, dr, nidx1, d_idx, sparse_count))
     return fail(DSA_ERR_UNSUPPORTED,
                 "dsa_sli_grad_kl_loss: D=%d (+%d), Nidx1=%d, D_idx=%d, topK=%d outside D in {128,256,512}, "
-                "D_idx in {128,256,512}, Nidx1 <= 128 with ceil8(Nidx1)*D_idx <= 32768, topK <= 2048",
+                "D_idx in {128,256,512}, Nidx1 <= 128 with ceil32(Nidx1)*D_idx <= 32768, topK <= 2048",
                 d, dr, nidx1, d_idx, sparse_count);
   if (batch > 65535 || (int64_t)batch * s1 > INT32_MAX)
     return fail(DSA_ERR_UNSUPPORTED, "dsa_sli_grad_kl_loss: too many rows");

@@ -199,7 +199,8 @@ struct LiScoreArgs {
   // block_table[b * max_blocks + t / page_bs] * page_bs + t % page_bs of `k`
   const int32_t* block_table = nullptr; int max_blocks = 0; int page_bs = 0; int64_t key_rows = 0;
 };
-constexpr int LI_MAX_BLOCKS = 4096;   // block-table row held in LDS by the paged score kernel
+constexpr int LI_MAX_BLOCKS = 8192;   // block-table row held in LDS by the paged score kernel
+constexpr int LI_TOPK_MAX_K = 16384;  // top-k: the selected keys and their indices sorted in LDS
 struct LiTopkArgs {
   const uint16_t* scores; int64_t ld; int io;
   const int32_t* row_start; const int32_t* act_q; const int32_t* act_k;

@@ -39,19 +39,14 @@ namespace dsa {
 
 namespace {
 
-#ifndef DSA_LI_NW
-#define DSA_LI_NW 8
-#endif
-#ifndef DSA_LI_BN
-#define DSA_LI_BN 64
-#endif
-#ifndef DSA_LI_NBUF
-#define DSA_LI_NBUF 3
-#endif
-constexpr int NW = DSA_LI_NW;  // waves (= query rows) per work-group
+// Tile shape (swept on the MI355X over 4 / 8 waves, 64 / 128 keys, 3 / 4 buffers: this
+// setting was the fastest at C2)
+constexpr int NW = 8;          // waves (= query rows) per work-group
+constexpr int KEYS_PER_TILE = 64;
+constexpr int RING = 3;
 
 template <int D> struct LiTile {
-  static constexpr int BN = D == 96 ? 128 : (D <= 128 ? DSA_LI_BN : 32);  // keys per LDS tile
+  static constexpr int BN = D == 96 ? 128 : (D <= 128 ? KEYS_PER_TILE : 32);  // keys per LDS tile
   static constexpr int CPR = D / 8;                  // 16-byte chunks per key row
   // chunk permutation mask (c ^ (k & SWZ), stays in the row): 16 consecutive key rows
   // then cover 16 distinct 16-byte bank groups, conflict-free for 16-lane LDS reads
@@ -59,7 +54,7 @@ template <int D> struct LiTile {
   static constexpr int SLOTS = BN * CPR;             // 16-byte slots per tile
   static constexpr int IPW = SLOTS / (NW * 64);      // direct-to-LDS loads per wave per tile
   static_assert(IPW >= 1 && IPW * NW * 64 == SLOTS, "tile must split evenly over the waves");
-  static constexpr int NBUF = DSA_LI_NBUF;           // LDS ring: tile t being read, the rest in flight
+  static constexpr int NBUF = RING;                  // LDS ring: tile t being read, the rest in flight
 };
 
 __device__ __forceinline__ float load_w(const void* w, int wdt, int64_t i) {

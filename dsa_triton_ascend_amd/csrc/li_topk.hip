@@ -6,18 +6,21 @@
 // and quantised score), the other slots get -1 / 0. The reference's device
 // path calls mint.topk / mint.sort here (lightning_indexer_triton.py:343-361).
 //
-// One 256-thread work-group per score row:
+// One 256-thread work-group per score row (any length: indices are 32-bit):
 //   1. Thread t owns the contiguous index range [32t, 32t+32) of the row; the
 //      16-bit scores are mapped to order-preserving keys u (ord16) and kept in
-//      VGPRs (rows longer than 8192 entries are streamed from memory instead).
+//      VGPRs (rows longer than 8192 entries are streamed from memory instead, in
+//      chunks of 8192).
 //   2. L > k: the k-th largest key T is found with two 256-bin LDS histograms:
 //      one over the high byte of the keys picks the bin holding the k-th largest
 //      (a scan from the top bin), one over the low byte of the keys in that bin
 //      picks T; the same scans give the number of keys above T.
 //   3. Order-preserving compaction: entries with u > T and the first
 //      k - count(u > T) entries with u == T (in index order) are written, in
-//      index order, as keys (u << 16 | index) into LDS; per-thread positions come
-//      from block exclusive scans of the per-thread counts.
+//      index order, to positions p < k as keys (u << 16 | x); p comes from block
+//      exclusive scans of the per-thread counts. Rows of up to 65536 entries carry
+//      x = 0xFFFF - index; longer rows (WIDE) carry x = p and keep the 32-bit index
+//      in a second LDS array at p (p, like the index, increases along the row).
 //   4. A stable LSD radix sort on the 16-bit score (4 passes of 4 bits, digits
 //      of the inverted key so larger scores come first; per-thread counter
 //      columns in LDS, no atomics). Stability preserves the index order of
@@ -153,9 +156,11 @@ __device__ __forceinline__ void radix_sort_desc16(uint32_t (&key)[E], uint32_t* 
   }
 }
 
-template <int E>
+template <int E, bool WIDE>
 __global__ __launch_bounds__(TPB) void li_topk_kernel(LiTopkArgs a) {
+  static_assert(E * TPB <= 65536, "compacted positions are 16-bit");
   __shared__ __attribute__((aligned(16))) uint32_t sbuf[E * TPB];
+  __shared__ int32_t sidx[WIDE ? E * TPB : 1];   // WIDE: row index of compacted position p
   __shared__ uint16_t cnt[16 * TPB];
   __shared__ uint32_t red[TPB / 64];
   __shared__ uint32_t hist[256 * HSUB];
@@ -242,12 +247,20 @@ __global__ __launch_bounds__(TPB) void li_topk_kernel(LiTopkArgs a) {
     const int i0 = ch * ROW_CACHED + t * RPT;
 #pragma unroll
     for (int e = 0; e < RPT; ++e) {
-      const uint32_t key = (u[e] << 16) | (0xFFFFu - (uint32_t)(i0 + e));
+      // x: the index (rows up to 65536) or the position, whose index goes to sidx
+      auto put = [&](uint32_t p) {
+        if constexpr (WIDE) {
+          sbuf[p] = (u[e] << 16) | p;
+          sidx[p] = i0 + e;
+        } else {
+          sbuf[p] = (u[e] << 16) | (0xFFFFu - (uint32_t)(i0 + e));
+        }
+      };
       if (u[e] > T) {
-        sbuf[pg + (pe < need ? pe : need)] = key;
+        put(pg + (pe < need ? pe : need));
         ++pg;
       } else if (u[e] == T && T != 0) {
-        if (pe < need) sbuf[pg + pe] = key;
+        if (pe < need) put(pg + pe);
         ++pe;
       }
     }
@@ -268,7 +281,8 @@ __global__ __launch_bounds__(TPB) void li_topk_kernel(LiTopkArgs a) {
     const int i = E * t + e;
     if (i < k) {
       if (i < nout) {
-        iout[i] = (int32_t)(0xFFFFu - (key[e] & 0xFFFFu));
+        if constexpr (WIDE) iout[i] = sidx[key[e] & 0xFFFFu];
+        else iout[i] = (int32_t)(0xFFFFu - (key[e] & 0xFFFFu));
         if (vout) vout[i] = unord16(key[e] >> 16);
       } else {
         iout[i] = -1;
@@ -281,16 +295,22 @@ __global__ __launch_bounds__(TPB) void li_topk_kernel(LiTopkArgs a) {
 }  // namespace
 }  // namespace dsa
 
+template <bool WIDE>
+static hipError_t launch_topk_e(const LiTopkArgs& a, int e, unsigned rows, hipStream_t s) {
+  const dim3 grid(rows), block(dsa::TPB);
+  if (e <= 1) hipLaunchKernelGGL((dsa::li_topk_kernel<1, WIDE>), grid, block, 0, s, a);
+  else if (e <= 2) hipLaunchKernelGGL((dsa::li_topk_kernel<2, WIDE>), grid, block, 0, s, a);
+  else if (e <= 4) hipLaunchKernelGGL((dsa::li_topk_kernel<4, WIDE>), grid, block, 0, s, a);
+  else if (e <= 8) hipLaunchKernelGGL((dsa::li_topk_kernel<8, WIDE>), grid, block, 0, s, a);
+  else if (e <= 16) hipLaunchKernelGGL((dsa::li_topk_kernel<16, WIDE>), grid, block, 0, s, a);
+  else if (e <= 32) hipLaunchKernelGGL((dsa::li_topk_kernel<32, WIDE>), grid, block, 0, s, a);
+  else hipLaunchKernelGGL((dsa::li_topk_kernel<64, WIDE>), grid, block, 0, s, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_li_topk(const LiTopkArgs& a, hipStream_t s) {
   const int64_t rows = (int64_t)a.total_rows * a.n2;
   if (rows <= 0) return hipSuccess;
   const int e = (a.k + dsa::TPB - 1) / dsa::TPB;
-  const dim3 grid((unsigned)rows), block(dsa::TPB);
-  if (e <= 1) hipLaunchKernelGGL(dsa::li_topk_kernel<1>, grid, block, 0, s, a);
-  else if (e <= 2) hipLaunchKernelGGL(dsa::li_topk_kernel<2>, grid, block, 0, s, a);
-  else if (e <= 4) hipLaunchKernelGGL(dsa::li_topk_kernel<4>, grid, block, 0, s, a);
-  else if (e <= 8) hipLaunchKernelGGL(dsa::li_topk_kernel<8>, grid, block, 0, s, a);
-  else if (e <= 16) hipLaunchKernelGGL(dsa::li_topk_kernel<16>, grid, block, 0, s, a);
-  else hipLaunchKernelGGL(dsa::li_topk_kernel<32>, grid, block, 0, s, a);
-  return hipGetLastError();
+  return a.s2 > 65536 ? launch_topk_e<true>(a, e, (unsigned)rows, s) : launch_topk_e<false>(a, e, (unsigned)rows, s);
 }

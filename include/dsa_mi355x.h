@@ -68,7 +68,7 @@ const char* dsa_last_error(void);
  * Rows with s1 >= act_q[b] are not written.
  *   query  [total_rows, N1, D] io dtype;  key [.., N2, D] io dtype;
  *   weights[total_rows, N1] in w_dtype (fp16 / bf16 / fp32);
- *   io_dtype DSA_DTYPE_BF16 or DSA_DTYPE_F16;  D a multiple of 32 up to 512;
+ *   io_dtype DSA_DTYPE_BF16 or DSA_DTYPE_F16;  D in {64, 96, 128, 256, 512};
  *   N1 % N2 == 0;  sparse_mode 0 or 3;  score_ld >= S2.
  *   max_rows_per_batch = max_b(row_start[b+1]-row_start[b]) (host-known bound);
  *   max_kv = max_b act_k[b] (host-known bound, <= S2).
@@ -88,7 +88,7 @@ int dsa_li_score(const void* query, const void* key, const void* weights, int io
  *   block_table [batch, max_blocks] int32: token t of batch b is cache row
  *     block_table[b*max_blocks + t/page_block_size]*page_block_size + t%page_block_size;
  *     a -1 block (or one past the cache) is a zero key row: its scores are 0.
- *   S2 = max_blocks * page_block_size (<= 65536, max_blocks <= 4096); score_ld >= S2.
+ *   S2 = max_blocks * page_block_size (max_blocks <= 8192); score_ld >= S2.
  * Everything else as dsa_li_score (act_k[b] keys visible; no key_start).
  */
 int dsa_li_score_paged(const void* query, const void* key_cache, const void* weights, int io_dtype,
@@ -106,7 +106,7 @@ int dsa_li_score_paged(const void* query, const void* key_cache, const void* wei
  * min(L, sparse_count) are written to indices[(r*N2+n2)*sparse_count + i]
  * (int32) and, if `values` is not NULL, their 16-bit score to values[...];
  * the remaining slots get index -1 and value 0. Rows with s1 >= act_q are all -1 / 0.
- * Requires S2 <= 65536.
+ * Any S2 (int32 indices); sparse_count <= 16384.
  */
 int dsa_li_topk(const uint16_t* scores, int64_t score_ld, int io_dtype,
                 const int32_t* row_start, const int32_t* act_q, const int32_t* act_k,

@@ -43,8 +43,8 @@ def test_invalid_arguments_return_status_without_gpu():
     assert st == _lib.DSA_ERR_INVALID and b"divisible" in lib.dsa_last_error()
     st = lib.dsa_li_score(p, p, p, 1, 2, p, p, p, p, 1, 1, 8, 1, 100, 16, 1, 16, 3, p, 16, None)
     assert st == _lib.DSA_ERR_UNSUPPORTED
-    st = lib.dsa_li_topk(p, 70000, 1, p, p, p, 1, 1, 1, 70000, 3, 64, p, None, None)
-    assert st == _lib.DSA_ERR_UNSUPPORTED and b"65536" in lib.dsa_last_error()
+    st = lib.dsa_li_topk(p, 70000, 1, p, p, p, 1, 1, 1, 70000, 3, 16385, p, None, None)
+    assert st == _lib.DSA_ERR_UNSUPPORTED and b"16384" in lib.dsa_last_error()
     base = [p, p, p, p, 1, p, 64, 1, None, 0, 0, p, p, p, p, 1, 1, 128, 512, 64, 16, 16, 3, 0.1,
             p, None, None, p, 1 << 30, 0, None]
     # `base` itself is valid and is never called: each case below breaks one field

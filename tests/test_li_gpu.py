@@ -193,6 +193,40 @@ def test_rows_longer_than_register_cache(dev, mode):
     run_case(dev, 1, 16, 12000, 8, 1, 64, 512, mode, "bf16", max_rows=10 ** 9)
 
 
+@pytest.mark.parametrize("S2,K", [(131072, 2048), (131072, 16384), (70000, 9000)])
+def test_long_context_rows(dev, S2, K):
+    """DeepSeek-V3.2's 128K context: 16 query rows at the end of a 131,072-key causal window
+    (each row sees 131,057 .. 131,072 keys; 32-bit indices, rows streamed in 16 chunks),
+    top-k 2048 and 16384 (the largest sparse_count, 64 keys per thread in the sort), and a
+    row length that is no multiple of the 8192-key chunk. Oracle on 6 of the rows, the
+    top-k invariants on all."""
+    B, S1, N1, N2, D = 1, 16, 64, 1, 128
+    run_case(dev, B, S1, S2, N1, N2, D, K, 3, "bf16", act_q=[S1], act_k=[S2], max_rows=4, w_scale=1 / 8)
+
+
+def test_pa_bsnd_128k_context(dev):
+    """Decode-time indexing over a 128K paged context with 32-token pages (4,097 block-table
+    entries per batch), one query row per batch."""
+    rng = np.random.RandomState(14)
+    B, N1, D, K, dtype, page = 2, 64, 128, 2048, "bf16", 32
+    lens = [131072, 100003]
+    bt, cache, dense = _paged(rng, B, lens, page, 1, D, dtype, spare=1)
+    q = torch.from_numpy(rng.randn(B, 1, N1, D).astype(np.float32)).to(DT[dtype])
+    w = torch.from_numpy(rng.randn(B, 1, N1).astype(np.float32) / 8).to(DT[dtype])
+    idx, val = lightning_indexer(q.to(dev), cache.to(dev), w.to(dev), actual_seq_lengths_key=lens,
+                                 block_table=bt.to(dev), layout_key="PA_BSND", sparse_count=K, sparse_mode=3,
+                                 return_value=True)
+    torch.cuda.synchronize()
+    gi, gv = idx.cpu().numpy(), val.float().cpu().numpy()
+    S2 = dense.shape[1]
+    Ls = np.array([min(l, S2) for l in lens])
+    check_topk_properties(gi.reshape(-1, K), gv.reshape(-1, K), Ls, K)
+    stats = check_li(gi, gv, _np(q), dense, _np(w), np.ones(B, int), np.asarray(lens), K, 3, dtype)
+    print(f"[li parity] PA 128K: {stats}")
+    assert stats.flips <= max(4, 0.02 * stats.elements), stats
+    assert gi.max() >= 65536   # indices past 16 bits are produced
+
+
 def test_heavy_ties_at_the_threshold(dev):
     """Keys repeat four distinct rows, so each score row holds only a few distinct values
     and the k-th largest sits inside a large run of ties (taken in index order)."""
