@@ -471,6 +471,18 @@ def main():
                                           "gathered_kv_bytes": kv_bytes}
             del sd, kw
             torch.cuda.empty_cache()
+            log("[bench] SFA prefill at the reference's perf_sfa shape (N1=64) ...")
+            sg = W.sfa_grad_inputs(device="cuda:0", seed=42, **W.GRAD_PERF)
+            kw = dict(query=sg.query, key=sg.key, value=sg.key, sparse_indices=sg.sparse_indices, **sg.kwargs())
+            _, ms64 = bench_sfa(kw, 20, 1, torch)
+            f64 = GRAD_PAIRS * 64 * (576 + 512) * 2.0
+            breakdown["sfa_prefill_n64"] = {"ms": round(ms64, 4), "tflops": round(f64 / ms64 / 1e9, 2),
+                                            "frac_mfma": round(f64 / ms64 / 1e9 / PEAK_BF16_TFLOPS, 4),
+                                            "algorithmic_flop": f64,
+                                            "shape": "BSND B=1 S1=512 S2=4096 N1=64 D=512+64 top-k 2048 causal bf16 "
+                                                     "(perf_sfa_triton.py:7-9)"}
+            del sg, kw
+            torch.cuda.empty_cache()
             log("[bench] SFA backward at the reference's grad perf shape ...")
             breakdown["sfa_grad"] = bench_grad(W, torch)
             torch.cuda.empty_cache()

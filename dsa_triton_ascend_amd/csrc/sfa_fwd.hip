@@ -47,6 +47,7 @@
 // accumulator never round-trips through HBM for unsplit rows.
 #include <climits>
 #include <mutex>
+#include <type_traits>
 
 #include "dsa_common.hpp"
 
@@ -606,7 +607,6 @@ __global__ __launch_bounds__(256) void sfa_merge_kernel(SfaArgs a, int splits, W
 
 // ---------------------------------------------------------------- kernel 2
 constexpr int NWV = 4;      // waves per work-group (one per SIMD)
-constexpr int HB = 128;     // heads per work-group (N1 <= 128, padded)
 constexpr int BN = 32;      // tokens per tile
 constexpr int NBUF = 3;     // gather ring: tile t read, t+1 and t+2 in flight
 constexpr int PP = BN + 8;  // P tile pitch (elements)
@@ -688,16 +688,28 @@ __device__ __forceinline__ float agpr_scale(float o, float f) {
   return o;
 }
 
-template <int IO, int D>
+// NH heads per work-group: 128 (N1 <= 128, padded), or 64 for N1 <= 64. With 128 each wave
+// owns a 32-head block of S^T over the whole contraction. With 64 there are two head
+// blocks, so the waves pair up: wave w computes the S^T of head block w % 2 over half w / 2
+// of the contraction and the two halves are added through LDS (both waves of a pair then
+// hold the same scores, and the first one writes P); the PV product and O are split over
+// the D columns as for 128, at half the size.
+template <int IO, int D, int NH>
 __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, int splits, int fuse_tok, Ws ws) {
   using C = Cfg<D>;
+  static_assert(NH == 128 || NH == 64, "heads per work-group");
+  constexpr int MT = NH / 32;                      // 32-head blocks
+  constexpr bool KSPLIT = NH == 64;                // S^T contraction split over wave pairs
+  constexpr int KSH = KSPLIT ? C::KS / 2 : C::KS;  // S^T k-steps per wave
+  static_assert(!KSPLIT || (C::KS % 2 == 0 && KSH <= C::KSN), "first half of the contraction is nope");
   __shared__ __attribute__((aligned(16))) uint8_t nope_buf[NBUF][C::NOPE];
   __shared__ __attribute__((aligned(16))) uint8_t rope_buf[NBUF][C::ROPE];
-  __shared__ __attribute__((aligned(16))) uint16_t pt[2][HB * PP];   // P of tiles t (PV) and t+1 (softmax)
-  __shared__ __attribute__((aligned(16))) uint16_t qrs[HB * QRP];   // Q rope of all heads
+  __shared__ __attribute__((aligned(16))) uint16_t pt[2][NH * PP];   // P of tiles t (PV) and t+1 (softmax)
+  __shared__ __attribute__((aligned(16))) uint16_t qrs[NH * QRP];   // Q rope of all heads
   __shared__ __attribute__((aligned(16))) int32_t s_ids[4][BN];   // token-id ring (tiles t+2 .. t+4)
-  __shared__ float s_alpha[2][HB];   // O rescale factors of tiles t and t+1
-  __shared__ float s_l[HB];   // 1 / row sum, per head
+  __shared__ float s_alpha[2][NH];   // O rescale factors of tiles t and t+1
+  __shared__ float s_l[NH];   // 1 / row sum, per head
+  __shared__ __attribute__((aligned(16))) float s_xch[KSPLIT ? NWV : 1][KSPLIT ? 16 * 64 : 4];   // S^T halves
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   // rows in reverse order: under causal masks the last rows of a batch hold the most
@@ -715,15 +727,21 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   // loads (padded heads are zeroed afterwards). Nothing here depends on the token
   // list: these loads are in flight while the row's token count and ids are
   // fetched (or, when the split lists its own tokens, from its block-table lookups on).
-  const int hq = wave * 32 + (lane & 31);
-  uint4 qf[C::KSN];
-  uint4 qrv[HB * (DR / 8) / (NWV * 64)];
+  const int kh = KSPLIT ? wave >> 1 : 0;   // this wave's half of the S^T contraction
+  const int hq = (KSPLIT ? wave & 1 : wave) * 32 + (lane & 31);
+  // Q^T nope fragments of this wave's k-steps kh * KSH + j (those inside the nope part)
+  constexpr int QF = KSH < C::KSN ? KSH : C::KSN;
+  uint4 qf[QF];
+  uint4 qrv[NH * (DR / 8) / (NWV * 64)];
   auto issue_q = [&]() __attribute__((always_inline)) {
     const uint16_t* qn = reinterpret_cast<const uint16_t*>(a.q) + ((int64_t)r * n1 + min(hq, n1 - 1)) * D;
 #pragma unroll
-    for (int ks = 0; ks < C::KSN; ++ks) qf[ks] = ldg16(qn + ks * 16 + (lane >> 5) * 8);
+    for (int j = 0; j < QF; ++j) {
+      const int ks = kh * KSH + j;
+      qf[j] = ldg16(qn + (ks < C::KSN ? ks : 0) * 16 + (lane >> 5) * 8);
+    }
 #pragma unroll
-    for (int j = 0; j < HB * (DR / 8) / (NWV * 64); ++j) {
+    for (int j = 0; j < NH * (DR / 8) / (NWV * 64); ++j) {
       const int h = (threadIdx.x >> 3) + j * (NWV * 64 / 8), e = (threadIdx.x & 7) * 8;
       qrv[j] = ldg16(reinterpret_cast<const uint16_t*>(a.qr) + ((int64_t)r * n1 + min(h, n1 - 1)) * DR + e);
     }
@@ -808,9 +826,9 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   wait_vmcnt<0>();
   if (hq >= n1)
 #pragma unroll
-    for (int ks = 0; ks < C::KSN; ++ks) qf[ks] = make_uint4(0, 0, 0, 0);
+    for (int j = 0; j < QF; ++j) qf[j] = make_uint4(0, 0, 0, 0);
 #pragma unroll
-  for (int j = 0; j < HB * (DR / 8) / (NWV * 64); ++j) {
+  for (int j = 0; j < NH * (DR / 8) / (NWV * 64); ++j) {
     const int h = (threadIdx.x >> 3) + j * (NWV * 64 / 8), e = (threadIdx.x & 7) * 8;
     *reinterpret_cast<uint4*>(qrs + h * QRP + e) = h < n1 ? qrv[j] : make_uint4(0, 0, 0, 0);
   }
@@ -825,9 +843,9 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
     float agpr_hint = 0.f;
     asm volatile("" : "+a"(agpr_hint));
   }
-  f32x16 o[4][C::NT];
+  f32x16 o[MT][C::NT];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int nt = 0; nt < C::NT; ++nt)
 #pragma unroll
@@ -837,9 +855,11 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   const int g16 = lane >> 4, c16 = lane & 15;
   constexpr int KQ = BN / 16;
 
-  // ---- S^T[32 tokens, 32 heads] of tile u for this wave; `spread(ks)` issues the
-  // loads scheduled after k-step ks (the next tile's gathers ride on this chain)
-  auto s_tile = [&](int u, auto&& spread) __attribute__((always_inline)) -> f32x16 {
+  // ---- S^T[32 tokens, 32 heads] of tile u for this wave over k-steps [K0, K0 + KSH),
+  // K0 = KH * KSH; `spread(j)` issues the loads scheduled after the chain's j-th step
+  // (the next tile's gathers ride on this chain)
+  auto s_tile_k = [&](int u, auto&& spread, auto khc) __attribute__((always_inline)) -> f32x16 {
+    constexpr int K0 = decltype(khc)::value * KSH;
     const uint8_t* nope = nope_buf[u % NBUF];
     const uint8_t* rope = rope_buf[u % NBUF];
     f32x16 sacc = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -850,24 +870,55 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
       return ks < C::KSN ? *reinterpret_cast<const uint4*>(arow + ks * 32)
                          : *reinterpret_cast<const uint4*>(rope + rope_off(tr, (ks - C::KSN) * 2 + kg));
     };
-    // the Q-rope B fragments (LDS) are fetched with the first operands, so the
-    // rope k-steps at the end of the chain do not wait on LDS
-    uint4 qr[(C::KS - C::KSN)];
+    // the Q-rope B fragments (LDS) of the chain's rope k-steps are fetched with the
+    // first operands, so the rope k-steps at the end of the chain do not wait on LDS
+    constexpr int NR = C::KS - C::KSN;
+    uint4 qr[NR];
 #pragma unroll
-    for (int j = 0; j < C::KS - C::KSN; ++j)
-      qr[j] = *reinterpret_cast<const uint4*>(qrs + hq * QRP + j * 16 + kg * 8);
+    for (int j = 0; j < NR; ++j)
+      if (C::KSN + j >= K0 && C::KSN + j < K0 + KSH)
+        qr[j] = *reinterpret_cast<const uint4*>(qrs + hq * QRP + j * 16 + kg * 8);
     uint4 af[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) af[j] = a_frag(j);
+    for (int j = 0; j < 4; ++j) af[j] = a_frag(K0 + j);
 #pragma unroll
-    for (int ks = 0; ks < C::KS; ++ks) {
-      const uint4 bq = ks < C::KSN ? qf[ks] : qr[ks - C::KSN];
-      sacc = Mfma<IO>::m32(af[ks & 3], bq, sacc);
-      if (ks + 4 < C::KS) af[ks & 3] = a_frag(ks + 4);
-      spread(ks);
+    for (int j = 0; j < KSH; ++j) {
+      const int ks = K0 + j;
+      const uint4 bq = ks < C::KSN ? qf[j < QF ? j : 0] : qr[ks >= C::KSN ? ks - C::KSN : 0];
+      sacc = Mfma<IO>::m32(af[j & 3], bq, sacc);
+      if (j + 4 < KSH) af[j & 3] = a_frag(ks + 4);
+      spread(j);
       __builtin_amdgcn_sched_barrier(0);
     }
     return sacc;
+  };
+  // the full S^T of tile u for this wave's head block: one chain, or (64 heads) this
+  // wave's half plus its partner's from LDS (the same sum in both waves of the pair)
+  auto s_tile = [&](int u, auto&& spread) __attribute__((always_inline)) -> f32x16 {
+    if constexpr (KSPLIT) {
+      const int kh_u = __builtin_amdgcn_readfirstlane(kh);
+      f32x16 sv = kh_u == 0 ? s_tile_k(u, spread, std::integral_constant<int, 0>{})
+                            : s_tile_k(u, spread, std::integral_constant<int, 1>{});
+      const int w_u = __builtin_amdgcn_readfirstlane(wave);
+      float* mine = &s_xch[w_u][0];
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<float4*>(mine + (g * 64 + lane) * 4) =
+            make_float4(sv[4 * g], sv[4 * g + 1], sv[4 * g + 2], sv[4 * g + 3]);
+      lds_barrier();   // both halves written; the partner's was read before the next tile's barrier
+      const float* other = &s_xch[w_u ^ 2][0];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 p = *reinterpret_cast<const float4*>(other + (g * 64 + lane) * 4);
+        sv[4 * g] += p.x;
+        sv[4 * g + 1] += p.y;
+        sv[4 * g + 2] += p.z;
+        sv[4 * g + 3] += p.w;
+      }
+      return sv;
+    } else {
+      return s_tile_k(u, spread, std::integral_constant<int, 0>{});
+    }
   };
 
   // ---- scores of tile u scaled; slots past the token list (partial last tile) masked
@@ -902,6 +953,7 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
     const float mb = m_used * LOG2E;
     float psum = 0.f;
     uint16_t* prow = pt[u & 1] + hq * PP + kg * 4;
+    const bool writer = !KSPLIT || kh == 0;   // one wave of a pair writes P and alpha
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       float p[4];
@@ -910,23 +962,23 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
         p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[g * 4 + j], LOG2E, -mb));
         psum += p[j];
       }
-      *reinterpret_cast<uint2*>(prow + g * 8) = make_uint2(pack2<IO>(p[0], p[1]), pack2<IO>(p[2], p[3]));
+      if (writer) *reinterpret_cast<uint2*>(prow + g * 8) = make_uint2(pack2<IO>(p[0], p[1]), pack2<IO>(p[2], p[3]));
     }
     l_part = l_part * alpha + psum;
-    s_alpha[u & 1][hq] = alpha;   // both lane halves hold the same head and value
+    if (writer) s_alpha[u & 1][hq] = alpha;   // both lane halves hold the same head and value
   };
 
-  // ---- O^T[this wave's D/4 columns, 128 heads] += V^T P^T for tile u. Every operand (P
+  // ---- O^T[this wave's D/4 columns, NH heads] += V^T P^T for tile u. Every operand (P
   // fragments of pt[u & 1] and transposed V reads for both 16-token steps) is
   // requested first; `between()` runs after the requests and before the MFMAs.
   auto pv_tile = [&](int u, auto&& between) __attribute__((always_inline)) {
     const uint8_t* nope = nope_buf[u % NBUF];
     const uint16_t* ptu = pt[u & 1];
-    uint4 pa[KQ][4], vb[KQ][C::NT];
+    uint4 pa[KQ][MT], vb[KQ][C::NT];
 #pragma unroll
     for (int kq = 0; kq < KQ; ++kq) {
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
         pa[kq][mt] = *reinterpret_cast<const uint4*>(ptu + (mt * 32 + (lane & 31)) * PP + kq * 16 + kg * 8);
 #pragma unroll
       for (int nt = 0; nt < C::NT; ++nt) {
@@ -943,7 +995,7 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
 #pragma unroll
       for (int nt = 0; nt < C::NT; ++nt)
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) o[mt][nt] = Mfma<IO>::m32(vb[kq][nt], pa[kq][mt], o[mt][nt]);
+        for (int mt = 0; mt < MT; ++mt) o[mt][nt] = Mfma<IO>::m32(vb[kq][nt], pa[kq][mt], o[mt][nt]);
   };
 
   // ---- software pipeline over tiles. Iteration t: (barrier) rescale O for tile t,
@@ -969,11 +1021,11 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
     else
       wait_vmcnt<1>();
     lds_barrier();     // P and alpha of tile t visible; tile t+1 resident; PV of tile t-1 done everywhere
-    const float a0 = s_alpha[t & 1][lane], a1 = s_alpha[t & 1][lane + 64];
+    const float a0 = s_alpha[t & 1][lane], a1 = NH > 64 ? s_alpha[t & 1][(lane + 64) % NH] : 1.f;
     if (__builtin_amdgcn_ballot_w64(a0 != 1.f || a1 != 1.f)) {
       // O^T layout: every element a lane holds in M tile mt belongs to head mt*32 + lane%32
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
+      for (int mt = 0; mt < MT; ++mt) {
         const float al = s_alpha[t & 1][mt * 32 + (lane & 31)];
 #pragma unroll
         for (int nt = 0; nt < C::NT; ++nt)
@@ -992,7 +1044,7 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
     f32x16 s1 = s_tile(t + 1, [&](int ks) {
 #pragma unroll
       for (int j = 0; j < C::GPW; ++j)
-        if (j * C::KS / C::GPW == ks) {
+        if (j * KSH / C::GPW == ks) {
           if (j < C::GPW - 1) gather_part<D>(j, kb, krb, ws.zero, krows, ix, gnope, grope, wave_u, lane);
           else ids_dma(t + 4);   // slot (t+4)%4 held the ids of tile t, read two iterations ago
         }
@@ -1008,13 +1060,14 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   // ---- epilogue
   const float l_tot = l_part + __shfl_xor(l_part, 32);
   __syncthreads();  // all PV reads of s_alpha / pt done before s_l is written
-  if (lane < 32) s_l[hq] = 1.f / l_tot;   // l > 0: a row or split holds at least one token
+  const bool owner = lane < 32 && kh == 0;   // one lane per head (a pair holds equal values)
+  if (owner) s_l[hq] = 1.f / l_tot;   // l > 0: a row or split holds at least one token
   if (direct) {
-    if (lane < 32 && hq < n1 && a.sm_max) {
+    if (owner && hq < n1 && a.sm_max) {
       a.sm_max[(int64_t)r * n1 + hq] = m_true;
       a.sm_sum[(int64_t)r * n1 + hq] = l_tot * exp2f((m_used - m_true) * LOG2E);
     }
-  } else if (lane < 32 && hq < n1) {
+  } else if (owner && hq < n1) {
     float* ps = ws.part_s + (((int64_t)r * splits + sp) * n1 + hq) * 3;
     ps[0] = m_used;
     ps[1] = m_true;
@@ -1027,7 +1080,7 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   // [16,24) of the 32-column group and lanes l >= 32 with [8,16) and [24,32): two
   // 16-byte stores per accumulator instead of sixteen 2-byte ones.
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
+  for (int mt = 0; mt < MT; ++mt) {
     const int h = mt * 32 + (lane & 31);
     const float inv = s_l[h];
     // one split: the output row; several: this split's normalised partial
@@ -1057,8 +1110,12 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
 
 template <int IO, int D>
 hipError_t launch_attn_d(const SfaArgs& a, hipStream_t s, int cap, int splits, int fuse_tok, Ws ws) {
-  hipLaunchKernelGGL((sfa_attn_kernel<IO, D>), dim3(a.total_rows, splits), dim3(NWV * 64), 0, s, a,
-                     cap, splits, fuse_tok, ws);
+  if (a.n1 <= 64)
+    hipLaunchKernelGGL((sfa_attn_kernel<IO, D, 64>), dim3(a.total_rows, splits), dim3(NWV * 64), 0, s, a,
+                       cap, splits, fuse_tok, ws);
+  else
+    hipLaunchKernelGGL((sfa_attn_kernel<IO, D, 128>), dim3(a.total_rows, splits), dim3(NWV * 64), 0, s, a,
+                       cap, splits, fuse_tok, ws);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;
   const int units = a.n1 * (D / 8);
