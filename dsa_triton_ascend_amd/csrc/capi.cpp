@@ -320,7 +320,7 @@ int dsa_sli_grad_kl_loss(const void* query, const void* key, const void* query_r
   if (!sli_grad_supported(d, dr, nidx1, d_idx, sparse_count))
     return fail(DSA_ERR_UNSUPPORTED,
                 "dsa_sli_grad_kl_loss: D=%d (+%d), Nidx1=%d, D_idx=%d, topK=%d outside D in {128,256,512}, "
-                "D_idx in {128,256,512}, Nidx1 <= 128 with ceil32(Nidx1)*D_idx <= 32768, topK <= 2048",
+                "D_idx in {128,256,512}, Nidx1 <= 128, topK <= 2048",
                 d, dr, nidx1, d_idx, sparse_count);
   if (batch > 65535 || (int64_t)batch * s1 > INT32_MAX)
     return fail(DSA_ERR_UNSUPPORTED, "dsa_sli_grad_kl_loss: too many rows");
@@ -354,8 +354,8 @@ int dsa_dense_li_softmax_lse(const void* query_index, const void* key_index, con
   if (batch <= 0 || s1 < 0 || s2 <= 0) return fail(DSA_ERR_INVALID, "dsa_dense_li_softmax_lse: non-positive shape");
   if (!dense_li_grad_supported(1, 1, 128, 0, nidx1, d_idx, s2))
     return fail(DSA_ERR_UNSUPPORTED,
-                "dsa_dense_li_softmax_lse: Nidx1=%d, D_idx=%d, S2=%d outside D_idx in {128,256,512}, Nidx1 <= 128 "
-                "with ceil32(Nidx1)*D_idx <= 32768, S2 <= 4096", nidx1, d_idx, s2);
+                "dsa_dense_li_softmax_lse: Nidx1=%d, D_idx=%d outside D_idx in {128,256,512}, Nidx1 <= 128",
+                nidx1, d_idx);
   if (batch > 65535 || (int64_t)batch * s1 > INT32_MAX)
     return fail(DSA_ERR_UNSUPPORTED, "dsa_dense_li_softmax_lse: too many rows");
   if (batch * s1 == 0) return DSA_OK;
@@ -386,9 +386,8 @@ int dsa_dense_li_grad_kl_loss(const void* query, const void* key, const void* qu
   if (dr != 0 && dr != 64) return fail(DSA_ERR_INVALID, "rope dim must be 64 (or 0 without rope), got %d", dr);
   if (!dense_li_grad_supported(n1, n2, d, dr, nidx1, d_idx, s2))
     return fail(DSA_ERR_UNSUPPORTED,
-                "dsa_dense_li_grad_kl_loss: D=%d (+%d), N1=%d, N2=%d, Nidx1=%d, D_idx=%d, S2=%d outside D, D_idx in "
-                "{128,256,512}, Nidx1 <= 128 with ceil32(Nidx1)*D_idx <= 32768, S2 <= 4096", d, dr, n1, n2,
-                nidx1, d_idx, s2);
+                "dsa_dense_li_grad_kl_loss: D=%d (+%d), N1=%d, N2=%d, Nidx1=%d, D_idx=%d outside D, D_idx in "
+                "{128,256,512}, Nidx1 <= 128", d, dr, n1, n2, nidx1, d_idx);
   if (batch > 65535 || (int64_t)batch * s1 > INT32_MAX)
     return fail(DSA_ERR_UNSUPPORTED, "dsa_dense_li_grad_kl_loss: too many rows");
   const size_t need = sli_grad_workspace_bytes(batch * s1, s2, (int64_t)batch * s2, d_idx);

@@ -50,6 +50,7 @@ struct SliArgs {
   float* p;        // [rows, topk] teacher sums
   float* dki_acc;  // [batch * s2, didx]
   float* row_loss; // [rows]
+  float* ibuf;     // [rows, topk] I / dI when a row has more than SLI_MAX_SLOTS slots
   // dense mode (sidx == nullptr: slot t is key t, up to S2 slots per row)
   int n2;                              // key heads of the teacher, stats [B, N2, S1, N1 / N2]
   const float* imax; const float* isum; // given indexer softmax stats [rows], or nullptr
@@ -271,16 +272,19 @@ __device__ __forceinline__ uint4 s_tr_frag(const uint16_t* X, int pitch, int c0,
   return make_uint4(lo.x, lo.y, hi.x, hi.y);
 }
 
-// One work-group (4 waves) per row; wave w < NGB owns indexer heads 32w..32w+31.
-// Per tile of 32 slots: dot^T[slot, head] = ki qi^T on 32x32x16 MFMAs (slots as M),
-// relu * w summed over the heads (half-wave shuffles, then across waves in LDS) is
-// I; in the second pass the same tiles give dW (per lane), ds = dI w [relu > 0]
-// (to LDS as [head][slot], split in two io-dtype parts), dQI[head, col] += ds ki
-// (registers) and dKI[slot, col] = ds^T qi, added at the slot's key row with fp32
-// atomics.
-template <int IO, int DI, int NGB>
+// One work-group (4 waves) per row. The row's qi block is taken in NHH passes of GP =
+// 32 NGB heads (NHH = 2 when the whole block would not fit LDS: Nidx1 > 64 at D_idx = 512);
+// wave w < NGB owns heads 32w..32w+31 of a pass. Per tile of 32 slots, dot^T[slot, head] =
+// ki qi^T on 32x32x16 MFMAs (slots as M), and relu * w summed over the heads (half-wave
+// shuffles, then across waves and passes) is I. The first sweep over the tiles keeps a
+// running max / sum of I (the softmax statistics: the LSE-only mode stops there) and
+// stores I per slot, in LDS or, for rows of more than SLI_MAX_SLOTS slots (BIG), in a
+// workspace row. The second sweep recomputes the dots and gives dW (per lane), ds = dI w
+// [relu > 0] (to LDS as [head][slot], split in two io-dtype parts), dQI[head, col] += ds ki
+// (registers) and dKI[slot, col] = ds^T qi, added at the slot's key row with fp32 atomics.
+template <int IO, int DI, int NGB, int NHH, bool BIG>
 __global__ __launch_bounds__(256) void sli_student_kernel(SliArgs a) {
-  constexpr int GP = 32 * NGB;         // heads, padded to whole blocks
+  constexpr int GP = 32 * NGB;         // heads of one pass, padded to whole blocks
   constexpr int QIP = DI + 8;          // qi / ki row pitch: odd count of 16-byte units
   constexpr int DP = SBT + 8;          // ds row pitch
   constexpr int KS = DI / 16;          // k-steps of the dots
@@ -293,7 +297,7 @@ __global__ __launch_bounds__(256) void sli_student_kernel(SliArgs a) {
   // indexer softmax is sharply peaked, ds reaches |w|, and one 16-bit rounding of it
   // alone would cost ~2^-11 relative on d_key_index
   __shared__ __attribute__((aligned(16))) uint16_t dSs[2][GP * DP];
-  __shared__ float s_i[SLI_MAX_SLOTS];  // I, then dI
+  __shared__ float s_i_lds[BIG ? 1 : SLI_MAX_SLOTS];  // I, then dI (BIG: a workspace row instead)
   __shared__ float s_w[GP];
   __shared__ float red[SWV][SBT];
   __shared__ float s_red[SWV];
@@ -324,14 +328,18 @@ __global__ __launch_bounds__(256) void sli_student_kernel(SliArgs a) {
     if (tid == 0) a.row_loss[r] = 0.f;
     return;
   }
+  float* s_i = BIG ? a.ibuf + (int64_t)r * a.topk : s_i_lds;
   const uint16_t* qib = reinterpret_cast<const uint16_t*>(a.qi);
   const uint16_t* kib = reinterpret_cast<const uint16_t*>(a.ki);
   const uint4 z4 = make_uint4(0, 0, 0, 0);
-  for (int i = tid; i < GP * (DI / 8); i += 256) {
-    const int g = i / (DI / 8), c = (i % (DI / 8)) * 8;
-    *reinterpret_cast<uint4*>(&QIs[g * QIP + c]) = g < G ? ldg16(qib + (qrow + g) * DI + c) : z4;
-  }
-  for (int g = tid; g < GP; g += 256) s_w[g] = g < G ? ld_w(a.w, a.wdt, qrow + g) : 0.f;
+  // qi rows and weights of pass hh: heads hh GP .. hh GP + GP - 1 (zero past Nidx1)
+  auto load_qi = [&](int hh) {
+    for (int i = tid; i < GP * (DI / 8); i += 256) {
+      const int g = i / (DI / 8), c = (i % (DI / 8)) * 8, gg = hh * GP + g;
+      *reinterpret_cast<uint4*>(&QIs[g * QIP + c]) = gg < G ? ldg16(qib + (qrow + gg) * DI + c) : z4;
+    }
+    for (int g = tid; g < GP; g += 256) s_w[g] = hh * GP + g < G ? ld_w(a.w, a.wdt, qrow + hh * GP + g) : 0.f;
+  };
   const int32_t* ids = a.sidx ? a.sidx + (int64_t)r * a.topk : nullptr;
 
   auto load_tile = [&](int t0, int nv) {
@@ -344,7 +352,7 @@ __global__ __launch_bounds__(256) void sli_student_kernel(SliArgs a) {
     if (tid < SBT) s_tok[tid] = tid < nv ? b * a.s2 + slot_key(a, ids, t0 + tid) : -1;
   };
   // dot^T of this wave's head block over the tile: element e -> slot m32_row(e, lane),
-  // head 32 wave + lane % 32
+  // head 32 wave + lane % 32 (of the current pass)
   auto dots = [&]() -> f32x16 {
     f32x16 acc = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     const uint16_t* arow = KIs + (lane & 31) * QIP + (lane >> 5) * 8;
@@ -355,32 +363,50 @@ __global__ __launch_bounds__(256) void sli_student_kernel(SliArgs a) {
                           *reinterpret_cast<const uint4*>(brow + ks * 16), acc);
     return acc;
   };
-  __syncthreads();
+  if (NHH == 1) load_qi(0);   // one pass: the block stays for both sweeps
 
-  // ---- pass 1: I per slot
+  // ---- first sweep: I per slot, with a running max / sum (wave 0, lanes < 32)
+  float run_m = -INFINITY, run_l = 0.f;
   for (int t0 = 0; t0 < n; t0 += SBT) {
     const int nv = n - t0 < SBT ? n - t0 : SBT;
     load_tile(t0, nv);
-    __syncthreads();
-    if (wave < NGB) {
-      const f32x16 acc = dots();
-      const float wg = s_w[32 * wave + (lane & 31)];
+    float iv = 0.f;   // thread tid < nv: I of slot t0 + tid, summed over the passes
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        float v = wg * fmaxf(acc[e], 0.f);
+    for (int hh = 0; hh < NHH; ++hh) {
+      if (NHH > 1) load_qi(hh);
+      __syncthreads();
+      if (wave < NGB) {
+        const f32x16 acc = dots();
+        const float wg = s_w[32 * wave + (lane & 31)];
 #pragma unroll
-        for (int o = 16; o >= 1; o >>= 1) v += __shfl_xor(v, o, 32);
-        if ((lane & 31) == 0) red[wave][m32_row(e, lane)] = v;
+        for (int e = 0; e < 16; ++e) {
+          float v = wg * fmaxf(acc[e], 0.f);
+#pragma unroll
+          for (int o = 16; o >= 1; o >>= 1) v += __shfl_xor(v, o, 32);
+          if ((lane & 31) == 0) red[wave][m32_row(e, lane)] = v;
+        }
+      }
+      __syncthreads();
+      if (tid < nv) {
+#pragma unroll
+        for (int w = 0; w < NGB; ++w) iv += red[w][tid];
       }
     }
-    __syncthreads();
-    if (tid < nv) {
-      float sv = 0.f;
+    if (tid < SBT) {
+      const float v = tid < nv ? iv : -INFINITY;
+      if (!lse_only && tid < nv) s_i[t0 + tid] = v;
+      float tm = v;
 #pragma unroll
-      for (int w = 0; w < NGB; ++w) sv += red[w][tid];
-      s_i[t0 + tid] = sv;
+      for (int o = 16; o >= 1; o >>= 1) tm = fmaxf(tm, __shfl_xor(tm, o, 32));
+      const float nm = fmaxf(run_m, tm);   // finite: a tile holds at least one slot
+      float e = tid < nv ? expf(v - nm) : 0.f;
+#pragma unroll
+      for (int o = 16; o >= 1; o >>= 1) e += __shfl_xor(e, o, 32);
+      run_l = run_l * expf(run_m - nm) + e;   // the first tile: exp(-inf) = 0
+      run_m = nm;
     }
-    __syncthreads();
+    // the next tile overwrites KIs and s_tok: every wave's dots and the reads of red
+    // are behind the barrier above or in program order before the next one
   }
   // ---- softmax of I over the n slots, dI = sI - p, the row's loss
   auto block_sum = [&](float v) {
@@ -398,22 +424,21 @@ __global__ __launch_bounds__(256) void sli_student_kernel(SliArgs a) {
     mx = a.imax[r];
     inv = 1.f / fmaxf(a.isum[r], SEPS);
   } else {
-    mx = -INFINITY;
-    for (int k = tid; k < n; k += 256) mx = fmaxf(mx, s_i[k]);
-    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    if (lane == 0) s_red[wave] = mx;
+    if (tid == 0) {
+      s_red[0] = run_m;
+      s_red[1] = run_l;
+    }
     __syncthreads();
-    mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    mx = s_red[0];
+    const float es = s_red[1];
     __syncthreads();
-    float es = 0.f;
-    for (int k = tid; k < n; k += 256) es += expf(s_i[k] - mx);
-    es = block_sum(es);
     if (lse_only) {
       if (tid == 0) { a.lse_max[r] = mx; a.lse_sum[r] = es; }
       return;
     }
     inv = ids ? 1.f / (es + SEPS) : 1.f / fmaxf(es, SEPS);
   }
+  __syncthreads();   // every I stored (BIG: in the workspace row) before it is read back
   float ls = 0.f;
   for (int k = tid; k < n; k += 256) {
     const float sv = expf(s_i[k] - mx) * inv;
@@ -425,82 +450,90 @@ __global__ __launch_bounds__(256) void sli_student_kernel(SliArgs a) {
   const float row_loss = block_sum(ls);
   if (tid == 0) a.row_loss[r] = row_loss;
 
-  // ---- pass 2
-  f32x16 dq[NCB];
-#pragma unroll
-  for (int j = 0; j < NCB; ++j)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) dq[j][e] = 0.f;
-  float dwl = 0.f;
-  for (int t0 = 0; t0 < n; t0 += SBT) {
-    const int nv = n - t0 < SBT ? n - t0 : SBT;
-    load_tile(t0, nv);
-    __syncthreads();
-    if (wave < NGB) {
-      const f32x16 acc = dots();
-      const int g = 32 * wave + (lane & 31);
-      const float wg = s_w[g];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int tk = m32_row(e, lane);
-        const float di = tk < nv ? s_i[t0 + tk] : 0.f;
-        dwl += fmaxf(acc[e], 0.f) * di;
-        const float ds = acc[e] > 0.f ? di * wg : 0.f;
-        const uint16_t hi = from_f32<IO>(ds);
-        dSs[0][g * DP + tk] = hi;
-        dSs[1][g * DP + tk] = from_f32<IO>(ds - to_f32<IO>(hi));
-      }
+  // ---- second sweep, per pass of GP heads
+#pragma unroll 1
+  for (int hh = 0; hh < NHH; ++hh) {
+    if (NHH > 1) {
+      __syncthreads();   // the previous pass is done with QIs, s_w and dSs
+      load_qi(hh);
     }
-    __syncthreads();
-    // dQI[head, col] += ds[head, slot] ki[slot, col]   (this wave's head block)
-    if (wave < NGB) {
-#pragma unroll
-      for (int kq = 0; kq < SBT / 16; ++kq) {
-        const int off = (32 * wave + (lane & 31)) * DP + kq * 16 + (lane >> 5) * 8;
-        const uint4 ah = *reinterpret_cast<const uint4*>(dSs[0] + off);
-        const uint4 al = *reinterpret_cast<const uint4*>(dSs[1] + off);
-#pragma unroll
-        for (int j = 0; j < NCB; ++j) {
-          const uint4 bv = s_tr_frag(KIs, QIP, 32 * j, kq * 16, lane);
-          dq[j] = Mfma<IO>::m32(ah, bv, dq[j]);
-          dq[j] = Mfma<IO>::m32(al, bv, dq[j]);
-        }
-      }
-    }
-    // dKI[slot, col] = ds^T qi over the heads, this wave's column blocks
-#pragma unroll
-    for (int jj = 0; jj < JK; ++jj) {
-      const int j = wave + SWV * jj;
-      if (j < NCB) {
-        f32x16 c = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kq = 0; kq < GP / 16; ++kq) {
-          const uint4 bv = s_tr_frag(QIs, QIP, 32 * j, kq * 16, lane);
-          c = Mfma<IO>::m32(s_tr_frag(dSs[0], DP, 0, kq * 16, lane), bv, c);
-          c = Mfma<IO>::m32(s_tr_frag(dSs[1], DP, 0, kq * 16, lane), bv, c);
-        }
-        float* dst = a.dki_acc + 32 * j + (lane & 31);
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int kr = s_tok[m32_row(e, lane)];
-          if (kr >= 0) unsafeAtomicAdd(dst + (int64_t)kr * DI, c[e]);
-        }
-      }
-    }
-    __syncthreads();   // the next tile overwrites KIs, dSs and s_tok
-  }
-  // ---- epilogue: dQI (element e -> head 32 wave + m32_row(e, lane), column 32 j + lane % 32), dW
-  if (wave < NGB) {
+    f32x16 dq[NCB];
 #pragma unroll
     for (int j = 0; j < NCB; ++j)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int g = 32 * wave + m32_row(e, lane);
-        if (g < G) dqio[(qrow + g) * DI + 32 * j + (lane & 31)] = from_f32<IO>(dq[j][e]);
+      for (int e = 0; e < 16; ++e) dq[j][e] = 0.f;
+    float dwl = 0.f;
+    for (int t0 = 0; t0 < n; t0 += SBT) {
+      const int nv = n - t0 < SBT ? n - t0 : SBT;
+      load_tile(t0, nv);
+      __syncthreads();
+      if (wave < NGB) {
+        const f32x16 acc = dots();
+        const int g = 32 * wave + (lane & 31);
+        const float wg = s_w[g];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int tk = m32_row(e, lane);
+          const float di = tk < nv ? s_i[t0 + tk] : 0.f;
+          dwl += fmaxf(acc[e], 0.f) * di;
+          const float ds = acc[e] > 0.f ? di * wg : 0.f;
+          const uint16_t hi = from_f32<IO>(ds);
+          dSs[0][g * DP + tk] = hi;
+          dSs[1][g * DP + tk] = from_f32<IO>(ds - to_f32<IO>(hi));
+        }
       }
-    const float v = dwl + __shfl_xor(dwl, 32);   // the two slot halves of head lane % 32
-    const int g = 32 * wave + lane;
-    if (lane < 32 && g < G) store_w(g, v);
+      __syncthreads();
+      // dQI[head, col] += ds[head, slot] ki[slot, col]   (this wave's head block)
+      if (wave < NGB) {
+#pragma unroll
+        for (int kq = 0; kq < SBT / 16; ++kq) {
+          const int off = (32 * wave + (lane & 31)) * DP + kq * 16 + (lane >> 5) * 8;
+          const uint4 ah = *reinterpret_cast<const uint4*>(dSs[0] + off);
+          const uint4 al = *reinterpret_cast<const uint4*>(dSs[1] + off);
+#pragma unroll
+          for (int j = 0; j < NCB; ++j) {
+            const uint4 bv = s_tr_frag(KIs, QIP, 32 * j, kq * 16, lane);
+            dq[j] = Mfma<IO>::m32(ah, bv, dq[j]);
+            dq[j] = Mfma<IO>::m32(al, bv, dq[j]);
+          }
+        }
+      }
+      // dKI[slot, col] = ds^T qi over the pass's heads, this wave's column blocks
+#pragma unroll
+      for (int jj = 0; jj < JK; ++jj) {
+        const int j = wave + SWV * jj;
+        if (j < NCB) {
+          f32x16 c = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int kq = 0; kq < GP / 16; ++kq) {
+            const uint4 bv = s_tr_frag(QIs, QIP, 32 * j, kq * 16, lane);
+            c = Mfma<IO>::m32(s_tr_frag(dSs[0], DP, 0, kq * 16, lane), bv, c);
+            c = Mfma<IO>::m32(s_tr_frag(dSs[1], DP, 0, kq * 16, lane), bv, c);
+          }
+          float* dst = a.dki_acc + 32 * j + (lane & 31);
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int kr = s_tok[m32_row(e, lane)];
+            if (kr >= 0) unsafeAtomicAdd(dst + (int64_t)kr * DI, c[e]);
+          }
+        }
+      }
+      __syncthreads();   // the next tile overwrites KIs, dSs and s_tok
+    }
+    // ---- dQI of the pass (element e -> head hh GP + 32 wave + m32_row(e, lane), column
+    // 32 j + lane % 32) and dW
+    if (wave < NGB) {
+#pragma unroll
+      for (int j = 0; j < NCB; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int g = hh * GP + 32 * wave + m32_row(e, lane);
+          if (g < G) dqio[(qrow + g) * DI + 32 * j + (lane & 31)] = from_f32<IO>(dq[j][e]);
+        }
+      const float v = dwl + __shfl_xor(dwl, 32);   // the two slot halves of head lane % 32
+      const int g = hh * GP + 32 * wave + lane;
+      if (lane < 32 && g < G) store_w(g, v);
+    }
   }
 }
 
@@ -528,17 +561,26 @@ __global__ void sli_finish_kernel(SliArgs a, int64_t n4, int rows) {
   }
 }
 
-// head blocks: the smallest of 1, 2, 4 covering Nidx1 / 32 (the qi block
-// 32 NGB x DI stays within SLI_MAX_GD elements, checked by the caller)
-template <int IO, int DI>
-void launch_student(const SliArgs& a, int rows, hipStream_t s) {
+// head blocks per pass: the smallest of 1, 2, 4 covering Nidx1 / 32 whose qi block
+// 32 NGB x DI stays within SLI_MAX_GD elements of LDS; otherwise passes of 64 heads.
+// Rows of more than SLI_MAX_SLOTS slots keep I / dI in the workspace (BIG).
+template <int IO, int DI, bool BIG>
+void launch_student_big(const SliArgs& a, int rows, hipStream_t s) {
   const int ngb = (a.nidx1 + 31) / 32;
   if (ngb <= 1)
-    hipLaunchKernelGGL((sli_student_kernel<IO, DI, 1>), dim3(rows), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((sli_student_kernel<IO, DI, 1, 1, BIG>), dim3(rows), dim3(256), 0, s, a);
   else if (ngb <= 2)
-    hipLaunchKernelGGL((sli_student_kernel<IO, DI, 2>), dim3(rows), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((sli_student_kernel<IO, DI, 2, 1, BIG>), dim3(rows), dim3(256), 0, s, a);
   else if constexpr (128 * DI <= SLI_MAX_GD)
-    hipLaunchKernelGGL((sli_student_kernel<IO, DI, 4>), dim3(rows), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((sli_student_kernel<IO, DI, 4, 1, BIG>), dim3(rows), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((sli_student_kernel<IO, DI, 2, 2, BIG>), dim3(rows), dim3(256), 0, s, a);
+}
+
+template <int IO, int DI>
+void launch_student(const SliArgs& a, int rows, hipStream_t s) {
+  if (a.topk > SLI_MAX_SLOTS && !a.lse_max) launch_student_big<IO, DI, true>(a, rows, s);
+  else launch_student_big<IO, DI, false>(a, rows, s);
 }
 
 template <int IO>
@@ -592,20 +634,19 @@ hipError_t launch_sli_io(const SliArgs& a, hipStream_t s) {
 
 size_t sli_grad_workspace_bytes(int rows, int topk, int64_t key_rows, int didx) {
   return dsa::salign((size_t)rows * topk * 4) + dsa::salign((size_t)key_rows * didx * 4) +
-         dsa::salign((size_t)rows * 4);
+         dsa::salign((size_t)rows * 4) + (topk > dsa::SLI_MAX_SLOTS ? dsa::salign((size_t)rows * topk * 4) : 0);
 }
 
 bool sli_grad_supported(int d, int dr, int nidx1, int didx, int topk) {
   const int dt = d + dr;
   const bool dt_ok = dt == 128 || dt == 192 || dt == 256 || dt == 320 || dt == 512 || dt == 576;
   const bool di_ok = didx == 128 || didx == 256 || didx == 512;
-  const int gp = (nidx1 + 31) / 32 * 32;
-  return dt_ok && di_ok && nidx1 >= 1 && nidx1 <= 128 && topk >= 1 && topk <= dsa::SLI_MAX_TOPK &&
-         (int64_t)gp * didx <= dsa::SLI_MAX_GD;
+  return dt_ok && di_ok && nidx1 >= 1 && nidx1 <= 128 && topk >= 1 && topk <= dsa::SLI_MAX_TOPK;
 }
 
 namespace {
-// workspace: teacher sums [rows, topk] | dKI accumulator [batch s2, didx] | row losses
+// workspace: teacher sums [rows, topk] | dKI accumulator [batch s2, didx] | row losses |
+// (rows of more than SLI_MAX_SLOTS slots) I / dI [rows, topk]
 hipError_t run_sli(dsa::SliArgs a, void* ws, hipStream_t s) {
   const int rows = a.batch * a.s1;
   char* base = reinterpret_cast<char*>(ws);
@@ -616,6 +657,7 @@ hipError_t run_sli(dsa::SliArgs a, void* ws, hipStream_t s) {
   a.row_loss = reinterpret_cast<float*>(base + off);
   // teacher sums and the dKI accumulator are contiguous up to the padding
   const int64_t n4 = (int64_t)off / 16;
+  a.ibuf = a.topk > dsa::SLI_MAX_SLOTS ? reinterpret_cast<float*>(base + off + dsa::salign((size_t)rows * 4)) : nullptr;
   const int blocks = (int)((n4 + 255) / 256 < 4096 ? ((n4 + 255) / 256 > 0 ? (n4 + 255) / 256 : 1) : 4096);
   hipLaunchKernelGGL(dsa::sli_zero_kernel, dim3(blocks), dim3(256), 0, s, reinterpret_cast<float4*>(base), n4);
   hipError_t e = hipGetLastError();
@@ -625,7 +667,7 @@ hipError_t run_sli(dsa::SliArgs a, void* ws, hipStream_t s) {
 }  // namespace
 
 bool dense_li_grad_supported(int n1, int n2, int d, int dr, int nidx1, int didx, int s2) {
-  if (n2 < 1 || n1 % n2 != 0 || s2 < 1 || s2 > dsa::SLI_MAX_SLOTS) return false;
+  if (n2 < 1 || n1 % n2 != 0 || s2 < 1) return false;
   return sli_grad_supported(d, dr, nidx1, didx, 1);
 }
 
@@ -647,7 +689,7 @@ hipError_t launch_dense_li_grad(const void* q, const void* k, const void* qr, co
                                 void* dw, float* loss, void* ws, hipStream_t s) {
   dsa::SliArgs a{q, k, qr, kr, qi, ki, w, io, wdt, nullptr, s2, sm_max, sm_sum, act_q, act_k,
                  batch, s1, s2, n1, d, dr, nidx1, didx, scale, dqi, dki, dw, loss,
-                 nullptr, nullptr, nullptr, n2, max_index, sum_index, nullptr, nullptr};
+                 nullptr, nullptr, nullptr, nullptr, n2, max_index, sum_index, nullptr, nullptr};
   return run_sli(a, ws, s);
 }
 
@@ -659,7 +701,7 @@ hipError_t launch_sli_grad(const void* q, const void* k, const void* qr, const v
                            void* ws, hipStream_t s) {
   dsa::SliArgs a{q, k, qr, kr, qi, ki, w, io, wdt, sidx, topk, sm_max, sm_sum, act_q, act_k,
                  batch, s1, s2, n1, d, dr, nidx1, didx, scale, dqi, dki, dw, loss,
-                 nullptr, nullptr, nullptr};
+                 nullptr, nullptr, nullptr, nullptr};
   a.n2 = 1;
   return run_sli(a, ws, s);
 }

@@ -268,8 +268,7 @@ size_t dsa_sli_grad_workspace_bytes(int batch, int s1, int s2, int sparse_count,
  * dr = 0), query_index [B,S1,Nidx1,D_idx], key_index [B,S2,1,D_idx] (io dtype),
  * weights [B,S1,Nidx1] (w_dtype), sm_max / sm_sum [B,1,S1,N1] fp32 (the forward's
  * stats), act_q / act_k [B]. Outputs in the inputs' dtypes; loss: one fp32.
- * D in {128,256,512}, D_idx in {128,256,512}, N1 <= 128, Nidx1 <= 128 with
- * ceil32(Nidx1) * D_idx <= 32768, sparse_count <= 2048.
+ * D in {128,256,512}, D_idx in {128,256,512}, N1 <= 128, Nidx1 <= 128, sparse_count <= 2048.
  */
 int dsa_sli_grad_kl_loss(const void* query, const void* key, const void* query_rope, const void* key_rope,
                          const void* query_index, const void* key_index, const void* weights, int io_dtype,
@@ -286,8 +285,8 @@ int dsa_sli_grad_kl_loss(const void* query, const void* key, const void* query_r
  * (b, s1 < act_q[b]) over keys t < min(max(act_k[b] - act_q[b] + s1 + 1, 0), s2):
  * softmax_max_index = max_t I[t], softmax_sum_index = sum_t exp(I[t] - max),
  * I[t] = sum_g w[g] relu(qi[g] . ki[t]); other rows get (-inf, 0). Outputs [B*S1] fp32
- * (the reference's [B,1,S1]). D_idx in {128,256,512}, Nidx1 <= 128 with
- * ceil32(Nidx1) * D_idx <= 32768, s2 <= 4096. Needs no workspace.
+ * (the reference's [B,1,S1]). D_idx in {128,256,512}, Nidx1 <= 128, any s2. Needs no
+ * workspace.
  */
 int dsa_dense_li_softmax_lse(const void* query_index, const void* key_index, const void* weights, int io_dtype,
                              int w_dtype, const int32_t* act_q, const int32_t* act_k, int batch, int s1, int s2,
@@ -310,8 +309,7 @@ size_t dsa_dense_li_grad_workspace_bytes(int batch, int s1, int s2, int d_idx);
  *  - indexer softmax sI = exp(I - max_index) / max(sum_index, 1e-8) from the given stats
  *    (max_index / sum_index [B*S1] fp32; a row with sum_index <= 0 gets zero gradients
  *    and no loss), or, with both NULL, from the row's own max and sum.
- * D in {128,256,512}, D_idx in {128,256,512}, N1 <= 128, Nidx1 <= 128 with
- * ceil32(Nidx1) * D_idx <= 32768, s2 <= 4096.
+ * D in {128,256,512}, D_idx in {128,256,512}, N1 <= 128, Nidx1 <= 128, any s2.
  */
 int dsa_dense_li_grad_kl_loss(const void* query, const void* key, const void* query_rope, const void* key_rope,
                               const void* query_index, const void* key_index, const void* weights, int io_dtype,

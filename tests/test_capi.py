@@ -249,8 +249,11 @@ def test_dense_loss_validation_matches_reference():
     lib = _lib.load()
     assert lib.dsa_dense_li_grad_workspace_bytes(1, 4, 2048, 128) >= 4 * 2048 * 4 + 2048 * 128 * 4
     one = ctypes.c_void_p(1)
-    assert lib.dsa_dense_li_softmax_lse(one, one, one, 1, 1, one, one, 1, 4, 8192, 32, 128, one, one,
-                                        None) == _lib.DSA_ERR_UNSUPPORTED   # S2 > 4096
+    assert lib.dsa_dense_li_softmax_lse(one, one, one, 1, 1, one, one, 1, 4, 8192, 32, 64, one, one,
+                                        None) == _lib.DSA_ERR_UNSUPPORTED   # D_idx = 64
+    # rows of more than 4096 keys keep the index scores in the workspace: it grows by rows x S2 fp32
+    assert (lib.dsa_dense_li_grad_workspace_bytes(1, 4, 8192, 128)
+            >= lib.dsa_dense_li_grad_workspace_bytes(1, 4, 4096, 128) + 4 * 8192 * 4)
     assert lib.dsa_dense_li_grad_kl_loss(one, one, None, None, one, one, one, 1, 1, one, one, None, None, one,
                                          one, 1, 4, 64, 6, 4, 128, 0, 32, 128, 1.0, one, one, one, one, one,
                                          1 << 30, None) == _lib.DSA_ERR_INVALID   # N1 % N2

@@ -116,7 +116,9 @@ def _check(lse, want_lse, got, want, what):
 
 
 CORE = [(1, 2, 64, 32, 32, d, nidx1, didx) for d in (128, 256, 512) for nidx1 in (32, 64, 128)
-        for didx in (128, 256, 512) if nidx1 * didx <= 32768]
+        for didx in (128, 256, 512)]
+# the reference's full core matrix (test_dense_loss_backward_triton.py:20-25, which includes its fp16
+# smoke's Nidx1 = 128 x D_idx = 512, :55-60) and its extra shapes (:27-31)
 EXTRA = [(1, 3, 96, 32, 32, 128, 32, 128), (1, 4, 128, 32, 32, 128, 32, 128)]
 
 
@@ -125,6 +127,18 @@ EXTRA = [(1, 3, 96, 32, 32, 128, 32, 128), (1, 4, 128, 32, 32, 128, 32, 128)]
 def test_dense_matrix(dev, B, S1, S2, N1, N2, D, Nidx1, Didx, dtype):
     lse, want_lse, got, want = _run(dev, B, S1, S2, N1, N2, D, Nidx1, Didx, dtype)
     _check(lse, want_lse, got, want, f"S1={S1} S2={S2} D={D} Nidx1={Nidx1} D_idx={Didx} {dtype}")
+
+
+@pytest.mark.parametrize("case", ["long_rows", "long_rows_wide_qi"])
+def test_dense_rows_longer_than_4096_keys(dev, case):
+    """S2 = 6000: every row sees 5997..6000 keys, past the 4096 index scores the student
+    keeps in LDS, so they live in the workspace (the LSE runs its statistics online);
+    also with the widest qi block (Nidx1 = 128 x D_idx = 512, taken in two passes)."""
+    kw = dict(B=1, S1=4, S2=6000, N1=16, N2=16, D=128, Nidx1=64, Didx=128, dtype="bf16")
+    if case == "long_rows_wide_qi":
+        kw.update(Nidx1=128, Didx=512, N2=1, dtype="fp16")
+    lse, want_lse, got, want = _run(dev, **kw)
+    _check(lse, want_lse, got, want, case)
 
 
 @pytest.mark.parametrize("case", ["mqa", "gqa4", "lengths", "no_rope", "own_stats"])

@@ -132,8 +132,7 @@ def run(dev, B, S1, S2, N1, D, G, Di, K, dtype, pattern="random", act_q=None, ac
 
 
 # the reference's strict group and its Triton-vs-numpy matrix (test_sli_grad_kl_loss_triton.py:
-# 17-20, 42-58) except its three Nidx1 = 128 x D_idx = 512 shapes (:47, :49, :55), which this
-# build refuses (test_kl_loss_unsupported_shape_is_refused)
+# 17-20, 42-58): every shape the reference says Triton must support
 CASES = [
     (1, 1, 2048, 32, 512, 8, 128, 1024),
     (1, 4, 2048, 64, 512, 16, 128, 1024),
@@ -141,11 +140,14 @@ CASES = [
     (1, 4, 2048, 64, 512, 64, 128, 2048),
     (1, 4, 2048, 32, 128, 32, 128, 1024),
     (1, 4, 2048, 64, 256, 64, 256, 1024),
+    (1, 4, 2048, 128, 512, 128, 512, 2048),
+    (1, 4, 2048, 32, 256, 128, 512, 1024),
     (1, 4, 2048, 32, 512, 64, 256, 2048),
     (1, 4, 2048, 64, 128, 32, 256, 1024),
     (1, 4, 2048, 128, 128, 32, 512, 2048),
     (1, 4, 2048, 128, 256, 64, 128, 1024),
     (1, 4, 2048, 128, 512, 128, 128, 2048),
+    (1, 4, 2048, 64, 512, 128, 512, 1024),
     (1, 4, 2048, 32, 256, 64, 512, 2048),
     (1, 4, 2048, 64, 512, 128, 256, 1024),
 ]
@@ -187,7 +189,8 @@ def test_kl_loss_patterns_and_lengths(dev, pattern):
 
 
 def test_kl_loss_unsupported_shape_is_refused(dev):
-    q, k, qr, kr, qi, ki, w, si = _inputs(1, 2, 256, 32, 512, 128, 512, 64, "fp16")
+    """Shapes outside the documented envelope (here D_idx = 64) are refused with ValueError."""
+    q, k, qr, kr, qi, ki, w, si = _inputs(1, 2, 256, 32, 512, 32, 64, 64, "fp16")
     sm = torch.zeros(1, 1, 2, 32)
     with pytest.raises(ValueError, match="outside"):
         sparse_lightning_indexer_grad_kl_loss(q.to(dev), k.to(dev), qi.to(dev), ki.to(dev), w.to(dev), si.to(dev),
