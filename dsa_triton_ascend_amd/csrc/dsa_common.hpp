@@ -215,10 +215,18 @@ struct SfaArgs {
   int batch, total_rows, n1, d, dr, s2; int64_t key_rows; int sparse_mode; float scale;
   void* out; float* sm_max; float* sm_sum;
   void* ws; size_t ws_bytes; int kv_splits;
+  // teacher mode (the indexer KL losses): for query row r = b * t_s1 + s1 and its slot list,
+  // t_p[r * t_ld + slot] = (1 / N1) sum_h exp(score - t_max[r N1 + h]) / (t_sum[r N1 + h] + 1e-8)
+  float* t_p = nullptr; int t_ld = 0; const float* t_max = nullptr; const float* t_sum = nullptr; int t_s1 = 0;
 };
 hipError_t launch_li_score(const LiScoreArgs& a, hipStream_t s);
 hipError_t launch_li_topk(const LiTopkArgs& a, hipStream_t s);
 hipError_t launch_sfa_fwd(const SfaArgs& a, hipStream_t s);
+// Teacher sums of the indexer KL losses on the attention kernel's S^T path (BSND keys
+// [B, S2, 1, D | 64]): slot i of row r is key row b * S2 + clip(sidx[r][i], 0, S2 - 1) (slot i
+// = key i when sidx is NULL), for the first min(topk, max(act_k - act_q + s1 + 1, 0)) slots;
+// a.ws holds sfa_token_ws_bytes(total_rows, topk, 1) bytes. D in {128, 256, 512}, Dr = 64.
+hipError_t launch_sfa_teacher(const SfaArgs& a, hipStream_t s);
 size_t sfa_workspace_bytes(int total_rows, int n1, int d, int topk, int sbs, int kv_splits);
 size_t sfa_workspace_zero_bytes();
 // The library's static per-device workspace of DSA_SFA_NOALLOC_SCRATCH_BYTES (its

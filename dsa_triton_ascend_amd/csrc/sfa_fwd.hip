@@ -694,7 +694,13 @@ __device__ __forceinline__ float agpr_scale(float o, float f) {
 // of the contraction and the two halves are added through LDS (both waves of a pair then
 // hold the same scores, and the first one writes P); the PV product and O are split over
 // the D columns as for 128, at half the size.
-template <int IO, int D, int NH>
+//
+// TEACH: the teacher sums of the indexer KL losses instead of attention. The S MFMAs take
+// their operands the other way round (S[head, token]: a lane holds 16 heads of one token),
+// each tile gives t_p[slot] = (1 / N1) sum_h exp(S scale - t_max[h]) / (t_sum[h] + 1e-8)
+// (in-lane over 16 heads, one lane-half swap, then across the head blocks in LDS), and
+// there is no PV product, softmax state or output.
+template <int IO, int D, int NH, bool TEACH>
 __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, int splits, int fuse_tok, Ws ws) {
   using C = Cfg<D>;
   static_assert(NH == 128 || NH == 64, "heads per work-group");
@@ -733,6 +739,7 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   constexpr int QF = KSH < C::KSN ? KSH : C::KSN;
   uint4 qf[QF];
   uint4 qrv[NH * (DR / 8) / (NWV * 64)];
+  float t_stat[2] = {0.f, 0.f};   // TEACH: max and sum of head threadIdx.x
   auto issue_q = [&]() __attribute__((always_inline)) {
     const uint16_t* qn = reinterpret_cast<const uint16_t*>(a.q) + ((int64_t)r * n1 + min(hq, n1 - 1)) * D;
 #pragma unroll
@@ -744,6 +751,11 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
     for (int j = 0; j < NH * (DR / 8) / (NWV * 64); ++j) {
       const int h = (threadIdx.x >> 3) + j * (NWV * 64 / 8), e = (threadIdx.x & 7) * 8;
       qrv[j] = ldg16(reinterpret_cast<const uint16_t*>(a.qr) + ((int64_t)r * n1 + min(h, n1 - 1)) * DR + e);
+    }
+    if constexpr (TEACH) {   // the row's softmax statistics, thread h < NH holds head h
+      const int h = threadIdx.x < NH ? threadIdx.x : 0;
+      t_stat[0] = a.t_max[(int64_t)r * n1 + min(h, n1 - 1)];
+      t_stat[1] = a.t_sum[(int64_t)r * n1 + min(h, n1 - 1)];
     }
     // keeps the loads here: without it they are sunk past the branches that
     // follow and issue only once the token count has arrived
@@ -767,7 +779,7 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
 
   if (ntok == 0) {
     wait_vmcnt<0>();   // the Q loads above are not used on this path
-    if (ntok_all == 0) {   // skipped row (every split sees it): zeros (out, stats), from split 0
+    if (!TEACH && ntok_all == 0) {   // skipped row (every split sees it): zeros (out, stats), from split 0
       if (sp == 0) {
         for (int i = threadIdx.x; i < n1 * D / 8; i += NWV * 64)
           stg16(out + (int64_t)r * n1 * D + i * 8, make_uint4(0, 0, 0, 0));
@@ -832,6 +844,18 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
     const int h = (threadIdx.x >> 3) + j * (NWV * 64 / 8), e = (threadIdx.x & 7) * 8;
     *reinterpret_cast<uint4*>(qrs + h * QRP + e) = h < n1 ? qrv[j] : make_uint4(0, 0, 0, 0);
   }
+  // TEACH: per-head statistics (log2 units) and the per-tile head sums share the P buffers
+  float* t_mx = reinterpret_cast<float*>(&pt[0][0]);   // [NH]
+  float* t_il = t_mx + NH;                              // [NH]
+  float* t_tp = t_il + NH;                              // [2][NWV][BN]
+  static_assert(!TEACH || (2 * NH + 2 * NWV * BN) * 4 <= (int)sizeof(pt), "teacher scratch fits the P buffers");
+  if constexpr (TEACH) {
+    if (threadIdx.x < NH) {
+      const bool real = (int)threadIdx.x < n1;
+      t_mx[threadIdx.x] = real ? t_stat[0] * LOG2E : 0.f;
+      t_il[threadIdx.x] = real ? 1.f / (t_stat[1] + 1e-8f) : 0.f;   // padded heads contribute 0
+    }
+  }
   lds_barrier();
   gather_tile<D>(kb, krb, ws.zero, krows, tile_idx(0), nope_buf[0], rope_buf[0], wave_u, lane);
   gather_tile<D>(kb, krb, ws.zero, krows, tile_idx(1), nope_buf[1], rope_buf[1], wave_u, lane);
@@ -885,7 +909,8 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
     for (int j = 0; j < KSH; ++j) {
       const int ks = K0 + j;
       const uint4 bq = ks < C::KSN ? qf[j < QF ? j : 0] : qr[ks >= C::KSN ? ks - C::KSN : 0];
-      sacc = Mfma<IO>::m32(af[j & 3], bq, sacc);
+      if constexpr (TEACH) sacc = Mfma<IO>::m32(bq, af[j & 3], sacc);   // S[head, token]
+      else sacc = Mfma<IO>::m32(af[j & 3], bq, sacc);                    // S^T[token, head]
       if (j + 4 < KSH) af[j & 3] = a_frag(ks + 4);
       spread(j);
       __builtin_amdgcn_sched_barrier(0);
@@ -1004,6 +1029,61 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   // the MFMAs, so the VALU softmax runs while the matrix core works. Buffers:
   // tile t (PV) and t+1 (S^T) are read, t+2 is loaded into the third; P and the
   // rescale factors are double-buffered by tile parity.
+  if constexpr (TEACH) {
+    // lane: token lane % 32 of the tile, heads 32 hb + m32_row(i, lane) of this wave's block
+    const int hb = KSPLIT ? wave & 1 : wave;
+    float tm[16], ti[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      tm[i] = t_mx[hb * 32 + m32_row(i, lane)];
+      ti[i] = t_il[hb * 32 + m32_row(i, lane)];
+    }
+    const float sl2 = a.scale * LOG2E, inv_n1 = 1.f / n1;
+    // this wave's head-block sum for every token of tile u, to t_tp[u & 1][wave]
+    auto teach_write = [&](int u, const f32x16& sv) __attribute__((always_inline)) {
+      float e = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) e += __builtin_amdgcn_exp2f(__builtin_fmaf(sv[i], sl2, -tm[i])) * ti[i];
+      e = add_half_swap(e);   // lane l ^ 32 holds the block's other 16 heads of the token
+      const int tok = lane & 31;
+      if (lane < 32 && (!KSPLIT || kh == 0)) t_tp[((u & 1) * NWV + wave) * BN + tok] = u * BN + tok < ntok ? e : 0.f;
+    };
+    // the sums of tile u over the head blocks (written before the last barrier) to t_p
+    auto teach_store = [&](int u) __attribute__((always_inline)) {
+      const int tok = threadIdx.x;
+      if (tok < BN && u * BN + tok < ntok) {
+        float sum = 0.f;
+#pragma unroll
+        for (int w = 0; w < NWV; ++w)
+          if (!KSPLIT || (w >> 1) == 0) sum += t_tp[((u & 1) * NWV + w) * BN + tok];
+        a.t_p[(int64_t)r * a.t_ld + t_beg + u * BN + tok] = sum * inv_n1;
+      }
+    };
+    wait_vmcnt<C::GPW - 1>();   // this wave's part of tile 0 landed; tile 1 may be in flight
+    lds_barrier();
+    teach_write(0, s_tile(0, [&](int) {}));
+    for (int t = 0; t + 1 < ntiles; ++t) {
+      if (t == 0) wait_vmcnt<0>(); else wait_vmcnt<1>();
+      lds_barrier();   // tile t+1 resident and tile t's sums visible; tile t's buffer free
+      teach_store(t);
+      const TileIdx ix = tile_idx(t + 2);
+      uint8_t* gnope = nope_buf[(t + 2) % NBUF];
+      uint8_t* grope = rope_buf[(t + 2) % NBUF];
+      teach_write(t + 1, s_tile(t + 1, [&](int ks) {
+#pragma unroll
+        for (int j = 0; j < C::GPW; ++j)
+          if (j * KSH / C::GPW == ks) {
+            if (j < C::GPW - 1) gather_part<D>(j, kb, krb, ws.zero, krows, ix, gnope, grope, wave_u, lane);
+            else ids_dma(t + 4);
+          }
+      }));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    wait_vmcnt<0>();   // the ring's last (unused) gathers land before the LDS is released
+    lds_barrier();
+    teach_store(ntiles - 1);
+    return;
+  }
   wait_vmcnt<C::GPW - 1>();   // this wave's part of tile 0 landed; tile 1 may be in flight
   lds_barrier();   // tile 0 visible
   {
@@ -1111,10 +1191,10 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
 template <int IO, int D>
 hipError_t launch_attn_d(const SfaArgs& a, hipStream_t s, int cap, int splits, int fuse_tok, Ws ws) {
   if (a.n1 <= 64)
-    hipLaunchKernelGGL((sfa_attn_kernel<IO, D, 64>), dim3(a.total_rows, splits), dim3(NWV * 64), 0, s, a,
+    hipLaunchKernelGGL((sfa_attn_kernel<IO, D, 64, false>), dim3(a.total_rows, splits), dim3(NWV * 64), 0, s, a,
                        cap, splits, fuse_tok, ws);
   else
-    hipLaunchKernelGGL((sfa_attn_kernel<IO, D, 128>), dim3(a.total_rows, splits), dim3(NWV * 64), 0, s, a,
+    hipLaunchKernelGGL((sfa_attn_kernel<IO, D, 128, false>), dim3(a.total_rows, splits), dim3(NWV * 64), 0, s, a,
                        cap, splits, fuse_tok, ws);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;
@@ -1126,6 +1206,42 @@ hipError_t launch_attn_d(const SfaArgs& a, hipStream_t s, int cap, int splits, i
     hipLaunchKernelGGL((sfa_merge_kernel<IO, D, 16>), dim3(a.total_rows, (units + 255) / 256), dim3(256), 0,
                        s, a, splits, ws);
   return hipGetLastError();
+}
+
+template <int IO, int D>
+hipError_t launch_teach_d(const SfaArgs& a, hipStream_t s, int cap, Ws ws) {
+  if (a.n1 <= 64)
+    hipLaunchKernelGGL((sfa_attn_kernel<IO, D, 64, true>), dim3(a.total_rows, 1), dim3(NWV * 64), 0, s, a, cap, 1, 0,
+                       ws);
+  else
+    hipLaunchKernelGGL((sfa_attn_kernel<IO, D, 128, true>), dim3(a.total_rows, 1), dim3(NWV * 64), 0, s, a, cap, 1,
+                       0, ws);
+  return hipGetLastError();
+}
+
+// The KL losses' slot list of row r = b * t_s1 + s1 as key rows of the BSND key tensor: the
+// first n = min(topk, max(act_k - act_q + s1 + 1, 0)) slots (rows s1 >= act_q: none), slot i
+// = sidx[r][i] clipped to [0, S2 - 1] (i itself without sidx), at key row b * S2 + id.
+__global__ __launch_bounds__(TOK_TPB) void sfa_slot_list_kernel(SfaArgs a, Ws ws) {
+  const int r = blockIdx.x;
+  const int tid = threadIdx.x;
+  if (r == 0)
+    for (int i = tid; i < 512 + DR; i += TOK_TPB) ws.zero[i] = 0;
+  const int b = r / a.t_s1, s1 = r - b * a.t_s1;
+  const int aq = a.act_q[b], ak = a.act_k[b];
+  int n = 0;
+  if (s1 < aq) {
+    n = ak - aq + s1 + 1;
+    n = n < 0 ? 0 : (n < a.topk ? n : a.topk);
+  }
+  const int32_t* ids = a.sidx ? a.sidx + (int64_t)r * a.topk : nullptr;
+  int32_t* out = ws.tokens + (int64_t)r * ws.tstride;
+  for (int i = tid; i < n; i += TOK_TPB) {
+    int id = ids ? ids[i] : i;
+    id = id < 0 ? 0 : (id > a.s2 - 1 ? a.s2 - 1 : id);
+    out[i] = b * a.s2 + id;
+  }
+  if (tid == 0) ws.counts[r] = n;
 }
 
 template <int IO>
@@ -1236,6 +1352,22 @@ hipError_t sfa_noalloc_workspace(hipStream_t s, void** ws) {
   }
   *ws = d.ptr;
   return hipSuccess;
+}
+
+hipError_t launch_sfa_teacher(const SfaArgs& a, hipStream_t s) {
+  if (a.total_rows <= 0) return hipSuccess;
+  const int cap = a.topk;
+  dsa::Ws ws = dsa::ws_layout(a.ws, a.total_rows, cap, a.n1, a.d, 1, nullptr);
+  hipLaunchKernelGGL(dsa::sfa_slot_list_kernel, dim3(a.total_rows), dim3(dsa::TOK_TPB), 0, s, a, ws);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const bool bf = a.io == dsa::IO_BF16;
+  switch (a.d) {
+    case 128: return bf ? dsa::launch_teach_d<dsa::IO_BF16, 128>(a, s, cap, ws) : dsa::launch_teach_d<dsa::IO_F16, 128>(a, s, cap, ws);
+    case 256: return bf ? dsa::launch_teach_d<dsa::IO_BF16, 256>(a, s, cap, ws) : dsa::launch_teach_d<dsa::IO_F16, 256>(a, s, cap, ws);
+    case 512: return bf ? dsa::launch_teach_d<dsa::IO_BF16, 512>(a, s, cap, ws) : dsa::launch_teach_d<dsa::IO_F16, 512>(a, s, cap, ws);
+  }
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_sfa_fwd(const SfaArgs& a, hipStream_t s) {

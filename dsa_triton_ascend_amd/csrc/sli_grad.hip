@@ -33,6 +33,7 @@ constexpr int SBT = 32;     // tokens per tile
 constexpr int SWV = 4;      // waves per work-group
 constexpr float SEPS = 1e-8f;
 constexpr float SLOG2E = 1.4426950408889634f;
+constexpr int DR_TEACH = 64;       // rope width of the attention-path teacher
 constexpr int SLI_MAX_TOPK = 2048;   // sparse slots per row
 constexpr int SLI_MAX_SLOTS = 4096;  // student keeps the row's I / dI in LDS (dense: S2)
 constexpr int SLI_MAX_GD = 64 * 512; // Nidx1 (padded to 32) x D_idx held in LDS
@@ -51,6 +52,7 @@ struct SliArgs {
   float* dki_acc;  // [batch * s2, didx]
   float* row_loss; // [rows]
   float* ibuf;     // [rows, topk] I / dI when a row has more than SLI_MAX_SLOTS slots
+  void* tok_ws;    // token lists of the attention-path teacher (sfa_token_ws_bytes(rows, topk, 1))
   // dense mode (sidx == nullptr: slot t is key t, up to S2 slots per row)
   int n2;                              // key heads of the teacher, stats [B, N2, S1, N1 / N2]
   const float* imax; const float* isum; // given indexer softmax stats [rows], or nullptr
@@ -608,6 +610,19 @@ hipError_t launch_sli_io(const SliArgs& a, hipStream_t s) {
       case 576: hipLaunchKernelGGL((sli_teacher_heads_kernel<IO, 576, 2>), g2, dim3(128), 0, s, a); break;
       default: return hipErrorInvalidValue;
     }
+  } else if (a.dr == DR_TEACH && (a.d == 128 || a.d == 256 || a.d == 512)) {
+    // one key head with rope: the attention kernel's S path (direct-to-LDS gather ring,
+    // all heads of a row per work-group) writes p
+    SfaArgs t{a.q, a.qr, a.k, a.kr, a.io, a.sidx, a.topk, 1, nullptr, 0, 0, nullptr, nullptr, a.act_q, a.act_k,
+              a.batch, rows, a.n1, a.d, a.dr, a.s2, (int64_t)a.batch * a.s2, 3, a.scale, nullptr, nullptr, nullptr,
+              a.tok_ws, sfa_token_ws_bytes(rows, a.topk, 1), 1};
+    t.t_p = a.p;
+    t.t_ld = a.topk;
+    t.t_max = a.sm_max;
+    t.t_sum = a.sm_sum;
+    t.t_s1 = a.s1;
+    const hipError_t e = launch_sfa_teacher(t, s);
+    if (e != hipSuccess) return e;
   } else switch (a.d + a.dr) {
     case 128: hipLaunchKernelGGL((sli_teacher_kernel<IO, 128>), tgrid, dim3(256), 0, s, a); break;
     case 192: hipLaunchKernelGGL((sli_teacher_kernel<IO, 192>), tgrid, dim3(256), 0, s, a); break;
@@ -634,7 +649,8 @@ hipError_t launch_sli_io(const SliArgs& a, hipStream_t s) {
 
 size_t sli_grad_workspace_bytes(int rows, int topk, int64_t key_rows, int didx) {
   return dsa::salign((size_t)rows * topk * 4) + dsa::salign((size_t)key_rows * didx * 4) +
-         dsa::salign((size_t)rows * 4) + (topk > dsa::SLI_MAX_SLOTS ? dsa::salign((size_t)rows * topk * 4) : 0);
+         dsa::salign((size_t)rows * 4) + (topk > dsa::SLI_MAX_SLOTS ? dsa::salign((size_t)rows * topk * 4) : 0) +
+         dsa::salign(sfa_token_ws_bytes(rows > 0 ? rows : 1, topk, 1));
 }
 
 bool sli_grad_supported(int d, int dr, int nidx1, int didx, int topk) {
@@ -646,7 +662,7 @@ bool sli_grad_supported(int d, int dr, int nidx1, int didx, int topk) {
 
 namespace {
 // workspace: teacher sums [rows, topk] | dKI accumulator [batch s2, didx] | row losses |
-// (rows of more than SLI_MAX_SLOTS slots) I / dI [rows, topk]
+// (rows of more than SLI_MAX_SLOTS slots) I / dI [rows, topk] | the teacher's token lists
 hipError_t run_sli(dsa::SliArgs a, void* ws, hipStream_t s) {
   const int rows = a.batch * a.s1;
   char* base = reinterpret_cast<char*>(ws);
@@ -657,7 +673,10 @@ hipError_t run_sli(dsa::SliArgs a, void* ws, hipStream_t s) {
   a.row_loss = reinterpret_cast<float*>(base + off);
   // teacher sums and the dKI accumulator are contiguous up to the padding
   const int64_t n4 = (int64_t)off / 16;
-  a.ibuf = a.topk > dsa::SLI_MAX_SLOTS ? reinterpret_cast<float*>(base + off + dsa::salign((size_t)rows * 4)) : nullptr;
+  size_t off2 = off + dsa::salign((size_t)rows * 4);
+  a.ibuf = a.topk > dsa::SLI_MAX_SLOTS ? reinterpret_cast<float*>(base + off2) : nullptr;
+  if (a.ibuf) off2 += dsa::salign((size_t)rows * a.topk * 4);
+  a.tok_ws = base + off2;
   const int blocks = (int)((n4 + 255) / 256 < 4096 ? ((n4 + 255) / 256 > 0 ? (n4 + 255) / 256 : 1) : 4096);
   hipLaunchKernelGGL(dsa::sli_zero_kernel, dim3(blocks), dim3(256), 0, s, reinterpret_cast<float4*>(base), n4);
   hipError_t e = hipGetLastError();
@@ -689,7 +708,7 @@ hipError_t launch_dense_li_grad(const void* q, const void* k, const void* qr, co
                                 void* dw, float* loss, void* ws, hipStream_t s) {
   dsa::SliArgs a{q, k, qr, kr, qi, ki, w, io, wdt, nullptr, s2, sm_max, sm_sum, act_q, act_k,
                  batch, s1, s2, n1, d, dr, nidx1, didx, scale, dqi, dki, dw, loss,
-                 nullptr, nullptr, nullptr, nullptr, n2, max_index, sum_index, nullptr, nullptr};
+                 nullptr, nullptr, nullptr, nullptr, nullptr, n2, max_index, sum_index, nullptr, nullptr};
   return run_sli(a, ws, s);
 }
 
@@ -701,7 +720,7 @@ hipError_t launch_sli_grad(const void* q, const void* k, const void* qr, const v
                            void* ws, hipStream_t s) {
   dsa::SliArgs a{q, k, qr, kr, qi, ki, w, io, wdt, sidx, topk, sm_max, sm_sum, act_q, act_k,
                  batch, s1, s2, n1, d, dr, nidx1, didx, scale, dqi, dki, dw, loss,
-                 nullptr, nullptr, nullptr, nullptr};
+                 nullptr, nullptr, nullptr, nullptr, nullptr};
   a.n2 = 1;
   return run_sli(a, ws, s);
 }

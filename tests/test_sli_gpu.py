@@ -181,6 +181,27 @@ def test_kl_loss_loose_shapes(dev, pattern):
     run(dev, 1, 4, 2048, 128, 512, 32, 128, 1024, "bf16", pattern=pattern, loose=True)
 
 
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_kl_loss_without_rope(dev, dtype):
+    """query_rope / key_rope omitted (the reference allows both None): the teacher's scores
+    are q . k alone; the oracle sees zero rope tensors."""
+    B, S1, S2, N1, D, G, Di, K = 1, 4, 1024, 64, 512, 32, 128, 512
+    q, k, qr, kr, qi, ki, w, si = _inputs(B, S1, S2, N1, D, G, Di, K, dtype)
+    qr0, kr0 = torch.zeros_like(qr), torch.zeros_like(kr)
+    scale = 1.0 / math.sqrt(D)
+    smax, ssum = _stats(q, k, qr0, kr0, scale, [S1], [S2])
+    g = lambda x: x.to(dev)
+    got = sparse_lightning_indexer_grad_kl_loss(g(q), g(k), g(qi), g(ki), g(w), g(si), g(smax), g(ssum),
+                                                scale_value=scale)
+    torch.cuda.synchronize()
+    f = lambda x: x.float().cpu().numpy()
+    want = SLI.sli_grad_kl_loss(f(q), f(k), f(qr0), f(kr0), f(qi), f(ki), f(w), si.numpy(), smax.numpy(),
+                                ssum.numpy(), scale, io_dtype=dtype)
+    atol, rtol = TOLS[dtype]
+    for name, gv, ref in zip(("d_query_index", "d_key_index", "d_weights", "loss"), got, want):
+        _close(f(gv), ref, atol, rtol, f"no rope {dtype}: {name}")
+
+
 @pytest.mark.parametrize("pattern", ["random", "repeated"])
 def test_kl_loss_patterns_and_lengths(dev, pattern):
     """Repeated ids (each slot adds to d_key_index), two batches with actual lengths:
