@@ -344,14 +344,29 @@ __global__ __launch_bounds__(256) void sli_student_kernel(SliArgs a) {
   };
   const int32_t* ids = a.sidx ? a.sidx + (int64_t)r * a.topk : nullptr;
 
-  auto load_tile = [&](int t0, int nv) {
-    for (int i = tid; i < SBT * (DI / 8); i += 256) {
+  // ki rows of a tile are fetched into registers one tile ahead (in flight while the
+  // current tile computes) and committed to LDS once every wave is done with it
+  constexpr int LPT = SBT * (DI / 8) / 256;   // 16-byte chunks per thread per tile
+  uint4 stage[LPT];
+  int stok = -1;
+  auto fetch_tile = [&](int t0) {
+    const int nv = n - t0 < SBT ? n - t0 : SBT;
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) {
+      const int i = tid + j * 256;
       const int t = i / (DI / 8), c = (i % (DI / 8)) * 8;
-      uint4 v = z4;
-      if (t < nv) v = ldg16(kib + ((int64_t)b * a.s2 + slot_key(a, ids, t0 + t)) * DI + c);
-      *reinterpret_cast<uint4*>(&KIs[t * QIP + c]) = v;
+      stage[j] = t < nv ? ldg16(kib + ((int64_t)b * a.s2 + slot_key(a, ids, t0 + t)) * DI + c) : z4;
     }
-    if (tid < SBT) s_tok[tid] = tid < nv ? b * a.s2 + slot_key(a, ids, t0 + tid) : -1;
+    if (tid < SBT) stok = tid < nv ? b * a.s2 + slot_key(a, ids, t0 + tid) : -1;
+  };
+  auto commit_tile = [&]() {
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) {
+      const int i = tid + j * 256;
+      const int t = i / (DI / 8), c = (i % (DI / 8)) * 8;
+      *reinterpret_cast<uint4*>(&KIs[t * QIP + c]) = stage[j];
+    }
+    if (tid < SBT) s_tok[tid] = stok;
   };
   // dot^T of this wave's head block over the tile: element e -> slot m32_row(e, lane),
   // head 32 wave + lane % 32 (of the current pass)
@@ -369,9 +384,11 @@ __global__ __launch_bounds__(256) void sli_student_kernel(SliArgs a) {
 
   // ---- first sweep: I per slot, with a running max / sum (wave 0, lanes < 32)
   float run_m = -INFINITY, run_l = 0.f;
+  fetch_tile(0);
   for (int t0 = 0; t0 < n; t0 += SBT) {
     const int nv = n - t0 < SBT ? n - t0 : SBT;
-    load_tile(t0, nv);
+    commit_tile();   // the previous tile's readers are behind the last barrier
+    if (t0 + SBT < n) fetch_tile(t0 + SBT);
     float iv = 0.f;   // thread tid < nv: I of slot t0 + tid, summed over the passes
 #pragma unroll
     for (int hh = 0; hh < NHH; ++hh) {
@@ -465,9 +482,11 @@ __global__ __launch_bounds__(256) void sli_student_kernel(SliArgs a) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) dq[j][e] = 0.f;
     float dwl = 0.f;
+    fetch_tile(0);
     for (int t0 = 0; t0 < n; t0 += SBT) {
       const int nv = n - t0 < SBT ? n - t0 : SBT;
-      load_tile(t0, nv);
+      commit_tile();
+      if (t0 + SBT < n) fetch_tile(t0 + SBT);
       __syncthreads();
       if (wave < NGB) {
         const f32x16 acc = dots();
