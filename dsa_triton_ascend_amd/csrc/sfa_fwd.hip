@@ -1188,9 +1188,420 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   }
 }
 
+// ---------------------------------------------------------------- kernel 2, 64-head form (D = 512)
+// One work-group of 8 waves (two per SIMD) per (query row, 64 heads, KV split), launched
+// for N1 <= 64 (the reference's perf_sfa shape). O^T and Q^T of 64 heads take half the
+// registers of the 128-head form, so two waves share each SIMD.
+//  * S^T[32 tokens, 32 heads] of head block hb = w % 2 is split over the contraction:
+//    wave w runs k-steps [9 q, 9 q + 9), q = w / 2 (Q^T fragments of those k-steps, rope
+//    included, in VGPRs). The four partial sums meet in LDS; wave (hb, q) adds the
+//    partials of token group q (tokens 8 q .. 8 q + 7: one 4-element group of the
+//    32x32 accumulator) and runs the softmax of those tokens.
+//  * Lazy rescaling across the four waves of a head block: P is computed against the
+//    shared exponent reference m_used, and a wave whose group holds a score above
+//    m_used + TAU raises a work-group flag. Every wave reads the flag after the next
+//    barrier; on that (rare) path the group maxima are read back, m_used moves to the
+//    tile maximum, P is recomputed from the scores kept in registers and O is rescaled,
+//    behind one more barrier. The first tile always takes it (m_used starts at -inf).
+//    The true maximum and the row sum are per wave and combined at the end.
+//  * Each wave owns 64 columns of O^T[512, 64 heads] and accumulates O^T += V^T P^T as
+//    the 128-head form does; the PV MFMAs of the previous tile are split around the
+//    exchange barrier so the matrix core has work while the partial sums travel.
+//  * Gathers: wave w copies the nope rows of tokens 4w .. 4w + 3, waves 0-3 the rope of
+//    tokens 8w .. 8w + 7, every wave its 4 ids of the tile four ahead (the last load of
+//    an iteration, so one vmcnt wait retires a tile in every wave).
+//  * Rows of more than 64 heads would run as two halves launched 8 work-groups apart
+//    (round-robin dispatch over the 8 XCDs puts them on one XCD, whose L2 then serves
+//    both halves' gathers); the launcher keeps such rows on the 128-head form.
+namespace w8 {
+constexpr int NW = 8;          // waves
+constexpr int HH = 64;         // heads per work-group
+constexpr int DD = 512;
+constexpr int KS = (DD + DR) / 16;   // S^T k-steps (36)
+constexpr int KSN = DD / 16;         // of which nope (32)
+constexpr int KQ = KS / 4;           // k-steps per wave (9)
+constexpr int PPH = BN + 8;          // P tile pitch (elements)
+}  // namespace w8
+
+template <int IO>
+__global__ __launch_bounds__(w8::NW * 64) void sfa_attn8_kernel(SfaArgs a, int splits, Ws ws) {
+  using C = Cfg<w8::DD>;
+  constexpr int D = w8::DD;
+  __shared__ __attribute__((aligned(16))) uint8_t nope_buf[NBUF][C::NOPE];
+  __shared__ __attribute__((aligned(16))) uint8_t rope_buf[NBUF][C::ROPE];
+  __shared__ __attribute__((aligned(16))) uint16_t pt[2][w8::HH * w8::PPH];   // P [head][token], by tile parity
+  __shared__ __attribute__((aligned(16))) float4 xch[2][4][3][64];   // S^T partials [hb][token group][source][lane]
+  __shared__ __attribute__((aligned(16))) int32_t s_ids[4][BN];      // token-id ring (tiles t+2 .. t+4)
+  __shared__ __attribute__((aligned(16))) float s_mx[2][w8::HH][4];   // group maxima [parity][head][group]
+  __shared__ float s_alpha[w8::HH];   // O rescale factors (rare path)
+  __shared__ int s_flag[2];           // a group exceeded m_used + TAU, by tile parity
+
+  // (row, head half, split) of this work-group; halves of one (row, split) 8 apart
+  const int nh = a.n1 > w8::HH ? 2 : 1;
+  const int nq = a.total_rows * splits;
+  const int x = blockIdx.x;
+  const int q = nh == 2 ? (x >> 4) * 8 + (x & 7) : x;
+  const int hh = nh == 2 ? (x >> 3) & 1 : 0;
+  if (q >= nq) return;
+  const int sp = q / a.total_rows;
+  const int r = a.total_rows - 1 - (q - sp * a.total_rows);   // long (late causal) rows first
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave_u = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hb = wave_u & 1, kq = wave_u >> 1;
+  const int n1 = a.n1;
+  const int h0 = hh * w8::HH;
+  const int hl = hb * 32 + (lane & 31);   // local head of this lane's S^T column
+  const int hs = h0 + hl;
+  const int ntok_all = ws.counts[r];
+  // Q^T fragments of k-steps 9 kq + j (nope, then rope), clamped heads zeroed below
+  uint4 qf[w8::KQ];
+  {
+    const int hc = hs < n1 ? hs : n1 - 1;
+    const uint16_t* qn = reinterpret_cast<const uint16_t*>(a.q) + ((int64_t)r * n1 + hc) * D + (lane >> 5) * 8;
+    const uint16_t* qrr = reinterpret_cast<const uint16_t*>(a.qr) + ((int64_t)r * n1 + hc) * DR + (lane >> 5) * 8;
+#pragma unroll
+    for (int j = 0; j < w8::KQ; ++j) {
+      const int ks = kq * w8::KQ + j;
+      qf[j] = ldg16(ks < w8::KSN ? qn + ks * 16 : qrr + (ks - w8::KSN) * 16);
+    }
+    asm volatile("" ::: "memory");   // the loads stay ahead of the token-count branch
+  }
+  const int per = ((ntok_all + splits - 1) / splits + BN - 1) / BN * BN;
+  const int t_beg = sp * per;
+  const int t_end = (t_beg + per < ntok_all ? t_beg + per : ntok_all);
+  const int ntok = t_end > t_beg ? t_end - t_beg : 0;
+  const int32_t* toks = ws.tokens + (int64_t)r * ws.tstride + t_beg;
+  uint16_t* out = reinterpret_cast<uint16_t*>(a.out);
+  if (ntok == 0) {
+    wait_vmcnt<0>();
+    if (ntok_all == 0 && sp == 0) {   // skipped row: zeros (out, stats) for this half's heads
+      const int hn = n1 - h0 < w8::HH ? n1 - h0 : w8::HH;
+      for (int i = tid; i < hn * D / 8; i += w8::NW * 64)
+        stg16(out + ((int64_t)r * n1 + h0) * D + i * 8, make_uint4(0, 0, 0, 0));
+      if (a.sm_max)
+        for (int h = tid; h < hn; h += w8::NW * 64) {
+          a.sm_max[(int64_t)r * n1 + h0 + h] = 0.f;
+          a.sm_sum[(int64_t)r * n1 + h0 + h] = 0.f;
+        }
+    }
+    return;
+  }
+  const int nact = (ntok_all + per - 1) / per;
+  const bool direct = nact == 1;
+  const uint16_t* kb = reinterpret_cast<const uint16_t*>(a.k);
+  const uint16_t* krb = reinterpret_cast<const uint16_t*>(a.kr);
+  const int krows = a.key_rows < INT_MAX ? (int)a.key_rows : INT_MAX;
+  const int ntiles = (ntok + BN - 1) / BN;
+  const int tr = lane & 31, kg = lane >> 5;
+  const int g16 = lane >> 4, c16 = lane & 15;
+
+  auto clamp_tile = [&](int t) { return t < ntiles ? t : ntiles - 1; };
+  // this wave's 4 ids of tile t into ring slot t % 4 (tiles past the end re-read the last)
+  auto ids_dma = [&](int t) {
+    if (lane == 0) lds_dma16_sbase_untracked(toks + clamp_tile(t) * BN + wave_u * 4, 0u, &s_ids[t & 3][wave_u * 4]);
+  };
+  // ids of tile t: x = token lane % 32 (the nope rows, by readlane), y = the rope token
+  // 8 (w % 4) + lane % 8; slots past the token list take the tile's first token
+  auto tile_ids = [&](int t) {
+    const int nvalid = ntok - clamp_tile(t) * BN < BN ? ntok - clamp_tile(t) * BN : BN;
+    const int k1 = lane & 31, k2 = 8 * (wave_u & 3) + (lane & 7);
+    const int first = s_ids[t & 3][0];
+    const int v1 = s_ids[t & 3][k1], v2 = s_ids[t & 3][k2];
+    return make_int2(k1 < nvalid ? v1 : first, k2 < nvalid ? v2 : first);
+  };
+  // gather part j of a tile: j < 4 the nope row of token 4w + j (all 64 lanes, one row),
+  // j = 4 the rope chunks of tokens 8w .. 8w + 7 (waves 0-3). Rows outside the key
+  // tensors read the zero row.
+  auto gather_part8 = [&](int j, int2 idv, uint8_t* nope, uint8_t* rope) __attribute__((always_inline)) {
+    if (j < 4) {
+      const int phys = __builtin_amdgcn_readlane(idv.x, wave_u * 4 + j);
+      const uint16_t* src = (uint32_t)phys < (uint32_t)krows ? kb + (int64_t)phys * D : ws.zero;
+      lds_dma16_sbase_untracked(src, lane * 16, nope + nope_off<D>(wave_u * 4 + j));
+    } else if (wave_u < 4) {
+      const uint16_t* src = (uint32_t)idv.y < (uint32_t)krows ? krb + (int64_t)idv.y * DR : ws.zero + 512;
+      lds_dma16_untracked(src + (lane >> 3) * 8, rope + wave_u * 1024);
+    }
+  };
+
+  // ---- prologue: ids of tiles 0..3, Q landed, flags cleared, then the first two gathers
+#pragma unroll
+  for (int t = 0; t < 4; ++t) ids_dma(t);
+  wait_vmcnt<0>();
+  if (hs >= n1)
+#pragma unroll
+    for (int j = 0; j < w8::KQ; ++j) qf[j] = make_uint4(0, 0, 0, 0);
+  if (tid < 2) s_flag[tid] = 0;
+  lds_barrier();
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int2 idv = tile_ids(u);
+#pragma unroll
+    for (int j = 0; j < 5; ++j) gather_part8(j, idv, nope_buf[u], rope_buf[u]);
+  }
+
+  float m_used = -INFINITY, m_true = -INFINITY, l_part = 0.f, l_prev = 0.f;
+  float s_keep[4] = {0.f, 0.f, 0.f, 0.f};
+  f32x16 o[2][2];   // O^T [head block mt][column block nt]
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[mt][nt][i] = 0.f;
+
+  // ---- partial S^T[32 tokens, 32 heads of hb] of tile u over this wave's 9 k-steps;
+  // spread(j) issues the loads scheduled after step j
+  auto s_part = [&](int u, auto&& spread) __attribute__((always_inline)) -> f32x16 {
+    const uint8_t* nope = nope_buf[u % NBUF];
+    const uint8_t* rope = rope_buf[u % NBUF];
+    const uint8_t* arow = nope + nope_off<D>(tr) + kg * 16;
+    const int k0 = kq * w8::KQ;
+    auto a_frag = [&](int ks) -> uint4 {
+      return ks < w8::KSN ? *reinterpret_cast<const uint4*>(arow + ks * 32)
+                          : *reinterpret_cast<const uint4*>(rope + rope_off(tr, (ks - w8::KSN) * 2 + kg));
+    };
+    f32x16 sacc = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    uint4 af[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) af[j] = a_frag(k0 + j);
+#pragma unroll
+    for (int j = 0; j < w8::KQ; ++j) {
+      sacc = Mfma<IO>::m32(af[j & 3], qf[j], sacc);
+      if (j + 4 < w8::KQ) af[j & 3] = a_frag(k0 + j + 4);
+      spread(j);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    return sacc;
+  };
+  // the three token groups this wave does not own go to LDS
+  auto xch_write = [&](const f32x16& sv) __attribute__((always_inline)) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      if (g != kq) xch[hb][g][kq < g ? kq : kq - 1][lane] = make_float4(sv[4 * g], sv[4 * g + 1], sv[4 * g + 2], sv[4 * g + 3]);
+  };
+  // this wave's group kq: its own partial plus the other three
+  auto xch_sum = [&](const f32x16& sv) __attribute__((always_inline)) -> float4 {
+    float4 s;
+    s.x = kq == 0 ? sv[0] : kq == 1 ? sv[4] : kq == 2 ? sv[8] : sv[12];
+    s.y = kq == 0 ? sv[1] : kq == 1 ? sv[5] : kq == 2 ? sv[9] : sv[13];
+    s.z = kq == 0 ? sv[2] : kq == 1 ? sv[6] : kq == 2 ? sv[10] : sv[14];
+    s.w = kq == 0 ? sv[3] : kq == 1 ? sv[7] : kq == 2 ? sv[11] : sv[15];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const float4 p = xch[hb][kq][j][lane];
+      s.x += p.x;
+      s.y += p.y;
+      s.z += p.z;
+      s.w += p.w;
+    }
+    return s;
+  };
+  // P of this wave's 4 tokens (lane) against m_used into pt[u & 1]; returns the sum
+  auto write_p = [&](int u) __attribute__((always_inline)) -> float {
+    const float mb = m_used * LOG2E;
+    float p[4], psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s_keep[i], LOG2E, -mb));
+      psum += p[i];
+    }
+    *reinterpret_cast<uint2*>(pt[u & 1] + hl * w8::PPH + 8 * kq + 4 * kg) =
+        make_uint2(pack2<IO>(p[0], p[1]), pack2<IO>(p[2], p[3]));
+    return psum;
+  };
+  // softmax of tile u for token group kq (tokens 8 kq + 4 (lane / 32) + i, head hl)
+  auto softmax8 = [&](int u, float4 sg) __attribute__((always_inline)) {
+    s_keep[0] = sg.x * a.scale;
+    s_keep[1] = sg.y * a.scale;
+    s_keep[2] = sg.z * a.scale;
+    s_keep[3] = sg.w * a.scale;
+    const int nvalid = ntok - u * BN;
+    if (nvalid < BN)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s_keep[i] = 8 * kq + 4 * kg + i < nvalid ? s_keep[i] : -INFINITY;
+    float mx = fmaxf(fmaxf(s_keep[0], s_keep[1]), fmaxf(s_keep[2], s_keep[3]));
+    mx = max_half_swap(mx);
+    if (lane < 32) s_mx[u & 1][hl][kq] = mx;
+    m_true = fmaxf(m_true, mx);
+    if (__builtin_amdgcn_ballot_w64(mx > m_used + lazy_tau<IO>()) && lane == 0) s_flag[u & 1] = 1;
+    l_prev = l_part;
+    l_part += write_p(u);
+  };
+  // the rare path for tile u (flag raised): m_used to the tile maximum where it moved,
+  // P rewritten, O rescaled
+  auto rare = [&](int u) __attribute__((always_inline)) {
+    const float4 mq = *reinterpret_cast<const float4*>(&s_mx[u & 1][hl][0]);
+    const float mt = fmaxf(fmaxf(mq.x, mq.y), fmaxf(mq.z, mq.w));
+    const float m_new = mt > m_used + lazy_tau<IO>() ? mt : m_used;
+    const float alpha = __builtin_amdgcn_exp2f((m_used - m_new) * LOG2E);   // 0 on the first tile
+    m_used = m_new;
+    l_part = l_prev * alpha + write_p(u);
+    if (kq == 0 && lane < 32) s_alpha[hl] = alpha;
+    lds_barrier();   // P rewritten, alpha written, the flag read by every wave
+    if (tid == 0) s_flag[u & 1] = 0;
+    const float a0 = s_alpha[lane & 31], a1 = s_alpha[32 + (lane & 31)];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        o[0][nt][i] *= a0;
+        o[1][nt][i] *= a1;
+      }
+  };
+  // PV operands of tile u, k-step ks (16 tokens): P^T fragments of both head blocks and
+  // V^T fragments of this wave's two 32-column blocks
+  auto pv_req = [&](int u, int ks, uint4 (&pa)[2], uint4 (&vb)[2]) __attribute__((always_inline)) {
+    const uint8_t* nope = nope_buf[u % NBUF];
+    const uint16_t* ptu = pt[u & 1];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+      pa[mt] = *reinterpret_cast<const uint4*>(ptu + (mt * 32 + (lane & 31)) * w8::PPH + ks * 16 + kg * 8);
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int col = wave_u * 64 + nt * 32 + (g16 & 1) * 16 + 4 * (c16 & 3);
+      const int tok0 = ks * 16 + (g16 >> 1) * 8 + (c16 >> 2);
+      const uint2 lo = ds_read_tr(nope + nope_off<D>(tok0) + col * 2);
+      const uint2 hi = ds_read_tr(nope + nope_off<D>(tok0 + 4) + col * 2);
+      vb[nt] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+    }
+  };
+  auto pv_mfma = [&](const uint4 (&pa)[2], const uint4 (&vb)[2]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) o[mt][nt] = Mfma<IO>::m32(vb[nt], pa[mt], o[mt][nt]);
+  };
+  // barrier at the top of iteration t (tile t+1 resident, P(t) and its flag visible),
+  // then the rare path of tile t when flagged
+  auto tile_top = [&](int t) __attribute__((always_inline)) {
+    if (t == 0)
+      wait_vmcnt<0>();
+    else
+      wait_vmcnt<1>();
+    lds_barrier();
+    if (__builtin_amdgcn_readfirstlane(s_flag[t & 1])) rare(t);
+  };
+
+  // ---- tile 0: this wave's gathers of tile 0 landed (tile 1's may be in flight)
+  if (wave_u < 4)
+    wait_vmcnt<5>();
+  else
+    wait_vmcnt<4>();
+  lds_barrier();
+  {
+    const f32x16 s0 = s_part(0, [&](int) {});
+    xch_write(s0);
+    lds_barrier();
+    softmax8(0, xch_sum(s0));
+  }
+  // ---- iteration t: S^T of tile t+1 (gathers of tile t+2 spread over it), the first
+  // half of PV(t), the partial exchange, then the softmax of tile t+1 beside the second
+  // half of PV(t). Buffers: t (PV) and t+1 (S^T) read, t+2 loading; P by parity.
+  for (int t = 0; t + 1 < ntiles; ++t) {
+    tile_top(t);
+    const int2 idv = tile_ids(t + 2);
+    uint8_t* gnope = nope_buf[(t + 2) % NBUF];   // held tile t-1, whose PV finished before the barrier
+    uint8_t* grope = rope_buf[(t + 2) % NBUF];
+    const f32x16 s1 = s_part(t + 1, [&](int j) {
+      if (j >= 1 && j <= 5) gather_part8(j - 1, idv, gnope, grope);
+      if (j == 7) ids_dma(t + 4);   // slot (t+4)%4 held the ids of tile t, read two iterations ago
+    });
+    uint4 pa0[2], vb0[2], pa1[2], vb1[2];
+    pv_req(t, 0, pa0, vb0);
+    pv_req(t, 1, pa1, vb1);
+    pv_mfma(pa0, vb0);
+    xch_write(s1);
+    lds_barrier();   // partials of tile t+1 visible
+    softmax8(t + 1, xch_sum(s1));
+    pv_mfma(pa1, vb1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  tile_top(ntiles - 1);
+  {
+    uint4 pa0[2], vb0[2], pa1[2], vb1[2];
+    pv_req(ntiles - 1, 0, pa0, vb0);
+    pv_req(ntiles - 1, 1, pa1, vb1);
+    pv_mfma(pa0, vb0);
+    pv_mfma(pa1, vb1);
+  }
+  wait_vmcnt<0>();   // the ring's last (unused) gathers land before the LDS is released
+
+  // ---- epilogue: per head, the four group waves' sums and true maxima
+  const float l_w = add_half_swap(l_part);   // lanes l and l ^ 32 hold other tokens of the head
+  float2* red = reinterpret_cast<float2*>(&xch[0][0][0][0]);   // [head][group]
+  lds_barrier();   // the last exchange reads are done
+  if (lane < 32) red[hl * 4 + kq] = make_float2(l_w, m_true);
+  lds_barrier();
+  float inv[2];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+    const int h = mt * 32 + (lane & 31);
+    float lt = 0.f, mtr = -INFINITY;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float2 v = red[h * 4 + g];
+      lt += v.x;
+      mtr = fmaxf(mtr, v.y);
+    }
+    inv[mt] = 1.f / lt;   // l > 0: a row or split holds at least one token
+    // statistics: wave (hb = mt, kq = 0) holds m_used of these heads
+    if (kq == 0 && hb == mt && lane < 32 && h0 + h < n1) {
+      const int64_t hr = (int64_t)r * n1 + h0 + h;
+      if (direct) {
+        if (a.sm_max) {
+          a.sm_max[hr] = mtr;
+          a.sm_sum[hr] = lt * exp2f((m_used - mtr) * LOG2E);
+        }
+      } else {
+        float* ps = ws.part_s + (((int64_t)r * splits + sp) * n1 + h0 + h) * 3;
+        ps[0] = m_used;
+        ps[1] = mtr;
+        ps[2] = lt;
+      }
+    }
+  }
+  // O^T layout: in accumulator (mt, nt) lane l holds head mt*32 + l%32 and, at index
+  // 4g + j, column 64 w + 32 nt + 8g + 4(l/32) + j; packed, then two lane-half swaps
+  // leave 16-byte runs (as in the 128-head form)
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+    const int ha = h0 + mt * 32 + (lane & 31);
+    const int hc = ha < n1 ? ha : n1 - 1;
+    uint16_t* orow = (direct ? out + ((int64_t)r * n1 + hc) * D
+                             : ws.part_o + (((int64_t)r * splits + sp) * n1 + hc) * D) +
+                     wave_u * 64 + (lane >> 5) * 8;
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      uint32_t d[4][2];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        d[g][0] = pack2<IO>(o[mt][nt][4 * g] * inv[mt], o[mt][nt][4 * g + 1] * inv[mt]);
+        d[g][1] = pack2<IO>(o[mt][nt][4 * g + 2] * inv[mt], o[mt][nt][4 * g + 3] * inv[mt]);
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        swap_halves(d[0][j], d[1][j]);
+        swap_halves(d[2][j], d[3][j]);
+      }
+      if (ha < n1) {
+        stg16(orow + nt * 32, make_uint4(d[0][0], d[0][1], d[1][0], d[1][1]));
+        stg16(orow + nt * 32 + 16, make_uint4(d[2][0], d[2][1], d[3][0], d[3][1]));
+      }
+    }
+  }
+}
+
 template <int IO, int D>
 hipError_t launch_attn_d(const SfaArgs& a, hipStream_t s, int cap, int splits, int fuse_tok, Ws ws) {
-  if (a.n1 <= 64)
+  // N1 <= 64: the 8-wave form (one work-group per row). Above 64 heads the 128-head form:
+  // split into two 64-head work-groups a row pays two serial prologues and its tiles run
+  // at about 1.5x the 128-head form's cycles (measured), so it stays one work-group.
+  if (D == w8::DD && !fuse_tok && a.n1 <= w8::HH) {   // token lists built by the token-list launch
+    const int64_t nq = (int64_t)a.total_rows * splits;
+    const int64_t grid = a.n1 > w8::HH ? (nq + 7) / 8 * 16 : nq;
+    hipLaunchKernelGGL(sfa_attn8_kernel<IO>, dim3((unsigned)grid), dim3(w8::NW * 64), 0, s, a, splits, ws);
+  } else if (a.n1 <= 64)
     hipLaunchKernelGGL((sfa_attn_kernel<IO, D, 64, false>), dim3(a.total_rows, splits), dim3(NWV * 64), 0, s, a,
                        cap, splits, fuse_tok, ws);
   else

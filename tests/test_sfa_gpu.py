@@ -322,6 +322,24 @@ def test_forced_kv_splits_with_empty_splits(dev, kv_splits):
     compare(out, smax, ssum, *o, what=f"kv_splits={kv_splits}")
 
 
+@pytest.mark.parametrize("N1", [16, 64])
+@pytest.mark.parametrize("kv_splits", [2, 5])
+def test_forced_kv_splits_block_size_2(dev, N1, kv_splits):
+    """KV splits over token lists built by the token-list launch (sparse_block_size 2): at
+    D = 512 and N1 <= 64 the 8-wave attention form writes the split partials and the merge
+    combines them, including splits past a short row's tokens."""
+    B, S1, S2, D, count, bs = 1, 8, 160, 512, 48, 2
+    q, k, v, qr, kr = _inputs(B, S1, S2, N1, D, "bf16", seed=23)
+    si = _ref_indices(B, S1, S2, count, bs, 3, seed=6)
+    out, smax, ssum = sparse_flash_attention(q.to(dev), k.to(dev), v.to(dev), torch.from_numpy(si).to(dev),
+                                             scale_value=0.05, query_rope=qr.to(dev), key_rope=kr.to(dev),
+                                             sparse_block_size=bs, sparse_mode=3, return_softmax_lse=True,
+                                             kv_splits=kv_splits)
+    o = SFA.sparse_flash_attention(_np(q), _np(k), None, si, 0.05, None, None, None, _np(qr), _np(kr), bs,
+                                   "BSND", "BSND", 3, True, io_dtype="bf16")
+    compare(out, smax, ssum, *o, what=f"N1={N1} bs={bs} kv_splits={kv_splits}")
+
+
 @pytest.mark.parametrize("mode", [0, 3])
 def test_split_token_lists_long_scan(dev, mode):
     """KV-split rows that list their own tokens when the scan spans several 2048-id
