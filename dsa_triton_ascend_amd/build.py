@@ -55,7 +55,8 @@ def build(verbose: bool = True) -> Path:
         for f in futs:
             f.result()
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-o", str(tmp), *map(str, objs)]
+    # hipBLASLt: the SFA backward's dense d_key / d_value products
+    cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-o", str(tmp), *map(str, objs), "-lhipblaslt"]
     p = subprocess.run(cmd, capture_output=True, text=True)
     if p.returncode != 0:
         raise RuntimeError(f"link failed:\n{p.stderr}")

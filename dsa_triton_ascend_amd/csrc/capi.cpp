@@ -291,6 +291,8 @@ int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, cons
   a.dk = d_key;
   a.dkr = d_key_rope;
   a.dv = d_value;
+  a.h_row_start = host_row_start;
+  a.h_act_k = host_act_k;
   return hip_status(launch_sfa_bwd(a, (hipStream_t)stream), "dsa_sfa_bwd launch");
 }
 

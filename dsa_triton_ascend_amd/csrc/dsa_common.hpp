@@ -249,6 +249,7 @@ struct SfaBwdArgs {
   SfaArgs f;   // forward arguments (q, qr, k, kr, indices, lengths, shapes, scale)
   const void* d_out; const void* out; const float* sm_max; const float* sm_sum;
   void* dq; void* dqr; void* dk; void* dkr; void* dv;
+  const int32_t* h_row_start; const int32_t* h_act_k;   // host copies (they size the library GEMMs)
 };
 // h_row_start [batch + 1] and h_act_k [batch]: host copies of the row offsets and kv
 // lengths (they size the per-batch dense buffers)

@@ -36,15 +36,20 @@
 //         [head][token];
 //       * dQ[head, col] += dS K, each wave owning a quarter of the 32-column
 //         blocks, the K operand read with ds_read_b64_tr_b16 from the tile;
-//  4. sfa_bwd_gemm_kernel (twice: d_key | d_key_rope, d_value) -- 128 x BN
-//     output tiles per batch on v_mfma_f32_32x32x16, operands streamed with
-//     direct-to-LDS loads through a 3-stage LDS ring two k-steps ahead, the k-range
-//     split over work-groups when the tiles alone do not fill the GPU; partial tiles are
-//     added into fp32 accumulators with global atomics (so the last bits may
-//     differ from run to run, the reference's deterministic=False contract,
-//     sparse_flash_attention_grad_triton.py:550);
-//  5. sfa_bwd_finish_kernel -- converts the accumulators to the io dtype.
+//  4. three library GEMMs per batch (hipBLASLt, bf16/fp16 in and out, fp32
+//     accumulation): [d_key | d_key_rope] = dS_T [q | q_rope] and d_value = P_T d_out
+//     into a batch-contiguous staging area of the workspace (these are plain dense
+//     products, the kind of work a tuned library GEMM does best; measured 0.35 ms at
+//     the grad perf shape against 0.74 ms for the hand-written GEMM kernels they
+//     replaced);
+//  5. sfa_bwd_place_kernel -- copies each batch's staged rows to key rows
+//     key_start[b] + t and writes zeros to the key rows no batch covers.
 #include <climits>
+#include <map>
+#include <mutex>
+#include <tuple>
+
+#include <hipblaslt/hipblaslt.h>
 
 #include "dsa_common.hpp"
 
@@ -56,8 +61,9 @@ constexpr int BH = 32;      // heads per work-group (rows kernel)
 constexpr int BT = 32;      // tokens per tile
 constexpr int BWV = 4;      // waves per work-group
 constexpr float BLOG2E = 1.4426950408889634f;
-constexpr int GBM = 128;    // GEMM tile rows (key tokens)
-constexpr int GBK = 64;     // GEMM k-step; dense rows are padded to a multiple of it
+constexpr int GBK = 64;     // dense rows are padded to a multiple of 64 (row, head) pairs
+constexpr size_t LT_WS = (size_t)128 << 20;  // workspace offered to the library GEMMs
+constexpr int LT_CANDIDATES = 64;            // algorithms timed per product shape
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -87,9 +93,11 @@ __device__ __forceinline__ uint4 tr_frag(const uint16_t* X, int pitch, int c0, i
 
 struct BwdWs {
   int64_t* boff;   // [batch + 1] dense-buffer offsets (elements)
-  float* dk;       // [key_rows, D]   fp32 accumulators
-  float* dkr;      // [key_rows, Dr]
-  float* dv;       // [key_rows, D]
+  int64_t* boffk;  // [batch + 1] staged-row offsets (prefix of nk)
+  uint16_t* sk;    // staged [sum nk, D]  d_key rows (io dtype)
+  uint16_t* skr;   // staged [sum nk, Dr] d_key_rope rows
+  uint16_t* sv;    // staged [sum nk, D]  d_value rows
+  void* lt_ws;     // LT_WS bytes for the library GEMMs
   uint16_t* dst;   // dS_T dense buffer (io dtype)
   uint16_t* pt;    // P_T dense buffer (io dtype)
   int64_t cap;     // elements per dense buffer
@@ -97,10 +105,13 @@ struct BwdWs {
 
 // Dense geometry of batch b: query rows [rs, rs + nq), key rows [ks, ks + nk)
 // (the tokens a row of the batch can select, t < min(act_k, S2)), dense rows of
-// kp = nq * N1 rounded up to GBK elements.
+// kp = nq * N1 rounded up to GBK elements. The host computes the same nk and kp from
+// its copies of row_start / act_k (bwd_host_geo) to size and address the GEMMs.
 struct BatchGeo {
   int rs, nq, ks, nk, kp;
 };
+
+__host__ __device__ inline int batch_nk(int act_k, int s2) { return act_k < 0 ? 0 : (act_k < s2 ? act_k : s2); }
 
 __host__ __device__ inline int dense_row(int nq, int n1) { return (nq * n1 + GBK - 1) / GBK * GBK; }
 
@@ -109,10 +120,7 @@ __device__ __forceinline__ BatchGeo batch_geo(const SfaArgs& f, int b) {
   g.rs = f.row_start[b];
   g.nq = f.row_start[b + 1] - g.rs;
   g.ks = f.key_start[b];
-  int nk = f.act_k[b] < f.s2 ? f.act_k[b] : f.s2;
-  const int64_t room = f.key_rows - g.ks;
-  nk = nk < 0 ? 0 : nk;
-  g.nk = (int64_t)nk < room ? nk : (int)(room > 0 ? room : 0);
+  g.nk = batch_nk(f.act_k[b], f.s2);
   g.kp = dense_row(g.nq, f.n1);
   return g;
 }
@@ -146,6 +154,27 @@ __global__ __launch_bounds__(256) void sfa_bwd_geo_kernel(SfaArgs f, BwdWs w) {
     off += (int64_t)g.nk * g.kp;
   }
   if (tid == 255) w.boff[f.batch] = off;
+  // staged-row offsets: the same prefix over nk
+  __syncthreads();
+  int64_t sk = 0;
+  for (int b = b0; b < b0 + per && b < f.batch; ++b) sk += batch_nk(f.act_k[b], f.s2);
+  part[tid] = sk;
+  __syncthreads();
+  if (tid == 0) {
+    int64_t run = 0;
+    for (int i = 0; i < 256; ++i) {
+      const int64_t v = part[i];
+      part[i] = run;
+      run += v;
+    }
+  }
+  __syncthreads();
+  off = part[tid];
+  for (int b = b0; b < b0 + per && b < f.batch; ++b) {
+    w.boffk[b] = off;
+    off += batch_nk(f.act_k[b], f.s2);
+  }
+  if (tid == 255) w.boffk[f.batch] = off;
 }
 
 // Clears n4 16-byte words of p (accumulators); dense buffers: up to the used size
@@ -392,227 +421,219 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
   }
 }
 
-// ---- dense GEMM per batch: C[t, n] = sum_k A[t, k] B[k, n] over the batch's
-// (row, head) pairs k. A: the dense dS_T (KV = false: d_key | d_key_rope, B = q |
-// q_rope) or P_T (KV = true: d_value, B = d_out) buffer; 128 x BN tiles, BN = 64 NB,
-// four waves as 2 (rows) x 2 (columns), each 64 x 32 NB. xt = m-tile * n-tiles +
-// n-tile, blockIdx.y = batch, blockIdx.z = k-split. Results are added to the fp32
-// accumulators (rows t < nk of the batch).
-template <int IO, int D, bool KV, int NB, int NST>
-__device__ __forceinline__ void gemm_tile(const SfaBwdArgs& a, const BwdWs& w, int ksplit, int xt,
-                                          uint8_t* lds) {
-  constexpr int N = KV ? D : D + BDR;
-  constexpr int BN = 64 * NB;
-  constexpr int NT = N / BN;
-  static_assert(N % BN == 0, "n-tiles cover the columns");
-  constexpr int AP = GBK + 8;          // A tile pitch (elements): 8 data chunks + 1 pad chunk per row
-  constexpr int BP = BN + 8;           // B tile pitch: 8 NB data chunks + 1 pad chunk
-  constexpr int ACR = AP / 8, BCR = BP / 8;            // 16-byte chunk slots per row
-  constexpr int NIA = GBM * ACR / 64, NIB = GBK * BCR / 64;   // 64-slot load instructions per k-step
-  static_assert(NIA * 64 == GBM * ACR && NIB * 64 == GBK * BCR, "slots fill whole instructions");
-  constexpr int NI = NIA + NIB;
-  constexpr int NMIN = NI / BWV;       // loads per wave per k-step, at least
-  constexpr int ABYTES = GBM * AP * 2, STAGE = ABYTES + GBK * BP * 2;
+// ---- staged library-GEMM rows to the outputs: key row kr of batch b (the last batch
+// with key_start[b] <= kr), t = kr - key_start[b], takes staged row boffk[b] + t when
+// t < nk and the batch has query rows; every other key row is zero. One thread per 8
+// elements of the [D | Dr | D] row.
+template <int D>
+__global__ __launch_bounds__(256) void sfa_bwd_place_kernel(SfaBwdArgs a, BwdWs w) {
   const SfaArgs& f = a.f;
-  const int b = blockIdx.y;
-  const BatchGeo g = batch_geo(f, b);
-  // xt -> (m-tile, n-tile): the NT tiles of an m-tile get x values 8 apart, so with
-  // round-robin dispatch over the 8 XCDs they run on one XCD and share its L2 copy
-  // of the A rows
-  const int grp = xt / (8 * NT), rem = xt % (8 * NT);
-  const int nt = rem / 8, mt = grp * 8 + rem % 8;
-  const int m0 = mt * GBM;
-  if (nt >= NT || m0 >= g.nk || w.boff[b + 1] > w.cap) return;
-  const int kper = ((g.kp + ksplit - 1) / ksplit + GBK - 1) / GBK * GBK;
-  const int kbeg = blockIdx.z * kper;
-  const int kend = kbeg + kper < g.kp ? kbeg + kper : g.kp;
-  if (kbeg >= kend) return;
-  const int nsteps = (kend - kbeg) / GBK;
-  const int kreal = g.nq * f.n1;   // k past this is padding: zero A columns, B rows clamped
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave & 1, wn = wave >> 1;
-  const uint16_t* abuf = (KV ? w.pt : w.dst) + w.boff[b];
-  const uint16_t* bq = reinterpret_cast<const uint16_t*>(KV ? a.d_out : a.f.q);
-  const uint16_t* bqr = reinterpret_cast<const uint16_t*>(a.f.qr);
-  const int64_t brow0 = (int64_t)g.rs * f.n1;   // B row of k = 0
-
-  // ---- k-step s goes global -> LDS stage s % NST with direct-to-LDS 16-byte loads:
-  // instruction q of the step fills slots [64 q, 64 q + 64) of the tile (A slots
-  // first, then B), slot = row * chunks-per-row + chunk; the pad chunk of a row
-  // re-reads its chunk 0. Every address is in bounds: A rows past the batch's tokens
-  // read its last token (their outputs are discarded), B rows past the batch's
-  // (row, head) pairs read its last pair (they meet zero A columns). Instructions
-  // are dealt round-robin to the waves; steps past the range re-load the last one,
-  // so each wave issues the same loads every step.
-  auto issue = [&](int step) __attribute__((always_inline)) {
-    const int st = step < nsteps ? step : nsteps - 1;
-    const int k0 = kbeg + st * GBK;
-    uint8_t* stage = lds + (step % NST) * STAGE;
-    for (int q = wave; q < NI; q += BWV) {
-      const int slot = (q < NIA ? q : q - NIA) * 64 + lane;
-      const void* src;
-      if (q < NIA) {
-        const int row = slot / ACR, ch = slot % ACR;
-        int t = m0 + row;
-        t = t < g.nk ? t : g.nk - 1;
-        src = abuf + (int64_t)t * g.kp + k0 + (ch < 8 ? ch : 0) * 8;
-      } else {
-        const int row = slot / BCR, ch = slot % BCR;
-        int k = k0 + row;
-        k = k < kreal ? k : kreal - 1;
-        const int n = nt * BN + (ch < 8 * NB ? ch : 0) * 8;
-        const int64_t r = brow0 + k;
-        src = (KV || n < D) ? (const void*)(bq + r * D + n) : (const void*)(bqr + r * BDR + (n - D));
-      }
-      lds_dma16_untracked(src, stage + (q < NIA ? q * 1024 : ABYTES + (q - NIA) * 1024));
+  constexpr int UK = D / 8, UR = BDR / 8, U = 2 * UK + UR;   // 8-element units per key row
+  const int64_t n = f.key_rows * U;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t kr = i / U;
+    const int u = (int)(i - kr * U);
+    int lo = 0, hi = f.batch - 1;   // last b with key_start[b] <= kr (key_start ascends)
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (f.key_start[mid] <= kr) lo = mid; else hi = mid - 1;
     }
-  };
-
-  f32x16 acc[2][NB];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < NB; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
-
-#pragma unroll
-  for (int s = 0; s < NST - 1; ++s) issue(s);
-  for (int s = 0; s < nsteps; ++s) {
-    // this wave's loads of step s have landed (the later NST - 2 steps may be in
-    // flight), then every wave's (the barrier also ends step s - 1's reads of the
-    // stage that the next issue refills)
-    wait_vmcnt<(NST - 2) * NMIN>();
-    lds_barrier();
-    issue(s + NST - 1);
-    const uint16_t* As = reinterpret_cast<const uint16_t*>(lds + (s % NST) * STAGE);
-    const uint16_t* Bs = reinterpret_cast<const uint16_t*>(lds + (s % NST) * STAGE + ABYTES);
-#pragma unroll
-    for (int ks = 0; ks < GBK / 16; ++ks) {
-      uint4 af[2], bfr[NB];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        af[i] = *reinterpret_cast<const uint4*>(&As[(64 * wm + 32 * i + (lane & 31)) * AP + ks * 16 + (lane >> 5) * 8]);
-#pragma unroll
-      for (int j = 0; j < NB; ++j) bfr[j] = tr_frag(Bs, BP, 32 * NB * wn + 32 * j, ks * 16, lane);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < NB; ++j) acc[i][j] = Mfma<IO>::m32(af[i], bfr[j], acc[i][j]);
+    const int b = lo;
+    const int64_t t = kr - f.key_start[b];
+    const bool covered = t >= 0 && t < batch_nk(f.act_k[b], f.s2) && f.row_start[b + 1] > f.row_start[b];
+    const int64_t sr = covered ? w.boffk[b] + t : 0;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (u < UK) {
+      if (covered) v = ldg16(w.sk + sr * D + u * 8);
+      stg16(reinterpret_cast<uint16_t*>(a.dk) + kr * D + u * 8, v);
+    } else if (u < UK + UR) {
+      if (covered) v = ldg16(w.skr + sr * BDR + (u - UK) * 8);
+      stg16(reinterpret_cast<uint16_t*>(a.dkr) + kr * BDR + (u - UK) * 8, v);
+    } else {
+      if (covered) v = ldg16(w.sv + sr * D + (u - UK - UR) * 8);
+      stg16(reinterpret_cast<uint16_t*>(a.dv) + kr * D + (u - UK - UR) * 8, v);
     }
-  }
-  wait_vmcnt<0>();   // the trailing re-loads land before the work-group's LDS is released
-
-  // ---- add the tile to the accumulators (rows past the batch's tokens skipped)
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      const int n = nt * BN + 32 * NB * wn + 32 * j + (lane & 31);
-      float* dst = KV ? w.dv + n : (n < D ? w.dk + n : w.dkr + (n - D));
-      const int ld = (KV || n < D) ? D : BDR;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int t = m0 + 64 * wm + 32 * i + m32_row(e, lane);
-        if (t < g.nk) unsafeAtomicAdd(dst + (int64_t)(g.ks + t) * ld, acc[i][j][e]);
-      }
-    }
-}
-
-// n-tile widths (in 64-column units) of the two GEMMs: d_key | d_key_rope spans
-// D + 64 columns (3, 5, 9 units), d_value D (2, 4, 8)
-template <int D> struct GemmNB;
-template <> struct GemmNB<128> { static constexpr int K = 3, V = 2; };
-template <> struct GemmNB<256> { static constexpr int K = 5, V = 4; };
-template <> struct GemmNB<512> { static constexpr int K = 3, V = 4; };
-
-// LDS ring depth: three stages (loads two k-steps ahead) when they fit
-template <int NB> struct GemmStages {
-  static constexpr int STAGE = GBM * (GBK + 8) * 2 + GBK * (64 * NB + 8) * 2;
-  static constexpr int NST = 3 * STAGE <= 160 * 1024 ? 3 : 2;
-};
-
-// One product per launch (d_key | d_key_rope, then d_value): each instance gets only
-// the registers its tile needs.
-template <int IO, int D, bool KV>
-__global__ __launch_bounds__(256) void sfa_bwd_gemm_kernel(SfaBwdArgs a, BwdWs w, int ksplit) {
-  constexpr int NB = KV ? GemmNB<D>::V : GemmNB<D>::K;
-  using S = GemmStages<NB>;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[S::NST * S::STAGE];
-  gemm_tile<IO, D, KV, NB, S::NST>(a, w, ksplit, blockIdx.x, lds);
-}
-
-// fp32 accumulator -> io dtype, 4 elements per step (every length is a multiple of 4)
-template <int IO>
-__global__ void sfa_bwd_finish_kernel(const float4* src, uint2* dst, int64_t n4) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x) {
-    const float4 v = src[i];
-    dst[i] = make_uint2(pack2<IO>(v.x, v.y), pack2<IO>(v.z, v.w));
   }
 }
 
 template <int IO, int D>
-hipError_t launch_bwd_d(const SfaBwdArgs& a, const SfaTokenLists& tl, const BwdWs& w, hipStream_t s) {
+hipError_t launch_rows_d(const SfaBwdArgs& a, const SfaTokenLists& tl, const BwdWs& w, hipStream_t s) {
   const SfaArgs& f = a.f;
   if (f.total_rows > 0) {
     const dim3 grid(f.total_rows, (f.n1 + BH - 1) / BH);
     hipLaunchKernelGGL((sfa_bwd_rows_kernel<IO, D>), grid, dim3(BWV * 64), 0, s, a, tl, w);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    // GEMM grid: every (m-tile, n-tile) of the largest batch; the k-range is split so
-    // each product fills about one round of one work-group per CU
-    constexpr int NTK = (D + BDR) / (64 * GemmNB<D>::K), NTV = D / (64 * GemmNB<D>::V);
-    const int mts = (f.s2 + GBM - 1) / GBM;
-    if (mts > 0) {
-      const int mts8 = (mts + 7) / 8 * 8;   // x covers whole groups of 8 m-tiles
-      auto splits = [&](int nt) {
-        const int64_t tiles = (int64_t)f.batch * mts * nt;
-        const int64_t k = 256 / tiles;
-        return (int)(k < 1 ? 1 : (k > 16 ? 16 : k));
-      };
-      const int kk = splits(NTK), kv = splits(NTV);
-      hipLaunchKernelGGL((sfa_bwd_gemm_kernel<IO, D, false>), dim3(mts8 * NTK, f.batch, kk), dim3(256), 0, s,
-                         a, w, kk);
-      hipLaunchKernelGGL((sfa_bwd_gemm_kernel<IO, D, true>), dim3(mts8 * NTV, f.batch, kv), dim3(256), 0, s,
-                         a, w, kv);
-      e = hipGetLastError();
-      if (e != hipSuccess) return e;
-    }
-  }
-  const int64_t kr = f.key_rows;
-  const struct { const float* src; void* dst; int64_t n; } outs[3] = {
-      {w.dk, a.dk, kr * D}, {w.dkr, a.dkr, kr * BDR}, {w.dv, a.dv, kr * D}};
-  for (const auto& o : outs) {
-    if (o.n == 0) continue;
-    const int64_t n4 = o.n / 4;
-    const int blocks = (int)((n4 + 255) / 256 < 4096 ? (n4 + 255) / 256 : 4096);
-    hipLaunchKernelGGL((sfa_bwd_finish_kernel<IO>), dim3(blocks), dim3(256), 0, s,
-                       reinterpret_cast<const float4*>(o.src), reinterpret_cast<uint2*>(o.dst), n4);
   }
   return hipGetLastError();
 }
 
 template <int IO>
-hipError_t launch_bwd_io(const SfaBwdArgs& a, const SfaTokenLists& tl, const BwdWs& w, hipStream_t s) {
+hipError_t launch_rows_io(const SfaBwdArgs& a, const SfaTokenLists& tl, const BwdWs& w, hipStream_t s) {
   switch (a.f.d) {
-    case 128: return launch_bwd_d<IO, 128>(a, tl, w, s);
-    case 256: return launch_bwd_d<IO, 256>(a, tl, w, s);
-    case 512: return launch_bwd_d<IO, 512>(a, tl, w, s);
+    case 128: return launch_rows_d<IO, 128>(a, tl, w, s);
+    case 256: return launch_rows_d<IO, 256>(a, tl, w, s);
+    case 512: return launch_rows_d<IO, 512>(a, tl, w, s);
   }
   return hipErrorInvalidValue;
 }
 
-// Workspace: token lists | batch offsets | fp32 accumulators (d_key, d_key_rope,
-// d_value) | dS_T | P_T. Returns the offset of dS_T; the two dense buffers share
-// the rest equally.
-size_t bwd_fixed_bytes(int total_rows, int batch, int topk, int sbs, int64_t key_rows, int d) {
+hipError_t launch_place(const SfaBwdArgs& a, const BwdWs& w, hipStream_t s) {
+  const int64_t units = a.f.key_rows * (2 * a.f.d + BDR) / 8;
+  if (units == 0) return hipSuccess;
+  const int blocks = (int)((units + 255) / 256 < 8192 ? (units + 255) / 256 : 8192);
+  switch (a.f.d) {
+    case 128: hipLaunchKernelGGL(sfa_bwd_place_kernel<128>, dim3(blocks), dim3(256), 0, s, a, w); break;
+    case 256: hipLaunchKernelGGL(sfa_bwd_place_kernel<256>, dim3(blocks), dim3(256), 0, s, a, w); break;
+    case 512: hipLaunchKernelGGL(sfa_bwd_place_kernel<512>, dim3(blocks), dim3(256), 0, s, a, w); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+// ---- library GEMMs. One hipBLASLt handle per device, created on the device's first
+// backward call (the library allocates its own small state then), and the algorithm
+// hipBLASLt's heuristic ranks first, cached per product shape. In column-major terms
+// the product of a batch is C^T [N x nk] = B^T [N x K] * A^T [K x nk]: B^T is the
+// row-major [K x N] operand (q, q_rope or d_out rows of the batch, ld N), A^T the
+// row-major dense [nk x kp] buffer (ld kp, its first K = nq * N1 columns), C^T the
+// row-major staged [nk x N] rows (ld N).
+struct LtCache {
+  std::mutex mu;
+  std::map<int, hipblasLtHandle_t> handle;
+  std::map<std::tuple<int, int, int, int, int, int64_t>, hipblasLtMatmulAlgo_t> algo;
+};
+LtCache& lt_cache() {
+  static LtCache c;
+  return c;
+}
+
+hipError_t lt_gemm(hipDataType dt, int n_cols, int nk, int k, const void* b_rows, const void* dense, int64_t kp,
+                   void* staged, void* ws, hipStream_t s) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return hipErrorInvalidDevice;
+  LtCache& c = lt_cache();
+  hipblasLtHandle_t h;
+  {
+    std::lock_guard<std::mutex> g(c.mu);
+    auto it = c.handle.find(dev);
+    if (it == c.handle.end()) {
+      if (hipblasLtCreate(&h) != HIPBLAS_STATUS_SUCCESS) return hipErrorNotInitialized;
+      c.handle[dev] = h;
+    } else {
+      h = it->second;
+    }
+  }
+  hipblasLtMatmulDesc_t desc = nullptr;
+  hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
+  hipblasLtMatmulPreference_t pref = nullptr;
+  hipError_t ret = hipErrorNotSupported;
+  const hipblasOperation_t op = HIPBLAS_OP_N;
+  const uint64_t wsb = LT_WS;
+  const float alpha = 1.f, beta = 0.f;
+  do {
+    if (hipblasLtMatmulDescCreate(&desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS) break;
+    if (hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_TRANSA, &op, sizeof(op)) != HIPBLAS_STATUS_SUCCESS ||
+        hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_TRANSB, &op, sizeof(op)) != HIPBLAS_STATUS_SUCCESS)
+      break;
+    if (hipblasLtMatrixLayoutCreate(&la, dt, n_cols, k, n_cols) != HIPBLAS_STATUS_SUCCESS ||
+        hipblasLtMatrixLayoutCreate(&lb, dt, k, nk, kp) != HIPBLAS_STATUS_SUCCESS ||
+        hipblasLtMatrixLayoutCreate(&lc, dt, n_cols, nk, n_cols) != HIPBLAS_STATUS_SUCCESS)
+      break;
+    hipblasLtMatmulAlgo_t algo;
+    const auto key = std::make_tuple(dev, (int)dt, n_cols, nk, k, kp);
+    bool have = false;
+    {
+      std::lock_guard<std::mutex> g(c.mu);
+      auto it = c.algo.find(key);
+      if (it != c.algo.end()) {
+        algo = it->second;
+        have = true;
+      }
+    }
+    if (!have) {
+      if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS ||
+          hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb, sizeof(wsb)) !=
+              HIPBLAS_STATUS_SUCCESS)
+        break;
+      hipblasLtMatmulHeuristicResult_t res[LT_CANDIDATES];
+      int nres = 0;
+      if (hipblasLtMatmulAlgoGetHeuristic(h, desc, la, lb, lc, lc, pref, LT_CANDIDATES, res, &nres) !=
+              HIPBLAS_STATUS_SUCCESS ||
+          nres < 1)
+        break;
+      algo = res[0].algo;
+      // The heuristic's first choice is not reliably the fastest here (measured up to
+      // 3x slower than others in its own list on these shapes): the first call of a
+      // shape times every candidate on the caller's stream and keeps the fastest. Under
+      // stream capture it keeps the heuristic's choice (timing needs a synchronisation).
+      hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+      if (hipStreamIsCapturing(s, &cap) == hipSuccess && cap == hipStreamCaptureStatusNone && nres > 1) {
+        hipEvent_t e0 = nullptr, e1 = nullptr;
+        if (hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess) {
+          float best = 1e30f;
+          for (int i = 0; i < nres; ++i) {
+            if (res[i].workspaceSize > LT_WS) continue;
+            auto run = [&]() {
+              return hipblasLtMatmul(h, desc, &alpha, b_rows, la, dense, lb, &beta, staged, lc, staged, lc,
+                                     &res[i].algo, ws, LT_WS, s);
+            };
+            if (run() != HIPBLAS_STATUS_SUCCESS) continue;   // warm-up; skips an algorithm that fails
+            float ms = 0.f;
+            if (hipEventRecord(e0, s) != hipSuccess) break;
+            for (int rep = 0; rep < 2; ++rep) run();
+            if (hipEventRecord(e1, s) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+                hipEventElapsedTime(&ms, e0, e1) != hipSuccess)
+              break;
+            if (ms < best) {
+              best = ms;
+              algo = res[i].algo;
+            }
+          }
+        }
+        if (e0) hipEventDestroy(e0);
+        if (e1) hipEventDestroy(e1);
+      }
+      std::lock_guard<std::mutex> g(c.mu);
+      c.algo[key] = algo;
+    }
+    if (hipblasLtMatmul(h, desc, &alpha, b_rows, la, dense, lb, &beta, staged, lc, staged, lc, &algo, ws, LT_WS, s) !=
+        HIPBLAS_STATUS_SUCCESS)
+      break;
+    ret = hipSuccess;
+  } while (false);
+  if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+  if (lc) hipblasLtMatrixLayoutDestroy(lc);
+  if (lb) hipblasLtMatrixLayoutDestroy(lb);
+  if (la) hipblasLtMatrixLayoutDestroy(la);
+  if (desc) hipblasLtMatmulDescDestroy(desc);
+  return ret;
+}
+
+// Host geometry (the device's batch_geo from the host copies): staged rows, dense
+// elements and, per batch, (nq, nk, kp, dense offset, staged offset).
+struct HostGeo {
+  int64_t staged = 0, dense = 0;
+};
+HostGeo bwd_host_geo(int batch, const int32_t* h_row_start, const int32_t* h_act_k, int s2, int n1) {
+  HostGeo g;
+  for (int b = 0; b < batch; ++b) {
+    const int nq = h_row_start[b + 1] - h_row_start[b];
+    const int nk = batch_nk(h_act_k[b], s2);
+    g.staged += nk;
+    g.dense += (int64_t)nk * dense_row(nq, n1);
+  }
+  return g;
+}
+
+// Workspace: token lists | batch offsets | staged offsets | staged d_key, d_key_rope,
+// d_value rows | library-GEMM workspace | dS_T | P_T. Returns the offset of dS_T; the
+// two dense buffers share the rest equally.
+size_t bwd_fixed_bytes(int total_rows, int batch, int topk, int sbs, int64_t staged, int d) {
   size_t off = align256(sfa_token_ws_bytes(total_rows > 0 ? total_rows : 1, topk, sbs));
-  off += align256((size_t)(batch + 1) * 8);
-  off += align256((size_t)key_rows * d * 4);
-  off += align256((size_t)key_rows * BDR * 4);
-  off += align256((size_t)key_rows * d * 4);
+  off += 2 * align256((size_t)(batch + 1) * 8);
+  off += align256((size_t)staged * d * 2);
+  off += align256((size_t)staged * BDR * 2);
+  off += align256((size_t)staged * d * 2);
+  off += LT_WS;
   return off;
 }
 
@@ -621,14 +642,9 @@ size_t bwd_fixed_bytes(int total_rows, int batch, int topk, int sbs, int64_t key
 
 size_t sfa_bwd_workspace_bytes(int batch, const int32_t* h_row_start, const int32_t* h_act_k, int s2,
                                int total_rows, int n1, int d, int topk, int sbs, int64_t key_rows) {
-  int64_t dense = 0;
-  for (int b = 0; b < batch; ++b) {
-    const int nq = h_row_start[b + 1] - h_row_start[b];
-    int nk = h_act_k[b] < s2 ? h_act_k[b] : s2;
-    nk = nk < 0 ? 0 : nk;
-    dense += (int64_t)nk * dsa::dense_row(nq, n1);
-  }
-  return dsa::bwd_fixed_bytes(total_rows, batch, topk, sbs, key_rows, d) + 2 * dsa::align256((size_t)dense * 2);
+  (void)key_rows;
+  const dsa::HostGeo g = dsa::bwd_host_geo(batch, h_row_start, h_act_k, s2, n1);
+  return dsa::bwd_fixed_bytes(total_rows, batch, topk, sbs, g.staged, d) + 2 * dsa::align256((size_t)g.dense * 2);
 }
 
 hipError_t launch_sfa_bwd(const SfaBwdArgs& a, hipStream_t s) {
@@ -637,35 +653,62 @@ hipError_t launch_sfa_bwd(const SfaBwdArgs& a, hipStream_t s) {
   SfaTokenLists tl{};
   hipError_t e = launch_sfa_token_lists(f, base, &tl, s);
   if (e != hipSuccess) return e;
+  const dsa::HostGeo hg = dsa::bwd_host_geo(f.batch, a.h_row_start, a.h_act_k, f.s2, f.n1);
   size_t off = dsa::align256(sfa_token_ws_bytes(f.total_rows > 0 ? f.total_rows : 1, f.topk, f.sbs));
   dsa::BwdWs w;
   w.boff = reinterpret_cast<int64_t*>(base + off);
   off += dsa::align256((size_t)(f.batch + 1) * 8);
-  char* acc0 = base + off;
-  w.dk = reinterpret_cast<float*>(base + off);
-  off += dsa::align256((size_t)f.key_rows * f.d * 4);
-  w.dkr = reinterpret_cast<float*>(base + off);
-  off += dsa::align256((size_t)f.key_rows * dsa::BDR * 4);
-  w.dv = reinterpret_cast<float*>(base + off);
-  off += dsa::align256((size_t)f.key_rows * f.d * 4);
-  const size_t acc_bytes = (size_t)(base + off - acc0);
+  w.boffk = reinterpret_cast<int64_t*>(base + off);
+  off += dsa::align256((size_t)(f.batch + 1) * 8);
+  w.sk = reinterpret_cast<uint16_t*>(base + off);
+  off += dsa::align256((size_t)hg.staged * f.d * 2);
+  w.skr = reinterpret_cast<uint16_t*>(base + off);
+  off += dsa::align256((size_t)hg.staged * dsa::BDR * 2);
+  w.sv = reinterpret_cast<uint16_t*>(base + off);
+  off += dsa::align256((size_t)hg.staged * f.d * 2);
+  w.lt_ws = base + off;
+  off += dsa::LT_WS;
   // the two dense buffers split what is left (256-byte aligned halves)
   const size_t rest = f.ws_bytes > off ? f.ws_bytes - off : 0;
   const size_t half = rest / 2 / 256 * 256;
   w.dst = reinterpret_cast<uint16_t*>(base + off);
   w.pt = reinterpret_cast<uint16_t*>(base + off + half);
   w.cap = (int64_t)(half / 2);
+  if (hg.dense > w.cap) return hipErrorInvalidValue;   // the caller's workspace is checked against this size
 
   hipLaunchKernelGGL(dsa::sfa_bwd_geo_kernel, dim3(1), dim3(256), 0, s, f, w);
   const int zb = 2048;
-  hipLaunchKernelGGL(dsa::sfa_bwd_zero_kernel, dim3(zb), dim3(256), 0, s, reinterpret_cast<uint4*>(acc0),
-                     (int64_t)(acc_bytes / 16), (const int64_t*)nullptr, (int64_t)0);
   hipLaunchKernelGGL(dsa::sfa_bwd_zero_kernel, dim3(zb), dim3(256), 0, s, reinterpret_cast<uint4*>(w.dst),
                      (int64_t)(half / 16), (const int64_t*)(w.boff + f.batch), w.cap);
   hipLaunchKernelGGL(dsa::sfa_bwd_zero_kernel, dim3(zb), dim3(256), 0, s, reinterpret_cast<uint4*>(w.pt),
                      (int64_t)(half / 16), (const int64_t*)(w.boff + f.batch), w.cap);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  return f.io == dsa::IO_BF16 ? dsa::launch_bwd_io<dsa::IO_BF16>(a, tl, w, s)
-                              : dsa::launch_bwd_io<dsa::IO_F16>(a, tl, w, s);
+  e = f.io == dsa::IO_BF16 ? dsa::launch_rows_io<dsa::IO_BF16>(a, tl, w, s)
+                           : dsa::launch_rows_io<dsa::IO_F16>(a, tl, w, s);
+  if (e != hipSuccess) return e;
+  // the three products of every batch holding query rows and key tokens
+  const hipDataType dt = f.io == dsa::IO_BF16 ? HIP_R_16BF : HIP_R_16F;
+  const uint16_t* q = reinterpret_cast<const uint16_t*>(f.q);
+  const uint16_t* qr = reinterpret_cast<const uint16_t*>(f.qr);
+  const uint16_t* go = reinterpret_cast<const uint16_t*>(a.d_out);
+  int64_t doff = 0, soff = 0;
+  for (int b = 0; b < f.batch; ++b) {
+    const int rs = a.h_row_start[b], nq = a.h_row_start[b + 1] - rs;
+    const int nk = dsa::batch_nk(a.h_act_k[b], f.s2);
+    const int kp = dsa::dense_row(nq, f.n1);
+    const int k = nq * f.n1;
+    if (nk > 0 && k > 0) {
+      const int64_t brow = (int64_t)rs * f.n1;
+      if ((e = dsa::lt_gemm(dt, f.d, nk, k, q + brow * f.d, w.dst + doff, kp, w.sk + soff * f.d, w.lt_ws, s)) != hipSuccess ||
+          (e = dsa::lt_gemm(dt, dsa::BDR, nk, k, qr + brow * dsa::BDR, w.dst + doff, kp, w.skr + soff * dsa::BDR,
+                            w.lt_ws, s)) != hipSuccess ||
+          (e = dsa::lt_gemm(dt, f.d, nk, k, go + brow * f.d, w.pt + doff, kp, w.sv + soff * f.d, w.lt_ws, s)) !=
+              hipSuccess)
+        return e;
+    }
+    doff += (int64_t)nk * kp;
+    soff += nk;
+  }
+  return dsa::launch_place(a, w, s);
 }
