@@ -90,6 +90,35 @@ template <> struct Mfma<IO_F16> {
   }
 };
 
+// 32x32x16 MFMA chains with the accumulator in arch VGPRs. In a kernel whose other
+// accumulators live in AGPRs the compiler selects the AGPR form for every builtin
+// MFMA, so a short-lived accumulator would take AGPRs too (and its VALU reads one
+// v_accvgpr_read each); written as inline asm, this one stays in VGPRs. The compiler
+// does not see these as MFMAs, so the caller ends every chain with vacc_drain()
+// before any VALU touches the accumulator or the chain's operand registers.
+typedef int i32x4v __attribute__((ext_vector_type(4)));
+template <int IO>
+__device__ __forceinline__ f32x16 mfma32_vacc_first(uint4 a, uint4 b) {   // A B
+  f32x16 c;
+  const i32x4v av = __builtin_bit_cast(i32x4v, a), bv = __builtin_bit_cast(i32x4v, b);
+  if constexpr (IO == IO_BF16)
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(c) : "v"(av), "v"(bv));
+  else
+    asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, 0" : "=&v"(c) : "v"(av), "v"(bv));
+  return c;
+}
+template <int IO>
+__device__ __forceinline__ void mfma32_vacc(f32x16& c, uint4 a, uint4 b) {   // c += A B
+  const i32x4v av = __builtin_bit_cast(i32x4v, a), bv = __builtin_bit_cast(i32x4v, b);
+  if constexpr (IO == IO_BF16)
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(av), "v"(bv));
+  else
+    asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(c) : "v"(av), "v"(bv));
+}
+// Wait states after the last MFMA of a VGPR chain: an 8-pass XDL result read (or
+// its operands overwritten) by VALU needs 11; 18 covers every XDL pass count.
+__device__ __forceinline__ void vacc_drain(f32x16& c) { asm volatile("s_nop 15\n\ts_nop 1" : "+v"(c)); }
+
 // Output layouts (CDNA3/CDNA4 MFMA, 64 lanes):
 //  32x32: lane l, acc[r] (r < 16) holds C[row = (r/4)*8 + (l/32)*4 + r%4][col = l%32]
 //  16x16: lane l, acc[r] (r < 4)  holds C[row = (l/16)*4 + r][col = l%16]
@@ -115,17 +144,19 @@ __device__ __forceinline__ void lds_barrier() {
 // as inline asm so the compiler does not track it: its wait insertion assumes
 // every LDS read may alias an outstanding direct-to-LDS load and would drain
 // the prefetched tiles (vmcnt 0) before each LDS read. Kernels using it order
-// these loads themselves with wait_vmcnt and lds_barrier.
+// these loads themselves with wait_vmcnt and lds_barrier. An LDS DMA reading M0
+// needs one wait state after the SALU write of M0 (the s_nop), and M0 is declared
+// clobbered so the compiler keeps nothing of its own there across the statement.
 __device__ __forceinline__ void lds_dma16_untracked(const void* gptr, void* lds_base) {
   const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds_base;
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gptr), "s"(m0) : "memory");
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gptr), "s"(m0) : "memory", "m0");
 }
 
 // Same with a wave-uniform base address (SGPR pair) and a per-lane 32-bit byte
 // offset: lane l reads sbase + voff[l] and writes LDS [lds_base + 16 l, +16).
 __device__ __forceinline__ void lds_dma16_sbase_untracked(const void* sbase, uint32_t voff, void* lds_base) {
   const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds_base;
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "s"(m0) : "memory");
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "s"(m0) : "memory", "m0");
 }
 
 // x[l] + x[l ^ 32] on every lane, with one v_permlane32_swap (VALU, no LDS).

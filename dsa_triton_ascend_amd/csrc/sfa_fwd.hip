@@ -660,12 +660,18 @@ __device__ __forceinline__ void gather_part(int j, const uint16_t* kb, const uin
                                             const uint16_t* zero, int krows, const TileIdx& ix,
                                             uint8_t* nope, uint8_t* rope, int wave_u, int lane) {
   using C = Cfg<D>;
+  // The empty asm statements pin the address arithmetic to this point of the caller's
+  // MFMA chain: the row ids are known before the chain, and without them the compiler
+  // computes every part's address up front, between the chain's first two MFMAs.
   if (j < 8) {
-    const int phys = ix.nope[j];   // wave-uniform: the row base goes in an SGPR pair
+    int phys = ix.nope[j];   // wave-uniform: the row base goes in an SGPR pair
+    asm volatile("" : "+s"(phys));
     const uint16_t* src = (uint32_t)phys < (uint32_t)krows ? kb + (int64_t)phys * D : zero;
     if (lane < C::LANES_ROW) lds_dma16_sbase_untracked(src, lane * 16, nope + nope_off<D>(wave_u * 8 + j));
   } else {
-    const uint16_t* src = (uint32_t)ix.rope < (uint32_t)krows ? krb + (int64_t)ix.rope * DR : zero + 512;
+    int rid = ix.rope;
+    asm volatile("" : "+v"(rid));
+    const uint16_t* src = (uint32_t)rid < (uint32_t)krows ? krb + (int64_t)rid * DR : zero + 512;
     lds_dma16_untracked(src + (lane >> 3) * 8, rope + wave_u * 1024);
   }
 }
@@ -723,6 +729,8 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   const int r = a.total_rows - 1 - (int)blockIdx.x;
   const int sp = blockIdx.y;
   const int n1 = a.n1;
+  const float cpos = a.scale > 0.f ? a.scale : a.scale < 0.f ? -a.scale : 1e-30f;
+  const float cl2 = cpos * LOG2E;
   // a scalar load (token-list kernel ran), waited for at its first use below
   const int ntok_pre = fuse_tok ? 0 : ws.counts[r];
   TokPrefetch pre{};
@@ -839,6 +847,29 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   if (hq >= n1)
 #pragma unroll
     for (int j = 0; j < QF; ++j) qf[j] = make_uint4(0, 0, 0, 0);
+  // The softmax works on raw scores with a positive scale cpos. A negative scale runs
+  // on the negated query instead (negating 16-bit floats is exact, and so are the
+  // products and their sums: -q.k exactly), so c s = |c| (-s). A zero scale becomes
+  // 1e-30: scores times it round to 0 and exp of them to exactly 1, as with 0, while
+  // masked slots (-inf) still give 0.
+  if constexpr (!TEACH) {
+    if (a.scale < 0.f) {
+#pragma unroll
+      for (int j = 0; j < QF; ++j) {
+        qf[j].x ^= 0x80008000u;
+        qf[j].y ^= 0x80008000u;
+        qf[j].z ^= 0x80008000u;
+        qf[j].w ^= 0x80008000u;
+      }
+#pragma unroll
+      for (int j = 0; j < NH * (DR / 8) / (NWV * 64); ++j) {
+        qrv[j].x ^= 0x80008000u;
+        qrv[j].y ^= 0x80008000u;
+        qrv[j].z ^= 0x80008000u;
+        qrv[j].w ^= 0x80008000u;
+      }
+    }
+  }
 #pragma unroll
   for (int j = 0; j < NH * (DR / 8) / (NWV * 64); ++j) {
     const int h = (threadIdx.x >> 3) + j * (NWV * 64 / 8), e = (threadIdx.x & 7) * 8;
@@ -909,8 +940,13 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
     for (int j = 0; j < KSH; ++j) {
       const int ks = K0 + j;
       const uint4 bq = ks < C::KSN ? qf[j < QF ? j : 0] : qr[ks >= C::KSN ? ks - C::KSN : 0];
-      if constexpr (TEACH) sacc = Mfma<IO>::m32(bq, af[j & 3], sacc);   // S[head, token]
-      else sacc = Mfma<IO>::m32(af[j & 3], bq, sacc);                    // S^T[token, head]
+      if constexpr (TEACH) {
+        sacc = Mfma<IO>::m32(bq, af[j & 3], sacc);   // S[head, token]
+      } else {                                         // S^T[token, head], accumulator in VGPRs
+        if (j == 0) sacc = mfma32_vacc_first<IO>(af[0], bq);
+        else mfma32_vacc<IO>(sacc, af[j & 3], bq);
+        if (j == KSH - 1) vacc_drain(sacc);   // before the last step's loads and any VALU
+      }
       if (j + 4 < KSH) af[j & 3] = a_frag(ks + 4);
       spread(j);
       __builtin_amdgcn_sched_barrier(0);
@@ -946,10 +982,8 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
     }
   };
 
-  // ---- scores of tile u scaled; slots past the token list (partial last tile) masked
-  auto scale_tile = [&](int u, f32x16& sv) __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) sv[i] *= a.scale;
+  // ---- raw scores of tile u: slots past the token list (partial last tile) masked
+  auto mask_tile = [&](int u, f32x16& sv) __attribute__((always_inline)) {
     const int nvalid = ntok - u * BN;
     if (nvalid < BN) {
 #pragma unroll
@@ -960,14 +994,16 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
     }
   };
 
-  // ---- online softmax of tile u for head hq (lane holds 16 scaled scores): P (io
-  // dtype) to pt[u & 1], the O rescale factor to s_alpha[u & 1]. Branch-free, so
-  // the scheduler can place it among the PV MFMAs it is issued with.
+  // ---- online softmax of tile u for head hq (lane holds 16 raw scores; the scale is
+  // positive, see cpos): P (io dtype) to pt[u & 1], the O rescale factor to
+  // s_alpha[u & 1]. Branch-free, so the scheduler can place it among the PV MFMAs it
+  // is issued with.
   auto softmax_tile = [&](int u, const f32x16& sv) __attribute__((always_inline)) {
     float mx = sv[0];
 #pragma unroll
     for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sv[i]);
-    mx = max_half_swap(mx);   // every tile holds at least one valid token: mx is finite
+    // every tile holds at least one valid token: mx is finite; max(c s) = c max(s), c > 0
+    mx = max_half_swap(mx) * cpos;
     m_true = fmaxf(m_true, mx);
     // lazy rescaling: the reference maximum moves only when the tile max exceeds it
     // by more than TAU; alpha is exactly 1 otherwise, and 1 on the first tile (O
@@ -984,7 +1020,7 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
       float p[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[g * 4 + j], LOG2E, -mb));
+        p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[g * 4 + j], cl2, -mb));
         psum += p[j];
       }
       if (writer) *reinterpret_cast<uint2*>(prow + g * 8) = make_uint2(pack2<IO>(p[0], p[1]), pack2<IO>(p[2], p[3]));
@@ -1088,7 +1124,7 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   lds_barrier();   // tile 0 visible
   {
     f32x16 s0 = s_tile(0, [&](int) {});
-    scale_tile(0, s0);
+    mask_tile(0, s0);
     softmax_tile(0, s0);
   }
   // barrier at the top of iteration t, then rescale O by alpha(t) when any head's
@@ -1129,7 +1165,7 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
           else ids_dma(t + 4);   // slot (t+4)%4 held the ids of tile t, read two iterations ago
         }
     });
-    scale_tile(t + 1, s1);
+    mask_tile(t + 1, s1);
     pv_tile(t, [&]() { softmax_tile(t + 1, s1); });
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -1139,7 +1175,6 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
 
   // ---- epilogue
   const float l_tot = l_part + __shfl_xor(l_part, 32);
-  __syncthreads();  // all PV reads of s_alpha / pt done before s_l is written
   const bool owner = lane < 32 && kh == 0;   // one lane per head (a pair holds equal values)
   if (owner) s_l[hq] = 1.f / l_tot;   // l > 0: a row or split holds at least one token
   if (direct) {
@@ -1153,7 +1188,9 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
     ps[1] = m_true;
     ps[2] = l_tot;
   }
-  __syncthreads();
+  // s_l (written only here) visible to every wave; an LDS-only barrier, so the
+  // statistics stores above are not waited for
+  lds_barrier();
   // O^T layout: in accumulator (mt, nt) lane l holds head h = mt*32 + l%32 and, at
   // index 4g + j, column wave*DW + nt*32 + 8g + 4(l/32) + j (g, j < 4). After scaling
   // and packing, two lane-half swaps leave lanes l < 32 with columns [0,8) and

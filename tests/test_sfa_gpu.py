@@ -119,6 +119,23 @@ def test_head_counts(dev, N1):
     compare(out, smax, ssum, *o, what=f"N1={N1}")
 
 
+@pytest.mark.parametrize("scale", [-0.05, 0.0])
+@pytest.mark.parametrize("N1", [16, 128])
+def test_non_positive_scale(dev, N1, scale):
+    """The softmax runs on raw scores times a positive scale: a negative scale_value
+    runs on the negated query, zero as 1e-30. Both must match the oracle (zero: every
+    valid token weighs the same, softmax_max 0), including partial last tiles."""
+    B, S1, S2, D, count = 1, 5, 100, 512, 70
+    q, k, v, qr, kr = _inputs(B, S1, S2, N1, D, "bf16", seed=6)
+    si = _ref_indices(B, S1, S2, count, 1, 3, seed=9)
+    out, smax, ssum = sparse_flash_attention(q.to(dev), k.to(dev), v.to(dev), torch.from_numpy(si).to(dev),
+                                             scale_value=scale, query_rope=qr.to(dev), key_rope=kr.to(dev),
+                                             sparse_mode=3, return_softmax_lse=True)
+    o = SFA.sparse_flash_attention(_np(q), _np(k), None, si, scale, query_rope=_np(qr), key_rope=_np(kr),
+                                   sparse_mode=3, return_softmax_lse=True, io_dtype="bf16")
+    compare(out, smax, ssum, *o, what=f"N1={N1} scale={scale}")
+
+
 def test_actual_lengths_and_skips(dev):
     """act_q > act_k (mode-3 leading rows skipped), a -1 in the middle of a row
     (scan stops), duplicate ids, ids beyond the threshold."""
