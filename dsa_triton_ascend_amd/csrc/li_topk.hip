@@ -276,17 +276,35 @@ __global__ __launch_bounds__(TPB) void li_topk_kernel(LiTopkArgs a) {
   for (int e = 0; e < E; ++e) key[e] = sbuf[E * t + e];
   __syncthreads();
   radix_sort_desc16<E>(key, sbuf, cnt, red);
+  // ranks E t .. E t + E - 1 of thread t: their index (or -1) and 16-bit value (or 0)
+  int32_t oi[E];
+  uint16_t ov[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    const int i = E * t + e;
-    if (i < k) {
-      if (i < nout) {
-        if constexpr (WIDE) iout[i] = sidx[key[e] & 0xFFFFu];
-        else iout[i] = (int32_t)(0xFFFFu - (key[e] & 0xFFFFu));
-        if (vout) vout[i] = unord16(key[e] >> 16);
-      } else {
-        iout[i] = -1;
-        if (vout) vout[i] = 0;
+    const bool ok = E * t + e < nout;
+    if constexpr (WIDE) oi[e] = ok ? sidx[key[e] & 0xFFFFu] : -1;
+    else oi[e] = ok ? (int32_t)(0xFFFFu - (key[e] & 0xFFFFu)) : -1;
+    ov[e] = ok ? unord16(key[e] >> 16) : (uint16_t)0;
+  }
+  // 16-byte stores when the thread's whole run lies inside the row and rows are
+  // 16-byte aligned (k % 8 == 0); the rest element by element
+  if (E % 8 == 0 && k % 8 == 0 && E * t + E <= k) {
+#pragma unroll
+    for (int e = 0; e < E; e += 4)
+      *reinterpret_cast<int4*>(iout + E * t + e) = make_int4(oi[e], oi[e + 1], oi[e + 2], oi[e + 3]);
+    if (vout)
+#pragma unroll
+      for (int e = 0; e < E; e += 8)
+        *reinterpret_cast<uint4*>(vout + E * t + e) =
+            make_uint4(ov[e] | ((uint32_t)ov[e + 1] << 16), ov[e + 2] | ((uint32_t)ov[e + 3] << 16),
+                       ov[e + 4] | ((uint32_t)ov[e + 5] << 16), ov[e + 6] | ((uint32_t)ov[e + 7] << 16));
+  } else {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int i = E * t + e;
+      if (i < k) {
+        iout[i] = oi[e];
+        if (vout) vout[i] = ov[e];
       }
     }
   }
