@@ -296,6 +296,30 @@ def test_c3_prefill_sampled(dev):
             what="C3 prefill (sampled rows)")
 
 
+@pytest.mark.parametrize("N1,dtype,mode", [(128, "bf16", 3), (128, "fp16", 3), (128, "bf16", 0)])
+def test_rows_mixed_lengths(dev, N1, dtype, mode):
+    """2 x 700 unsplit rows of 128 heads at D = 512 (more rows than CUs) whose token
+    counts vary from 0 to 8 tiles: ids cut short by a -1 at a random position (rows
+    without tokens among rows with tokens), partial last tiles. Every row is checked
+    against the oracle."""
+    B, S1, S2, D, count = 2, 700, 900, 512, 256
+    q, k, v, qr, kr = _inputs(B, S1, S2, N1, D, dtype, seed=11)
+    si = _ref_indices(B, S1, S2, count, 1, mode, seed=12)
+    rng = np.random.RandomState(13)
+    cut = rng.randint(0, count + 1, size=(B, S1))
+    cut[rng.rand(B, S1) < 0.4] = count   # most rows keep every id
+    for b in range(B):
+        for s in range(S1):
+            si[b, s, 0, cut[b, s]:] = -1
+    out, smax, ssum = sparse_flash_attention(q.to(dev), k.to(dev), v.to(dev), torch.from_numpy(si).to(dev),
+                                             scale_value=0.04, query_rope=qr.to(dev), key_rope=kr.to(dev),
+                                             sparse_mode=mode, return_softmax_lse=True)
+    torch.cuda.synchronize()
+    o = SFA.sparse_flash_attention(_np(q), _np(k), None, si, 0.04, query_rope=_np(qr), key_rope=_np(kr),
+                                   sparse_mode=mode, return_softmax_lse=True, io_dtype=dtype)
+    compare(out, smax, ssum, *o, what=f"mixed rows N1={N1} {dtype} m{mode}")
+
+
 def test_pa_many_rows_token_list(dev):
     """PA_BSND with 1,088 query rows, so the one-wave-per-row token-list kernel runs with a
     block table: shuffled pages, a missing (-1) page, a -1 in the middle of a row (the scan
