@@ -538,49 +538,52 @@ __global__ __launch_bounds__(256) void sfa_merge_kernel(SfaArgs a, int splits, W
   constexpr int MERGE_MAX_SPLITS = MS, MU = 16 / MS;
   const int r = blockIdx.x;
   const int n1 = a.n1;
-  const int ntok_all = ws.counts[r];
-  const int per = ((ntok_all + splits - 1) / splits + 31) / 32 * 32;
-  const int nact = ntok_all > 0 ? (ntok_all + per - 1) / per : 0;
-  if (nact <= 1) return;
   constexpr int CH = D / 8;
   const int units = n1 * CH;
   const float* ps = ws.part_s + (int64_t)r * splits * n1 * 3;
   const uint16_t* po = ws.part_o + (int64_t)r * splits * n1 * D;
   uint16_t* out = reinterpret_cast<uint16_t*>(a.out) + (int64_t)r * n1 * D;
   const int u0 = blockIdx.y * 256 * MU + threadIdx.x;
+  // every split's partial and statistics are requested before the row's token count
+  // (which says how many splits hold tokens) has arrived: one memory round trip instead
+  // of two; the entries of splits past the row's tokens are in bounds and never used
   uint4 v[MU][MERGE_MAX_SPLITS];
+  float sm_u[MU][MERGE_MAX_SPLITS], sm_t[MU][MERGE_MAX_SPLITS], sm_l[MU][MERGE_MAX_SPLITS];
 #pragma unroll
   for (int k = 0; k < MU; ++k) {
     const int u = u0 + k * 256;
     const int uc = u < units ? u : units - 1;
 #pragma unroll
     for (int sp = 0; sp < MERGE_MAX_SPLITS; ++sp)
-      if (sp < nact) v[k][sp] = ldg16(po + ((int64_t)sp * n1 + uc / CH) * D + (uc % CH) * 8);
+      if (sp < splits) {
+        v[k][sp] = ldg16(po + ((int64_t)sp * n1 + uc / CH) * D + (uc % CH) * 8);
+        const float* q = ps + ((int64_t)sp * n1 + uc / CH) * 3;
+        sm_u[k][sp] = q[0];
+        sm_t[k][sp] = q[1];
+        sm_l[k][sp] = q[2];
+      }
   }
+  const int ntok_all = ws.counts[r];
+  const int per = ((ntok_all + splits - 1) / splits + 31) / 32 * 32;
+  const int nact = ntok_all > 0 ? (ntok_all + per - 1) / per : 0;
+  if (nact <= 1) return;
 #pragma unroll
   for (int k = 0; k < MU; ++k) {
     const int u = u0 + k * 256;
     if (u >= units) continue;
     const int h = u / CH;
-    float mu[MERGE_MAX_SPLITS], ls[MERGE_MAX_SPLITS];
     float M = -INFINITY, mt = -INFINITY;
 #pragma unroll
-    for (int sp = 0; sp < MERGE_MAX_SPLITS; ++sp) {
-      mu[sp] = -INFINITY;
-      ls[sp] = 0.f;
+    for (int sp = 0; sp < MERGE_MAX_SPLITS; ++sp)
       if (sp < nact) {
-        const float* q = ps + ((int64_t)sp * n1 + h) * 3;
-        mu[sp] = q[0];
-        ls[sp] = q[2];
-        M = fmaxf(M, mu[sp]);
-        mt = fmaxf(mt, q[1]);
+        M = fmaxf(M, sm_u[k][sp]);
+        mt = fmaxf(mt, sm_t[k][sp]);
       }
-    }
     float w[MERGE_MAX_SPLITS];
     float L = 0.f;
 #pragma unroll
     for (int sp = 0; sp < MERGE_MAX_SPLITS; ++sp) {
-      w[sp] = sp < nact ? ls[sp] * exp2f((mu[sp] - M) * LOG2E) : 0.f;
+      w[sp] = sp < nact ? sm_l[k][sp] * exp2f((sm_u[k][sp] - M) * LOG2E) : 0.f;
       L += w[sp];
     }
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
