@@ -140,27 +140,45 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
   // k = s / CPR. Every lane always issues its loads (keys past L_blk re-read the
   // last visible key, whose columns are never stored), so each wave has exactly
   // IPW loads per tile in flight and one partial vmcnt wait retires a tile.
+  // When the batch's key rows span less than 4 GiB from kbase (S2 * N2 * D < 2^31)
+  // the byte offset of a load is a per-lane constant plus one scalar tile offset,
+  // and a full tile's loads take the SGPR-base form: one VALU add per load.
   const int ntiles = (L_blk + T::BN - 1) / T::BN;
-  auto dma = [&](int tile) {
-    uint16_t* buf = kt[tile % T::NBUF];
+  const uint32_t ksb = (uint32_t)(a.n2 * D * 2);   // key row stride in bytes
+  const bool off32 = !PAGED && (uint64_t)(uint32_t)a.s2 * ksb <= 0xFFFFFFFFull;
+  int dk[T::IPW];          // key row of load j within the tile
+  uint32_t dcb[T::IPW];    // byte offset of its 16-byte chunk within the row
+  uint32_t doff[T::IPW];   // dk * ksb + dcb
 #pragma unroll
-    for (int j = 0; j < T::IPW; ++j) {
-      const int i = wave * T::IPW + j;
-      const int slot = i * 64 + lane;
-      const int k = slot / T::CPR;
-      const int c = (slot % T::CPR) ^ (k & T::SWZ);
-      int s2 = tile * T::BN + k;
-      s2 = s2 < L_blk ? s2 : L_blk - 1;
-      int64_t row = s2;
-      if constexpr (PAGED) {
-        bool ok;
-        row = phys_row(s2, ok);
+  for (int j = 0; j < T::IPW; ++j) {
+    const int slot = (wave * T::IPW + j) * 64 + lane;
+    dk[j] = slot / T::CPR;
+    dcb[j] = 16u * (uint32_t)((slot % T::CPR) ^ (dk[j] & T::SWZ));
+    doff[j] = (uint32_t)dk[j] * ksb + dcb[j];
+  }
+  auto dma = [&](int tile, uint16_t* buf) {
+    if (off32 && (tile + 1) * T::BN <= L_blk) {
+      const uint32_t toff = (uint32_t)(tile * T::BN) * ksb;
+#pragma unroll
+      for (int j = 0; j < T::IPW; ++j)
+        lds_dma16_sbase_untracked(kbase, toff + doff[j], buf + (wave * T::IPW + j) * 512);
+    } else {
+#pragma unroll
+      for (int j = 0; j < T::IPW; ++j) {
+        int s2 = tile * T::BN + dk[j];
+        s2 = s2 < L_blk ? s2 : L_blk - 1;
+        int64_t row = s2;
+        if constexpr (PAGED) {
+          bool ok;
+          row = phys_row(s2, ok);
+        }
+        lds_dma16_untracked(reinterpret_cast<const char*>(kbase) + row * (int64_t)ksb + dcb[j],
+                            buf + (wave * T::IPW + j) * 512);
       }
-      lds_dma16_untracked(kbase + row * kstride + c * 8, buf + i * 512);
     }
   };
 #pragma unroll
-  for (int j = 0; j < T::NBUF - 1; ++j) dma(j);
+  for (int j = 0; j < T::NBUF - 1; ++j) dma(j, kt[j]);
 
   // ---- per-row operands: Q fragments (A) and head weights
   uint4 qf[QREG ? MT : 1][QREG ? KK : 1];
@@ -195,20 +213,26 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
       }
   }
 
+  // Scores go out through a buffer store whose range is the row's visible keys:
+  // the hardware drops every lane past L_row, and lanes of an empty slot are
+  // given an offset past it, so no lane needs a compare or an exec mask.
   uint16_t* srow = a.scores + (r * a.n2 + n2) * a.ld;
+  const __amdgpu_buffer_rsrc_t srd =
+      __builtin_amdgcn_make_buffer_rsrc(srow, (short)0, L_row * 2, 0x00020000);
+  constexpr int OOB = 1 << 30;
 
   // ---- main loop, software-pipelined by 32-key subtile: the MFMAs of subtile
   // j are interleaved with the relu*w epilogue of subtile j-1 (ping-pong
   // accumulators), so the wave's VALU work co-executes with its MFMAs.
   f32x16 acc[2][MT];
-  int pend_key0 = -1;   // first key of the subtile whose epilogue is pending (-1: none)
-
-  auto zero = [&](f32x16(&c)[MT]) {
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) c[mt][i] = 0.f;
-  };
+      for (int i = 0; i < 16; ++i) acc[u][mt][i] = 0.f;
+  int pend_key0 = -1;   // first key of the subtile whose epilogue is pending (-1: none)
+
   // Scores of a subtile wait in a register slot and are written at the start of
   // the next tile, before its K loads are issued, so the stores never hold up
   // the partial vmcnt wait for the tile in flight. Slots pair up: lanes 0-31
@@ -221,18 +245,23 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
   auto flush = [&]() {
 #pragma unroll
     for (int m = 0; m < NSLOT; m += 2) {
+      const int klo = pk[m], khi = m + 1 < NSLOT ? pk[m + 1] : -1;   // wave-uniform
+      if (klo < 0 && khi < 0) continue;
       const bool hi = lane >= 32;
-      const int k0 = (hi && m + 1 < NSLOT) ? pk[m + 1] : (hi ? -1 : pk[m]);
       float v = (hi && m + 1 < NSLOT) ? pv[m + 1] : pv[m];
-      const int s2 = k0 + (lane & 31);
-      if (k0 >= 0 && s2 < L_row) {
-        if constexpr (PAGED) {
-          bool ok;
-          phys_row(s2, ok);
-          v = ok ? v : 0.f;
-        }
-        srow[s2] = from_f32<IO>(v);
+      int s2;
+      if (klo >= 0 && khi == klo + 32) {
+        s2 = klo + lane;
+      } else {
+        const int kb = hi ? khi : klo;
+        s2 = kb >= 0 ? kb + (lane & 31) : OOB;
       }
+      if constexpr (PAGED) {
+        bool ok;
+        phys_row(s2 < L_row ? s2 : 0, ok);
+        v = ok ? v : 0.f;
+      }
+      __builtin_amdgcn_raw_buffer_store_b16(from_f32<IO>(v), srd, s2 * 2, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < NSLOT; ++i) pk[i] = -1;
@@ -243,56 +272,48 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
     pv[slot] = add_half_swap(p);
     pk[slot] = key0;
   };
-  // per-lane chunk offsets of the B-fragment reads (rows are 8-aligned per subtile,
-  // so a row's permutation key is lane & SWZ): chunk 2 kk + h sits at
-  // GS * (kk / JN) + ((2 (kk % JN) + h) ^ (lane & SWZ)), h = lane >> 5
+  // Per-lane B-fragment read addresses in buffer 0, subtile 0 (rows are 8-aligned
+  // per subtile, so a row's permutation key is lane & SWZ): chunk 2 kk + h sits at
+  // GS * (kk / JN) + ((2 (kk % JN) + h) ^ (lane & SWZ)), h = lane >> 5. The buffer
+  // and subtile offsets are compile-time in the unrolled ring below and go into the
+  // reads' offset field.
   constexpr int GS = T::SWZ + 1, JN = GS / 2;
-  int coff[JN];
+  constexpr int KC = KK < 8 ? KK : 8;              // k-steps whose fragments are read together
+  const uint16_t* rp[JN];
 #pragma unroll
-  for (int j = 0; j < JN; ++j) coff[j] = 8 * ((2 * j + (lane >> 5)) ^ (lane & T::SWZ));
-  // one subtile: MFMAs into `cur` from the LDS rows at `bp`; epilogue of `prev` interleaved
-  // `hp` (std::true_type / std::false_type): whether `prev` holds a pending subtile; a
-  // compile-time flag so each variant is one straight-line block for the scheduler.
-  auto step = [&](auto hp, f32x16(&cur)[MT], f32x16(&prev)[MT], const uint16_t* bp, int prev_key0,
-                  int slot) {
+  for (int j = 0; j < JN; ++j) rp[j] = &kt[0][(lane & 31) * D] + 8 * ((2 * j + (lane >> 5)) ^ (lane & T::SWZ));
+  auto bread = [&](auto bufc, int sub, int kk) -> uint4 {
+    constexpr int BUF = decltype(bufc)::value;
+    return *reinterpret_cast<const uint4*>(rp[kk % JN] + BUF * T::BN * D + sub * 32 * D + 8 * GS * (kk / JN));
+  };
+  // MFMAs of one k-chunk into `cur` with the B fragments `bf`; the epilogue of
+  // `prev` interleaved when `hp` (std::true_type / std::false_type)
+  auto chunk = [&](auto hp, f32x16(&cur)[MT], f32x16(&prev)[MT], const uint4 (&bf)[KC], int k0, float (&p4)[4]) {
     constexpr bool has_prev = decltype(hp)::value;
-    constexpr int KC = KK < 8 ? KK : 8;
     constexpr int EPK = (MT * 16 + KK - 1) / KK;   // epilogue elements per k-step
-    float p4[4] = {0.f, 0.f, 0.f, 0.f};
-    zero(cur);
 #pragma unroll
-    for (int k0 = 0; k0 < KK; k0 += KC) {
-      uint4 bf[KC];
+    for (int j = 0; j < KC; ++j) {
+      const int kk = k0 + j;
 #pragma unroll
-      for (int j = 0; j < KC; ++j) {
-        const int kk = k0 + j;   // logical chunk 2 kk + (lane >> 5) of this lane's key row
-        bf[j] = *reinterpret_cast<const uint4*>(bp + 8 * GS * (kk / JN) + coff[kk % JN]);
-      }
-#pragma unroll
-      for (int j = 0; j < KC; ++j) {
-        const int kk = k0 + j;
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          uint4 af;
-          if constexpr (QREG) {
-            af = qf[mt][kk];
-          } else {
-            const int m = mt * 32 + (lane & 31);
-            af = (row_ok && m < G) ? ldg16(qrow + (int64_t)m * D + kk * 16 + (lane >> 5) * 8)
-                                   : make_uint4(0, 0, 0, 0);
-          }
-          cur[mt] = Mfma<IO>::m32(af, bf[j], cur[mt]);
+      for (int mt = 0; mt < MT; ++mt) {
+        uint4 af;
+        if constexpr (QREG) {
+          af = qf[mt][kk];
+        } else {
+          const int m = mt * 32 + (lane & 31);
+          af = (row_ok && m < G) ? ldg16(qrow + (int64_t)m * D + kk * 16 + (lane >> 5) * 8)
+                                 : make_uint4(0, 0, 0, 0);
         }
-        if constexpr (has_prev) {
+        cur[mt] = Mfma<IO>::m32(af, bf[j], kk == 0 ? f32x16{} : cur[mt]);
+      }
+      if constexpr (has_prev) {
 #pragma unroll
-          for (int q = 0; q < EPK; ++q) {
-            const int e = kk * EPK + q;
-            if (e < MT * 16) p4[e & 3] += fmaxf(prev[e >> 4][e & 15], 0.f) * wv[e >> 4][e & 15];
-          }
+        for (int q = 0; q < EPK; ++q) {
+          const int e = kk * EPK + q;
+          if (e < MT * 16) p4[e & 3] += fmaxf(prev[e >> 4][e & 15], 0.f) * wv[e >> 4][e & 15];
         }
       }
     }
-    if constexpr (has_prev) finish(p4, prev_key0, slot);
   };
   auto drain = [&](f32x16(&prev)[MT], int key0, int slot) {
     float p4[4] = {0.f, 0.f, 0.f, 0.f};
@@ -301,37 +322,69 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
     finish(p4, key0, slot);
   };
 
-  // Tile t is read from LDS buffer t % 3 while tile t+1 has landed (or is
+  // One tile from LDS buffer BUF = t % 3 while tile t+1 has landed (or is
   // landing) in the next buffer and tile t+2 is being loaded into the third.
-  wait_vmcnt<0>();
-  lds_barrier();
-  for (int t = 0; t < ntiles; ++t) {
-    flush();            // scores of tile t-1
-    dma(t + T::NBUF - 1);   // its buffer held tile t-1, released by the last barrier
-    const uint16_t* bp0 = &kt[t % T::NBUF][(lane & 31) * D];
-    if (t * T::BN < L_row) {  // wave-uniform: this row sees part of the tile
-      if constexpr (NSUB % 2 == 0) {
-        if (pend_key0 >= 0)
-          step(std::true_type{}, acc[0], acc[1], bp0, pend_key0, 0);
-        else
-          step(std::false_type{}, acc[0], acc[1], bp0, 0, 0);
-        step(std::true_type{}, acc[1], acc[0], bp0 + 32 * D, t * T::BN, 1);
+  // Right after the barrier a wave first requests its first B fragments, then
+  // writes the previous tile's scores and issues the loads of tile t+2, which
+  // all overlap the wait for the LDS reads.
+  auto tile_body = [&](auto bufc, int t) {
+    constexpr int BUF = decltype(bufc)::value;
+    constexpr int NXT = (BUF + T::NBUF - 1) % T::NBUF;   // buffer of tile t+2: held tile t-1
+    if (t * T::BN < L_row) {   // wave-uniform: this row sees part of the tile
+      uint4 bf[KC];
 #pragma unroll
-        for (int sub = 2; sub < NSUB; sub += 2) {
-          step(std::true_type{}, acc[0], acc[1], bp0 + sub * 32 * D, t * T::BN + (sub - 1) * 32, sub);
-          step(std::true_type{}, acc[1], acc[0], bp0 + (sub + 1) * 32 * D, t * T::BN + sub * 32, sub + 1);
+      for (int j = 0; j < KC; ++j) bf[j] = bread(bufc, 0, j);
+      flush();            // scores of tile t-1
+      dma(t + T::NBUF - 1, kt[NXT]);
+      if constexpr (NSUB % 2 == 0) {
+#pragma unroll
+        for (int sub = 0; sub < NSUB; ++sub) {
+          f32x16(&cur)[MT] = acc[sub & 1];
+          f32x16(&prev)[MT] = acc[(sub + 1) & 1];
+          float p4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int k0 = 0; k0 < KK; k0 += KC) {
+            if (sub > 0 || k0 > 0)
+#pragma unroll
+              for (int j = 0; j < KC; ++j) bf[j] = bread(bufc, sub, k0 + j);
+            chunk(std::true_type{}, cur, prev, bf, k0, p4);
+          }
+          // sub 0 finishes the pending subtile of the previous tile (none at the
+          // row's first tile: its zeroed accumulators give a slot that is not stored)
+          finish(p4, sub == 0 ? pend_key0 : t * T::BN + (sub - 1) * 32, sub);
         }
         pend_key0 = t * T::BN + (NSUB - 1) * 32;
       } else {
-        step(std::false_type{}, acc[0], acc[1], bp0, 0, 0);
+        float p4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k0 = 0; k0 < KK; k0 += KC) {
+          if (k0 > 0)
+#pragma unroll
+            for (int j = 0; j < KC; ++j) bf[j] = bread(bufc, 0, k0 + j);
+          chunk(std::false_type{}, acc[0], acc[1], bf, k0, p4);
+        }
         drain(acc[0], t * T::BN, 0);
       }
-    } else if (pend_key0 >= 0) {
-      drain(acc[1], pend_key0, 0);
-      pend_key0 = -1;
+    } else {
+      flush();
+      dma(t + T::NBUF - 1, kt[NXT]);
+      if (pend_key0 >= 0) {
+        drain(acc[1], pend_key0, 0);
+        pend_key0 = -1;
+      }
     }
     wait_vmcnt<T::IPW * (T::NBUF - 2)>();   // this wave's part of tile t+1 has landed
     lds_barrier();
+  };
+  static_assert(T::NBUF == 3, "the ring below is unrolled for three buffers");
+  wait_vmcnt<0>();
+  lds_barrier();
+  for (int t = 0; t < ntiles; t += 3) {
+    tile_body(std::integral_constant<int, 0>{}, t);
+    if (t + 1 >= ntiles) break;
+    tile_body(std::integral_constant<int, 1>{}, t + 1);
+    if (t + 2 >= ntiles) break;
+    tile_body(std::integral_constant<int, 2>{}, t + 2);
   }
   flush();
   if (pend_key0 >= 0) {
