@@ -156,26 +156,24 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
     dcb[j] = 16u * (uint32_t)((slot % T::CPR) ^ (dk[j] & T::SWZ));
     doff[j] = (uint32_t)dk[j] * ksb + dcb[j];
   }
-  auto dma = [&](int tile, uint16_t* buf) {
+  auto dma_part = [&](int tile, uint16_t* buf, int j) {   // load j of this wave for a tile
     if (off32 && (tile + 1) * T::BN <= L_blk) {
-      const uint32_t toff = (uint32_t)(tile * T::BN) * ksb;
-#pragma unroll
-      for (int j = 0; j < T::IPW; ++j)
-        lds_dma16_sbase_untracked(kbase, toff + doff[j], buf + (wave * T::IPW + j) * 512);
+      lds_dma16_sbase_untracked(kbase, (uint32_t)(tile * T::BN) * ksb + doff[j], buf + (wave * T::IPW + j) * 512);
     } else {
-#pragma unroll
-      for (int j = 0; j < T::IPW; ++j) {
-        int s2 = tile * T::BN + dk[j];
-        s2 = s2 < L_blk ? s2 : L_blk - 1;
-        int64_t row = s2;
-        if constexpr (PAGED) {
-          bool ok;
-          row = phys_row(s2, ok);
-        }
-        lds_dma16_untracked(reinterpret_cast<const char*>(kbase) + row * (int64_t)ksb + dcb[j],
-                            buf + (wave * T::IPW + j) * 512);
+      int s2 = tile * T::BN + dk[j];
+      s2 = s2 < L_blk ? s2 : L_blk - 1;
+      int64_t row = s2;
+      if constexpr (PAGED) {
+        bool ok;
+        row = phys_row(s2, ok);
       }
+      lds_dma16_untracked(reinterpret_cast<const char*>(kbase) + row * (int64_t)ksb + dcb[j],
+                          buf + (wave * T::IPW + j) * 512);
     }
+  };
+  auto dma = [&](int tile, uint16_t* buf) {
+#pragma unroll
+    for (int j = 0; j < T::IPW; ++j) dma_part(tile, buf, j);
   };
 #pragma unroll
   for (int j = 0; j < T::NBUF - 1; ++j) dma(j, kt[j]);
@@ -287,8 +285,10 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
     return *reinterpret_cast<const uint4*>(rp[kk % JN] + BUF * T::BN * D + sub * 32 * D + 8 * GS * (kk / JN));
   };
   // MFMAs of one k-chunk into `cur` with the B fragments `bf`; the epilogue of
-  // `prev` interleaved when `hp` (std::true_type / std::false_type)
-  auto chunk = [&](auto hp, f32x16(&cur)[MT], f32x16(&prev)[MT], const uint4 (&bf)[KC], int k0, float (&p4)[4]) {
+  // `prev` interleaved when `hp` (std::true_type / std::false_type); `hook` runs
+  // after the MFMAs of the chunk's second k-step
+  auto chunk = [&](auto hp, f32x16(&cur)[MT], f32x16(&prev)[MT], const uint4 (&bf)[KC], int k0, float (&p4)[4],
+                   auto&& hook) {
     constexpr bool has_prev = decltype(hp)::value;
     constexpr int EPK = (MT * 16 + KK - 1) / KK;   // epilogue elements per k-step
 #pragma unroll
@@ -313,6 +313,7 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
           if (e < MT * 16) p4[e & 3] += fmaxf(prev[e >> 4][e & 15], 0.f) * wv[e >> 4][e & 15];
         }
       }
+      if (j == 1) hook();
     }
   };
   auto drain = [&](f32x16(&prev)[MT], int key0, int slot) {
@@ -325,8 +326,11 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
   // One tile from LDS buffer BUF = t % 3 while tile t+1 has landed (or is
   // landing) in the next buffer and tile t+2 is being loaded into the third.
   // Right after the barrier a wave first requests its first B fragments, then
-  // writes the previous tile's scores and issues the loads of tile t+2, which
-  // all overlap the wait for the LDS reads.
+  // writes the previous tile's scores (overlapping the wait for the LDS reads).
+  // Its loads of tile t+2 are spread over the subtiles, load j after the second
+  // k-step of subtile j % NSUB: a direct-to-LDS load holds the wave's issue for
+  // tens of cycles, and issued together at the tile start they stopped both
+  // waves of a SIMD at the same time (about 1% of the kernel at C2).
   auto tile_body = [&](auto bufc, int t) {
     constexpr int BUF = decltype(bufc)::value;
     constexpr int NXT = (BUF + T::NBUF - 1) % T::NBUF;   // buffer of tile t+2: held tile t-1
@@ -335,7 +339,6 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
 #pragma unroll
       for (int j = 0; j < KC; ++j) bf[j] = bread(bufc, 0, j);
       flush();            // scores of tile t-1
-      dma(t + T::NBUF - 1, kt[NXT]);
       if constexpr (NSUB % 2 == 0) {
 #pragma unroll
         for (int sub = 0; sub < NSUB; ++sub) {
@@ -347,7 +350,12 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
             if (sub > 0 || k0 > 0)
 #pragma unroll
               for (int j = 0; j < KC; ++j) bf[j] = bread(bufc, sub, k0 + j);
-            chunk(std::true_type{}, cur, prev, bf, k0, p4);
+            chunk(std::true_type{}, cur, prev, bf, k0, p4, [&]() {
+              if (k0 == 0)
+#pragma unroll
+                for (int j = 0; j < T::IPW; ++j)
+                  if (j % NSUB == sub) dma_part(t + T::NBUF - 1, kt[NXT], j);
+            });
           }
           // sub 0 finishes the pending subtile of the previous tile (none at the
           // row's first tile: its zeroed accumulators give a slot that is not stored)
@@ -355,13 +363,14 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
         }
         pend_key0 = t * T::BN + (NSUB - 1) * 32;
       } else {
+        dma(t + T::NBUF - 1, kt[NXT]);
         float p4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int k0 = 0; k0 < KK; k0 += KC) {
           if (k0 > 0)
 #pragma unroll
             for (int j = 0; j < KC; ++j) bf[j] = bread(bufc, 0, k0 + j);
-          chunk(std::false_type{}, acc[0], acc[1], bf, k0, p4);
+          chunk(std::false_type{}, acc[0], acc[1], bf, k0, p4, []() {});
         }
         drain(acc[0], t * T::BN, 0);
       }
