@@ -45,6 +45,7 @@
 //  5. sfa_bwd_place_kernel -- copies each batch's staged rows to key rows
 //     key_start[b] + t and writes zeros to the key rows no batch covers.
 #include <climits>
+#include <type_traits>
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -335,29 +336,64 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
 
     // ---- S^T (waves 0, 1: halves of the [nope | rope] k-range) and dP^T (waves 2,
     // 3: halves of the nope range), tokens as M, heads as N
+    // The chain has a compile-time length per role, so it is unrolled with its
+    // operand reads four k-steps ahead (one wave per SIMD: nothing else covers a
+    // read that is issued just before its MFMA).
     {
-      const bool is_s = wave < 2;
-      const int nks = is_s ? C::KS_S / 2 : C::KS_P / 2;
-      const int ks0 = (wave & 1) * nks;
-      const uint16_t* arow = Ks + (lane & 31) * C::QP + (lane >> 5) * 8 + ks0 * 16;
-      const uint16_t* brow = (is_s ? Qs + (lane & 31) * C::QP : dOs + (lane & 31) * C::OP) + (lane >> 5) * 8 + ks0 * 16;
-      f32x16 sacc = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      for (int ks = 0; ks < nks; ++ks)
-        sacc = Mfma<IO>::m32(*reinterpret_cast<const uint4*>(arow + ks * 16),
-                             *reinterpret_cast<const uint4*>(brow + ks * 16), sacc);
+      auto chain = [&](auto nks_c, const uint16_t* arow, const uint16_t* brow) __attribute__((always_inline)) {
+        constexpr int NKS = decltype(nks_c)::value;
+        constexpr int AH = NKS < 4 ? NKS : 4;
+        uint4 ar[AH], br[AH];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) part[wave][i][lane] = sacc[i];
+        for (int i = 0; i < AH; ++i) {
+          ar[i] = *reinterpret_cast<const uint4*>(arow + i * 16);
+          br[i] = *reinterpret_cast<const uint4*>(brow + i * 16);
+        }
+        f32x16 sacc = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+          // pinned order (the scheduler would otherwise regroup the reads next to
+          // their MFMAs): the MFMA of step ks, then the reads of step ks + AH
+          __builtin_amdgcn_sched_barrier(0);
+          sacc = Mfma<IO>::m32(ar[ks % AH], br[ks % AH], sacc);
+          __builtin_amdgcn_sched_barrier(0);
+          if (ks + AH < NKS) {
+            ar[ks % AH] = *reinterpret_cast<const uint4*>(arow + (ks + AH) * 16);
+            br[ks % AH] = *reinterpret_cast<const uint4*>(brow + (ks + AH) * 16);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) part[wave][i][lane] = sacc[i];
+      };
+      const uint16_t* krow = Ks + (lane & 31) * C::QP + (lane >> 5) * 8;
+      if (wave < 2) {
+        constexpr int N = C::KS_S / 2;
+        chain(std::integral_constant<int, N>{}, krow + (wave & 1) * N * 16,
+              Qs + (lane & 31) * C::QP + (lane >> 5) * 8 + (wave & 1) * N * 16);
+      } else {
+        constexpr int N = C::KS_P / 2;
+        chain(std::integral_constant<int, N>{}, krow + (wave & 1) * N * 16,
+              dOs + (lane & 31) * C::OP + (lane >> 5) * 8 + (wave & 1) * N * 16);
+      }
     }
     lds_barrier();
 
     // ---- P and dS of the tile (fp32 -> io dtype): dS to LDS as [head][token] for
     // dQ, both to the dense buffers (a store group = 32 heads of one token)
+    float svs[4], dps[4];   // all partial sums requested first
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = wave * 4 + j;
+      svs[j] = part[0][i][lane] + part[1][i][lane];
+      dps[j] = part[2][i][lane] + part[3][i][lane];
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int i = wave * 4 + j;
       const int tk = m32_row(i, lane), h = lane & 31;
-      const float sv = part[0][i][lane] + part[1][i][lane];
-      const float dp = part[2][i][lane] + part[3][i][lane];
+      const float sv = svs[j];
+      const float dp = dps[j];
       float p = 0.f, ds = 0.f;
       if (tk < nv && h < hn) {
         p = __builtin_amdgcn_exp2f(sv * sl2 - s_m[h]) * s_il[h];
@@ -374,16 +410,26 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
     }
     lds_barrier();
 
-    // ---- dQ[head, col] += dS[head, token] K[token, col]   (this wave's column blocks)
+    // ---- dQ[head, col] += dS[head, token] K[token, col]   (this wave's column blocks;
+    // every operand of the phase is requested before its MFMAs)
+    {
+      uint4 av[BT / 16], bv[C::JQ][BT / 16];
 #pragma unroll
-    for (int jj = 0; jj < C::JQ; ++jj) {
-      const int j = wave + BWV * jj;
-      if (j < C::NBQ) {
+      for (int kq = 0; kq < BT / 16; ++kq)
+        av[kq] = *reinterpret_cast<const uint4*>(dSs + (lane & 31) * C::PP + kq * 16 + (lane >> 5) * 8);
 #pragma unroll
-        for (int kq = 0; kq < BT / 16; ++kq) {
-          const uint4 av = *reinterpret_cast<const uint4*>(dSs + (lane & 31) * C::PP + kq * 16 + (lane >> 5) * 8);
-          dq[jj] = Mfma<IO>::m32(av, tr_frag(Ks, C::QP, 32 * j, kq * 16, lane), dq[jj]);
-        }
+      for (int jj = 0; jj < C::JQ; ++jj) {
+        const int j = wave + BWV * jj;
+        if (j < C::NBQ)
+#pragma unroll
+          for (int kq = 0; kq < BT / 16; ++kq) bv[jj][kq] = tr_frag(Ks, C::QP, 32 * j, kq * 16, lane);
+      }
+#pragma unroll
+      for (int jj = 0; jj < C::JQ; ++jj) {
+        const int j = wave + BWV * jj;
+        if (j < C::NBQ)
+#pragma unroll
+          for (int kq = 0; kq < BT / 16; ++kq) dq[jj] = Mfma<IO>::m32(av[kq], bv[jj][kq], dq[jj]);
       }
     }
     lds_barrier();   // the next tile overwrites Ks, dSs and s_tok
