@@ -36,8 +36,10 @@
 //         [head][token];
 //       * dQ[head, col] += dS K, each wave owning a quarter of the 32-column
 //         blocks, the K operand read with ds_read_b64_tr_b16 from the tile;
-//  4. three library GEMMs per batch (hipBLASLt, bf16/fp16 in and out, fp32
-//     accumulation): [d_key | d_key_rope] = dS_T [q | q_rope] and d_value = P_T d_out
+//  4. two library GEMMs per batch (hipBLASLt, bf16/fp16 in and out, fp32
+//     accumulation): [d_key | d_key_rope] = dS_T [q | q_rope] (one product: the rows
+//     kernel writes [q | q_rope] to a concatenated workspace buffer as it loads it;
+//     a separate 64-column d_key_rope product took 0.10 ms) and d_value = P_T d_out,
 //     into a batch-contiguous staging area of the workspace (these are plain dense
 //     products, the kind of work a tuned library GEMM does best; measured 0.35 ms at
 //     the grad perf shape against 0.74 ms for the hand-written GEMM kernels they
@@ -95,8 +97,8 @@ __device__ __forceinline__ uint4 tr_frag(const uint16_t* X, int pitch, int c0, i
 struct BwdWs {
   int64_t* boff;   // [batch + 1] dense-buffer offsets (elements)
   int64_t* boffk;  // [batch + 1] staged-row offsets (prefix of nk)
-  uint16_t* sk;    // staged [sum nk, D]  d_key rows (io dtype)
-  uint16_t* skr;   // staged [sum nk, Dr] d_key_rope rows
+  uint16_t* skc;   // staged [sum nk, D + Dr] d_key | d_key_rope rows (io dtype)
+  uint16_t* qcat;  // [total_rows * N1, D + Dr] q | q_rope (written by the rows kernel)
   uint16_t* sv;    // staged [sum nk, D]  d_value rows
   void* lt_ws;     // LT_WS bytes for the library GEMMs
   uint16_t* dst;   // dS_T dense buffer (io dtype)
@@ -233,6 +235,7 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
       if (h < hn) {
         const int64_t hr = (int64_t)r * n1 + h0 + h;
         v = c < D ? ldg16(qb + hr * D + c) : ldg16(qrb + hr * BDR + (c - D));
+        stg16(w.qcat + hr * C::DT + c, v);   // the B operand of the [d_key | d_key_rope] product
       }
       *reinterpret_cast<uint4*>(&Qs[h * C::QP + c]) = v;
     }
@@ -490,10 +493,10 @@ __global__ __launch_bounds__(256) void sfa_bwd_place_kernel(SfaBwdArgs a, BwdWs 
     const int64_t sr = covered ? w.boffk[b] + t : 0;
     uint4 v = make_uint4(0, 0, 0, 0);
     if (u < UK) {
-      if (covered) v = ldg16(w.sk + sr * D + u * 8);
+      if (covered) v = ldg16(w.skc + sr * (D + BDR) + u * 8);
       stg16(reinterpret_cast<uint16_t*>(a.dk) + kr * D + u * 8, v);
     } else if (u < UK + UR) {
-      if (covered) v = ldg16(w.skr + sr * BDR + (u - UK) * 8);
+      if (covered) v = ldg16(w.skc + sr * (D + BDR) + D + (u - UK) * 8);
       stg16(reinterpret_cast<uint16_t*>(a.dkr) + kr * BDR + (u - UK) * 8, v);
     } else {
       if (covered) v = ldg16(w.sv + sr * D + (u - UK - UR) * 8);
@@ -673,12 +676,12 @@ HostGeo bwd_host_geo(int batch, const int32_t* h_row_start, const int32_t* h_act
 // Workspace: token lists | batch offsets | staged offsets | staged d_key, d_key_rope,
 // d_value rows | library-GEMM workspace | dS_T | P_T. Returns the offset of dS_T; the
 // two dense buffers share the rest equally.
-size_t bwd_fixed_bytes(int total_rows, int batch, int topk, int sbs, int64_t staged, int d) {
+size_t bwd_fixed_bytes(int total_rows, int batch, int topk, int sbs, int64_t staged, int d, int n1) {
   size_t off = align256(sfa_token_ws_bytes(total_rows > 0 ? total_rows : 1, topk, sbs));
   off += 2 * align256((size_t)(batch + 1) * 8);
+  off += align256((size_t)staged * (d + BDR) * 2);
   off += align256((size_t)staged * d * 2);
-  off += align256((size_t)staged * BDR * 2);
-  off += align256((size_t)staged * d * 2);
+  off += align256((size_t)(total_rows > 0 ? total_rows : 0) * n1 * (d + BDR) * 2);
   off += LT_WS;
   return off;
 }
@@ -690,7 +693,7 @@ size_t sfa_bwd_workspace_bytes(int batch, const int32_t* h_row_start, const int3
                                int total_rows, int n1, int d, int topk, int sbs, int64_t key_rows) {
   (void)key_rows;
   const dsa::HostGeo g = dsa::bwd_host_geo(batch, h_row_start, h_act_k, s2, n1);
-  return dsa::bwd_fixed_bytes(total_rows, batch, topk, sbs, g.staged, d) + 2 * dsa::align256((size_t)g.dense * 2);
+  return dsa::bwd_fixed_bytes(total_rows, batch, topk, sbs, g.staged, d, n1) + 2 * dsa::align256((size_t)g.dense * 2);
 }
 
 hipError_t launch_sfa_bwd(const SfaBwdArgs& a, hipStream_t s) {
@@ -706,12 +709,12 @@ hipError_t launch_sfa_bwd(const SfaBwdArgs& a, hipStream_t s) {
   off += dsa::align256((size_t)(f.batch + 1) * 8);
   w.boffk = reinterpret_cast<int64_t*>(base + off);
   off += dsa::align256((size_t)(f.batch + 1) * 8);
-  w.sk = reinterpret_cast<uint16_t*>(base + off);
-  off += dsa::align256((size_t)hg.staged * f.d * 2);
-  w.skr = reinterpret_cast<uint16_t*>(base + off);
-  off += dsa::align256((size_t)hg.staged * dsa::BDR * 2);
+  w.skc = reinterpret_cast<uint16_t*>(base + off);
+  off += dsa::align256((size_t)hg.staged * (f.d + dsa::BDR) * 2);
   w.sv = reinterpret_cast<uint16_t*>(base + off);
   off += dsa::align256((size_t)hg.staged * f.d * 2);
+  w.qcat = reinterpret_cast<uint16_t*>(base + off);
+  off += dsa::align256((size_t)(f.total_rows > 0 ? f.total_rows : 0) * f.n1 * (f.d + dsa::BDR) * 2);
   w.lt_ws = base + off;
   off += dsa::LT_WS;
   // the two dense buffers split what is left (256-byte aligned halves)
@@ -733,10 +736,8 @@ hipError_t launch_sfa_bwd(const SfaBwdArgs& a, hipStream_t s) {
   e = f.io == dsa::IO_BF16 ? dsa::launch_rows_io<dsa::IO_BF16>(a, tl, w, s)
                            : dsa::launch_rows_io<dsa::IO_F16>(a, tl, w, s);
   if (e != hipSuccess) return e;
-  // the three products of every batch holding query rows and key tokens
+  // the two products of every batch holding query rows and key tokens
   const hipDataType dt = f.io == dsa::IO_BF16 ? HIP_R_16BF : HIP_R_16F;
-  const uint16_t* q = reinterpret_cast<const uint16_t*>(f.q);
-  const uint16_t* qr = reinterpret_cast<const uint16_t*>(f.qr);
   const uint16_t* go = reinterpret_cast<const uint16_t*>(a.d_out);
   int64_t doff = 0, soff = 0;
   for (int b = 0; b < f.batch; ++b) {
@@ -746,9 +747,9 @@ hipError_t launch_sfa_bwd(const SfaBwdArgs& a, hipStream_t s) {
     const int k = nq * f.n1;
     if (nk > 0 && k > 0) {
       const int64_t brow = (int64_t)rs * f.n1;
-      if ((e = dsa::lt_gemm(dt, f.d, nk, k, q + brow * f.d, w.dst + doff, kp, w.sk + soff * f.d, w.lt_ws, s)) != hipSuccess ||
-          (e = dsa::lt_gemm(dt, dsa::BDR, nk, k, qr + brow * dsa::BDR, w.dst + doff, kp, w.skr + soff * dsa::BDR,
-                            w.lt_ws, s)) != hipSuccess ||
+      const int dt_w = f.d + dsa::BDR;
+      if ((e = dsa::lt_gemm(dt, dt_w, nk, k, w.qcat + brow * dt_w, w.dst + doff, kp, w.skc + soff * dt_w, w.lt_ws,
+                            s)) != hipSuccess ||
           (e = dsa::lt_gemm(dt, f.d, nk, k, go + brow * f.d, w.pt + doff, kp, w.sv + soff * f.d, w.lt_ws, s)) !=
               hipSuccess)
         return e;

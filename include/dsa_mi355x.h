@@ -199,10 +199,11 @@ int dsa_sfa_fwd_noalloc(const void* query, const void* query_rope, const void* k
                         int kv_splits, void* stream);
 
 /*
- * Workspace bytes for dsa_sfa_bwd: the token lists of total_rows rows, fp32
- * accumulators for d_key, d_key_rope and d_value over key_rows key rows, and two
- * dense io-dtype buffers of sum_b min(act_k[b], s2) * ceil64(rows_b * N1) elements
- * (rows_b = host_row_start[b+1] - host_row_start[b]). host_row_start [batch + 1] and
+ * Workspace bytes for dsa_sfa_bwd: the token lists of total_rows rows, a staging
+ * area of sum_b min(act_k[b], s2) rows of [d_key | d_key_rope | d_value] (io dtype),
+ * a [total_rows * N1, D + 64] copy of [query | query_rope], 128 MiB for the library
+ * GEMMs, and two dense io-dtype buffers of sum_b min(act_k[b], s2) * ceil64(rows_b *
+ * N1) elements (rows_b = host_row_start[b+1] - host_row_start[b]). host_row_start [batch + 1] and
  * host_act_k [batch] are host copies of the row offsets and kv lengths. Needs no
  * initialisation. No counterpart in the reference (it allocates its buffers per
  * call, sparse_flash_attention_grad_triton.py:634-642).
