@@ -25,16 +25,16 @@
 //     rows), so both passes select exactly the same tokens;
 //  2. sfa_bwd_geo_kernel -- per-batch offsets of the dense buffers; clears the
 //     fp32 accumulators and the used part of the dense buffers;
-//  3. sfa_bwd_rows_kernel -- one work-group (4 waves) per (query row, block of
-//     32 heads). Q | Q rope and dO of the block sit in LDS for the whole row; the
-//     row's tokens are processed in tiles of 32 gathered [D | Dr] rows:
+//  3. sfa_bwd_rows_kernel -- one work-group (8 waves, two per SIMD) per (query
+//     row, block of 32 heads). Q | Q rope and dO of the block sit in LDS for the
+//     whole row; the row's tokens are processed in tiles of 32 gathered [D | Dr] rows:
 //       * S^T = K Q^T and dP^T = K_nope dO^T on v_mfma_f32_32x32x16 (tokens as
-//         M, heads as N), their k-ranges split over the four waves and summed
-//         through LDS;
+//         M, heads as N), their k-ranges split in quarters over waves 0-3 (S^T)
+//         and 4-7 (dP^T) and summed through LDS;
 //       * P and dS in fp32, stored in the io dtype to the dense buffers (32
 //         consecutive heads of one token per store group) and dS also to LDS as
 //         [head][token];
-//       * dQ[head, col] += dS K, each wave owning a quarter of the 32-column
+//       * dQ[head, col] += dS K, each wave owning an eighth of the 32-column
 //         blocks, the K operand read with ds_read_b64_tr_b16 from the tile;
 //  4. two library GEMMs per batch (hipBLASLt, bf16/fp16 in and out, fp32
 //     accumulation): [d_key | d_key_rope] = dS_T [q | q_rope] (one product: the rows
@@ -62,7 +62,7 @@ namespace {
 constexpr int BDR = 64;     // rope width
 constexpr int BH = 32;      // heads per work-group (rows kernel)
 constexpr int BT = 32;      // tokens per tile
-constexpr int BWV = 4;      // waves per work-group
+constexpr int BWV = 8;      // waves per work-group (two per SIMD)
 constexpr float BLOG2E = 1.4426950408889634f;
 constexpr int GBK = 64;     // dense rows are padded to a multiple of 64 (row, head) pairs
 constexpr size_t LT_WS = (size_t)128 << 20;  // workspace offered to the library GEMMs
@@ -79,7 +79,8 @@ template <int D> struct BCfg {
   static constexpr int JQ = (NBQ + BWV - 1) / BWV;     // dQ blocks per wave, at most
   static constexpr int KS_S = DT / 16;                 // k-steps of S^T
   static constexpr int KS_P = D / 16;                  // of dP^T
-  static_assert(KS_S % 2 == 0 && KS_P % 2 == 0, "k-ranges split in halves");
+  static_assert(KS_S % 4 == 0 && KS_P % 4 == 0, "k-ranges split in quarters");
+  static constexpr int KCH = (BT * (DT / 8) + BWV * 64 - 1) / (BWV * 64);   // 16-byte gather chunks per thread
 };
 
 // MFMA 32x32x16 operand whose K runs down the rows of a row-major 16-bit LDS
@@ -198,7 +199,7 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
   __shared__ __attribute__((aligned(16))) uint16_t Ks[BT * C::QP];    // [token][nope | rope]
   __shared__ __attribute__((aligned(16))) uint16_t dOs[BH * C::OP];   // [head][D]
   __shared__ __attribute__((aligned(16))) uint16_t dSs[BH * C::PP];   // [head][token]
-  __shared__ float part[BWV][16][64];   // S^T / dP^T k-range partials, MFMA layout
+  __shared__ float part[BWV][16][64];   // S^T (waves 0-3) / dP^T (4-7) k-range partials, MFMA layout
   __shared__ int s_tok[BT];             // the tile's token index within the batch (-1: none)
   __shared__ int s_idr[4][BT];          // token-id ring: the ids of tile t in slot t % 4
   __shared__ float s_m[BH], s_il[BH], s_dl[BH];
@@ -263,7 +264,7 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
     dl += __shfl_xor(dl, 1);
     dl += __shfl_xor(dl, 2);
     dl += __shfl_xor(dl, 4);
-    if (part8 == 0) {
+    if (part8 == 0 && h < BH) {
       float m = 0.f, il = 0.f;
       if (h < hn) {
         const int64_t hr = (int64_t)r * n1 + h0 + h;
@@ -287,8 +288,8 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
   // ---- gathers of a tile's [nope | rope] rows into registers (rows outside the key
   // tensors and slots past the list are zero), two register sets: the next two
   // tiles' rows are in flight while one is computed
-  constexpr int KCH = BT * (C::DT / 8) / (BWV * 64);   // 16-byte chunks per thread
-  static_assert(KCH * BWV * 64 == BT * (C::DT / 8), "tile splits evenly");
+  constexpr int KCH = C::KCH;   // 16-byte chunks per thread (the last one on part of the threads)
+  constexpr int NCH = BT * (C::DT / 8);
   uint4 ka[KCH], kbr[KCH];
   int pa = -1, pb = -1;
   auto gather = [&](int t0, uint4 (&kreg)[KCH], int& ptok) __attribute__((always_inline)) {
@@ -298,7 +299,7 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
     for (int i = 0; i < KCH; ++i) {
       const int idx = tid + BWV * 64 * i;
       const int t = idx / (C::DT / 8), c = (idx % (C::DT / 8)) * 8;
-      const int p = t < nvt ? ids[t] : -1;
+      const int p = idx < NCH && t < nvt ? ids[t] : -1;
       uint4 v = z4;
       if ((uint32_t)p < (uint32_t)krows)
         v = c < D ? ldg16(kb + (int64_t)p * D + c) : ldg16(krb + (int64_t)p * BDR + (c - D));
@@ -327,7 +328,7 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
       const int idx = tid + BWV * 64 * i;
-      *reinterpret_cast<uint4*>(&Ks[(idx / (C::DT / 8)) * C::QP + (idx % (C::DT / 8)) * 8]) = kreg[i];
+      if (idx < NCH) *reinterpret_cast<uint4*>(&Ks[(idx / (C::DT / 8)) * C::QP + (idx % (C::DT / 8)) * 8]) = kreg[i];
     }
     if (tid < BT) {
       s_tok[tid] = ptok;
@@ -337,11 +338,10 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
     load_ids(t0 + 4 * BT);
     if (t0 + 2 * BT < ntok) gather(t0 + 2 * BT, kreg, ptok);
 
-    // ---- S^T (waves 0, 1: halves of the [nope | rope] k-range) and dP^T (waves 2,
-    // 3: halves of the nope range), tokens as M, heads as N
-    // The chain has a compile-time length per role, so it is unrolled with its
-    // operand reads four k-steps ahead (one wave per SIMD: nothing else covers a
-    // read that is issued just before its MFMA).
+    // ---- S^T (waves 0-3: quarters of the [nope | rope] k-range) and dP^T (waves
+    // 4-7: quarters of the nope range), tokens as M, heads as N. The chain has a
+    // compile-time length per role, so it is unrolled with its operand reads four
+    // k-steps ahead.
     {
       auto chain = [&](auto nks_c, const uint16_t* arow, const uint16_t* brow) __attribute__((always_inline)) {
         constexpr int NKS = decltype(nks_c)::value;
@@ -370,30 +370,31 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
         for (int i = 0; i < 16; ++i) part[wave][i][lane] = sacc[i];
       };
       const uint16_t* krow = Ks + (lane & 31) * C::QP + (lane >> 5) * 8;
-      if (wave < 2) {
-        constexpr int N = C::KS_S / 2;
-        chain(std::integral_constant<int, N>{}, krow + (wave & 1) * N * 16,
-              Qs + (lane & 31) * C::QP + (lane >> 5) * 8 + (wave & 1) * N * 16);
+      if (wave < 4) {
+        constexpr int N = C::KS_S / 4;
+        chain(std::integral_constant<int, N>{}, krow + (wave & 3) * N * 16,
+              Qs + (lane & 31) * C::QP + (lane >> 5) * 8 + (wave & 3) * N * 16);
       } else {
-        constexpr int N = C::KS_P / 2;
-        chain(std::integral_constant<int, N>{}, krow + (wave & 1) * N * 16,
-              dOs + (lane & 31) * C::OP + (lane >> 5) * 8 + (wave & 1) * N * 16);
+        constexpr int N = C::KS_P / 4;
+        chain(std::integral_constant<int, N>{}, krow + (wave & 3) * N * 16,
+              dOs + (lane & 31) * C::OP + (lane >> 5) * 8 + (wave & 3) * N * 16);
       }
     }
     lds_barrier();
 
     // ---- P and dS of the tile (fp32 -> io dtype): dS to LDS as [head][token] for
     // dQ, both to the dense buffers (a store group = 32 heads of one token)
-    float svs[4], dps[4];   // all partial sums requested first
+    constexpr int RPW = 16 / BWV;   // accumulator registers of the tile per wave
+    float svs[RPW], dps[RPW];   // all partial sums requested first
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int i = wave * 4 + j;
-      svs[j] = part[0][i][lane] + part[1][i][lane];
-      dps[j] = part[2][i][lane] + part[3][i][lane];
+    for (int j = 0; j < RPW; ++j) {
+      const int i = wave * RPW + j;
+      svs[j] = (part[0][i][lane] + part[1][i][lane]) + (part[2][i][lane] + part[3][i][lane]);
+      dps[j] = (part[4][i][lane] + part[5][i][lane]) + (part[6][i][lane] + part[7][i][lane]);
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int i = wave * 4 + j;
+    for (int j = 0; j < RPW; ++j) {
+      const int i = wave * RPW + j;
       const int tk = m32_row(i, lane), h = lane & 31;
       const float sv = svs[j];
       const float dp = dps[j];
