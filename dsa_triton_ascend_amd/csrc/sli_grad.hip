@@ -558,6 +558,326 @@ __global__ __launch_bounds__(256) void sli_student_kernel(SliArgs a) {
   }
 }
 
+// Wave-per-tile student for D_idx = 128, Nidx1 <= 32 MT and rows of at most
+// SLI_MAX_SLOTS slots. One work-group (4 waves) per row; wave w takes the 32-slot
+// tiles w, w + 4, ... of both sweeps, so no block barrier is needed per tile. Heads
+// are the MFMA M dimension (dots[head, slot] = qi ki^T, the row's qi fragments in
+// VGPRs): a lane holds 16 heads of one slot, and I = sum_g w[g] relu(dots) is an
+// in-lane sum plus one lane-half swap. A wave stages its tile's ki rows in a private
+// LDS tile (fetched one tile ahead into registers) and writes the tile's ds (hi and
+// lo parts, as in sli_student_kernel) to a private [slot][head] LDS tile; from there
+// dQI[head, col] += ds ki is accumulated in registers over the wave's tiles (the
+// four partials are added once per row, in wave order) and dKI[slot, col] = ds^T qi
+// is added at the slot's key row with fp32 atomics.
+template <int IO, int MT>
+__global__ __launch_bounds__(256) void sli_student_wt_kernel(SliArgs a) {
+  constexpr int DI = 128;
+  constexpr int GP = 32 * MT;          // heads, padded to whole blocks
+  constexpr int QIP = DI + 8;          // qi / ki row pitch: odd count of 16-byte units
+  constexpr int DSP = GP + 8;          // ds tile row pitch ([slot][head])
+  constexpr int KK = DI / 16;          // k-steps of the dots
+  constexpr int NCB = DI / 32;         // 32-column blocks of dQI / dKI
+  constexpr int NW = 4;                // waves
+  constexpr int LPW = SBT * (DI / 8) / 64;   // 16-byte ki chunks per lane per tile
+  static_assert(NW * SBT * QIP * 2 >= GP * DI * 4, "the dQI sum fits the ki tiles");
+  __shared__ __attribute__((aligned(16))) uint16_t QIs[GP * QIP];
+  __shared__ __attribute__((aligned(16))) uint16_t KIw[NW][SBT * QIP];
+  __shared__ __attribute__((aligned(16))) uint16_t dSw[NW][2][SBT * DSP];
+  __shared__ float s_i[SLI_MAX_SLOTS];   // I, then dI
+  __shared__ float s_w[GP];
+  __shared__ float s_st[NW][2];          // the waves' running max / sum of I
+  __shared__ float s_red[NW];
+  __shared__ float s_dw[NW][GP];
+  __shared__ int s_key[NW][SBT];         // key row of each slot of the wave's tile (-1: none)
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = blockIdx.x;
+  int b, s1;
+  const int n = row_slots(a, r, b, s1);
+  const int G = a.nidx1;
+  uint16_t* dqio = reinterpret_cast<uint16_t*>(a.dqi);
+  const int64_t qrow = (int64_t)r * G;
+  auto store_w = [&](int g, float v) {
+    if (a.wdt == DSA_DTYPE_F32) reinterpret_cast<float*>(a.dw)[qrow + g] = v;
+    else if (a.wdt == DSA_DTYPE_BF16) reinterpret_cast<uint16_t*>(a.dw)[qrow + g] = f32_to_bf16_rne(v);
+    else reinterpret_cast<uint16_t*>(a.dw)[qrow + g] = f32_to_f16_rne(v);
+  };
+  const bool lse_only = a.lse_max != nullptr;
+  if (lse_only && n == 0) {
+    if (tid == 0) { a.lse_max[r] = -INFINITY; a.lse_sum[r] = 0.f; }
+    return;
+  }
+  if (n == 0 || (a.isum && !(a.isum[r] > 0.f))) {
+    for (int i = tid; i < G * DI; i += 256) dqio[qrow * DI + i] = 0;
+    for (int g = tid; g < G; g += 256) store_w(g, 0.f);
+    if (tid == 0) a.row_loss[r] = 0.f;
+    return;
+  }
+  const uint16_t* qib = reinterpret_cast<const uint16_t*>(a.qi);
+  const uint16_t* kib = reinterpret_cast<const uint16_t*>(a.ki);
+  const uint4 z4 = make_uint4(0, 0, 0, 0);
+  // the qi block and weights (zero past Nidx1): to LDS for dKI, and the dots' A
+  // fragments (head 32 mt + lane % 32, k = 16 kk + 8 (lane / 32) ..) to VGPRs
+  for (int i = tid; i < GP * (DI / 8); i += 256) {
+    const int g = i / (DI / 8), c = (i % (DI / 8)) * 8;
+    *reinterpret_cast<uint4*>(&QIs[g * QIP + c]) = g < G ? ldg16(qib + (qrow + g) * DI + c) : z4;
+  }
+  for (int g = tid; g < GP; g += 256) s_w[g] = g < G ? ld_w(a.w, a.wdt, qrow + g) : 0.f;
+  uint4 qf[MT][KK];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      const int g = 32 * mt + (lane & 31);
+      qf[mt][kk] = g < G ? ldg16(qib + (qrow + g) * DI + kk * 16 + (lane >> 5) * 8) : z4;
+    }
+  __syncthreads();
+  float wv[MT][16];   // weight of head 32 mt + m32_row(e, lane)
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) wv[mt][e] = s_w[32 * mt + m32_row(e, lane)];
+  const int32_t* ids = a.sidx ? a.sidx + (int64_t)r * a.topk : nullptr;
+  const int ntiles = (n + SBT - 1) / SBT;
+  uint16_t* const kt = KIw[wave];
+  uint16_t* const dsh = dSw[wave][0];
+  uint16_t* const dsl = dSw[wave][1];
+
+  // ki rows of tile t: lane l holds chunks l + 64 j of the 32 x DI tile
+  uint4 stg[LPW];
+  int skey = -1;
+  auto fetch = [&](int t) {
+    const int t0 = t * SBT, nv = n - t0 < SBT ? n - t0 : SBT;
+#pragma unroll
+    for (int j = 0; j < LPW; ++j) {
+      const int i = lane + 64 * j;
+      const int row = i / (DI / 8), c = (i % (DI / 8)) * 8;
+      stg[j] = row < nv ? ldg16(kib + ((int64_t)b * a.s2 + slot_key(a, ids, t0 + row)) * DI + c) : z4;
+    }
+    if (lane < SBT) skey = lane < nv ? b * a.s2 + slot_key(a, ids, t0 + lane) : -1;
+  };
+  // this wave's reads of its previous tile are complete (LDS runs a wave's accesses in order)
+  auto commit = [&]() {
+#pragma unroll
+    for (int j = 0; j < LPW; ++j) {
+      const int i = lane + 64 * j;
+      *reinterpret_cast<uint4*>(&kt[(i / (DI / 8)) * QIP + (i % (DI / 8)) * 8]) = stg[j];
+    }
+    if (lane < SBT) s_key[wave][lane] = skey;
+  };
+  // dots of the tile in kt: acc[mt] element e -> head 32 mt + m32_row(e, lane), slot lane % 32
+  auto dots = [&](f32x16 (&acc)[MT]) {
+    uint4 bk[KK];
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+      bk[kk] = *reinterpret_cast<const uint4*>(kt + (lane & 31) * QIP + kk * 16 + (lane >> 5) * 8);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[mt][i] = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt] = Mfma<IO>::m32(qf[mt][kk], bk[kk], acc[mt]);
+  };
+  auto max32 = [](float v) {
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 32));
+    return v;
+  };
+  auto sum32 = [](float v) {
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) v += __shfl_xor(v, o, 32);
+    return v;
+  };
+
+  // ---- first sweep: I per slot, with this wave's running max / sum
+  float run_m = -INFINITY, run_l = 0.f;
+  if (wave < ntiles) fetch(wave);
+  for (int t = wave; t < ntiles; t += NW) {
+    commit();
+    if (t + NW < ntiles) fetch(t + NW);
+    f32x16 acc[MT];
+    dots(acc);
+    float p4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) p4[e & 3] += fmaxf(acc[mt][e], 0.f) * wv[mt][e];
+    const float iv = add_half_swap((p4[0] + p4[1]) + (p4[2] + p4[3]));   // slot lane % 32, both halves
+    const int t0 = t * SBT, nv = n - t0 < SBT ? n - t0 : SBT, slot = lane & 31;
+    const bool ok = slot < nv;
+    if (!lse_only && lane < 32 && ok) s_i[t0 + slot] = iv;
+    const float nm = fmaxf(run_m, max32(ok ? iv : -INFINITY));   // finite: the tile holds a slot
+    const float ex = sum32(ok ? expf(iv - nm) : 0.f);
+    run_l = run_l * expf(run_m - nm) + ex;   // the first tile: exp(-inf) = 0
+    run_m = nm;
+  }
+  if (lane == 0) {
+    s_st[wave][0] = run_m;
+    s_st[wave][1] = run_l;
+  }
+  auto block_sum = [&](float v) {
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    if (lane == 0) s_red[wave] = v;
+    __syncthreads();
+    const float t = s_red[0] + s_red[1] + s_red[2] + s_red[3];
+    __syncthreads();
+    return t;
+  };
+  __syncthreads();   // the waves' statistics and every I
+  float mx, inv;
+  if (a.isum) {
+    mx = a.imax[r];
+    inv = 1.f / fmaxf(a.isum[r], SEPS);
+  } else {
+    float m = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) m = fmaxf(m, s_st[w][0]);
+    float es = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+      if (s_st[w][0] > -INFINITY) es += s_st[w][1] * expf(s_st[w][0] - m);
+    mx = m;
+    if (lse_only) {
+      if (tid == 0) { a.lse_max[r] = mx; a.lse_sum[r] = es; }
+      return;
+    }
+    inv = ids ? 1.f / (es + SEPS) : 1.f / fmaxf(es, SEPS);
+  }
+  float ls = 0.f;
+  for (int k = tid; k < n; k += 256) {
+    const float sv = expf(s_i[k] - mx) * inv;
+    const float pv = a.p[(int64_t)r * a.topk + k];
+    const float pc = fmaxf(pv, SEPS), sc = fmaxf(sv, SEPS);
+    ls += pc * (logf(pc) - logf(sc));
+    s_i[k] = sv - pv;   // dI
+  }
+  const float row_loss = block_sum(ls);   // its barriers also publish every dI
+  if (tid == 0) a.row_loss[r] = row_loss;
+
+  // ---- second sweep
+  f32x16 dq[MT][NCB];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int j = 0; j < NCB; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) dq[mt][j][e] = 0.f;
+  float dwp[MT][16];   // dW of head 32 mt + m32_row(e, lane) over this lane's slots
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dwp[mt][e] = 0.f;
+  if (wave < ntiles) fetch(wave);
+  for (int t = wave; t < ntiles; t += NW) {
+    commit();
+    if (t + NW < ntiles) fetch(t + NW);
+    f32x16 acc[MT];
+    dots(acc);
+    const int t0 = t * SBT, nv = n - t0 < SBT ? n - t0 : SBT, slot = lane & 31;
+    const float di = slot < nv ? s_i[t0 + slot] : 0.f;
+    // ds = dI w [dots > 0] to the [slot][head] tile, hi and lo parts; elements
+    // 4q .. 4q + 3 are heads 32 mt + 8 q + 4 (lane / 32) + 0 .. 3 (one 8-byte store)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint16_t hi[4], lo[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int e = 4 * q + u;
+          const float x = acc[mt][e];
+          dwp[mt][e] += fmaxf(x, 0.f) * di;
+          const float dsv = x > 0.f ? di * wv[mt][e] : 0.f;
+          hi[u] = from_f32<IO>(dsv);
+          lo[u] = from_f32<IO>(dsv - to_f32<IO>(hi[u]));
+        }
+        const int col = 32 * mt + 8 * q + 4 * (lane >> 5);
+        *reinterpret_cast<uint2*>(dsh + slot * DSP + col) =
+            make_uint2(hi[0] | ((uint32_t)hi[1] << 16), hi[2] | ((uint32_t)hi[3] << 16));
+        *reinterpret_cast<uint2*>(dsl + slot * DSP + col) =
+            make_uint2(lo[0] | ((uint32_t)lo[1] << 16), lo[2] | ((uint32_t)lo[3] << 16));
+      }
+    // dQI[head, col] += ds[head, slot] ki[slot, col]
+#pragma unroll
+    for (int kq = 0; kq < SBT / 16; ++kq) {
+      uint4 ah[MT], al[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        ah[mt] = s_tr_frag(dsh, DSP, 32 * mt, kq * 16, lane);
+        al[mt] = s_tr_frag(dsl, DSP, 32 * mt, kq * 16, lane);
+      }
+#pragma unroll
+      for (int j = 0; j < NCB; ++j) {
+        const uint4 bv = s_tr_frag(kt, QIP, 32 * j, kq * 16, lane);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          dq[mt][j] = Mfma<IO>::m32(ah[mt], bv, dq[mt][j]);
+          dq[mt][j] = Mfma<IO>::m32(al[mt], bv, dq[mt][j]);
+        }
+      }
+    }
+    // dKI[slot, col] = sum_head ds[head, slot] qi[head, col], added at the slot's key row
+    f32x16 c[NCB];
+#pragma unroll
+    for (int j = 0; j < NCB; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) c[j][e] = 0.f;
+#pragma unroll
+    for (int kq = 0; kq < GP / 16; ++kq) {
+      const int off = (lane & 31) * DSP + kq * 16 + (lane >> 5) * 8;
+      const uint4 ah = *reinterpret_cast<const uint4*>(dsh + off);
+      const uint4 al = *reinterpret_cast<const uint4*>(dsl + off);
+#pragma unroll
+      for (int j = 0; j < NCB; ++j) {
+        const uint4 bv = s_tr_frag(QIs, QIP, 32 * j, kq * 16, lane);
+        c[j] = Mfma<IO>::m32(ah, bv, c[j]);
+        c[j] = Mfma<IO>::m32(al, bv, c[j]);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int kr = s_key[wave][m32_row(e, lane)];
+      if (kr >= 0) {
+        float* dst = a.dki_acc + (int64_t)kr * DI + (lane & 31);
+#pragma unroll
+        for (int j = 0; j < NCB; ++j) unsafeAtomicAdd(dst + 32 * j, c[j][e]);
+      }
+    }
+  }
+  // ---- dW: each head's sum over this wave's slots (the 32 lanes of its half), then
+  // over the waves
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float v = sum32(dwp[mt][e]);
+      if ((lane & 31) == 0) s_dw[wave][32 * mt + m32_row(e, lane)] = v;
+    }
+  // ---- dQI: the waves' partials added in wave order in LDS (the ki tiles are free)
+  float* const qacc = reinterpret_cast<float*>(&KIw[0][0]);   // [GP][DI]
+  __syncthreads();
+#pragma unroll 1
+  for (int w = 0; w < NW; ++w) {
+    if (wave == w) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int j = 0; j < NCB; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            float* p = qacc + (32 * mt + m32_row(e, lane)) * DI + 32 * j + (lane & 31);
+            *p = (w == 0 ? 0.f : *p) + dq[mt][j][e];
+          }
+    }
+    __syncthreads();
+  }
+  for (int i = tid; i < G * DI; i += 256) dqio[qrow * DI + i] = from_f32<IO>(qacc[i]);
+  for (int g = tid; g < G; g += 256) store_w(g, (s_dw[0][g] + s_dw[1][g]) + (s_dw[2][g] + s_dw[3][g]));
+}
+
 // dKI accumulator -> io dtype; the loss as the row-ordered sum of the row losses
 template <int IO>
 __global__ void sli_finish_kernel(SliArgs a, int64_t n4, int rows) {
@@ -600,6 +920,14 @@ void launch_student_big(const SliArgs& a, int rows, hipStream_t s) {
 
 template <int IO, int DI>
 void launch_student(const SliArgs& a, int rows, hipStream_t s) {
+  if constexpr (DI == 128) {
+    // D_idx = 128, Nidx1 <= 64, rows within SLI_MAX_SLOTS slots: the wave-per-tile form
+    if (a.nidx1 <= 64 && a.topk <= SLI_MAX_SLOTS) {
+      if (a.nidx1 <= 32) hipLaunchKernelGGL((sli_student_wt_kernel<IO, 1>), dim3(rows), dim3(256), 0, s, a);
+      else hipLaunchKernelGGL((sli_student_wt_kernel<IO, 2>), dim3(rows), dim3(256), 0, s, a);
+      return;
+    }
+  }
   if (a.topk > SLI_MAX_SLOTS && !a.lse_max) launch_student_big<IO, DI, true>(a, rows, s);
   else launch_student_big<IO, DI, false>(a, rows, s);
 }
