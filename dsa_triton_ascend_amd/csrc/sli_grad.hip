@@ -214,36 +214,89 @@ __global__ __launch_bounds__(NKT * 64) void sli_teacher_heads_kernel(SliArgs a) 
   f32x16 pacc;
 #pragma unroll
   for (int e = 0; e < 16; ++e) pacc[e] = 0.f;
-  for (int h = 0; h < a.n1; ++h) {
+  // Head h + 1's q rows (and key rows, when its key head changes) are loaded into
+  // registers while head h computes (PF: when they fit in 16 chunks per thread; wider
+  // rows load in place); LDS-only barriers, so the loads in flight are not drained by
+  // them (a full __syncthreads() would wait for them).
+  constexpr int QL = (32 * (DT / 8) + NT - 1) / NT, KL = (NKT * 32 * (DT / 8) + NT - 1) / NT;
+  constexpr bool PF = QL + KL <= 16;
+  uint4 qst[PF ? QL : 1], kst[PF ? KL : 1];
+  auto stage = [&](int h) {
     const int kvh = h / G, g = h - kvh * G;
-    __syncthreads();   // the previous head's MFMAs are done with Qs / Ks
-    for (int i = tid; i < 32 * (DT / 8); i += NT) {
+#pragma unroll
+    for (int j = 0; j < QL; ++j) {
+      const int i = tid + j * NT;
       const int rr = i / (DT / 8), c = (i % (DT / 8)) * 8;
       uint4 v = z4;
-      if (s0 + rr < a.s1) {
+      if (i < 32 * (DT / 8) && s0 + rr < a.s1) {
         const int64_t hr = ((int64_t)b * a.s1 + s0 + rr) * a.n1 + h;
         v = c < D ? ldg16(qb + hr * D + c) : ldg16(qrb + hr * a.dr + (c - D));
       }
-      *reinterpret_cast<uint4*>(&Qs[rr * QP + c]) = v;
+      qst[j] = v;
     }
-    if (g == 0) {
-      for (int i = tid; i < NKT * 32 * (DT / 8); i += NT) {
-        const int j = i / (DT / 8), c = (i % (DT / 8)) * 8;
+    if (g == 0)
+#pragma unroll
+      for (int j = 0; j < KL; ++j) {
+        const int i = tid + j * NT;
+        const int jr = i / (DT / 8), c = (i % (DT / 8)) * 8;
         uint4 v = z4;
-        if (t0 + j < a.s2) {
-          const int64_t kr = ((int64_t)b * a.s2 + t0 + j) * a.n2 + kvh;
+        if (i < NKT * 32 * (DT / 8) && t0 + jr < a.s2) {
+          const int64_t kr = ((int64_t)b * a.s2 + t0 + jr) * a.n2 + kvh;
           v = c < D ? ldg16(kb + kr * D + c) : ldg16(krb + kr * a.dr + (c - D));
         }
-        *reinterpret_cast<uint4*>(&Ks[j * QP + c]) = v;
+        kst[j] = v;
       }
+  };
+  if constexpr (PF) stage(0);
+  for (int h = 0; h < a.n1; ++h) {
+    const int kvh = h / G, g = h - kvh * G;
+    lds_barrier();   // the previous head's MFMAs are done with Qs / Ks
+    if constexpr (PF) {
+#pragma unroll
+      for (int j = 0; j < QL; ++j) {
+        const int i = tid + j * NT;
+        if (i < 32 * (DT / 8)) *reinterpret_cast<uint4*>(&Qs[(i / (DT / 8)) * QP + (i % (DT / 8)) * 8]) = qst[j];
+      }
+      if (g == 0)
+#pragma unroll
+        for (int j = 0; j < KL; ++j) {
+          const int i = tid + j * NT;
+          if (i < NKT * 32 * (DT / 8))
+            *reinterpret_cast<uint4*>(&Ks[(i / (DT / 8)) * QP + (i % (DT / 8)) * 8]) = kst[j];
+        }
+    } else {
+      for (int i = tid; i < 32 * (DT / 8); i += NT) {
+        const int rr = i / (DT / 8), c = (i % (DT / 8)) * 8;
+        uint4 v = z4;
+        if (s0 + rr < a.s1) {
+          const int64_t hr = ((int64_t)b * a.s1 + s0 + rr) * a.n1 + h;
+          v = c < D ? ldg16(qb + hr * D + c) : ldg16(qrb + hr * a.dr + (c - D));
+        }
+        *reinterpret_cast<uint4*>(&Qs[rr * QP + c]) = v;
+      }
+      if (g == 0)
+        for (int i = tid; i < NKT * 32 * (DT / 8); i += NT) {
+          const int j = i / (DT / 8), c = (i % (DT / 8)) * 8;
+          uint4 v = z4;
+          if (t0 + j < a.s2) {
+            const int64_t kr = ((int64_t)b * a.s2 + t0 + j) * a.n2 + kvh;
+            v = c < D ? ldg16(kb + kr * D + c) : ldg16(krb + kr * a.dr + (c - D));
+          }
+          *reinterpret_cast<uint4*>(&Ks[j * QP + c]) = v;
+        }
     }
+    // this head's statistics are requested before the next head's rows (loads retire
+    // in order, so waiting for them does not wait for the prefetch)
     float m = 0.f, il = 0.f;
     if (my_n > 0) {
       const int64_t si = (((int64_t)b * a.n2 + kvh) * a.s1 + my_s1) * G + g;
       m = a.sm_max[si] * SLOG2E;
-      il = 1.f / (a.sm_sum[si] + SEPS);
+      il = a.sm_sum[si];
     }
-    __syncthreads();
+    if constexpr (PF)
+      if (h + 1 < a.n1) stage(h + 1);
+    il = my_n > 0 ? 1.f / (il + SEPS) : 0.f;
+    lds_barrier();
     const uint16_t* arow = Ks + (wave * 32 + (lane & 31)) * QP + (lane >> 5) * 8;
     const uint16_t* brow = Qs + (lane & 31) * QP + (lane >> 5) * 8;
     f32x16 sc = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
