@@ -40,12 +40,14 @@
 //     accumulation): [d_key | d_key_rope] = dS_T [q | q_rope] (one product: the rows
 //     kernel writes [q | q_rope] to a concatenated workspace buffer as it loads it;
 //     a separate 64-column d_key_rope product took 0.10 ms) and d_value = P_T d_out,
-//     into a batch-contiguous staging area of the workspace (these are plain dense
-//     products, the kind of work a tuned library GEMM does best; measured 0.35 ms at
-//     the grad perf shape against 0.74 ms for the hand-written GEMM kernels they
-//     replaced);
-//  5. sfa_bwd_place_kernel -- copies each batch's staged rows to key rows
-//     key_start[b] + t and writes zeros to the key rows no batch covers.
+//     into a batch-contiguous staging area of the workspace, each as one
+//     strided-batched product over BSPLIT chunks of the contraction with fp32
+//     partials (the outputs alone have too few tiles to fill the GPU); these are
+//     plain dense products, the kind of work a tuned library GEMM does best
+//     (measured 0.35 ms at the grad perf shape against 0.74 ms for the hand-written
+//     GEMM kernels they replaced);
+//  5. sfa_bwd_place_kernel -- adds each batch's staged partials into key rows
+//     key_start[b] + t (io dtype) and writes zeros to the key rows no batch covers.
 #include <climits>
 #include <type_traits>
 #include <map>
@@ -67,6 +69,11 @@ constexpr float BLOG2E = 1.4426950408889634f;
 constexpr int GBK = 64;     // dense rows are padded to a multiple of 64 (row, head) pairs
 constexpr size_t LT_WS = (size_t)128 << 20;  // workspace offered to the library GEMMs
 constexpr int LT_CANDIDATES = 64;            // algorithms timed per product shape
+// Split of the products' contraction (the batch's (row, head) pairs): with M = key rows
+// and N = D + Dr or D the output has few tiles (about 64 - 144 at the grad perf shape for
+// 256 CUs), so the contraction is cut into BSPLIT chunks, run as one strided-batched
+// GEMM writing fp32 partials that the place kernel adds.
+constexpr int BSPLIT = 4;
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -98,9 +105,10 @@ __device__ __forceinline__ uint4 tr_frag(const uint16_t* X, int pitch, int c0, i
 struct BwdWs {
   int64_t* boff;   // [batch + 1] dense-buffer offsets (elements)
   int64_t* boffk;  // [batch + 1] staged-row offsets (prefix of nk)
-  uint16_t* skc;   // staged [sum nk, D + Dr] d_key | d_key_rope rows (io dtype)
+  float* skc;      // staged [split][sum nk, D + Dr] d_key | d_key_rope partials (fp32)
   uint16_t* qcat;  // [total_rows * N1, D + Dr] q | q_rope (written by the rows kernel)
-  uint16_t* sv;    // staged [sum nk, D]  d_value rows
+  float* sv;       // staged [split][sum nk, D] d_value partials (fp32)
+  int split;       // partials per staged row (1 or BSPLIT)
   void* lt_ws;     // LT_WS bytes for the library GEMMs
   uint16_t* dst;   // dS_T dense buffer (io dtype)
   uint16_t* pt;    // P_T dense buffer (io dtype)
@@ -475,7 +483,7 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
 // with key_start[b] <= kr), t = kr - key_start[b], takes staged row boffk[b] + t when
 // t < nk and the batch has query rows; every other key row is zero. One thread per 8
 // elements of the [D | Dr | D] row.
-template <int D>
+template <int IO, int D>
 __global__ __launch_bounds__(256) void sfa_bwd_place_kernel(SfaBwdArgs a, BwdWs w) {
   const SfaArgs& f = a.f;
   constexpr int UK = D / 8, UR = BDR / 8, U = 2 * UK + UR;   // 8-element units per key row
@@ -492,15 +500,27 @@ __global__ __launch_bounds__(256) void sfa_bwd_place_kernel(SfaBwdArgs a, BwdWs 
     const int64_t t = kr - f.key_start[b];
     const bool covered = t >= 0 && t < batch_nk(f.act_k[b], f.s2) && f.row_start[b + 1] > f.row_start[b];
     const int64_t sr = covered ? w.boffk[b] + t : 0;
+    const int64_t srows = w.boffk[f.batch];   // staged rows per partial
+    // the sum of the split's fp32 partials of 8 consecutive elements, in the io dtype
+    auto sum8 = [&](const float* p, int64_t pstride) {
+      float4 lo = make_float4(0.f, 0.f, 0.f, 0.f), hi = lo;
+      for (int c = 0; c < w.split; ++c) {
+        const float4 x = reinterpret_cast<const float4*>(p + c * pstride)[0];
+        const float4 y = reinterpret_cast<const float4*>(p + c * pstride)[1];
+        lo.x += x.x; lo.y += x.y; lo.z += x.z; lo.w += x.w;
+        hi.x += y.x; hi.y += y.y; hi.z += y.z; hi.w += y.w;
+      }
+      return make_uint4(pack2<IO>(lo.x, lo.y), pack2<IO>(lo.z, lo.w), pack2<IO>(hi.x, hi.y), pack2<IO>(hi.z, hi.w));
+    };
     uint4 v = make_uint4(0, 0, 0, 0);
     if (u < UK) {
-      if (covered) v = ldg16(w.skc + sr * (D + BDR) + u * 8);
+      if (covered) v = sum8(w.skc + sr * (D + BDR) + u * 8, srows * (D + BDR));
       stg16(reinterpret_cast<uint16_t*>(a.dk) + kr * D + u * 8, v);
     } else if (u < UK + UR) {
-      if (covered) v = ldg16(w.skc + sr * (D + BDR) + D + (u - UK) * 8);
+      if (covered) v = sum8(w.skc + sr * (D + BDR) + D + (u - UK) * 8, srows * (D + BDR));
       stg16(reinterpret_cast<uint16_t*>(a.dkr) + kr * BDR + (u - UK) * 8, v);
     } else {
-      if (covered) v = ldg16(w.sv + sr * D + (u - UK - UR) * 8);
+      if (covered) v = sum8(w.sv + sr * D + (u - UK - UR) * 8, srows * D);
       stg16(reinterpret_cast<uint16_t*>(a.dv) + kr * D + (u - UK - UR) * 8, v);
     }
   }
@@ -530,10 +550,20 @@ hipError_t launch_place(const SfaBwdArgs& a, const BwdWs& w, hipStream_t s) {
   const int64_t units = a.f.key_rows * (2 * a.f.d + BDR) / 8;
   if (units == 0) return hipSuccess;
   const int blocks = (int)((units + 255) / 256 < 8192 ? (units + 255) / 256 : 8192);
+  const bool bf = a.f.io == IO_BF16;
   switch (a.f.d) {
-    case 128: hipLaunchKernelGGL(sfa_bwd_place_kernel<128>, dim3(blocks), dim3(256), 0, s, a, w); break;
-    case 256: hipLaunchKernelGGL(sfa_bwd_place_kernel<256>, dim3(blocks), dim3(256), 0, s, a, w); break;
-    case 512: hipLaunchKernelGGL(sfa_bwd_place_kernel<512>, dim3(blocks), dim3(256), 0, s, a, w); break;
+    case 128:
+      if (bf) hipLaunchKernelGGL((sfa_bwd_place_kernel<IO_BF16, 128>), dim3(blocks), dim3(256), 0, s, a, w);
+      else hipLaunchKernelGGL((sfa_bwd_place_kernel<IO_F16, 128>), dim3(blocks), dim3(256), 0, s, a, w);
+      break;
+    case 256:
+      if (bf) hipLaunchKernelGGL((sfa_bwd_place_kernel<IO_BF16, 256>), dim3(blocks), dim3(256), 0, s, a, w);
+      else hipLaunchKernelGGL((sfa_bwd_place_kernel<IO_F16, 256>), dim3(blocks), dim3(256), 0, s, a, w);
+      break;
+    case 512:
+      if (bf) hipLaunchKernelGGL((sfa_bwd_place_kernel<IO_BF16, 512>), dim3(blocks), dim3(256), 0, s, a, w);
+      else hipLaunchKernelGGL((sfa_bwd_place_kernel<IO_F16, 512>), dim3(blocks), dim3(256), 0, s, a, w);
+      break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -549,15 +579,17 @@ hipError_t launch_place(const SfaBwdArgs& a, const BwdWs& w, hipStream_t s) {
 struct LtCache {
   std::mutex mu;
   std::map<int, hipblasLtHandle_t> handle;
-  std::map<std::tuple<int, int, int, int, int, int64_t>, hipblasLtMatmulAlgo_t> algo;
+  std::map<std::tuple<int, int, int, int, int, int64_t, int>, hipblasLtMatmulAlgo_t> algo;
 };
 LtCache& lt_cache() {
   static LtCache c;
   return c;
 }
 
-hipError_t lt_gemm(hipDataType dt, int n_cols, int nk, int k, const void* b_rows, const void* dense, int64_t kp,
-                   void* staged, void* ws, hipStream_t s) {
+// staged[c][t, col] = sum over j in chunk c of dense[t, j] b_rows[j, col] (fp32), for the
+// `split` equal chunks of the contraction k, as one strided-batched product.
+hipError_t lt_gemm(hipDataType dt, int n_cols, int nk, int k, int split, const void* b_rows, const void* dense,
+                   int64_t kp, float* staged, int64_t split_stride, void* ws, hipStream_t s) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return hipErrorInvalidDevice;
   LtCache& c = lt_cache();
@@ -584,12 +616,30 @@ hipError_t lt_gemm(hipDataType dt, int n_cols, int nk, int k, const void* b_rows
     if (hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_TRANSA, &op, sizeof(op)) != HIPBLAS_STATUS_SUCCESS ||
         hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_TRANSB, &op, sizeof(op)) != HIPBLAS_STATUS_SUCCESS)
       break;
-    if (hipblasLtMatrixLayoutCreate(&la, dt, n_cols, k, n_cols) != HIPBLAS_STATUS_SUCCESS ||
-        hipblasLtMatrixLayoutCreate(&lb, dt, k, nk, kp) != HIPBLAS_STATUS_SUCCESS ||
-        hipblasLtMatrixLayoutCreate(&lc, dt, n_cols, nk, n_cols) != HIPBLAS_STATUS_SUCCESS)
+    const int kc = k / split;
+    if (hipblasLtMatrixLayoutCreate(&la, dt, n_cols, kc, n_cols) != HIPBLAS_STATUS_SUCCESS ||
+        hipblasLtMatrixLayoutCreate(&lb, dt, kc, nk, kp) != HIPBLAS_STATUS_SUCCESS ||
+        hipblasLtMatrixLayoutCreate(&lc, HIP_R_32F, n_cols, nk, n_cols) != HIPBLAS_STATUS_SUCCESS)
       break;
+    if (split > 1) {
+      const int32_t bc = split;
+      const int64_t sa = (int64_t)kc * n_cols, sb = kc, sc = split_stride;
+      if (hipblasLtMatrixLayoutSetAttribute(la, HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &bc, sizeof(bc)) !=
+              HIPBLAS_STATUS_SUCCESS ||
+          hipblasLtMatrixLayoutSetAttribute(la, HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &sa, sizeof(sa)) !=
+              HIPBLAS_STATUS_SUCCESS ||
+          hipblasLtMatrixLayoutSetAttribute(lb, HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &bc, sizeof(bc)) !=
+              HIPBLAS_STATUS_SUCCESS ||
+          hipblasLtMatrixLayoutSetAttribute(lb, HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &sb, sizeof(sb)) !=
+              HIPBLAS_STATUS_SUCCESS ||
+          hipblasLtMatrixLayoutSetAttribute(lc, HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &bc, sizeof(bc)) !=
+              HIPBLAS_STATUS_SUCCESS ||
+          hipblasLtMatrixLayoutSetAttribute(lc, HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &sc, sizeof(sc)) !=
+              HIPBLAS_STATUS_SUCCESS)
+        break;
+    }
     hipblasLtMatmulAlgo_t algo;
-    const auto key = std::make_tuple(dev, (int)dt, n_cols, nk, k, kp);
+    const auto key = std::make_tuple(dev, (int)dt, n_cols, nk, k, kp, split);
     bool have = false;
     {
       std::lock_guard<std::mutex> g(c.mu);
@@ -680,8 +730,8 @@ HostGeo bwd_host_geo(int batch, const int32_t* h_row_start, const int32_t* h_act
 size_t bwd_fixed_bytes(int total_rows, int batch, int topk, int sbs, int64_t staged, int d, int n1) {
   size_t off = align256(sfa_token_ws_bytes(total_rows > 0 ? total_rows : 1, topk, sbs));
   off += 2 * align256((size_t)(batch + 1) * 8);
-  off += align256((size_t)staged * (d + BDR) * 2);
-  off += align256((size_t)staged * d * 2);
+  off += align256((size_t)BSPLIT * staged * (d + BDR) * 4);
+  off += align256((size_t)BSPLIT * staged * d * 4);
   off += align256((size_t)(total_rows > 0 ? total_rows : 0) * n1 * (d + BDR) * 2);
   off += LT_WS;
   return off;
@@ -710,10 +760,17 @@ hipError_t launch_sfa_bwd(const SfaBwdArgs& a, hipStream_t s) {
   off += dsa::align256((size_t)(f.batch + 1) * 8);
   w.boffk = reinterpret_cast<int64_t*>(base + off);
   off += dsa::align256((size_t)(f.batch + 1) * 8);
-  w.skc = reinterpret_cast<uint16_t*>(base + off);
-  off += dsa::align256((size_t)hg.staged * (f.d + dsa::BDR) * 2);
-  w.sv = reinterpret_cast<uint16_t*>(base + off);
-  off += dsa::align256((size_t)hg.staged * f.d * 2);
+  w.skc = reinterpret_cast<float*>(base + off);
+  off += dsa::align256((size_t)dsa::BSPLIT * hg.staged * (f.d + dsa::BDR) * 4);
+  w.sv = reinterpret_cast<float*>(base + off);
+  off += dsa::align256((size_t)dsa::BSPLIT * hg.staged * f.d * 4);
+  // the contraction split applies to every batch: each batch's (row, head) count is
+  // then a multiple of BSPLIT * 64 and large enough for the split to pay
+  w.split = dsa::BSPLIT;
+  for (int b = 0; b < f.batch; ++b) {
+    const int kb_ = (a.h_row_start[b + 1] - a.h_row_start[b]) * f.n1;
+    if (dsa::batch_nk(a.h_act_k[b], f.s2) > 0 && kb_ > 0 && (kb_ % (dsa::BSPLIT * 64) != 0 || kb_ < 4096)) w.split = 1;
+  }
   w.qcat = reinterpret_cast<uint16_t*>(base + off);
   off += dsa::align256((size_t)(f.total_rows > 0 ? f.total_rows : 0) * f.n1 * (f.d + dsa::BDR) * 2);
   w.lt_ws = base + off;
@@ -749,10 +806,10 @@ hipError_t launch_sfa_bwd(const SfaBwdArgs& a, hipStream_t s) {
     if (nk > 0 && k > 0) {
       const int64_t brow = (int64_t)rs * f.n1;
       const int dt_w = f.d + dsa::BDR;
-      if ((e = dsa::lt_gemm(dt, dt_w, nk, k, w.qcat + brow * dt_w, w.dst + doff, kp, w.skc + soff * dt_w, w.lt_ws,
-                            s)) != hipSuccess ||
-          (e = dsa::lt_gemm(dt, f.d, nk, k, go + brow * f.d, w.pt + doff, kp, w.sv + soff * f.d, w.lt_ws, s)) !=
-              hipSuccess)
+      if ((e = dsa::lt_gemm(dt, dt_w, nk, k, w.split, w.qcat + brow * dt_w, w.dst + doff, kp, w.skc + soff * dt_w,
+                            hg.staged * dt_w, w.lt_ws, s)) != hipSuccess ||
+          (e = dsa::lt_gemm(dt, f.d, nk, k, w.split, go + brow * f.d, w.pt + doff, kp, w.sv + soff * f.d,
+                            hg.staged * f.d, w.lt_ws, s)) != hipSuccess)
         return e;
     }
     doff += (int64_t)nk * kp;

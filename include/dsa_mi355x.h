@@ -200,7 +200,8 @@ int dsa_sfa_fwd_noalloc(const void* query, const void* query_rope, const void* k
 
 /*
  * Workspace bytes for dsa_sfa_bwd: the token lists of total_rows rows, a staging
- * area of sum_b min(act_k[b], s2) rows of [d_key | d_key_rope | d_value] (io dtype),
+ * area of 4 fp32 partials of sum_b min(act_k[b], s2) rows of [d_key | d_key_rope |
+ * d_value],
  * a [total_rows * N1, D + 64] copy of [query | query_rope], 128 MiB for the library
  * GEMMs, and two dense io-dtype buffers of sum_b min(act_k[b], s2) * ceil64(rows_b *
  * N1) elements (rows_b = host_row_start[b+1] - host_row_start[b]). host_row_start [batch + 1] and
