@@ -57,6 +57,7 @@ struct SliArgs {
   int n2;                              // key heads of the teacher, stats [B, N2, S1, N1 / N2]
   const float* imax; const float* isum; // given indexer softmax stats [rows], or nullptr
   float* lse_max; float* lse_sum;       // set: the student only writes the stats
+  int dki_km;      // dense mode: dKI from sli_dki_km_kernel (the student leaves dI in p)
 };
 
 
@@ -622,7 +623,7 @@ __global__ __launch_bounds__(256) void sli_student_kernel(SliArgs a) {
 // dQI[head, col] += ds ki is accumulated in registers over the wave's tiles (the
 // four partials are added once per row, in wave order) and dKI[slot, col] = ds^T qi
 // is added at the slot's key row with fp32 atomics.
-template <int IO, int MT>
+template <int IO, int MT, bool KM>
 __global__ __launch_bounds__(256) void sli_student_wt_kernel(SliArgs a) {
   constexpr int DI = 128;
   constexpr int GP = 32 * MT;          // heads, padded to whole blocks
@@ -806,6 +807,7 @@ __global__ __launch_bounds__(256) void sli_student_wt_kernel(SliArgs a) {
     const float pc = fmaxf(pv, SEPS), sc = fmaxf(sv, SEPS);
     ls += pc * (logf(pc) - logf(sc));
     s_i[k] = sv - pv;   // dI
+    if constexpr (KM) a.p[(int64_t)r * a.topk + k] = sv - pv;   // for the key-major dKI pass
   }
   const float row_loss = block_sum(ls);   // its barriers also publish every dI
   if (tid == 0) a.row_loss[r] = row_loss;
@@ -873,6 +875,8 @@ __global__ __launch_bounds__(256) void sli_student_wt_kernel(SliArgs a) {
       }
     }
     // dKI[slot, col] = sum_head ds[head, slot] qi[head, col], added at the slot's key row
+    // (KM: by the key-major pass instead)
+    if constexpr (!KM) {
     f32x16 c[NCB];
 #pragma unroll
     for (int j = 0; j < NCB; ++j)
@@ -898,6 +902,7 @@ __global__ __launch_bounds__(256) void sli_student_wt_kernel(SliArgs a) {
 #pragma unroll
         for (int j = 0; j < NCB; ++j) unsafeAtomicAdd(dst + 32 * j, c[j][e]);
       }
+    }
     }
   }
   // ---- dW: each head's sum over this wave's slots (the 32 lanes of its half), then
@@ -929,6 +934,155 @@ __global__ __launch_bounds__(256) void sli_student_wt_kernel(SliArgs a) {
   }
   for (int i = tid; i < G * DI; i += 256) dqio[qrow * DI + i] = from_f32<IO>(qacc[i]);
   for (int g = tid; g < G; g += 256) store_w(g, (s_dw[0][g] + s_dw[1][g]) + (s_dw[2][g] + s_dw[3][g]));
+}
+
+// Key-major dKI of the dense loss (slot t = key t): dKI[t, col] = sum over the rows r
+// that see key t and the heads g of ds[r, g, t] qi[r, g, col], ds = dI[r, t] w[r, g]
+// [qi[r, g] . ki[t] > 0] (dI left in p by the student). One work-group per (tile of
+// 128 keys, group of KM_RPG rows, batch); wave w owns keys 32w .. 32w + 31 of the tile
+// and keeps their ki fragments in registers. Per row the dots are recomputed with heads
+// as M (qi and w staged in LDS, double-buffered: the next row's arrive in registers
+// while this row computes); in that accumulator layout a lane holds 16 heads of one
+// key, and one v_permlane32_swap per register pair turns two groups of four heads into
+// the ds^T operand [key, 8 heads] of the dKI product, which accumulates in registers
+// over the group's rows. One fp32 atomic add per element and row group at the end.
+constexpr int KM_RPG = 32;   // rows per work-group
+template <int IO, int MT>
+__global__ __launch_bounds__(256) void sli_dki_km_kernel(SliArgs a) {
+  constexpr int DI = 128, GP = 32 * MT, QIP = DI + 8, KK = DI / 16, NCB = DI / 32;
+  constexpr int QL = GP * (DI / 8) / 256;   // 16-byte qi chunks per thread and row
+  __shared__ __attribute__((aligned(16))) uint16_t QIs[2][GP * QIP];
+  __shared__ __attribute__((aligned(16))) float Ws[2][GP];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int b = blockIdx.z;
+  const int k0 = blockIdx.x * 128 + 32 * wave;   // this wave's first key
+  const int key = k0 + (lane & 31);
+  const int G = a.nidx1;
+  const int aq = a.act_q[b], ak = a.act_k[b];
+  const int off = ak - aq + 1;                    // row s1 sees keys < min(s1 + off, S2)
+  // the rows of this group that see any key of the tile
+  int s_lo = blockIdx.y * KM_RPG, s_hi = s_lo + KM_RPG;
+  s_hi = s_hi < aq ? s_hi : aq;
+  s_hi = s_hi < a.s1 ? s_hi : a.s1;
+  const int first_vis = blockIdx.x * 128 - off + 1;   // smallest s1 with s1 + off > tile start
+  s_lo = s_lo > first_vis ? s_lo : first_vis;
+  if (s_lo >= s_hi) return;
+  const uint16_t* qib = reinterpret_cast<const uint16_t*>(a.qi);
+  const uint16_t* kib = reinterpret_cast<const uint16_t*>(a.ki);
+  const uint4 z4 = make_uint4(0, 0, 0, 0);
+  // ki fragments of this wave's keys (B of the dots: key lane % 32, k = 16 kk + 8 (lane / 32) ..)
+  uint4 bk[KK];
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk)
+    bk[kk] = key < a.s2 ? ldg16(kib + ((int64_t)b * a.s2 + key) * DI + kk * 16 + (lane >> 5) * 8) : z4;
+  uint4 qst[QL];
+  float wst = 0.f, dst_ = 0.f;
+  auto row_ok = [&](int s1) {
+    const int64_t r = (int64_t)b * a.s1 + s1;
+    return !(a.isum && !(a.isum[r] > 0.f));       // rows with an empty indexer softmax have no dI
+  };
+  auto stage = [&](int s1) {
+    const int64_t qrow = ((int64_t)b * a.s1 + s1) * G;
+#pragma unroll
+    for (int j = 0; j < QL; ++j) {
+      const int i = tid + 256 * j;
+      const int g = i / (DI / 8), c = (i % (DI / 8)) * 8;
+      qst[j] = g < G ? ldg16(qib + (qrow + g) * DI + c) : z4;
+    }
+    if (tid < GP) wst = tid < G ? ld_w(a.w, a.wdt, qrow + tid) : 0.f;
+    const int n = s1 + off < a.s2 ? s1 + off : a.s2;   // the row's keys
+    dst_ = key < n ? a.p[((int64_t)b * a.s1 + s1) * a.topk + key] : 0.f;
+  };
+  auto put = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < QL; ++j) {
+      const int i = tid + 256 * j;
+      *reinterpret_cast<uint4*>(&QIs[buf][(i / (DI / 8)) * QIP + (i % (DI / 8)) * 8]) = qst[j];
+    }
+    if (tid < GP) Ws[buf][tid] = wst;
+  };
+  f32x16 c[NCB];
+#pragma unroll
+  for (int j = 0; j < NCB; ++j)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) c[j][e] = 0.f;
+  stage(s_lo);
+  for (int s1 = s_lo; s1 < s_hi; ++s1) {
+    const int buf = (s1 - s_lo) & 1;
+    put(buf);
+    const float di = dst_;   // dI of this lane's key (0 past the row's keys)
+    if (s1 + 1 < s_hi) stage(s1 + 1);
+    lds_barrier();   // this row's qi and w (the other buffer is rewritten only after the next barrier)
+    if (!row_ok(s1)) continue;
+    const uint16_t* q = QIs[buf];
+    // dots[head, key]: element e of mt -> head 32 mt + m32_row(e, lane), key lane % 32
+    f32x16 acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[mt][e] = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const uint4 af = *reinterpret_cast<const uint4*>(q + (32 * mt + (lane & 31)) * QIP + kk * 16 + (lane >> 5) * 8);
+        acc[mt] = Mfma<IO>::m32(af, bk[kk], acc[mt]);
+      }
+    // ds in the io dtype (hi, and lo = the rounding error), packed four heads per
+    // register pair: group q of mt holds heads 32 mt + 8 q + 4 (lane / 32) + 0 .. 3
+    uint32_t hp[MT][4][2], lp[MT][4][2];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int qg = 0; qg < 4; ++qg) {
+        const float4 w4 = *reinterpret_cast<const float4*>(&Ws[buf][32 * mt + 8 * qg + 4 * (lane >> 5)]);
+        const float wq[4] = {w4.x, w4.y, w4.z, w4.w};
+        float dsv[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) dsv[u] = acc[mt][4 * qg + u] > 0.f ? di * wq[u] : 0.f;
+        uint16_t hi[4], lo[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          hi[u] = from_f32<IO>(dsv[u]);
+          lo[u] = from_f32<IO>(dsv[u] - to_f32<IO>(hi[u]));
+        }
+        hp[mt][qg][0] = hi[0] | ((uint32_t)hi[1] << 16);
+        hp[mt][qg][1] = hi[2] | ((uint32_t)hi[3] << 16);
+        lp[mt][qg][0] = lo[0] | ((uint32_t)lo[1] << 16);
+        lp[mt][qg][1] = lo[2] | ((uint32_t)lo[3] << 16);
+      }
+    // dKI[key, col] += sum over heads: k-step kq covers heads 16 kq .. 16 kq + 15 (groups
+    // 2 (kq % 2) and 2 (kq % 2) + 1 of mt = kq / 2); after the half swap lane l holds
+    // heads 16 kq + 8 (l / 32) + 0 .. 7 of key l % 32, the A operand
+#pragma unroll
+    for (int kq = 0; kq < GP / 16; ++kq) {
+      const int mt = kq / 2, g0 = 2 * (kq % 2);
+      uint32_t xh0 = hp[mt][g0][0], xh1 = hp[mt][g0][1], yh0 = hp[mt][g0 + 1][0], yh1 = hp[mt][g0 + 1][1];
+      uint32_t xl0 = lp[mt][g0][0], xl1 = lp[mt][g0][1], yl0 = lp[mt][g0 + 1][0], yl1 = lp[mt][g0 + 1][1];
+      swap_halves(xh0, yh0);
+      swap_halves(xh1, yh1);
+      swap_halves(xl0, yl0);
+      swap_halves(xl1, yl1);
+      const uint4 ah = make_uint4(xh0, xh1, yh0, yh1), al = make_uint4(xl0, xl1, yl0, yl1);
+#pragma unroll
+      for (int j = 0; j < NCB; ++j) {
+        const uint4 bv = s_tr_frag(q, QIP, 32 * j, kq * 16, lane);
+        c[j] = Mfma<IO>::m32(ah, bv, c[j]);
+        c[j] = Mfma<IO>::m32(al, bv, c[j]);
+      }
+    }
+  }
+  // element e of c[j]: key k0 + m32_row(e, lane), column 32 j + lane % 32
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int kt = k0 + m32_row(e, lane);
+    if (kt < a.s2) {
+      float* dst = a.dki_acc + ((int64_t)b * a.s2 + kt) * DI + (lane & 31);
+#pragma unroll
+      for (int j = 0; j < NCB; ++j) unsafeAtomicAdd(dst + 32 * j, c[j][e]);
+    }
+  }
 }
 
 // dKI accumulator -> io dtype; the loss as the row-ordered sum of the row losses
@@ -976,8 +1130,16 @@ void launch_student(const SliArgs& a, int rows, hipStream_t s) {
   if constexpr (DI == 128) {
     // D_idx = 128, Nidx1 <= 64, rows within SLI_MAX_SLOTS slots: the wave-per-tile form
     if (a.nidx1 <= 64 && a.topk <= SLI_MAX_SLOTS) {
-      if (a.nidx1 <= 32) hipLaunchKernelGGL((sli_student_wt_kernel<IO, 1>), dim3(rows), dim3(256), 0, s, a);
-      else hipLaunchKernelGGL((sli_student_wt_kernel<IO, 2>), dim3(rows), dim3(256), 0, s, a);
+      if (a.dki_km) {
+        if (a.nidx1 <= 32) hipLaunchKernelGGL((sli_student_wt_kernel<IO, 1, true>), dim3(rows), dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((sli_student_wt_kernel<IO, 2, true>), dim3(rows), dim3(256), 0, s, a);
+        const dim3 g((a.s2 + 127) / 128, (a.s1 + KM_RPG - 1) / KM_RPG, a.batch);
+        if (a.nidx1 <= 32) hipLaunchKernelGGL((sli_dki_km_kernel<IO, 1>), g, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((sli_dki_km_kernel<IO, 2>), g, dim3(256), 0, s, a);
+      } else {
+        if (a.nidx1 <= 32) hipLaunchKernelGGL((sli_student_wt_kernel<IO, 1, false>), dim3(rows), dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((sli_student_wt_kernel<IO, 2, false>), dim3(rows), dim3(256), 0, s, a);
+      }
       return;
     }
   }
@@ -1109,6 +1271,7 @@ hipError_t launch_dense_li_grad(const void* q, const void* k, const void* qr, co
   dsa::SliArgs a{q, k, qr, kr, qi, ki, w, io, wdt, nullptr, s2, sm_max, sm_sum, act_q, act_k,
                  batch, s1, s2, n1, d, dr, nidx1, didx, scale, dqi, dki, dw, loss,
                  nullptr, nullptr, nullptr, nullptr, nullptr, n2, max_index, sum_index, nullptr, nullptr};
+  a.dki_km = didx == 128 && nidx1 <= 64 && s2 <= dsa::SLI_MAX_SLOTS;
   return run_sli(a, ws, s);
 }
 
