@@ -88,6 +88,9 @@ template <int D> struct BCfg {
   static constexpr int KS_P = D / 16;                  // of dP^T
   static_assert(KS_S % 4 == 0 && KS_P % 4 == 0, "k-ranges split in quarters");
   static constexpr int KCH = (BT * (DT / 8) + BWV * 64 - 1) / (BWV * 64);   // 16-byte gather chunks per thread
+  // words of the selected-token bitmap (batches of up to 32 ZBW key tokens clear their
+  // dense slices in the rows kernel); D = 128 keeps two work-groups per CU
+  static constexpr int ZBW = D == 128 ? 2048 : 4096;
 };
 
 // MFMA 32x32x16 operand whose K runs down the rows of a row-major 16-bit LDS
@@ -113,6 +116,7 @@ struct BwdWs {
   uint16_t* dst;   // dS_T dense buffer (io dtype)
   uint16_t* pt;    // P_T dense buffer (io dtype)
   int64_t cap;     // elements per dense buffer
+  int zfuse;       // the rows kernel writes the zeros of the dense buffers (no clear kernels)
 };
 
 // Dense geometry of batch b: query rows [rs, rs + nq), key rows [ks, ks + nk)
@@ -211,6 +215,7 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
   __shared__ int s_tok[BT];             // the tile's token index within the batch (-1: none)
   __shared__ int s_idr[4][BT];          // token-id ring: the ids of tile t in slot t % 4
   __shared__ float s_m[BH], s_il[BH], s_dl[BH];
+  __shared__ uint32_t s_sel[C::ZBW];    // the batch tokens this row writes to the dense buffers
 
   const SfaArgs& f = a.f;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -232,6 +237,7 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
   const int rl = r - g.rs;
   const bool dense_ok = rl >= 0 && rl < g.nq && w.boff[b + 1] <= w.cap;
   const int64_t dbase = w.boff[b] + (int64_t)rl * n1 + h0;
+  const bool zf = w.zfuse && dense_ok;   // the host checked nk <= 32 ZBW and N1 % 8 == 0
 
   // ---- the block's Q | Q rope and dO (rows past the heads are zero), stats
   {
@@ -341,6 +347,7 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
     if (tid < BT) {
       s_tok[tid] = ptok;
       s_idr[(t0 / BT + 3) & 3][tid] = idreg;   // ids of tile t+3, loaded during tile t-1
+      if (zf && ptok >= 0) atomicOr(&s_sel[ptok >> 5], 1u << (ptok & 31));
     }
     lds_barrier();
     load_ids(t0 + 4 * BT);
@@ -446,6 +453,8 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
     }
     lds_barrier();   // the next tile overwrites Ks, dSs and s_tok
   };
+  if (zf)
+    for (int i = tid; i < (g.nk + 31) / 32; i += BWV * 64) s_sel[i] = 0;
   // prologue: the ids of tiles 0-2 straight to the ring, tile 3's into idreg
   if (tid < 3 * BT) s_idr[tid / BT][tid % BT] = tid < ntok ? toks[tid] : -1;
   load_ids(3 * BT);
@@ -475,6 +484,18 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
           else dqro[hr * BDR + (col - D)] = v;
         }
       }
+    }
+  }
+
+  // ---- zeros of this (row, head block)'s dense slice at the tokens it did not write
+  // (the last tile's barrier published every bit): 8 threads per token, 16 bytes of
+  // one buffer each; the slice is 16-byte aligned as N1 % 8 == 0 and kp % 64 == 0
+  if (zf) {
+    const int q = tid & 7;
+    if ((q & 3) * 8 < hn) {
+      uint16_t* zb = (q < 4 ? w.dst : w.pt) + dbase + (q & 3) * 8;
+      for (int t = tid >> 3; t < g.nk; t += BWV * 8)
+        if (!((s_sel[t >> 5] >> (t & 31)) & 1u)) stg16(zb + (int64_t)t * g.kp, z4);
     }
   }
 }
@@ -782,13 +803,24 @@ hipError_t launch_sfa_bwd(const SfaBwdArgs& a, hipStream_t s) {
   w.pt = reinterpret_cast<uint16_t*>(base + off + half);
   w.cap = (int64_t)(half / 2);
   if (hg.dense > w.cap) return hipErrorInvalidValue;   // the caller's workspace is checked against this size
+  // the rows kernel writes the zeros itself when every batch's tokens fit its bitmap
+  // and the (row, head block) slices are 16-byte aligned
+  int max_nk = 0;
+  for (int b = 0; b < f.batch; ++b) {
+    const int nk = dsa::batch_nk(a.h_act_k[b], f.s2);
+    max_nk = nk > max_nk ? nk : max_nk;
+  }
+  const int zbw = f.d == 128 ? dsa::BCfg<128>::ZBW : (f.d == 256 ? dsa::BCfg<256>::ZBW : dsa::BCfg<512>::ZBW);
+  w.zfuse = f.n1 % 8 == 0 && (int64_t)max_nk <= 32 * (int64_t)zbw;
 
   hipLaunchKernelGGL(dsa::sfa_bwd_geo_kernel, dim3(1), dim3(256), 0, s, f, w);
-  const int zb = 2048;
-  hipLaunchKernelGGL(dsa::sfa_bwd_zero_kernel, dim3(zb), dim3(256), 0, s, reinterpret_cast<uint4*>(w.dst),
-                     (int64_t)(half / 16), (const int64_t*)(w.boff + f.batch), w.cap);
-  hipLaunchKernelGGL(dsa::sfa_bwd_zero_kernel, dim3(zb), dim3(256), 0, s, reinterpret_cast<uint4*>(w.pt),
-                     (int64_t)(half / 16), (const int64_t*)(w.boff + f.batch), w.cap);
+  if (!w.zfuse) {
+    const int zb = 2048;
+    hipLaunchKernelGGL(dsa::sfa_bwd_zero_kernel, dim3(zb), dim3(256), 0, s, reinterpret_cast<uint4*>(w.dst),
+                       (int64_t)(half / 16), (const int64_t*)(w.boff + f.batch), w.cap);
+    hipLaunchKernelGGL(dsa::sfa_bwd_zero_kernel, dim3(zb), dim3(256), 0, s, reinterpret_cast<uint4*>(w.pt),
+                       (int64_t)(half / 16), (const int64_t*)(w.boff + f.batch), w.cap);
+  }
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   e = f.io == dsa::IO_BF16 ? dsa::launch_rows_io<dsa::IO_BF16>(a, tl, w, s)

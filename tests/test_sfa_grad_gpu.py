@@ -210,3 +210,31 @@ def test_grad_linear_in_d_out_at_perf_shape(dev):
         ref = a + b
         err = (ab - ref).abs().max().item()
         assert err <= 2e-2 * ref.abs().max().item() + 1e-3, f"{name}: linearity error {err}"
+
+
+@pytest.mark.parametrize("N1,D", [(16, 256), (8, 128), (4, 512)])
+def test_grad_poisoned_workspace(dev, N1, D):
+    """Every element of the dense dS^T / P^T buffers that the library products read is
+    written by the call itself (values at the selected tokens, zeros elsewhere, by the
+    rows kernel when N1 % 8 == 0, else by clear kernels): a workspace filled with NaN
+    bytes beforehand gives the same gradients bit for bit as a fresh one."""
+    from dsa_triton_ascend_amd.sparse_flash_attention_grad import GradPlan, INT64_MAX
+    B, S1, S2, count = 2, 8, 256, 64
+    q, k, v, qr, kr, do = _inputs(B, S1, S2, N1, D, "bf16", seed=11)
+    si = _ref_indices(B, S1, S2, count, 1, 3, seed=5)
+    scale = 1.0 / math.sqrt(D + 64)
+    g = lambda x: x.to(dev)
+    q, k, qr, kr, do, sit = g(q), g(k), g(qr), g(kr), g(do), g(torch.from_numpy(si))
+    out, smax, ssum = sparse_flash_attention(q, k, k, sit, scale_value=scale, query_rope=qr, key_rope=kr,
+                                             sparse_mode=3, return_softmax_lse=True)
+    plan = lambda: GradPlan(q, k, k, sit, do, out, smax, ssum, scale, qr, kr, None, None, 1, "BSND", 3,
+                            INT64_MAX, INT64_MAX, False)
+    clean = plan()
+    clean.ws.zero_()
+    want = [x.clone() for x in clean.run()]
+    dirty = plan()
+    dirty.ws.fill_(0xFF)
+    got = dirty.run()
+    torch.cuda.synchronize()
+    for name, a, b in zip(("dq", "dk", "dv", "dqr", "dkr"), got, want):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), f"N1={N1} D={D}: {name} differs"
