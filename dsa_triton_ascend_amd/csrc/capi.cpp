@@ -298,7 +298,8 @@ int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, cons
 
 size_t dsa_sli_grad_workspace_bytes(int batch, int s1, int s2, int sparse_count, int d_idx) {
   if (batch <= 0 || s1 < 0 || s2 <= 0 || sparse_count <= 0 || d_idx <= 0) return 0;
-  return sli_grad_workspace_bytes(batch * s1, sparse_count, (int64_t)batch * s2, d_idx);
+  return sli_grad_workspace_bytes(batch * s1, sparse_count, (int64_t)batch * s2, d_idx,
+                                  sli_km_sparse_ld(batch * s1, sparse_count, s2, d_idx));
 }
 
 int dsa_sli_grad_kl_loss(const void* query, const void* key, const void* query_rope, const void* key_rope,
@@ -326,7 +327,8 @@ int dsa_sli_grad_kl_loss(const void* query, const void* key, const void* query_r
                 d, dr, nidx1, d_idx, sparse_count);
   if (batch > 65535 || (int64_t)batch * s1 > INT32_MAX)
     return fail(DSA_ERR_UNSUPPORTED, "dsa_sli_grad_kl_loss: too many rows");
-  const size_t need = sli_grad_workspace_bytes(batch * s1, sparse_count, (int64_t)batch * s2, d_idx);
+  const size_t need = sli_grad_workspace_bytes(batch * s1, sparse_count, (int64_t)batch * s2, d_idx,
+                                               sli_km_sparse_ld(batch * s1, sparse_count, s2, d_idx));
   if (workspace_bytes < need)
     return fail(DSA_ERR_INVALID, "dsa_sli_grad_kl_loss: workspace of %zu bytes required, %zu given", need,
                 workspace_bytes);
@@ -341,7 +343,7 @@ int dsa_sli_grad_kl_loss(const void* query, const void* key, const void* query_r
 
 size_t dsa_dense_li_grad_workspace_bytes(int batch, int s1, int s2, int d_idx) {
   if (batch <= 0 || s1 < 0 || s2 <= 0 || d_idx <= 0) return 0;
-  return sli_grad_workspace_bytes(batch * s1, s2, (int64_t)batch * s2, d_idx);
+  return sli_grad_workspace_bytes(batch * s1, s2, (int64_t)batch * s2, d_idx, 0);
 }
 
 int dsa_dense_li_softmax_lse(const void* query_index, const void* key_index, const void* weights, int io_dtype,
@@ -392,7 +394,7 @@ int dsa_dense_li_grad_kl_loss(const void* query, const void* key, const void* qu
                 "{128,256,512}, Nidx1 <= 128", d, dr, n1, n2, nidx1, d_idx);
   if (batch > 65535 || (int64_t)batch * s1 > INT32_MAX)
     return fail(DSA_ERR_UNSUPPORTED, "dsa_dense_li_grad_kl_loss: too many rows");
-  const size_t need = sli_grad_workspace_bytes(batch * s1, s2, (int64_t)batch * s2, d_idx);
+  const size_t need = sli_grad_workspace_bytes(batch * s1, s2, (int64_t)batch * s2, d_idx, 0);
   if (workspace_bytes < need)
     return fail(DSA_ERR_INVALID, "dsa_dense_li_grad_kl_loss: workspace of %zu bytes required, %zu given", need,
                 workspace_bytes);

@@ -289,7 +289,9 @@ size_t sfa_bwd_workspace_bytes(int batch, const int32_t* h_row_start, const int3
 hipError_t launch_sfa_bwd(const SfaBwdArgs& a, hipStream_t s);
 
 // sparse lightning-indexer grad KL loss (BSND)
-size_t sli_grad_workspace_bytes(int rows, int topk, int64_t key_rows, int didx);
+// row stride of the sparse loss's per-key dI buffer (0: no key-major dKI pass)
+int sli_km_sparse_ld(int rows, int topk, int s2, int didx);
+size_t sli_grad_workspace_bytes(int rows, int topk, int64_t key_rows, int didx, int km_ld);
 bool sli_grad_supported(int d, int dr, int nidx1, int didx, int topk);
 hipError_t launch_sli_grad(const void* q, const void* k, const void* qr, const void* kr, const void* qi,
                            const void* ki, const void* w, int io, int wdt, const int32_t* sidx, int topk,

@@ -57,7 +57,9 @@ struct SliArgs {
   int n2;                              // key heads of the teacher, stats [B, N2, S1, N1 / N2]
   const float* imax; const float* isum; // given indexer softmax stats [rows], or nullptr
   float* lse_max; float* lse_sum;       // set: the student only writes the stats
-  int dki_km;      // dense mode: dKI from sli_dki_km_kernel (the student leaves dI in p)
+  int dki_km;      // dKI from sli_dki_km_kernel: the student leaves dI per key in dib
+  float* dib;      // [rows, dib_ld] dI per (row, key): p itself in dense mode, else a zeroed
+  int dib_ld;      // buffer the student adds each slot's dI into (repeated keys add)
 };
 
 
@@ -807,7 +809,10 @@ __global__ __launch_bounds__(256) void sli_student_wt_kernel(SliArgs a) {
     const float pc = fmaxf(pv, SEPS), sc = fmaxf(sv, SEPS);
     ls += pc * (logf(pc) - logf(sc));
     s_i[k] = sv - pv;   // dI
-    if constexpr (KM) a.p[(int64_t)r * a.topk + k] = sv - pv;   // for the key-major dKI pass
+    if constexpr (KM) {   // for the key-major dKI pass
+      if (ids) unsafeAtomicAdd(a.dib + (int64_t)r * a.dib_ld + slot_key(a, ids, k), sv - pv);
+      else a.p[(int64_t)r * a.topk + k] = sv - pv;
+    }
   }
   const float row_loss = block_sum(ls);   // its barriers also publish every dI
   if (tid == 0) a.row_loss[r] = row_loss;
@@ -936,9 +941,11 @@ __global__ __launch_bounds__(256) void sli_student_wt_kernel(SliArgs a) {
   for (int g = tid; g < G; g += 256) store_w(g, (s_dw[0][g] + s_dw[1][g]) + (s_dw[2][g] + s_dw[3][g]));
 }
 
-// Key-major dKI of the dense loss (slot t = key t): dKI[t, col] = sum over the rows r
-// that see key t and the heads g of ds[r, g, t] qi[r, g, col], ds = dI[r, t] w[r, g]
-// [qi[r, g] . ki[t] > 0] (dI left in p by the student). One work-group per (tile of
+// Key-major dKI: dKI[t, col] = sum over the rows r and heads g of ds[r, g, t] qi[r, g, col],
+// ds = dI[r, t] w[r, g] [qi[r, g] . ki[t] > 0], with dI[r, t] the student's dI summed over
+// the row's slots that hold key t (zero for keys the row does not use). In dense mode a row's
+// keys are t < min(s1 + act_k - act_q + 1, S2) (slot t = key t) and dI sits in p; in sparse
+// mode every key of the row is read from the dense buffer dib. One work-group per (tile of
 // 128 keys, group of KM_RPG rows, batch); wave w owns keys 32w .. 32w + 31 of the tile
 // and keeps their ki fragments in registers. Per row the dots are recomputed with heads
 // as M (qi and w staged in LDS, double-buffered: the next row's arrive in registers
@@ -965,8 +972,9 @@ __global__ __launch_bounds__(256) void sli_dki_km_kernel(SliArgs a) {
   int s_lo = blockIdx.y * KM_RPG, s_hi = s_lo + KM_RPG;
   s_hi = s_hi < aq ? s_hi : aq;
   s_hi = s_hi < a.s1 ? s_hi : a.s1;
+  const bool dense = a.sidx == nullptr;
   const int first_vis = blockIdx.x * 128 - off + 1;   // smallest s1 with s1 + off > tile start
-  s_lo = s_lo > first_vis ? s_lo : first_vis;
+  if (dense) s_lo = s_lo > first_vis ? s_lo : first_vis;
   if (s_lo >= s_hi) return;
   const uint16_t* qib = reinterpret_cast<const uint16_t*>(a.qi);
   const uint16_t* kib = reinterpret_cast<const uint16_t*>(a.ki);
@@ -991,8 +999,8 @@ __global__ __launch_bounds__(256) void sli_dki_km_kernel(SliArgs a) {
       qst[j] = g < G ? ldg16(qib + (qrow + g) * DI + c) : z4;
     }
     if (tid < GP) wst = tid < G ? ld_w(a.w, a.wdt, qrow + tid) : 0.f;
-    const int n = s1 + off < a.s2 ? s1 + off : a.s2;   // the row's keys
-    dst_ = key < n ? a.p[((int64_t)b * a.s1 + s1) * a.topk + key] : 0.f;
+    const int n = dense && s1 + off < a.s2 ? s1 + off : a.s2;   // the row's keys
+    dst_ = key < n ? a.dib[((int64_t)b * a.s1 + s1) * a.dib_ld + key] : 0.f;
   };
   auto put = [&](int buf) {
 #pragma unroll
@@ -1209,8 +1217,17 @@ hipError_t launch_sli_io(const SliArgs& a, hipStream_t s) {
 }  // namespace
 }  // namespace dsa
 
-size_t sli_grad_workspace_bytes(int rows, int topk, int64_t key_rows, int didx) {
+int sli_km_sparse_ld(int rows, int topk, int s2, int didx) {
+  // the key-major pass reads every key of a row: worth it while the rows use a large
+  // share of the keys (it replaces D_idx fp32 atomics per slot)
+  if (didx != 128 || topk > dsa::SLI_MAX_SLOTS || (int64_t)s2 > 4LL * topk) return 0;
+  if ((int64_t)rows * s2 * 4 > ((int64_t)512 << 20)) return 0;
+  return s2;
+}
+
+size_t sli_grad_workspace_bytes(int rows, int topk, int64_t key_rows, int didx, int km_ld) {
   return dsa::salign((size_t)rows * topk * 4) + dsa::salign((size_t)key_rows * didx * 4) +
+         dsa::salign((size_t)rows * km_ld * 4) +
          dsa::salign((size_t)rows * 4) + (topk > dsa::SLI_MAX_SLOTS ? dsa::salign((size_t)rows * topk * 4) : 0) +
          dsa::salign(sfa_token_ws_bytes(rows > 0 ? rows : 1, topk, 1));
 }
@@ -1223,17 +1240,27 @@ bool sli_grad_supported(int d, int dr, int nidx1, int didx, int topk) {
 }
 
 namespace {
-// workspace: teacher sums [rows, topk] | dKI accumulator [batch s2, didx] | row losses |
-// (rows of more than SLI_MAX_SLOTS slots) I / dI [rows, topk] | the teacher's token lists
-hipError_t run_sli(dsa::SliArgs a, void* ws, hipStream_t s) {
+// workspace: teacher sums [rows, topk] | dKI accumulator [batch s2, didx] | (sparse
+// key-major pass) dI per key [rows, km_ld] | row losses | (rows of more than SLI_MAX_SLOTS
+// slots) I / dI [rows, topk] | the teacher's token lists
+hipError_t run_sli(dsa::SliArgs a, void* ws, int km_ld, hipStream_t s) {
   const int rows = a.batch * a.s1;
   char* base = reinterpret_cast<char*>(ws);
   a.p = reinterpret_cast<float*>(base);
   size_t off = dsa::salign((size_t)rows * a.topk * 4);
   a.dki_acc = reinterpret_cast<float*>(base + off);
   off += dsa::salign((size_t)a.batch * a.s2 * a.didx * 4);
+  if (a.sidx) {
+    a.dib = reinterpret_cast<float*>(base + off);
+    a.dib_ld = km_ld;
+    off += dsa::salign((size_t)rows * km_ld * 4);
+    a.dki_km = km_ld > 0 && a.didx == 128 && a.nidx1 <= 64 && a.topk <= dsa::SLI_MAX_SLOTS;
+  } else {
+    a.dib = a.p;
+    a.dib_ld = a.topk;
+  }
   a.row_loss = reinterpret_cast<float*>(base + off);
-  // teacher sums and the dKI accumulator are contiguous up to the padding
+  // teacher sums, the dKI accumulator and the dI buffer are contiguous up to the padding
   const int64_t n4 = (int64_t)off / 16;
   size_t off2 = off + dsa::salign((size_t)rows * 4);
   a.ibuf = a.topk > dsa::SLI_MAX_SLOTS ? reinterpret_cast<float*>(base + off2) : nullptr;
@@ -1272,7 +1299,7 @@ hipError_t launch_dense_li_grad(const void* q, const void* k, const void* qr, co
                  batch, s1, s2, n1, d, dr, nidx1, didx, scale, dqi, dki, dw, loss,
                  nullptr, nullptr, nullptr, nullptr, nullptr, n2, max_index, sum_index, nullptr, nullptr};
   a.dki_km = didx == 128 && nidx1 <= 64 && s2 <= dsa::SLI_MAX_SLOTS;
-  return run_sli(a, ws, s);
+  return run_sli(a, ws, 0, s);
 }
 
 hipError_t launch_sli_grad(const void* q, const void* k, const void* qr, const void* kr, const void* qi,
@@ -1285,5 +1312,5 @@ hipError_t launch_sli_grad(const void* q, const void* k, const void* qr, const v
                  batch, s1, s2, n1, d, dr, nidx1, didx, scale, dqi, dki, dw, loss,
                  nullptr, nullptr, nullptr, nullptr, nullptr};
   a.n2 = 1;
-  return run_sli(a, ws, s);
+  return run_sli(a, ws, sli_km_sparse_ld(batch * s1, topk, s2, didx), s);
 }

@@ -217,3 +217,10 @@ def test_kl_loss_unsupported_shape_is_refused(dev):
         sparse_lightning_indexer_grad_kl_loss(q.to(dev), k.to(dev), qi.to(dev), ki.to(dev), w.to(dev), si.to(dev),
                                               sm.to(dev), sm.to(dev) + 1, query_rope=qr.to(dev),
                                               key_rope=kr.to(dev), scale_value=0.05)
+
+
+@pytest.mark.parametrize("pattern", ["random", "repeated"])
+def test_kl_loss_few_slots_per_key(dev, pattern):
+    """D_idx = 128 with S2 > 4 top-k: d_key_index by per-slot atomics in the student
+    (shorter lists take the key-major pass over a per-key dI buffer, as the other cases)."""
+    run(dev, 1, 4, 4096, 32, 512, 64, 128, 512, "bf16", pattern)
