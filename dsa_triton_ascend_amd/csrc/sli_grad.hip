@@ -700,6 +700,13 @@ __global__ __launch_bounds__(256) void sli_student_wt_kernel(SliArgs a) {
   uint16_t* const dsh = dSw[wave][0];
   uint16_t* const dsl = dSw[wave][1];
 
+  // sparse mode: the ids of the next tile to fetch (slot lane % 32), loaded one tile
+  // ahead so that a fetch never waits for an id load
+  int idn = 0;
+  auto load_ids = [&](int t) {
+    const int sl = t * SBT + (lane & 31);
+    if (ids) idn = sl < n ? ids[sl] : 0;
+  };
   // ki rows of tile t: lane l holds chunks l + 64 j of the 32 x DI tile
   uint4 stg[LPW];
   int skey = -1;
@@ -709,9 +716,23 @@ __global__ __launch_bounds__(256) void sli_student_wt_kernel(SliArgs a) {
     for (int j = 0; j < LPW; ++j) {
       const int i = lane + 64 * j;
       const int row = i / (DI / 8), c = (i % (DI / 8)) * 8;
-      stg[j] = row < nv ? ldg16(kib + ((int64_t)b * a.s2 + slot_key(a, ids, t0 + row)) * DI + c) : z4;
+      const int key = ids ? clip_id(__shfl(idn, row), a.s2) : t0 + row;
+      stg[j] = row < nv ? ldg16(kib + ((int64_t)b * a.s2 + key) * DI + c) : z4;
     }
-    if (lane < SBT) skey = lane < nv ? b * a.s2 + slot_key(a, ids, t0 + lane) : -1;
+    if (lane < SBT) skey = lane < nv ? b * a.s2 + (ids ? clip_id(idn, a.s2) : t0 + lane) : -1;
+  };
+  auto first_fetch = [&]() {
+    if (wave < ntiles) {
+      load_ids(wave);
+      fetch(wave);
+      load_ids(wave + NW);
+    }
+  };
+  auto next_fetch = [&](int t) {
+    if (t + NW < ntiles) {
+      fetch(t + NW);
+      load_ids(t + 2 * NW);
+    }
   };
   // this wave's reads of its previous tile are complete (LDS runs a wave's accesses in order)
   auto commit = [&]() {
@@ -750,10 +771,10 @@ __global__ __launch_bounds__(256) void sli_student_wt_kernel(SliArgs a) {
 
   // ---- first sweep: I per slot, with this wave's running max / sum
   float run_m = -INFINITY, run_l = 0.f;
-  if (wave < ntiles) fetch(wave);
+  first_fetch();
   for (int t = wave; t < ntiles; t += NW) {
     commit();
-    if (t + NW < ntiles) fetch(t + NW);
+    next_fetch(t);
     f32x16 acc[MT];
     dots(acc);
     float p4[4] = {0.f, 0.f, 0.f, 0.f};
@@ -830,14 +851,34 @@ __global__ __launch_bounds__(256) void sli_student_wt_kernel(SliArgs a) {
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int e = 0; e < 16; ++e) dwp[mt][e] = 0.f;
-  if (wave < ntiles) fetch(wave);
+  first_fetch();
   for (int t = wave; t < ntiles; t += NW) {
     commit();
-    if (t + NW < ntiles) fetch(t + NW);
+    next_fetch(t);
     f32x16 acc[MT];
     dots(acc);
     const int t0 = t * SBT, nv = n - t0 < SBT ? n - t0 : SBT, slot = lane & 31;
     const float di = slot < nv ? s_i[t0 + slot] : 0.f;
+    if constexpr (KM) {
+      // w factored out of dQI (applied once per row): the tile holds dI [dots > 0] as
+      // hi and lo parts of dI, so an element is a mask and two ANDs
+      const uint16_t dih = from_f32<IO>(di), dil = from_f32<IO>(di - to_f32<IO>(dih));
+      const uint32_t dih2 = dih * 0x10001u, dil2 = dil * 0x10001u;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          uint32_t mp[2];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) dwp[mt][4 * q + u] += fmaxf(acc[mt][4 * q + u], 0.f) * di;
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            mp[h] = (acc[mt][4 * q + 2 * h] > 0.f ? 0xFFFFu : 0u) | (acc[mt][4 * q + 2 * h + 1] > 0.f ? 0xFFFF0000u : 0u);
+          const int col = 32 * mt + 8 * q + 4 * (lane >> 5);
+          *reinterpret_cast<uint2*>(dsh + slot * DSP + col) = make_uint2(mp[0] & dih2, mp[1] & dih2);
+          *reinterpret_cast<uint2*>(dsl + slot * DSP + col) = make_uint2(mp[0] & dil2, mp[1] & dil2);
+        }
+    } else {
     // ds = dI w [dots > 0] to the [slot][head] tile, hi and lo parts; elements
     // 4q .. 4q + 3 are heads 32 mt + 8 q + 4 (lane / 32) + 0 .. 3 (one 8-byte store)
 #pragma unroll
@@ -860,6 +901,7 @@ __global__ __launch_bounds__(256) void sli_student_wt_kernel(SliArgs a) {
         *reinterpret_cast<uint2*>(dsl + slot * DSP + col) =
             make_uint2(lo[0] | ((uint32_t)lo[1] << 16), lo[2] | ((uint32_t)lo[3] << 16));
       }
+    }
     // dQI[head, col] += ds[head, slot] ki[slot, col]
 #pragma unroll
     for (int kq = 0; kq < SBT / 16; ++kq) {
@@ -932,7 +974,8 @@ __global__ __launch_bounds__(256) void sli_student_wt_kernel(SliArgs a) {
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             float* p = qacc + (32 * mt + m32_row(e, lane)) * DI + 32 * j + (lane & 31);
-            *p = (w == 0 ? 0.f : *p) + dq[mt][j][e];
+            const float v = KM ? dq[mt][j][e] * wv[mt][e] : dq[mt][j][e];   // KM: the factored w
+            *p = (w == 0 ? 0.f : *p) + v;
           }
     }
     __syncthreads();
@@ -986,11 +1029,9 @@ __global__ __launch_bounds__(256) void sli_dki_km_kernel(SliArgs a) {
     bk[kk] = key < a.s2 ? ldg16(kib + ((int64_t)b * a.s2 + key) * DI + kk * 16 + (lane >> 5) * 8) : z4;
   uint4 qst[QL];
   float wst = 0.f, dst_ = 0.f;
-  auto row_ok = [&](int s1) {
-    const int64_t r = (int64_t)b * a.s1 + s1;
-    return !(a.isum && !(a.isum[r] > 0.f));       // rows with an empty indexer softmax have no dI
-  };
+  bool okst = true;   // rows with an empty indexer softmax have no dI
   auto stage = [&](int s1) {
+    okst = !(a.isum && !(a.isum[(int64_t)b * a.s1 + s1] > 0.f));
     const int64_t qrow = ((int64_t)b * a.s1 + s1) * G;
 #pragma unroll
     for (int j = 0; j < QL; ++j) {
@@ -1020,9 +1061,10 @@ __global__ __launch_bounds__(256) void sli_dki_km_kernel(SliArgs a) {
     const int buf = (s1 - s_lo) & 1;
     put(buf);
     const float di = dst_;   // dI of this lane's key (0 past the row's keys)
+    const bool ok = __builtin_amdgcn_readfirstlane((int)okst) != 0;   // the same for every lane
     if (s1 + 1 < s_hi) stage(s1 + 1);
     lds_barrier();   // this row's qi and w (the other buffer is rewritten only after the next barrier)
-    if (!row_ok(s1)) continue;
+    if (!ok) continue;
     const uint16_t* q = QIs[buf];
     // dots[head, key]: element e of mt -> head 32 mt + m32_row(e, lane), key lane % 32
     f32x16 acc[MT];
