@@ -128,7 +128,23 @@ __device__ __forceinline__ int m32_row(int r, int lane) { return (r >> 2) * 8 + 
 __device__ __forceinline__ int m16_row(int r, int lane) { return (lane >> 4) * 4 + r; }
 
 // ------------------------------------------------------------------ misc
-__device__ __forceinline__ uint4 ldg16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+// 16-byte load from global memory, addressed as such: a generic pointer can make the
+// compiler emit flat loads (for instance where it turns `c ? load(p) : zero` into a
+// load from a selected address), and a flat load is counted by lgkmcnt as well, so
+// every later LDS wait would also wait for it.
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ldg16(const void* p) {
+  return __builtin_bit_cast(uint4, *(const __attribute__((address_space(1))) u32x4v*)p);
+}
+
+// c ? ldg16(p) : zeros. Written with a plain vector type on purpose: `c ? ldg16(p) : z`
+// with z a named uint4 (a class type) makes the compiler select between p and the
+// address of a zero copy in scratch and issue one flat load from the result.
+__device__ __forceinline__ uint4 ldg16_or0(bool c, const void* p) {
+  u32x4v v = {0u, 0u, 0u, 0u};
+  if (c) v = *(const __attribute__((address_space(1))) u32x4v*)p;
+  return __builtin_bit_cast(uint4, v);
+}
 
 // Work-group barrier that orders LDS accesses only. __syncthreads() is a
 // release/acquire fence on all address spaces, which makes every wave drain its

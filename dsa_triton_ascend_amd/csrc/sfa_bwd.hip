@@ -256,7 +256,7 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
     }
     for (int i = tid; i < BH * (D / 8); i += BWV * 64) {
       const int h = i / (D / 8), c = (i % (D / 8)) * 8;
-      const uint4 v = h < hn ? ldg16(gob + ((int64_t)r * n1 + h0 + h) * D + c) : z4;
+      const uint4 v = ldg16_or0(h < hn, gob + ((int64_t)r * n1 + h0 + h) * D + c);
       *reinterpret_cast<uint4*>(&dOs[h * C::OP + c]) = v;
     }
     // delta = dO . O (fp32) per head: 8 threads per head, D/8 columns each

@@ -394,7 +394,7 @@ __global__ __launch_bounds__(256) void sli_student_kernel(SliArgs a) {
   auto load_qi = [&](int hh) {
     for (int i = tid; i < GP * (DI / 8); i += 256) {
       const int g = i / (DI / 8), c = (i % (DI / 8)) * 8, gg = hh * GP + g;
-      *reinterpret_cast<uint4*>(&QIs[g * QIP + c]) = gg < G ? ldg16(qib + (qrow + gg) * DI + c) : z4;
+      *reinterpret_cast<uint4*>(&QIs[g * QIP + c]) = ldg16_or0(gg < G, qib + (qrow + gg) * DI + c);
     }
     for (int g = tid; g < GP; g += 256) s_w[g] = hh * GP + g < G ? ld_w(a.w, a.wdt, qrow + hh * GP + g) : 0.f;
   };
@@ -411,7 +411,7 @@ __global__ __launch_bounds__(256) void sli_student_kernel(SliArgs a) {
     for (int j = 0; j < LPT; ++j) {
       const int i = tid + j * 256;
       const int t = i / (DI / 8), c = (i % (DI / 8)) * 8;
-      stage[j] = t < nv ? ldg16(kib + ((int64_t)b * a.s2 + slot_key(a, ids, t0 + t)) * DI + c) : z4;
+      stage[j] = ldg16_or0(t < nv, kib + ((int64_t)b * a.s2 + slot_key(a, ids, t0 + (t < nv ? t : 0))) * DI + c);
     }
     if (tid < SBT) stok = tid < nv ? b * a.s2 + slot_key(a, ids, t0 + tid) : -1;
   };
@@ -639,7 +639,7 @@ __global__ __launch_bounds__(256) void sli_student_wt_kernel(SliArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t QIs[GP * QIP];
   __shared__ __attribute__((aligned(16))) uint16_t KIw[NW][SBT * QIP];
   __shared__ __attribute__((aligned(16))) uint16_t dSw[NW][2][SBT * DSP];
-  __shared__ float s_i[SLI_MAX_SLOTS];   // I, then dI
+  __shared__ __attribute__((aligned(16))) float s_i[SLI_MAX_SLOTS];   // I, then dI
   __shared__ float s_w[GP];
   __shared__ float s_st[NW][2];          // the waves' running max / sum of I
   __shared__ float s_red[NW];
@@ -677,7 +677,7 @@ __global__ __launch_bounds__(256) void sli_student_wt_kernel(SliArgs a) {
   // fragments (head 32 mt + lane % 32, k = 16 kk + 8 (lane / 32) ..) to VGPRs
   for (int i = tid; i < GP * (DI / 8); i += 256) {
     const int g = i / (DI / 8), c = (i % (DI / 8)) * 8;
-    *reinterpret_cast<uint4*>(&QIs[g * QIP + c]) = g < G ? ldg16(qib + (qrow + g) * DI + c) : z4;
+    *reinterpret_cast<uint4*>(&QIs[g * QIP + c]) = ldg16_or0(g < G, qib + (qrow + g) * DI + c);
   }
   for (int g = tid; g < GP; g += 256) s_w[g] = g < G ? ld_w(a.w, a.wdt, qrow + g) : 0.f;
   uint4 qf[MT][KK];
@@ -686,7 +686,7 @@ __global__ __launch_bounds__(256) void sli_student_wt_kernel(SliArgs a) {
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
       const int g = 32 * mt + (lane & 31);
-      qf[mt][kk] = g < G ? ldg16(qib + (qrow + g) * DI + kk * 16 + (lane >> 5) * 8) : z4;
+      qf[mt][kk] = ldg16_or0(g < G, qib + (qrow + g) * DI + kk * 16 + (lane >> 5) * 8);
     }
   __syncthreads();
   float wv[MT][16];   // weight of head 32 mt + m32_row(e, lane)
@@ -717,7 +717,7 @@ __global__ __launch_bounds__(256) void sli_student_wt_kernel(SliArgs a) {
       const int i = lane + 64 * j;
       const int row = i / (DI / 8), c = (i % (DI / 8)) * 8;
       const int key = ids ? clip_id(__shfl(idn, row), a.s2) : t0 + row;
-      stg[j] = row < nv ? ldg16(kib + ((int64_t)b * a.s2 + key) * DI + c) : z4;
+      stg[j] = ldg16_or0(row < nv, kib + ((int64_t)b * a.s2 + key) * DI + c);
     }
     if (lane < SBT) skey = lane < nv ? b * a.s2 + (ids ? clip_id(idn, a.s2) : t0 + lane) : -1;
   };
@@ -837,6 +837,24 @@ __global__ __launch_bounds__(256) void sli_student_wt_kernel(SliArgs a) {
   }
   const float row_loss = block_sum(ls);   // its barriers also publish every dI
   if (tid == 0) a.row_loss[r] = row_loss;
+  // KM: dI of slot pairs (2m, 2m + 1) as packed hi and lo parts in the io dtype (the
+  // ds tiles' LDS, unused in this mode), and dI = 0 past the row's slots up to the
+  // last tile's end
+  uint32_t* const s_dih = reinterpret_cast<uint32_t*>(&dSw[0][0][0]);
+  uint32_t* const s_dil = s_dih + SLI_MAX_SLOTS / 2;
+  if constexpr (KM) {
+    static_assert(sizeof(dSw) >= SLI_MAX_SLOTS * 4, "the dI pairs fit the ds tiles");
+    for (int m = tid; m < ntiles * (SBT / 2); m += 256) {
+      const float d0 = 2 * m < n ? s_i[2 * m] : 0.f, d1 = 2 * m + 1 < n ? s_i[2 * m + 1] : 0.f;
+      const uint16_t h0 = from_f32<IO>(d0), h1 = from_f32<IO>(d1);
+      const uint16_t l0 = from_f32<IO>(d0 - to_f32<IO>(h0)), l1 = from_f32<IO>(d1 - to_f32<IO>(h1));
+      s_dih[m] = h0 | ((uint32_t)h1 << 16);
+      s_dil[m] = l0 | ((uint32_t)l1 << 16);
+      if (2 * m >= n) s_i[2 * m] = 0.f;
+      if (2 * m + 1 >= n) s_i[2 * m + 1] = 0.f;
+    }
+    __syncthreads();
+  }
 
   // ---- second sweep
   f32x16 dq[MT][NCB];
@@ -846,11 +864,85 @@ __global__ __launch_bounds__(256) void sli_student_wt_kernel(SliArgs a) {
     for (int j = 0; j < NCB; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) dq[mt][j][e] = 0.f;
+  float dwh[MT] = {};   // KM: dW of head 32 mt + lane % 32 over this lane's slots
+  if constexpr (KM) {
+    // dots with slots as M (acc[mt] element e: slot m32_row(e, lane), head 32 mt +
+    // lane % 32). A lane then holds one head and four groups of four consecutive
+    // slots, so the dQI operand [head, 8 slots] of k-step kq is the masked dI pairs of
+    // groups 2 kq and 2 kq + 1 after one half swap per register pair: no LDS round
+    // trip for ds; w is applied to dQI once per row.
+    first_fetch();
+    for (int t = wave; t < ntiles; t += NW) {
+      commit();
+      next_fetch(t);
+      f32x16 acc[MT];
+      {
+        uint4 bk[KK];
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk)
+          bk[kk] = *reinterpret_cast<const uint4*>(kt + (lane & 31) * QIP + kk * 16 + (lane >> 5) * 8);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) acc[mt][i] = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) acc[mt] = Mfma<IO>::m32(bk[kk], qf[mt][kk], acc[mt]);
+      }
+      // group g of this lane: slots t0 + 8 g + 4 (lane / 32) + 0 .. 3
+      const int sb = t * SBT + 4 * (lane >> 5);
+      float dv[16];
+      uint32_t hp[8], lp[8];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 f = *reinterpret_cast<const float4*>(&s_i[sb + 8 * g]);
+        dv[4 * g] = f.x; dv[4 * g + 1] = f.y; dv[4 * g + 2] = f.z; dv[4 * g + 3] = f.w;
+        const uint2 h = *reinterpret_cast<const uint2*>(&s_dih[(sb + 8 * g) / 2]);
+        const uint2 l = *reinterpret_cast<const uint2*>(&s_dil[(sb + 8 * g) / 2]);
+        hp[2 * g] = h.x; hp[2 * g + 1] = h.y;
+        lp[2 * g] = l.x; lp[2 * g + 1] = l.y;
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        float dw = 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) dw += fmaxf(acc[mt][e], 0.f) * dv[e];
+        dwh[mt] += dw;
+#pragma unroll
+        for (int kq = 0; kq < SBT / 16; ++kq) {
+          uint32_t xh[2], yh[2], xl[2], yl[2];
+#pragma unroll
+          for (int pp = 0; pp < 2; ++pp) {
+            const int ex = 8 * kq + 2 * pp, ey = ex + 4;
+            const uint32_t mx = (acc[mt][ex] > 0.f ? 0xFFFFu : 0u) | (acc[mt][ex + 1] > 0.f ? 0xFFFF0000u : 0u);
+            const uint32_t my = (acc[mt][ey] > 0.f ? 0xFFFFu : 0u) | (acc[mt][ey + 1] > 0.f ? 0xFFFF0000u : 0u);
+            xh[pp] = mx & hp[4 * kq + pp];
+            xl[pp] = mx & lp[4 * kq + pp];
+            yh[pp] = my & hp[4 * kq + 2 + pp];
+            yl[pp] = my & lp[4 * kq + 2 + pp];
+          }
+          swap_halves(xh[0], yh[0]);
+          swap_halves(xh[1], yh[1]);
+          swap_halves(xl[0], yl[0]);
+          swap_halves(xl[1], yl[1]);
+          const uint4 ah = make_uint4(xh[0], xh[1], yh[0], yh[1]), al = make_uint4(xl[0], xl[1], yl[0], yl[1]);
+#pragma unroll
+          for (int j = 0; j < NCB; ++j) {
+            const uint4 bv = s_tr_frag(kt, QIP, 32 * j, kq * 16, lane);
+            dq[mt][j] = Mfma<IO>::m32(ah, bv, dq[mt][j]);
+            dq[mt][j] = Mfma<IO>::m32(al, bv, dq[mt][j]);
+          }
+        }
+      }
+    }
+  }
   float dwp[MT][16];   // dW of head 32 mt + m32_row(e, lane) over this lane's slots
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int e = 0; e < 16; ++e) dwp[mt][e] = 0.f;
+  if constexpr (!KM) {
   first_fetch();
   for (int t = wave; t < ntiles; t += NW) {
     commit();
@@ -859,26 +951,6 @@ __global__ __launch_bounds__(256) void sli_student_wt_kernel(SliArgs a) {
     dots(acc);
     const int t0 = t * SBT, nv = n - t0 < SBT ? n - t0 : SBT, slot = lane & 31;
     const float di = slot < nv ? s_i[t0 + slot] : 0.f;
-    if constexpr (KM) {
-      // w factored out of dQI (applied once per row): the tile holds dI [dots > 0] as
-      // hi and lo parts of dI, so an element is a mask and two ANDs
-      const uint16_t dih = from_f32<IO>(di), dil = from_f32<IO>(di - to_f32<IO>(dih));
-      const uint32_t dih2 = dih * 0x10001u, dil2 = dil * 0x10001u;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          uint32_t mp[2];
-#pragma unroll
-          for (int u = 0; u < 4; ++u) dwp[mt][4 * q + u] += fmaxf(acc[mt][4 * q + u], 0.f) * di;
-#pragma unroll
-          for (int h = 0; h < 2; ++h)
-            mp[h] = (acc[mt][4 * q + 2 * h] > 0.f ? 0xFFFFu : 0u) | (acc[mt][4 * q + 2 * h + 1] > 0.f ? 0xFFFF0000u : 0u);
-          const int col = 32 * mt + 8 * q + 4 * (lane >> 5);
-          *reinterpret_cast<uint2*>(dsh + slot * DSP + col) = make_uint2(mp[0] & dih2, mp[1] & dih2);
-          *reinterpret_cast<uint2*>(dsl + slot * DSP + col) = make_uint2(mp[0] & dil2, mp[1] & dil2);
-        }
-    } else {
     // ds = dI w [dots > 0] to the [slot][head] tile, hi and lo parts; elements
     // 4q .. 4q + 3 are heads 32 mt + 8 q + 4 (lane / 32) + 0 .. 3 (one 8-byte store)
 #pragma unroll
@@ -901,7 +973,6 @@ __global__ __launch_bounds__(256) void sli_student_wt_kernel(SliArgs a) {
         *reinterpret_cast<uint2*>(dsl + slot * DSP + col) =
             make_uint2(lo[0] | ((uint32_t)lo[1] << 16), lo[2] | ((uint32_t)lo[3] << 16));
       }
-    }
     // dQI[head, col] += ds[head, slot] ki[slot, col]
 #pragma unroll
     for (int kq = 0; kq < SBT / 16; ++kq) {
@@ -922,8 +993,6 @@ __global__ __launch_bounds__(256) void sli_student_wt_kernel(SliArgs a) {
       }
     }
     // dKI[slot, col] = sum_head ds[head, slot] qi[head, col], added at the slot's key row
-    // (KM: by the key-major pass instead)
-    if constexpr (!KM) {
     f32x16 c[NCB];
 #pragma unroll
     for (int j = 0; j < NCB; ++j)
@@ -950,10 +1019,17 @@ __global__ __launch_bounds__(256) void sli_student_wt_kernel(SliArgs a) {
         for (int j = 0; j < NCB; ++j) unsafeAtomicAdd(dst + 32 * j, c[j][e]);
       }
     }
-    }
   }
-  // ---- dW: each head's sum over this wave's slots (the 32 lanes of its half), then
-  // over the waves
+  }
+  // ---- dW: each head's sum over this wave's slots (KM: the two lane halves; else
+  // the 32 lanes of its half), then over the waves
+  if constexpr (KM) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const float v = dwh[mt] + __shfl_xor(dwh[mt], 32);
+      if (lane < 32) s_dw[wave][32 * mt + lane] = v;
+    }
+  } else {
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -961,6 +1037,7 @@ __global__ __launch_bounds__(256) void sli_student_wt_kernel(SliArgs a) {
       const float v = sum32(dwp[mt][e]);
       if ((lane & 31) == 0) s_dw[wave][32 * mt + m32_row(e, lane)] = v;
     }
+  }
   // ---- dQI: the waves' partials added in wave order in LDS (the ki tiles are free)
   float* const qacc = reinterpret_cast<float*>(&KIw[0][0]);   // [GP][DI]
   __syncthreads();
@@ -1026,7 +1103,7 @@ __global__ __launch_bounds__(256) void sli_dki_km_kernel(SliArgs a) {
   uint4 bk[KK];
 #pragma unroll
   for (int kk = 0; kk < KK; ++kk)
-    bk[kk] = key < a.s2 ? ldg16(kib + ((int64_t)b * a.s2 + key) * DI + kk * 16 + (lane >> 5) * 8) : z4;
+    bk[kk] = ldg16_or0(key < a.s2, kib + ((int64_t)b * a.s2 + key) * DI + kk * 16 + (lane >> 5) * 8);
   uint4 qst[QL];
   float wst = 0.f, dst_ = 0.f;
   bool okst = true;   // rows with an empty indexer softmax have no dI
@@ -1037,7 +1114,7 @@ __global__ __launch_bounds__(256) void sli_dki_km_kernel(SliArgs a) {
     for (int j = 0; j < QL; ++j) {
       const int i = tid + 256 * j;
       const int g = i / (DI / 8), c = (i % (DI / 8)) * 8;
-      qst[j] = g < G ? ldg16(qib + (qrow + g) * DI + c) : z4;
+      qst[j] = ldg16_or0(g < G, qib + (qrow + g) * DI + c);
     }
     if (tid < GP) wst = tid < G ? ld_w(a.w, a.wdt, qrow + tid) : 0.f;
     const int n = dense && s1 + off < a.s2 ? s1 + off : a.s2;   // the row's keys
