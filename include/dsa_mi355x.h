@@ -246,7 +246,9 @@ int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, cons
 
 /*
  * Workspace bytes for dsa_sli_grad_kl_loss: fp32 teacher sums [batch*s1, sparse_count],
- * an fp32 d_key_index accumulator [batch*s2, d_idx] and the row losses. Needs no
+ * an fp32 d_key_index accumulator [batch*s2, d_idx], for d_idx = 128 with s2 <= 4 *
+ * sparse_count an fp32 per-key dI buffer [batch*s1, s2] (at most 512 MiB; the key-major
+ * d_key_index pass), the row losses and the teacher's token lists. Needs no
  * initialisation. No counterpart in the reference (it allocates its buffers per call,
  * sparse_lightning_indexer_grad_kl_loss_triton.py:375-392).
  */
