@@ -1061,6 +1061,293 @@ __global__ __launch_bounds__(256) void sli_student_wt_kernel(SliArgs a) {
   for (int g = tid; g < G; g += 256) store_w(g, (s_dw[0][g] + s_dw[1][g]) + (s_dw[2][g] + s_dw[3][g]));
 }
 
+// Head-split student for the key-major mode and the softmax-LSE mode (D_idx = 128,
+// 32 < Nidx1 <= 64, rows of at most SLI_MAX_SLOTS slots). One work-group of 8 waves per
+// row: wave w takes heads 32 (w / 4) .. + 31 of the 32-slot tiles w % 4, w % 4 + 4, ...,
+// so each wave holds half the dQI accumulators of the four-wave form and two waves fit
+// on each SIMD. The two waves of a tile fetch half its ki rows each into a shared,
+// double-buffered LDS tile (one LDS barrier per tile step; every wave runs the same
+// number of steps). Sweep 1 leaves the two half sums of I per slot in LDS; the row's
+// max and sum of exp(I - max) come from block reductions afterwards. Sweep 2 takes
+// the dots with slots as M, as in the four-wave key-major form.
+template <int IO>
+__global__ __launch_bounds__(512) void sli_student_hs_kernel(SliArgs a) {
+  constexpr int DI = 128;
+  constexpr int QIP = DI + 8;          // ki row pitch: odd count of 16-byte units
+  constexpr int KK = DI / 16;          // k-steps of the dots
+  constexpr int NCB = DI / 32;         // 32-column blocks of dQI
+  constexpr int NW = 8, NP = 4;        // waves, tile streams
+  constexpr int LPW = SBT / 2 * (DI / 8) / 64;   // 16-byte ki chunks per lane (half a tile)
+  __shared__ __attribute__((aligned(16))) uint16_t KIw[NP][2][SBT * QIP];
+  __shared__ __attribute__((aligned(16))) float s_i[SLI_MAX_SLOTS];    // I (heads 0-31 part), then I, dI
+  __shared__ __attribute__((aligned(16))) float s_ip[SLI_MAX_SLOTS];   // I (heads 32-63 part)
+  __shared__ __attribute__((aligned(16))) uint32_t s_dih[SLI_MAX_SLOTS / 2], s_dil[SLI_MAX_SLOTS / 2];
+  __shared__ float s_red[NW];
+  __shared__ float s_dw[NP][64];
+  static_assert(sizeof(KIw) >= 64 * DI * 4, "the dQI sum fits the ki tiles");
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hh = wave >> 2, pi = wave & 3;   // head half, tile stream
+  const int r = blockIdx.x;
+  int b, s1;
+  const int n = row_slots(a, r, b, s1);
+  const int G = a.nidx1;
+  uint16_t* dqio = reinterpret_cast<uint16_t*>(a.dqi);
+  const int64_t qrow = (int64_t)r * G;
+  auto store_w = [&](int g, float v) {
+    if (a.wdt == DSA_DTYPE_F32) reinterpret_cast<float*>(a.dw)[qrow + g] = v;
+    else if (a.wdt == DSA_DTYPE_BF16) reinterpret_cast<uint16_t*>(a.dw)[qrow + g] = f32_to_bf16_rne(v);
+    else reinterpret_cast<uint16_t*>(a.dw)[qrow + g] = f32_to_f16_rne(v);
+  };
+  const bool lse_only = a.lse_max != nullptr;
+  if (lse_only && n == 0) {
+    if (tid == 0) { a.lse_max[r] = -INFINITY; a.lse_sum[r] = 0.f; }
+    return;
+  }
+  if (n == 0 || (a.isum && !(a.isum[r] > 0.f))) {
+    for (int i = tid; i < G * DI; i += 512) dqio[qrow * DI + i] = 0;
+    for (int g = tid; g < G; g += 512) store_w(g, 0.f);
+    if (tid == 0) a.row_loss[r] = 0.f;
+    return;
+  }
+  const uint16_t* qib = reinterpret_cast<const uint16_t*>(a.qi);
+  const uint16_t* kib = reinterpret_cast<const uint16_t*>(a.ki);
+  // this wave's heads: qi fragments (head 32 hh + lane % 32, k = 16 kk + 8 (lane / 32) ..)
+  // and the weight of head 32 hh + m32_row(e, lane)
+  const int gq = 32 * hh + (lane & 31);
+  uint4 qf[KK];
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk) qf[kk] = ldg16_or0(gq < G, qib + (qrow + gq) * DI + kk * 16 + (lane >> 5) * 8);
+  float wv[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int g = 32 * hh + m32_row(e, lane);
+    wv[e] = g < G ? ld_w(a.w, a.wdt, qrow + g) : 0.f;
+  }
+  const int32_t* ids = a.sidx ? a.sidx + (int64_t)r * a.topk : nullptr;
+  const int ntiles = (n + SBT - 1) / SBT;
+  const int nsteps = (ntiles + NP - 1) / NP;
+
+  // half hh of tile t: rows 16 hh .. 16 hh + 15; lane l holds chunks l + 64 j
+  int idn = 0;   // sparse mode: ids of the next tile to fetch (slot lane % 32), one tile ahead
+  auto load_ids = [&](int t) {
+    const int sl = t * SBT + (lane & 31);
+    if (ids) idn = sl < n ? ids[sl] : 0;
+  };
+  uint4 stg[LPW];
+  auto fetch = [&](int t) {
+    const int t0 = t * SBT, nv = n - t0 < SBT ? n - t0 : SBT;
+#pragma unroll
+    for (int j = 0; j < LPW; ++j) {
+      const int i = lane + 64 * j;
+      const int row = 16 * hh + i / (DI / 8), c = (i % (DI / 8)) * 8;
+      const int key = ids ? clip_id(__shfl(idn, row), a.s2) : t0 + row;
+      stg[j] = ldg16_or0(row < nv, kib + ((int64_t)b * a.s2 + key) * DI + c);
+    }
+  };
+  auto commit = [&](uint16_t* kt) {
+#pragma unroll
+    for (int j = 0; j < LPW; ++j) {
+      const int i = lane + 64 * j;
+      *reinterpret_cast<uint4*>(&kt[(16 * hh + i / (DI / 8)) * QIP + (i % (DI / 8)) * 8]) = stg[j];
+    }
+  };
+  auto first_fetch = [&]() {
+    if (pi < ntiles) {
+      load_ids(pi);
+      fetch(pi);
+      load_ids(pi + NP);
+    }
+  };
+  auto next_fetch = [&](int t) {
+    if (t + NP < ntiles) {
+      fetch(t + NP);
+      load_ids(t + 2 * NP);
+    }
+  };
+  auto bk_read = [&](const uint16_t* kt, uint4 (&bk)[KK]) {
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+      bk[kk] = *reinterpret_cast<const uint4*>(kt + (lane & 31) * QIP + kk * 16 + (lane >> 5) * 8);
+  };
+
+  // ---- first sweep: this wave's half of I per slot (heads as M: in-lane sums)
+  float* const s_ih = hh == 0 ? s_i : s_ip;
+  first_fetch();
+  for (int st = 0; st < nsteps; ++st) {
+    const int t = pi + NP * st;
+    uint16_t* const kt = KIw[pi][st & 1];
+    if (t < ntiles) commit(kt);
+    lds_barrier();   // both halves of the tile (the buffer's previous tile was read before the last barrier)
+    next_fetch(t);
+    if (t < ntiles) {
+      uint4 bk[KK];
+      bk_read(kt, bk);
+      f32x16 acc = {};
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) acc = Mfma<IO>::m32(qf[kk], bk[kk], acc);
+      float p4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int e = 0; e < 16; ++e) p4[e & 3] += fmaxf(acc[e], 0.f) * wv[e];
+      const float iv = add_half_swap((p4[0] + p4[1]) + (p4[2] + p4[3]));
+      const int t0 = t * SBT, slot = lane & 31;
+      if (lane < 32 && t0 + slot < n) s_ih[t0 + slot] = iv;
+    }
+  }
+  __syncthreads();
+  // I = both halves; the row's max and sum of exp(I - max)
+  auto block_red = [&](float v, bool is_max) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const float u = __shfl_xor(v, o);
+      v = is_max ? fmaxf(v, u) : v + u;
+    }
+    if (lane == 0) s_red[wave] = v;
+    __syncthreads();
+    float t = s_red[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) t = is_max ? fmaxf(t, s_red[w]) : t + s_red[w];
+    __syncthreads();
+    return t;
+  };
+  float lm = -INFINITY;
+  for (int k = tid; k < n; k += 512) {
+    const float iv = s_i[k] + s_ip[k];
+    s_i[k] = iv;
+    lm = fmaxf(lm, iv);
+  }
+  float mx, inv;
+  if (a.isum) {
+    mx = a.imax[r];
+    inv = 1.f / fmaxf(a.isum[r], SEPS);
+  } else {
+    mx = block_red(lm, true);   // its barriers also publish every I
+    float le = 0.f;
+    for (int k = tid; k < n; k += 512) le += expf(s_i[k] - mx);
+    const float es = block_red(le, false);
+    if (lse_only) {
+      if (tid == 0) { a.lse_max[r] = mx; a.lse_sum[r] = es; }
+      return;
+    }
+    inv = ids ? 1.f / (es + SEPS) : 1.f / fmaxf(es, SEPS);
+  }
+  // dI, the row's KL term, and dI per key for the key-major dKI pass
+  float ls = 0.f;
+  for (int k = tid; k < n; k += 512) {
+    const float sv = expf(s_i[k] - mx) * inv;
+    const float pv = a.p[(int64_t)r * a.topk + k];
+    const float pc = fmaxf(pv, SEPS), sc = fmaxf(sv, SEPS);
+    ls += pc * (logf(pc) - logf(sc));
+    s_i[k] = sv - pv;
+    if (ids) unsafeAtomicAdd(a.dib + (int64_t)r * a.dib_ld + slot_key(a, ids, k), sv - pv);
+    else a.p[(int64_t)r * a.topk + k] = sv - pv;
+  }
+  const float row_loss = block_red(ls, false);   // its barriers also publish every dI
+  if (tid == 0) a.row_loss[r] = row_loss;
+  // dI of slot pairs as packed hi / lo parts, and dI = 0 past the row's slots
+  for (int m = tid; m < ntiles * (SBT / 2); m += 512) {
+    const float d0 = 2 * m < n ? s_i[2 * m] : 0.f, d1 = 2 * m + 1 < n ? s_i[2 * m + 1] : 0.f;
+    const uint16_t h0 = from_f32<IO>(d0), h1 = from_f32<IO>(d1);
+    const uint16_t l0 = from_f32<IO>(d0 - to_f32<IO>(h0)), l1 = from_f32<IO>(d1 - to_f32<IO>(h1));
+    s_dih[m] = h0 | ((uint32_t)h1 << 16);
+    s_dil[m] = l0 | ((uint32_t)l1 << 16);
+    if (2 * m >= n) s_i[2 * m] = 0.f;
+    if (2 * m + 1 >= n) s_i[2 * m + 1] = 0.f;
+  }
+  __syncthreads();
+
+  // ---- second sweep: dots with slots as M (element e: slot m32_row(e, lane), head
+  // 32 hh + lane % 32); dQI[head, :] += (mask dI)[head, slots] ki[slots, :], the
+  // operand from the masked dI pairs after one half swap per register pair
+  f32x16 dq[NCB];
+#pragma unroll
+  for (int j = 0; j < NCB; ++j)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dq[j][e] = 0.f;
+  float dwh = 0.f;   // dW of head 32 hh + lane % 32 over this lane's slots
+  first_fetch();
+  for (int st = 0; st < nsteps; ++st) {
+    const int t = pi + NP * st;
+    uint16_t* const kt = KIw[pi][st & 1];
+    if (t < ntiles) commit(kt);
+    lds_barrier();
+    next_fetch(t);
+    if (t < ntiles) {
+      uint4 bk[KK];
+      bk_read(kt, bk);
+      f32x16 acc = {};
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) acc = Mfma<IO>::m32(bk[kk], qf[kk], acc);
+      const int sb = t * SBT + 4 * (lane >> 5);   // group g: slots sb + 8 g + 0 .. 3
+      float dv[16];
+      uint32_t hp[8], lp[8];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 f = *reinterpret_cast<const float4*>(&s_i[sb + 8 * g]);
+        dv[4 * g] = f.x; dv[4 * g + 1] = f.y; dv[4 * g + 2] = f.z; dv[4 * g + 3] = f.w;
+        const uint2 h = *reinterpret_cast<const uint2*>(&s_dih[(sb + 8 * g) / 2]);
+        const uint2 l = *reinterpret_cast<const uint2*>(&s_dil[(sb + 8 * g) / 2]);
+        hp[2 * g] = h.x; hp[2 * g + 1] = h.y;
+        lp[2 * g] = l.x; lp[2 * g + 1] = l.y;
+      }
+      float dw = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) dw += fmaxf(acc[e], 0.f) * dv[e];
+      dwh += dw;
+#pragma unroll
+      for (int kq = 0; kq < SBT / 16; ++kq) {
+        uint32_t xh[2], yh[2], xl[2], yl[2];
+#pragma unroll
+        for (int pp = 0; pp < 2; ++pp) {
+          const int ex = 8 * kq + 2 * pp, ey = ex + 4;
+          const uint32_t mx2 = (acc[ex] > 0.f ? 0xFFFFu : 0u) | (acc[ex + 1] > 0.f ? 0xFFFF0000u : 0u);
+          const uint32_t my2 = (acc[ey] > 0.f ? 0xFFFFu : 0u) | (acc[ey + 1] > 0.f ? 0xFFFF0000u : 0u);
+          xh[pp] = mx2 & hp[4 * kq + pp];
+          xl[pp] = mx2 & lp[4 * kq + pp];
+          yh[pp] = my2 & hp[4 * kq + 2 + pp];
+          yl[pp] = my2 & lp[4 * kq + 2 + pp];
+        }
+        swap_halves(xh[0], yh[0]);
+        swap_halves(xh[1], yh[1]);
+        swap_halves(xl[0], yl[0]);
+        swap_halves(xl[1], yl[1]);
+        const uint4 ah = make_uint4(xh[0], xh[1], yh[0], yh[1]), al = make_uint4(xl[0], xl[1], yl[0], yl[1]);
+#pragma unroll
+        for (int j = 0; j < NCB; ++j) {
+          const uint4 bv = s_tr_frag(kt, QIP, 32 * j, kq * 16, lane);
+          dq[j] = Mfma<IO>::m32(ah, bv, dq[j]);
+          dq[j] = Mfma<IO>::m32(al, bv, dq[j]);
+        }
+      }
+    }
+  }
+  // ---- dW per head over the tile streams; dQI (times the factored w) summed in stream
+  // order in LDS (the ki tiles are free)
+  {
+    const float v = dwh + __shfl_xor(dwh, 32);
+    if (lane < 32) s_dw[pi][32 * hh + lane] = v;
+  }
+  float* const qacc = reinterpret_cast<float*>(&KIw[0][0][0]);   // [64][DI]
+  __syncthreads();
+#pragma unroll 1
+  for (int p = 0; p < NP; ++p) {
+    if (pi == p) {
+#pragma unroll
+      for (int j = 0; j < NCB; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          float* q = qacc + (32 * hh + m32_row(e, lane)) * DI + 32 * j + (lane & 31);
+          const float v = dq[j][e] * wv[e];
+          *q = (p == 0 ? 0.f : *q) + v;
+        }
+    }
+    __syncthreads();
+  }
+  for (int i = tid; i < G * DI; i += 512) dqio[qrow * DI + i] = from_f32<IO>(qacc[i]);
+  for (int g = tid; g < G; g += 512) store_w(g, (s_dw[0][g] + s_dw[1][g]) + (s_dw[2][g] + s_dw[3][g]));
+}
+
 // Key-major dKI: dKI[t, col] = sum over the rows r and heads g of ds[r, g, t] qi[r, g, col],
 // ds = dI[r, t] w[r, g] [qi[r, g] . ki[t] > 0], with dI[r, t] the student's dI summed over
 // the row's slots that hold key t (zero for keys the row does not use). In dense mode a row's
@@ -1257,6 +1544,15 @@ void launch_student(const SliArgs& a, int rows, hipStream_t s) {
   if constexpr (DI == 128) {
     // D_idx = 128, Nidx1 <= 64, rows within SLI_MAX_SLOTS slots: the wave-per-tile form
     if (a.nidx1 <= 64 && a.topk <= SLI_MAX_SLOTS) {
+      if (a.nidx1 > 32 && (a.dki_km || a.lse_max)) {
+        // 33 - 64 heads: the eight-wave head-split form (stats only, or dKI left to the key-major pass)
+        hipLaunchKernelGGL((sli_student_hs_kernel<IO>), dim3(rows), dim3(512), 0, s, a);
+        if (a.dki_km) {
+          const dim3 g((a.s2 + 127) / 128, (a.s1 + KM_RPG - 1) / KM_RPG, a.batch);
+          hipLaunchKernelGGL((sli_dki_km_kernel<IO, 2>), g, dim3(256), 0, s, a);
+        }
+        return;
+      }
       if (a.dki_km) {
         if (a.nidx1 <= 32) hipLaunchKernelGGL((sli_student_wt_kernel<IO, 1, true>), dim3(rows), dim3(256), 0, s, a);
         else hipLaunchKernelGGL((sli_student_wt_kernel<IO, 2, true>), dim3(rows), dim3(256), 0, s, a);
