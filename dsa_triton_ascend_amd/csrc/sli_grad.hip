@@ -190,9 +190,16 @@ __global__ __launch_bounds__(NKT * 64) void sli_teacher_heads_kernel(SliArgs a) 
   __shared__ __attribute__((aligned(16))) uint16_t Ks[NKT * 32 * QP];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int nrb = (a.s1 + 31) / 32;
-  const int b = blockIdx.x / nrb, s0 = (blockIdx.x - b * nrb) * 32;
-  const int t0 = blockIdx.y * (NKT * 32);
+  // XCD-aware order: work-group L runs on XCD L % 8, so XCD x takes the contiguous
+  // range [x C, x C + C) of the key-block-major order (C = gridDim.x / 8): the row blocks
+  // that share a key block run on one XCD and read its key tiles through one L2
+  const int nrb = (a.s1 + 31) / 32, nx = a.batch * nrb;
+  const int cpx = gridDim.x / 8;
+  const int mo = (int)(blockIdx.x % 8) * cpx + (int)(blockIdx.x / 8);
+  if (mo >= nx * ((a.s2 + NKT * 32 - 1) / (NKT * 32))) return;
+  const int rbk = mo % nx;
+  const int b = rbk / nrb, s0 = (rbk - b * nrb) * 32;
+  const int t0 = (mo / nx) * (NKT * 32);
   const int aq = a.act_q[b], ak = a.act_k[b];
   auto slots = [&](int s1) {
     if (s1 >= a.s1 || s1 >= aq) return 0;
@@ -1584,8 +1591,10 @@ hipError_t launch_sli_io(const SliArgs& a, hipStream_t s) {
   }
   const dim3 tgrid(rows, (a.n1 + SBH - 1) / SBH);
   if (a.n2 > 1) {
+    // one-dimensional grids rounded up to whole XCD rounds (the kernel maps the ids)
     const int nrb = (a.s1 + 31) / 32;
-    const dim3 g4(a.batch * nrb, (a.s2 + 127) / 128), g2(a.batch * nrb, (a.s2 + 63) / 64);
+    const int64_t n4 = (int64_t)a.batch * nrb * ((a.s2 + 127) / 128), n2 = (int64_t)a.batch * nrb * ((a.s2 + 63) / 64);
+    const dim3 g4((unsigned)((n4 + 7) / 8 * 8)), g2((unsigned)((n2 + 7) / 8 * 8));
     switch (a.d + a.dr) {
       case 128: hipLaunchKernelGGL((sli_teacher_heads_kernel<IO, 128, 4>), g4, dim3(256), 0, s, a); break;
       case 192: hipLaunchKernelGGL((sli_teacher_heads_kernel<IO, 192, 4>), g4, dim3(256), 0, s, a); break;
