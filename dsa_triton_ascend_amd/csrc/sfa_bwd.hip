@@ -298,6 +298,10 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
 #pragma unroll
     for (int i = 0; i < 16; ++i) dq[jj][i] = 0.f;
   const float sl2 = f.scale * BLOG2E;
+  // the B operand of this wave's S^T / dP^T quarter (Q | Q rope or dO of the block's heads,
+  // the same for every tile) stays in VGPRs: read from LDS once, after the prologue's barrier
+  constexpr int NBQ4 = C::KS_S / 4;   // k-steps of an S^T quarter (>= those of a dP^T quarter)
+  uint4 bq[NBQ4];
 
   // ---- gathers of a tile's [nope | rope] rows into registers (rows outside the key
   // tensors and slots past the list are zero), two register sets: the next two
@@ -358,27 +362,21 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
     // compile-time length per role, so it is unrolled with its operand reads four
     // k-steps ahead.
     {
-      auto chain = [&](auto nks_c, const uint16_t* arow, const uint16_t* brow) __attribute__((always_inline)) {
+      auto chain = [&](auto nks_c, const uint16_t* arow) __attribute__((always_inline)) {
         constexpr int NKS = decltype(nks_c)::value;
         constexpr int AH = NKS < 4 ? NKS : 4;
-        uint4 ar[AH], br[AH];
+        uint4 ar[AH];
 #pragma unroll
-        for (int i = 0; i < AH; ++i) {
-          ar[i] = *reinterpret_cast<const uint4*>(arow + i * 16);
-          br[i] = *reinterpret_cast<const uint4*>(brow + i * 16);
-        }
+        for (int i = 0; i < AH; ++i) ar[i] = *reinterpret_cast<const uint4*>(arow + i * 16);
         f32x16 sacc = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) {
           // pinned order (the scheduler would otherwise regroup the reads next to
-          // their MFMAs): the MFMA of step ks, then the reads of step ks + AH
+          // their MFMAs): the MFMA of step ks, then the read of step ks + AH
           __builtin_amdgcn_sched_barrier(0);
-          sacc = Mfma<IO>::m32(ar[ks % AH], br[ks % AH], sacc);
+          sacc = Mfma<IO>::m32(ar[ks % AH], bq[ks], sacc);
           __builtin_amdgcn_sched_barrier(0);
-          if (ks + AH < NKS) {
-            ar[ks % AH] = *reinterpret_cast<const uint4*>(arow + (ks + AH) * 16);
-            br[ks % AH] = *reinterpret_cast<const uint4*>(brow + (ks + AH) * 16);
-          }
+          if (ks + AH < NKS) ar[ks % AH] = *reinterpret_cast<const uint4*>(arow + (ks + AH) * 16);
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -387,12 +385,10 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
       const uint16_t* krow = Ks + (lane & 31) * C::QP + (lane >> 5) * 8;
       if (wave < 4) {
         constexpr int N = C::KS_S / 4;
-        chain(std::integral_constant<int, N>{}, krow + (wave & 3) * N * 16,
-              Qs + (lane & 31) * C::QP + (lane >> 5) * 8 + (wave & 3) * N * 16);
+        chain(std::integral_constant<int, N>{}, krow + (wave & 3) * N * 16);
       } else {
         constexpr int N = C::KS_P / 4;
-        chain(std::integral_constant<int, N>{}, krow + (wave & 3) * N * 16,
-              dOs + (lane & 31) * C::OP + (lane >> 5) * 8 + (wave & 3) * N * 16);
+        chain(std::integral_constant<int, N>{}, krow + (wave & 3) * N * 16);
       }
     }
     lds_barrier();
@@ -459,6 +455,16 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
   if (tid < 3 * BT) s_idr[tid / BT][tid % BT] = tid < ntok ? toks[tid] : -1;
   load_ids(3 * BT);
   lds_barrier();
+  if (wave < 4) {
+    const uint16_t* brow = Qs + (lane & 31) * C::QP + (lane >> 5) * 8 + (wave & 3) * (C::KS_S / 4) * 16;
+#pragma unroll
+    for (int i = 0; i < NBQ4; ++i) bq[i] = *reinterpret_cast<const uint4*>(brow + i * 16);
+  } else {
+    const uint16_t* brow = dOs + (lane & 31) * C::OP + (lane >> 5) * 8 + (wave & 3) * (C::KS_P / 4) * 16;
+#pragma unroll
+    for (int i = 0; i < NBQ4; ++i)
+      bq[i] = i < C::KS_P / 4 ? *reinterpret_cast<const uint4*>(brow + i * 16) : make_uint4(0, 0, 0, 0);
+  }
   if (ntok > 0) gather(0, ka, pa);
   if (ntok > BT) gather(BT, kbr, pb);
   for (int t0 = 0; t0 < ntok; t0 += 2 * BT) {
