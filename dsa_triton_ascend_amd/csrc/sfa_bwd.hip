@@ -207,12 +207,10 @@ __global__ void sfa_bwd_zero_kernel(uint4* p, int64_t n4, const int64_t* used_el
 template <int IO, int D>
 __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, SfaTokenLists tl, BwdWs w) {
   using C = BCfg<D>;
-  __shared__ __attribute__((aligned(16))) uint16_t Qs[BH * C::QP];    // [head][nope | rope]
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[BT * C::QP];    // [token][nope | rope]
-  __shared__ __attribute__((aligned(16))) uint16_t dOs[BH * C::OP];   // [head][D]
-  __shared__ __attribute__((aligned(16))) uint16_t dSs[BH * C::PP];   // [head][token]
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BT * C::QP];    // [token][nope | rope], tiles t, t - 1
+  __shared__ __attribute__((aligned(16))) uint16_t dSs[2][BH * C::PP];   // [head][token], tiles t, t - 1
   __shared__ float part[BWV][16][64];   // S^T (waves 0-3) / dP^T (4-7) k-range partials, MFMA layout
-  __shared__ int s_tok[BT];             // the tile's token index within the batch (-1: none)
+  __shared__ int s_tok[2][BT];          // the tile's token index within the batch (-1: none)
   __shared__ int s_idr[4][BT];          // token-id ring: the ids of tile t in slot t % 4
   __shared__ float s_m[BH], s_il[BH], s_dl[BH];
   __shared__ uint32_t s_sel[C::ZBW];    // the batch tokens this row writes to the dense buffers
@@ -246,18 +244,11 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
     const uint16_t* gob = reinterpret_cast<const uint16_t*>(a.d_out);
     for (int i = tid; i < BH * (C::DT / 8); i += BWV * 64) {
       const int h = i / (C::DT / 8), c = (i % (C::DT / 8)) * 8;
-      uint4 v = z4;
       if (h < hn) {
         const int64_t hr = (int64_t)r * n1 + h0 + h;
-        v = c < D ? ldg16(qb + hr * D + c) : ldg16(qrb + hr * BDR + (c - D));
+        const uint4 v = c < D ? ldg16(qb + hr * D + c) : ldg16(qrb + hr * BDR + (c - D));
         stg16(w.qcat + hr * C::DT + c, v);   // the B operand of the [d_key | d_key_rope] product
       }
-      *reinterpret_cast<uint4*>(&Qs[h * C::QP + c]) = v;
-    }
-    for (int i = tid; i < BH * (D / 8); i += BWV * 64) {
-      const int h = i / (D / 8), c = (i % (D / 8)) * 8;
-      const uint4 v = ldg16_or0(h < hn, gob + ((int64_t)r * n1 + h0 + h) * D + c);
-      *reinterpret_cast<uint4*>(&dOs[h * C::OP + c]) = v;
     }
     // delta = dO . O (fp32) per head: 8 threads per head, D/8 columns each
     const uint16_t* ob = reinterpret_cast<const uint16_t*>(a.out);
@@ -298,10 +289,30 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
 #pragma unroll
     for (int i = 0; i < 16; ++i) dq[jj][i] = 0.f;
   const float sl2 = f.scale * BLOG2E;
-  // the B operand of this wave's S^T / dP^T quarter (Q | Q rope or dO of the block's heads,
-  // the same for every tile) stays in VGPRs: read from LDS once, after the prologue's barrier
+  // the B operand of this wave's S^T / dP^T quarter (Q | Q rope or dO of head h0 + lane % 32,
+  // the same for every tile) stays in VGPRs, loaded once from global memory
   constexpr int NBQ4 = C::KS_S / 4;   // k-steps of an S^T quarter (>= those of a dP^T quarter)
   uint4 bq[NBQ4];
+  {
+    const int hb = lane & 31;
+    const int64_t hr = (int64_t)r * n1 + h0 + (hb < hn ? hb : 0);
+    if (wave < 4) {
+      const uint16_t* qb = reinterpret_cast<const uint16_t*>(f.q);
+      const uint16_t* qrb = reinterpret_cast<const uint16_t*>(f.qr);
+#pragma unroll
+      for (int i = 0; i < NBQ4; ++i) {
+        const int c = ((wave & 3) * (C::KS_S / 4) + i) * 16 + (lane >> 5) * 8;
+        bq[i] = ldg16_or0(hb < hn, c < D ? qb + hr * D + c : qrb + hr * BDR + (c - D));
+      }
+    } else {
+      const uint16_t* gob = reinterpret_cast<const uint16_t*>(a.d_out);
+#pragma unroll
+      for (int i = 0; i < NBQ4; ++i) {
+        const int c = ((wave & 3) * (C::KS_P / 4) + i) * 16 + (lane >> 5) * 8;
+        bq[i] = ldg16_or0(hb < hn && i < C::KS_P / 4, gob + hr * D + (i < C::KS_P / 4 ? c : 0));
+      }
+    }
+  }
 
   // ---- gathers of a tile's [nope | rope] rows into registers (rows outside the key
   // tensors and slots past the list are zero), two register sets: the next two
@@ -341,15 +352,48 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
   // one tile: its rows from the register set `kreg` to LDS, then that set is
   // refilled with the rows two tiles ahead. Barriers order LDS only (lds_barrier):
   // a full __syncthreads() would also wait for the gathers in flight.
+  // ---- dQ[head, col] += dS[head, token] K[token, col] of tile tp (this wave's column
+  // blocks; every operand of the phase is requested before its MFMAs)
+  auto dq_phase = [&](int tp) __attribute__((always_inline)) {
+    const uint16_t* const kt = Ks[tp & 1];
+    const uint16_t* const dst = dSs[tp & 1];
+    uint4 av[BT / 16], bv[C::JQ][BT / 16];
+#pragma unroll
+    for (int kq = 0; kq < BT / 16; ++kq)
+      av[kq] = *reinterpret_cast<const uint4*>(dst + (lane & 31) * C::PP + kq * 16 + (lane >> 5) * 8);
+#pragma unroll
+    for (int jj = 0; jj < C::JQ; ++jj) {
+      const int j = wave + BWV * jj;
+      if (j < C::NBQ)
+#pragma unroll
+        for (int kq = 0; kq < BT / 16; ++kq) bv[jj][kq] = tr_frag(kt, C::QP, 32 * j, kq * 16, lane);
+    }
+#pragma unroll
+    for (int jj = 0; jj < C::JQ; ++jj) {
+      const int j = wave + BWV * jj;
+      if (j < C::NBQ)
+#pragma unroll
+        for (int kq = 0; kq < BT / 16; ++kq) dq[jj] = Mfma<IO>::m32(av[kq], bv[jj][kq], dq[jj]);
+    }
+  };
+  // One tile in two barrier-separated phases: [S^T / dP^T of tile t, and dQ of tile t - 1]
+  // then [P and dS of tile t]. K tiles, dS tiles and the token indices are double-buffered
+  // (slot t & 1), so the dQ of a tile runs beside the next tile's products. Hazards: slot
+  // t & 1 is rewritten at the start of tile t + 2, after every wave has passed the second
+  // barrier of tile t + 1, which follows the last reads of tile t (its dQ); part is
+  // rewritten by tile t + 1's products after its first barrier, which follows tile t's
+  // P / dS reads of it.
   auto tile = [&](int t0, uint4 (&kreg)[KCH], int& ptok) __attribute__((always_inline)) {
     const int nv = ntok - t0 < BT ? ntok - t0 : BT;
+    const int tcur = t0 / BT, sl = tcur & 1;
+    uint16_t* const kt = Ks[sl];
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
       const int idx = tid + BWV * 64 * i;
-      if (idx < NCH) *reinterpret_cast<uint4*>(&Ks[(idx / (C::DT / 8)) * C::QP + (idx % (C::DT / 8)) * 8]) = kreg[i];
+      if (idx < NCH) *reinterpret_cast<uint4*>(&kt[(idx / (C::DT / 8)) * C::QP + (idx % (C::DT / 8)) * 8]) = kreg[i];
     }
     if (tid < BT) {
-      s_tok[tid] = ptok;
+      s_tok[sl][tid] = ptok;
       s_idr[(t0 / BT + 3) & 3][tid] = idreg;   // ids of tile t+3, loaded during tile t-1
       if (zf && ptok >= 0) atomicOr(&s_sel[ptok >> 5], 1u << (ptok & 31));
     }
@@ -382,7 +426,7 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
 #pragma unroll
         for (int i = 0; i < 16; ++i) part[wave][i][lane] = sacc[i];
       };
-      const uint16_t* krow = Ks + (lane & 31) * C::QP + (lane >> 5) * 8;
+      const uint16_t* krow = kt + (lane & 31) * C::QP + (lane >> 5) * 8;
       if (wave < 4) {
         constexpr int N = C::KS_S / 4;
         chain(std::integral_constant<int, N>{}, krow + (wave & 3) * N * 16);
@@ -391,6 +435,7 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
         chain(std::integral_constant<int, N>{}, krow + (wave & 3) * N * 16);
       }
     }
+    if (tcur > 0) dq_phase(tcur - 1);
     lds_barrier();
 
     // ---- P and dS of the tile (fp32 -> io dtype): dS to LDS as [head][token] for
@@ -415,39 +460,14 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
         ds = p * (dp - s_dl[h]) * f.scale;
       }
       const uint16_t ds16 = from_f32<IO>(ds);
-      dSs[h * C::PP + tk] = ds16;
-      const int tb = s_tok[tk];
+      dSs[sl][h * C::PP + tk] = ds16;
+      const int tb = s_tok[sl][tk];
       if (tb >= 0 && h < hn) {
         const int64_t di = dbase + (int64_t)tb * g.kp + h;
         w.dst[di] = ds16;
         w.pt[di] = from_f32<IO>(p);
       }
     }
-    lds_barrier();
-
-    // ---- dQ[head, col] += dS[head, token] K[token, col]   (this wave's column blocks;
-    // every operand of the phase is requested before its MFMAs)
-    {
-      uint4 av[BT / 16], bv[C::JQ][BT / 16];
-#pragma unroll
-      for (int kq = 0; kq < BT / 16; ++kq)
-        av[kq] = *reinterpret_cast<const uint4*>(dSs + (lane & 31) * C::PP + kq * 16 + (lane >> 5) * 8);
-#pragma unroll
-      for (int jj = 0; jj < C::JQ; ++jj) {
-        const int j = wave + BWV * jj;
-        if (j < C::NBQ)
-#pragma unroll
-          for (int kq = 0; kq < BT / 16; ++kq) bv[jj][kq] = tr_frag(Ks, C::QP, 32 * j, kq * 16, lane);
-      }
-#pragma unroll
-      for (int jj = 0; jj < C::JQ; ++jj) {
-        const int j = wave + BWV * jj;
-        if (j < C::NBQ)
-#pragma unroll
-          for (int kq = 0; kq < BT / 16; ++kq) dq[jj] = Mfma<IO>::m32(av[kq], bv[jj][kq], dq[jj]);
-      }
-    }
-    lds_barrier();   // the next tile overwrites Ks, dSs and s_tok
   };
   if (zf)
     for (int i = tid; i < (g.nk + 31) / 32; i += BWV * 64) s_sel[i] = 0;
@@ -455,21 +475,15 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
   if (tid < 3 * BT) s_idr[tid / BT][tid % BT] = tid < ntok ? toks[tid] : -1;
   load_ids(3 * BT);
   lds_barrier();
-  if (wave < 4) {
-    const uint16_t* brow = Qs + (lane & 31) * C::QP + (lane >> 5) * 8 + (wave & 3) * (C::KS_S / 4) * 16;
-#pragma unroll
-    for (int i = 0; i < NBQ4; ++i) bq[i] = *reinterpret_cast<const uint4*>(brow + i * 16);
-  } else {
-    const uint16_t* brow = dOs + (lane & 31) * C::OP + (lane >> 5) * 8 + (wave & 3) * (C::KS_P / 4) * 16;
-#pragma unroll
-    for (int i = 0; i < NBQ4; ++i)
-      bq[i] = i < C::KS_P / 4 ? *reinterpret_cast<const uint4*>(brow + i * 16) : make_uint4(0, 0, 0, 0);
-  }
   if (ntok > 0) gather(0, ka, pa);
   if (ntok > BT) gather(BT, kbr, pb);
   for (int t0 = 0; t0 < ntok; t0 += 2 * BT) {
     tile(t0, ka, pa);
     if (t0 + BT < ntok) tile(t0 + BT, kbr, pb);
+  }
+  if (ntok > 0) {   // the last tile's dQ, after its dS is complete
+    lds_barrier();
+    dq_phase((ntok - 1) / BT);
   }
 
   // ---- d_query | d_query_rope of the block's heads (zeros for rows without tokens)
