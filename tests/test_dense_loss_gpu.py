@@ -242,3 +242,4 @@ def test_dense_perf_shape_full_call_matches_single_rows(dev):
     rel = np.linalg.norm(_np(full[1]) - want[1]) / np.linalg.norm(want[1])
     print(f"[dense parity] perf shape d_key_index relative Frobenius error {rel:.2e}")
     assert rel <= 1e-2
+

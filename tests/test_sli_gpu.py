@@ -224,3 +224,10 @@ def test_kl_loss_few_slots_per_key(dev, pattern):
     """D_idx = 128 with S2 > 4 top-k: d_key_index by per-slot atomics in the student
     (shorter lists take the key-major pass over a per-key dI buffer, as the other cases)."""
     run(dev, 1, 4, 4096, 32, 512, 64, 128, 512, "bf16", pattern)
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_kl_loss_48_indexer_heads(dev, dtype):
+    """Nidx1 = 48 at D_idx = 128 (head-split student with padded heads, key-major pass over
+    the per-key dI buffer), repeated ids included."""
+    run(dev, 1, 4, 1024, 32, 512, 48, 128, 512, dtype, pattern="repeated")
