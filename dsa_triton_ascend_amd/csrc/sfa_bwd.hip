@@ -544,13 +544,21 @@ __global__ __launch_bounds__(256) void sfa_bwd_place_kernel(SfaBwdArgs a, BwdWs 
     const int64_t srows = w.boffk[f.batch];   // staged rows per partial
     // the sum of the split's fp32 partials of 8 consecutive elements, in the io dtype
     auto sum8 = [&](const float* p, int64_t pstride) {
+      // every partial's loads are issued before the first add (unrolled to BSPLIT)
+      float4 x[BSPLIT], y[BSPLIT];
+#pragma unroll
+      for (int c = 0; c < BSPLIT; ++c)
+        if (c < w.split) {
+          x[c] = reinterpret_cast<const float4*>(p + c * pstride)[0];
+          y[c] = reinterpret_cast<const float4*>(p + c * pstride)[1];
+        }
       float4 lo = make_float4(0.f, 0.f, 0.f, 0.f), hi = lo;
-      for (int c = 0; c < w.split; ++c) {
-        const float4 x = reinterpret_cast<const float4*>(p + c * pstride)[0];
-        const float4 y = reinterpret_cast<const float4*>(p + c * pstride)[1];
-        lo.x += x.x; lo.y += x.y; lo.z += x.z; lo.w += x.w;
-        hi.x += y.x; hi.y += y.y; hi.z += y.z; hi.w += y.w;
-      }
+#pragma unroll
+      for (int c = 0; c < BSPLIT; ++c)
+        if (c < w.split) {
+          lo.x += x[c].x; lo.y += x[c].y; lo.z += x[c].z; lo.w += x[c].w;
+          hi.x += y[c].x; hi.y += y[c].y; hi.z += y[c].z; hi.w += y[c].w;
+        }
       return make_uint4(pack2<IO>(lo.x, lo.y), pack2<IO>(lo.z, lo.w), pack2<IO>(hi.x, hi.y), pack2<IO>(hi.z, hi.w));
     };
     uint4 v = make_uint4(0, 0, 0, 0);
