@@ -529,13 +529,13 @@ __device__ int split_token_list(const SfaArgs& a, int r, int sp, int splits, con
 // Merge of the KV-split partials of the rows whose tokens span several splits
 // (the attention kernel writes single-split and skipped rows itself). Work-group
 // (row, blockIdx.y) covers units u = (head u / (D/8), columns 8 (u % (D/8)) ..+8),
-// 16 / MS per thread for at most MS splits, every partial load issued before any
+// one unit per thread for at most MS splits, every partial load issued before any
 // is used. Split s left O_s / l_s (io dtype) and (m_used_s, m_true_s, l_s); per
 // head M = max m_used_s, w_s = l_s 2^((m_used_s - M) log2 e),
 // out = sum_s w_s (O_s / l_s) / sum_s w_s; softmax_max / sum as for an unsplit row.
 template <int IO, int D, int MS>
 __global__ __launch_bounds__(256) void sfa_merge_kernel(SfaArgs a, int splits, Ws ws) {
-  constexpr int MERGE_MAX_SPLITS = MS, MU = 16 / MS;
+  constexpr int MERGE_MAX_SPLITS = MS, MU = 1;   // units per thread (more were slower: fewer waves in flight)
   const int r = blockIdx.x;
   const int n1 = a.n1;
   constexpr int CH = D / 8;
@@ -1651,7 +1651,7 @@ hipError_t launch_attn_d(const SfaArgs& a, hipStream_t s, int cap, int splits, i
   if (e != hipSuccess || splits == 1) return e;
   const int units = a.n1 * (D / 8);
   if (splits <= 4)
-    hipLaunchKernelGGL((sfa_merge_kernel<IO, D, 4>), dim3(a.total_rows, (units + 1023) / 1024), dim3(256), 0,
+    hipLaunchKernelGGL((sfa_merge_kernel<IO, D, 4>), dim3(a.total_rows, (units + 255) / 256), dim3(256), 0,
                        s, a, splits, ws);
   else
     hipLaunchKernelGGL((sfa_merge_kernel<IO, D, 16>), dim3(a.total_rows, (units + 255) / 256), dim3(256), 0,
