@@ -1742,7 +1742,7 @@ hipError_t launch_sfa_token_lists(const SfaArgs& a, void* ws_base, SfaTokenLists
   tl->tokens = ws.tokens;
   tl->tstride = ws.tstride;
   if (a.total_rows <= 0) return hipSuccess;
-  if (a.sbs == 1 && a.total_rows >= 1024)
+  if (a.sbs == 1 && a.total_rows >= 256)
     hipLaunchKernelGGL(dsa::sfa_tokens1_kernel, dim3((a.total_rows + dsa::TOK1_ROWS - 1) / dsa::TOK1_ROWS),
                        dim3(64 * dsa::TOK1_ROWS), 0, s, a, cap, ws);
   else
@@ -1832,7 +1832,7 @@ hipError_t launch_sfa_fwd(const SfaArgs& a, hipStream_t s) {
   // GPU; a few rows are spread over a whole work-group each.
   const int fuse_tok = splits > 1 && a.sbs == 1;
   if (!fuse_tok) {
-    if (a.sbs == 1 && a.total_rows >= 1024)
+    if (a.sbs == 1 && a.total_rows >= 256)
       hipLaunchKernelGGL(dsa::sfa_tokens1_kernel, dim3((a.total_rows + dsa::TOK1_ROWS - 1) / dsa::TOK1_ROWS),
                          dim3(64 * dsa::TOK1_ROWS), 0, s, a, cap, ws);
     else
