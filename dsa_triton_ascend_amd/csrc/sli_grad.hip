@@ -1368,12 +1368,14 @@ __global__ __launch_bounds__(512) void sli_student_hs_kernel(SliArgs a) {
 // the ds^T operand [key, 8 heads] of the dKI product, which accumulates in registers
 // over the group's rows. One fp32 atomic add per element and row group at the end.
 constexpr int KM_RPG = 32;   // rows per work-group
-template <int IO, int MT>
+template <int IO, int MT, bool EW>
 __global__ __launch_bounds__(256) void sli_dki_km_kernel(SliArgs a) {
   constexpr int DI = 128, GP = 32 * MT, QIP = DI + 8, KK = DI / 16, NCB = DI / 32;
   constexpr int QL = GP * (DI / 8) / 256;   // 16-byte qi chunks per thread and row
   __shared__ __attribute__((aligned(16))) uint16_t QIs[2][GP * QIP];
   __shared__ __attribute__((aligned(16))) float Ws[2][GP];
+  __shared__ __attribute__((aligned(16))) uint16_t Ws16[EW ? 2 : 1][EW ? GP : 4];   // EW: the weights' own bits
+  __shared__ __attribute__((aligned(16))) float s_di[EW ? 4 : 1][32];               // EW: dI of the wave's keys
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int b = blockIdx.z;
@@ -1400,6 +1402,7 @@ __global__ __launch_bounds__(256) void sli_dki_km_kernel(SliArgs a) {
     bk[kk] = ldg16_or0(key < a.s2, kib + ((int64_t)b * a.s2 + key) * DI + kk * 16 + (lane >> 5) * 8);
   uint4 qst[QL];
   float wst = 0.f, dst_ = 0.f;
+  uint16_t wst16 = 0;
   bool okst = true;   // rows with an empty indexer softmax have no dI
   auto stage = [&](int s1) {
     okst = !(a.isum && !(a.isum[(int64_t)b * a.s1 + s1] > 0.f));
@@ -1410,7 +1413,10 @@ __global__ __launch_bounds__(256) void sli_dki_km_kernel(SliArgs a) {
       const int g = i / (DI / 8), c = (i % (DI / 8)) * 8;
       qst[j] = ldg16_or0(g < G, qib + (qrow + g) * DI + c);
     }
-    if (tid < GP) wst = tid < G ? ld_w(a.w, a.wdt, qrow + tid) : 0.f;
+    if (tid < GP) {
+      if constexpr (EW) wst16 = tid < G ? reinterpret_cast<const uint16_t*>(a.w)[qrow + tid] : (uint16_t)0;
+      else wst = tid < G ? ld_w(a.w, a.wdt, qrow + tid) : 0.f;
+    }
     const int n = dense && s1 + off < a.s2 ? s1 + off : a.s2;   // the row's keys
     dst_ = key < n ? a.dib[((int64_t)b * a.s1 + s1) * a.dib_ld + key] : 0.f;
   };
@@ -1420,7 +1426,10 @@ __global__ __launch_bounds__(256) void sli_dki_km_kernel(SliArgs a) {
       const int i = tid + 256 * j;
       *reinterpret_cast<uint4*>(&QIs[buf][(i / (DI / 8)) * QIP + (i % (DI / 8)) * 8]) = qst[j];
     }
-    if (tid < GP) Ws[buf][tid] = wst;
+    if (tid < GP) {
+      if constexpr (EW) Ws16[buf][tid] = wst16;
+      else Ws[buf][tid] = wst;
+    }
   };
   f32x16 c[NCB];
 #pragma unroll
@@ -1450,6 +1459,49 @@ __global__ __launch_bounds__(256) void sli_dki_km_kernel(SliArgs a) {
         const uint4 af = *reinterpret_cast<const uint4*>(q + (32 * mt + (lane & 31)) * QIP + kk * 16 + (lane >> 5) * 8);
         acc[mt] = Mfma<IO>::m32(af, bk[kk], acc[mt]);
       }
+    if constexpr (EW) {
+      // weights in the io dtype: [dot > 0] w is exact in it, so dKI[key, :] += dI[key]
+      // sum_h ([dot > 0] w)[key, h] qi[h, :] takes one MFMA per k-step, and dI scales the
+      // product in fp32 (no hi / lo split)
+      if (lane < 32) s_di[wave][lane] = di;
+      float dv[16];   // dI of key m32_row(e, lane): groups of four consecutive keys
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 f = *reinterpret_cast<const float4*>(&s_di[wave][8 * g + 4 * (lane >> 5)]);
+        dv[4 * g] = f.x; dv[4 * g + 1] = f.y; dv[4 * g + 2] = f.z; dv[4 * g + 3] = f.w;
+      }
+      uint32_t mp[MT][4][2];   // group q of mt: heads 32 mt + 8 q + 4 (lane / 32) + 0 .. 3
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int qg = 0; qg < 4; ++qg) {
+          const uint2 wp = *reinterpret_cast<const uint2*>(&Ws16[buf][32 * mt + 8 * qg + 4 * (lane >> 5)]);
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const uint32_t m = (acc[mt][4 * qg + 2 * h] > 0.f ? 0xFFFFu : 0u) |
+                               (acc[mt][4 * qg + 2 * h + 1] > 0.f ? 0xFFFF0000u : 0u);
+            mp[mt][qg][h] = m & (h == 0 ? wp.x : wp.y);
+          }
+        }
+      uint4 aw[GP / 16];
+#pragma unroll
+      for (int kq = 0; kq < GP / 16; ++kq) {
+        const int mt = kq / 2, g0 = 2 * (kq % 2);
+        uint32_t x0 = mp[mt][g0][0], x1 = mp[mt][g0][1], y0 = mp[mt][g0 + 1][0], y1 = mp[mt][g0 + 1][1];
+        swap_halves(x0, y0);
+        swap_halves(x1, y1);
+        aw[kq] = make_uint4(x0, x1, y0, y1);
+      }
+#pragma unroll
+      for (int j = 0; j < NCB; ++j) {
+        f32x16 t = {};
+#pragma unroll
+        for (int kq = 0; kq < GP / 16; ++kq) t = Mfma<IO>::m32(aw[kq], s_tr_frag(q, QIP, 32 * j, kq * 16, lane), t);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) c[j][e] += dv[e] * t[e];
+      }
+      continue;
+    }
     // ds in the io dtype (hi, and lo = the rounding error), packed four heads per
     // register pair: group q of mt holds heads 32 mt + 8 q + 4 (lane / 32) + 0 .. 3
     uint32_t hp[MT][4][2], lp[MT][4][2];
@@ -1546,6 +1598,15 @@ void launch_student_big(const SliArgs& a, int rows, hipStream_t s) {
     hipLaunchKernelGGL((sli_student_kernel<IO, DI, 2, 2, BIG>), dim3(rows), dim3(256), 0, s, a);
 }
 
+// the key-major dKI pass; the exact-weight form when the weights are in the io dtype
+template <int IO, int MT>
+void launch_km(const SliArgs& a, hipStream_t s) {
+  const dim3 g((a.s2 + 127) / 128, (a.s1 + KM_RPG - 1) / KM_RPG, a.batch);
+  const bool ew = a.wdt == (IO == IO_BF16 ? DSA_DTYPE_BF16 : DSA_DTYPE_F16);
+  if (ew) hipLaunchKernelGGL((sli_dki_km_kernel<IO, MT, true>), g, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((sli_dki_km_kernel<IO, MT, false>), g, dim3(256), 0, s, a);
+}
+
 template <int IO, int DI>
 void launch_student(const SliArgs& a, int rows, hipStream_t s) {
   if constexpr (DI == 128) {
@@ -1554,18 +1615,14 @@ void launch_student(const SliArgs& a, int rows, hipStream_t s) {
       if (a.nidx1 > 32 && (a.dki_km || a.lse_max)) {
         // 33 - 64 heads: the eight-wave head-split form (stats only, or dKI left to the key-major pass)
         hipLaunchKernelGGL((sli_student_hs_kernel<IO>), dim3(rows), dim3(512), 0, s, a);
-        if (a.dki_km) {
-          const dim3 g((a.s2 + 127) / 128, (a.s1 + KM_RPG - 1) / KM_RPG, a.batch);
-          hipLaunchKernelGGL((sli_dki_km_kernel<IO, 2>), g, dim3(256), 0, s, a);
-        }
+        if (a.dki_km) launch_km<IO, 2>(a, s);
         return;
       }
       if (a.dki_km) {
         if (a.nidx1 <= 32) hipLaunchKernelGGL((sli_student_wt_kernel<IO, 1, true>), dim3(rows), dim3(256), 0, s, a);
         else hipLaunchKernelGGL((sli_student_wt_kernel<IO, 2, true>), dim3(rows), dim3(256), 0, s, a);
-        const dim3 g((a.s2 + 127) / 128, (a.s1 + KM_RPG - 1) / KM_RPG, a.batch);
-        if (a.nidx1 <= 32) hipLaunchKernelGGL((sli_dki_km_kernel<IO, 1>), g, dim3(256), 0, s, a);
-        else hipLaunchKernelGGL((sli_dki_km_kernel<IO, 2>), g, dim3(256), 0, s, a);
+        if (a.nidx1 <= 32) launch_km<IO, 1>(a, s);
+        else launch_km<IO, 2>(a, s);
       } else {
         if (a.nidx1 <= 32) hipLaunchKernelGGL((sli_student_wt_kernel<IO, 1, false>), dim3(rows), dim3(256), 0, s, a);
         else hipLaunchKernelGGL((sli_student_wt_kernel<IO, 2, false>), dim3(rows), dim3(256), 0, s, a);

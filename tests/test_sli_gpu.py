@@ -99,7 +99,8 @@ def _stats_chunked(q, k, qr, kr, scale, act_q, act_k, chunk=32):
     return torch.from_numpy(sm_max), torch.from_numpy(sm_sum)
 
 
-def run(dev, B, S1, S2, N1, D, G, Di, K, dtype, pattern="random", act_q=None, act_k=None, loose=False):
+def run(dev, B, S1, S2, N1, D, G, Di, K, dtype, pattern="random", act_q=None, act_k=None, loose=False,
+        w_f32=False):
     """One call against the oracle. ``loose``: the reference's loose group
     (test_sli_grad_kl_loss_triton.py:191-211, shapes with S1 >= 512 or deep d_key_index
     sums): bf16 d_query_index at (0.1, 0.1) and d_key_index not compared elementwise;
@@ -111,7 +112,7 @@ def run(dev, B, S1, S2, N1, D, G, Di, K, dtype, pattern="random", act_q=None, ac
     smax, ssum = _stats(q, k, qr, kr, scale, aq, ak)
     g = lambda x: x.to(dev)
     dqi, dki, dw, loss = sparse_lightning_indexer_grad_kl_loss(
-        g(q), g(k), g(qi), g(ki), g(w), g(si), g(smax), g(ssum), query_rope=g(qr), key_rope=g(kr),
+        g(q), g(k), g(qi), g(ki), g(w.float() if w_f32 else w), g(si), g(smax), g(ssum), query_rope=g(qr), key_rope=g(kr),
         actual_seq_qlen=act_q, actual_seq_klen=act_k, scale_value=scale)
     torch.cuda.synchronize()
     f = lambda x: x.float().cpu().numpy()
@@ -120,6 +121,7 @@ def run(dev, B, S1, S2, N1, D, G, Di, K, dtype, pattern="random", act_q=None, ac
     atol, rtol = TOLS[dtype]
     what = f"B{B} S1={S1} S2={S2} N1={N1} D={D} Nidx1={G} Didx={Di} K={K} {dtype} {pattern}"
     assert dqi.shape == qi.shape and dki.shape == ki.shape and dw.shape == w.shape and loss.shape == (1,)
+    dw = dw.to(w.dtype) if w_f32 else dw
     for name, got, ref in zip(("d_query_index", "d_key_index", "d_weights", "loss"), (dqi, dki, dw, loss), want):
         assert np.all(np.isfinite(f(got))), f"{what}: {name} not finite"
         if loose and name == "d_key_index":
@@ -231,3 +233,10 @@ def test_kl_loss_48_indexer_heads(dev, dtype):
     """Nidx1 = 48 at D_idx = 128 (head-split student with padded heads, key-major pass over
     the per-key dI buffer), repeated ids included."""
     run(dev, 1, 4, 1024, 32, 512, 48, 128, 512, dtype, pattern="repeated")
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_kl_loss_fp32_weights(dev, dtype):
+    """float32 weights (the same values as the io-dtype case): the key-major d_key_index pass
+    then takes the hi / lo split of ds instead of the exact-weight form."""
+    run(dev, 1, 4, 1024, 32, 512, 64, 128, 512, dtype, pattern="repeated", w_f32=True)
