@@ -1618,11 +1618,9 @@ void launch_student(const SliArgs& a, int rows, hipStream_t s) {
         if (a.dki_km) launch_km<IO, 2>(a, s);
         return;
       }
-      if (a.dki_km) {
-        if (a.nidx1 <= 32) hipLaunchKernelGGL((sli_student_wt_kernel<IO, 1, true>), dim3(rows), dim3(256), 0, s, a);
-        else hipLaunchKernelGGL((sli_student_wt_kernel<IO, 2, true>), dim3(rows), dim3(256), 0, s, a);
-        if (a.nidx1 <= 32) launch_km<IO, 1>(a, s);
-        else launch_km<IO, 2>(a, s);
+      if (a.dki_km) {   // <= 32 heads here (more take the head-split form above)
+        hipLaunchKernelGGL((sli_student_wt_kernel<IO, 1, true>), dim3(rows), dim3(256), 0, s, a);
+        launch_km<IO, 1>(a, s);
       } else {
         if (a.nidx1 <= 32) hipLaunchKernelGGL((sli_student_wt_kernel<IO, 1, false>), dim3(rows), dim3(256), 0, s, a);
         else hipLaunchKernelGGL((sli_student_wt_kernel<IO, 2, false>), dim3(rows), dim3(256), 0, s, a);
