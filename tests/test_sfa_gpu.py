@@ -257,16 +257,17 @@ def _climbing_inputs(S1, N1, D, dtype, climbs, seed=0):
     return (t(q[None]), t(k[None, :, None]), t(qr[None]), t(kr[None, :, None]), scale)
 
 
+@pytest.mark.parametrize("N1", [32, 128])
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 @pytest.mark.parametrize("D", [128, 512])
 @pytest.mark.parametrize("climbs", [(15.0,), (35.0, 15.0, 22.0)])
-def test_climbing_score_spread(dev, dtype, D, climbs):
+def test_climbing_score_spread(dev, dtype, D, climbs, N1):
     """Rows whose per-tile score maxima climb by 15-35 nats (total spread ~100-180 nats):
     with the exponent reference held back by the lazy-rescale threshold, P = exp(s - m_used)
     reaches e^TAU before it is packed to the io dtype. Outputs must stay finite and match
     the oracle, unsplit (one work-group per row) and over forced KV splits (each split
     listing its own tokens and a merge)."""
-    S1, N1 = 4, 32
+    S1 = 4
     q, k, qr, kr, scale = _climbing_inputs(S1, N1, D, dtype, climbs)
     si = np.tile(np.arange(256, dtype=np.int32), (1, S1, 1, 1))
     o = SFA.sparse_flash_attention(_np(q), _np(k), None, si, scale, query_rope=_np(qr), key_rope=_np(kr),
@@ -287,13 +288,33 @@ def test_c3_prefill_sampled(dev):
     out, smax, ssum = sparse_flash_attention(inp.query, inp.key, inp.key, inp.sparse_indices,
                                              **inp.kwargs())
     torch.cuda.synchronize()
-    rows = [(0, s) for s in (0, 1, 2047, 2048, 4095)] + [(0, s) for s in range(3, 4096, 511)]
+    # 128 stride-sampled rows over the whole causal triangle plus its corners
+    rows = [(0, s) for s in sorted(set(range(5, 4096, 32)) | {0, 1, 2047, 2048, 4095})]
+    assert len(rows) >= 128
     o = SFA.sparse_flash_attention(_np(inp.query), _np(inp.key), None, inp.sparse_indices.cpu().numpy(),
                                    inp.scale_value, query_rope=_np(inp.query_rope), key_rope=_np(inp.key_rope),
                                    sparse_mode=3, return_softmax_lse=True, io_dtype="bf16", rows=rows)
     s = [r[1] for r in rows]
     compare(out[:, s], smax[:, :, s], ssum[:, :, s], o[0][:, s], o[1][:, :, s], o[2][:, :, s],
             what="C3 prefill (sampled rows)")
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_perf_sfa_shape_forward(dev, dtype):
+    """The reference's perf_sfa shape (perf_sfa_triton.py:7-9: B=1, S1=512, S2=4096, N1=64,
+    top-k 2048, D=512+64, causal) -- the bench's sfa_prefill_n64 line: every one of the 512
+    rows against the oracle. Rows near the end select 2048 tokens (64 tiles), so the
+    64-head forward's lazy rescaling runs over full-length rows."""
+    inp = W.sfa_prefill_inputs(B=1, S1=512, S2=4096, N1=64, D=512, sparse_count=2048, device=dev,
+                               seed=42, dtype=DT[dtype])
+    out, smax, ssum = sparse_flash_attention(inp.query, inp.key, inp.key, inp.sparse_indices,
+                                             **inp.kwargs())
+    torch.cuda.synchronize()
+    o = SFA.sparse_flash_attention(_np(inp.query), _np(inp.key), None, inp.sparse_indices.cpu().numpy(),
+                                   inp.scale_value, query_rope=_np(inp.query_rope), key_rope=_np(inp.key_rope),
+                                   sparse_mode=3, return_softmax_lse=True, io_dtype=dtype)
+    compare(out, smax, ssum, *o, what=f"perf_sfa shape N1=64 {dtype} (all 512 rows)")
 
 
 @pytest.mark.parametrize("N1,dtype,mode", [(128, "bf16", 3), (128, "fp16", 3), (128, "bf16", 0)])
@@ -363,12 +384,12 @@ def test_forced_kv_splits_with_empty_splits(dev, kv_splits):
     compare(out, smax, ssum, *o, what=f"kv_splits={kv_splits}")
 
 
-@pytest.mark.parametrize("N1", [16, 64])
+@pytest.mark.parametrize("N1", [16, 64, 128])
 @pytest.mark.parametrize("kv_splits", [2, 5])
 def test_forced_kv_splits_block_size_2(dev, N1, kv_splits):
     """KV splits over token lists built by the token-list launch (sparse_block_size 2): at
-    D = 512 and N1 <= 64 the 8-wave attention form writes the split partials and the merge
-    combines them, including splits past a short row's tokens."""
+    D = 512 the 8-wave attention forms (N1 <= 64, and N1 = 128) write the split
+    partials and the merge combines them, including splits past a short row's tokens."""
     B, S1, S2, D, count, bs = 1, 8, 160, 512, 48, 2
     q, k, v, qr, kr = _inputs(B, S1, S2, N1, D, "bf16", seed=23)
     si = _ref_indices(B, S1, S2, count, bs, 3, seed=6)
