@@ -55,8 +55,9 @@ def build(verbose: bool = True) -> Path:
         for f in futs:
             f.result()
     tmp = LIB.with_suffix(".so.tmp")
-    # hipBLASLt: the SFA backward's dense d_key / d_value products
-    cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-o", str(tmp), *map(str, objs), "-lhipblaslt"]
+    # hipBLASLt (the SFA backward's dense d_key / d_value products) is loaded with dlopen on
+    # the first backward call, so it is not a load-time dependency of the library
+    cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-o", str(tmp), *map(str, objs), "-ldl"]
     p = subprocess.run(cmd, capture_output=True, text=True)
     if p.returncode != 0:
         raise RuntimeError(f"link failed:\n{p.stderr}")

@@ -272,6 +272,9 @@ int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, cons
   if (batch > 65535) return fail(DSA_ERR_UNSUPPORTED, "dsa_sfa_bwd: batch > 65535");
   if (host_row_start[0] != 0 || host_row_start[batch] > total_rows)
     return fail(DSA_ERR_INVALID, "dsa_sfa_bwd: host_row_start must start at 0 and end within total_rows");
+  for (int b = 0; b < batch; ++b)   // the host copies size and place the library GEMMs
+    if (host_row_start[b + 1] < host_row_start[b])
+      return fail(DSA_ERR_INVALID, "dsa_sfa_bwd: host_row_start must be non-decreasing");
   const size_t need = sfa_bwd_workspace_bytes(batch, host_row_start, host_act_k, s2, total_rows, n1, d,
                                               sparse_count, sparse_block_size, key_rows);
   if (workspace_bytes < need)
@@ -293,7 +296,14 @@ int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, cons
   a.dv = d_value;
   a.h_row_start = host_row_start;
   a.h_act_k = host_act_k;
-  return hip_status(launch_sfa_bwd(a, (hipStream_t)stream), "dsa_sfa_bwd launch");
+  const hipError_t e = launch_sfa_bwd(a, (hipStream_t)stream);
+  if (e == hipErrorSharedObjectInitFailed)
+    return fail(DSA_ERR_UNSUPPORTED, "dsa_sfa_bwd: %s", sfa_bwd_library_error());
+  if (e == hipErrorStreamCaptureUnsupported)
+    return fail(DSA_ERR_UNSUPPORTED,
+                "dsa_sfa_bwd: the first call on a device creates its hipBLASLt handle and must run "
+                "outside stream capture");
+  return hip_status(e, "dsa_sfa_bwd launch");
 }
 
 size_t dsa_sli_grad_workspace_bytes(int batch, int s1, int s2, int sparse_count, int d_idx) {

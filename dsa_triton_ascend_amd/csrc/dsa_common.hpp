@@ -303,6 +303,8 @@ struct SfaBwdArgs {
 size_t sfa_bwd_workspace_bytes(int batch, const int32_t* h_row_start, const int32_t* h_act_k, int s2,
                                int total_rows, int n1, int d, int topk, int sbs, int64_t key_rows);
 hipError_t launch_sfa_bwd(const SfaBwdArgs& a, hipStream_t s);
+// Why the backward's library GEMMs are unavailable (hipBLASLt failed to load), else ""
+const char* sfa_bwd_library_error();
 
 // sparse lightning-indexer grad KL loss (BSND)
 // row stride of the sparse loss's per-key dI buffer (0: no key-major dKI pass)

@@ -36,7 +36,8 @@
 //         [head][token];
 //       * dQ[head, col] += dS K, each wave owning an eighth of the 32-column
 //         blocks, the K operand read with ds_read_b64_tr_b16 from the tile;
-//  4. two library GEMMs per batch (hipBLASLt, bf16/fp16 in and out, fp32
+//  4. two library GEMMs per batch (hipBLASLt, loaded on first use; a fixed algorithm per
+//     shape, so results are reproducible across processes; bf16/fp16 in and out, fp32
 //     accumulation): [d_key | d_key_rope] = dS_T [q | q_rope] (one product: the rows
 //     kernel writes [q | q_rope] to a concatenated workspace buffer as it loads it;
 //     a separate 64-column d_key_rope product took 0.10 ms) and d_value = P_T d_out,
@@ -48,13 +49,16 @@
 //     GEMM kernels they replaced);
 //  5. sfa_bwd_place_kernel -- adds each batch's staged partials into key rows
 //     key_start[b] + t (io dtype) and writes zeros to the key rows no batch covers.
+#include <dlfcn.h>
+
 #include <climits>
 #include <type_traits>
 #include <map>
 #include <mutex>
+#include <string>
 #include <tuple>
 
-#include <hipblaslt/hipblaslt.h>
+#include <hipblaslt/hipblaslt.h>   // types and prototypes only: the library is loaded with dlopen
 
 #include "dsa_common.hpp"
 
@@ -68,7 +72,7 @@ constexpr int BWV = 8;      // waves per work-group (two per SIMD)
 constexpr float BLOG2E = 1.4426950408889634f;
 constexpr int GBK = 64;     // dense rows are padded to a multiple of 64 (row, head) pairs
 constexpr size_t LT_WS = (size_t)128 << 20;  // workspace offered to the library GEMMs
-constexpr int LT_CANDIDATES = 64;            // algorithms timed per product shape
+constexpr int LT_CANDIDATES = 64;            // length of the heuristic's ranked list
 // Split of the products' contraction (the batch's (row, head) pairs): with M = key rows
 // and N = D + Dr or D the output has few tiles (about 64 - 144 at the grad perf shape for
 // 256 CUs), so the contraction is cut into BSPLIT chunks, run as one strided-batched
@@ -110,6 +114,7 @@ struct BwdWs {
   int64_t* boffk;  // [batch + 1] staged-row offsets (prefix of nk)
   float* skc;      // staged [split][sum nk, D + Dr] d_key | d_key_rope partials (fp32)
   uint16_t* qcat;  // [total_rows * N1, D + Dr] q | q_rope (written by the rows kernel)
+  uint16_t* gocat; // [total_rows * N1, D] d_out (written by the rows kernel)
   float* sv;       // staged [split][sum nk, D] d_value partials (fp32)
   int split;       // partials per staged row (1 or BSPLIT)
   void* lt_ws;     // LT_WS bytes for the library GEMMs
@@ -247,7 +252,10 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
       if (h < hn) {
         const int64_t hr = (int64_t)r * n1 + h0 + h;
         const uint4 v = c < D ? ldg16(qb + hr * D + c) : ldg16(qrb + hr * BDR + (c - D));
-        stg16(w.qcat + hr * C::DT + c, v);   // the B operand of the [d_key | d_key_rope] product
+        // the B operand of the [d_key | d_key_rope] product; zeros for a row without tokens
+        // (inactive rows among them), so that whatever its q holds (NaN included) never
+        // reaches d_key through the zero columns of its dS
+        stg16(w.qcat + hr * C::DT + c, ntok > 0 ? v : z4);
       }
     }
     // delta = dO . O (fp32) per head: 8 threads per head, D/8 columns each
@@ -258,6 +266,8 @@ __global__ __launch_bounds__(BWV * 64) void sfa_bwd_rows_kernel(SfaBwdArgs a, Sf
       const int64_t hr = (int64_t)r * n1 + h0 + h;
       for (int c = part8 * 8; c < D; c += 64) {
         const uint4 o = ldg16(ob + hr * D + c), gv = ldg16(gob + hr * D + c);
+        // the B operand of the d_value product (zeros for a row without tokens, as above)
+        stg16(w.gocat + hr * D + c, ntok > 0 ? gv : z4);
         const uint32_t ow[4] = {o.x, o.y, o.z, o.w}, gw[4] = {gv.x, gv.y, gv.z, gv.w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -618,13 +628,82 @@ hipError_t launch_place(const SfaBwdArgs& a, const BwdWs& w, hipStream_t s) {
   return hipGetLastError();
 }
 
-// ---- library GEMMs. One hipBLASLt handle per device, created on the device's first
-// backward call (the library allocates its own small state then), and the algorithm
-// hipBLASLt's heuristic ranks first, cached per product shape. In column-major terms
-// the product of a batch is C^T [N x nk] = B^T [N x K] * A^T [K x nk]: B^T is the
-// row-major [K x N] operand (q, q_rope or d_out rows of the batch, ld N), A^T the
-// row-major dense [nk x kp] buffer (ld kp, its first K = nq * N1 columns), C^T the
-// row-major staged [nk x N] rows (ld N).
+// ---- library GEMMs. hipBLASLt is loaded (dlopen) by the first backward call, so the
+// indexer / forward library has no load-time dependency on it. One handle per device,
+// created on that device's first backward call outside stream capture (the library
+// allocates its own small state then). The algorithm of a product is fixed per shape: the
+// entry of hipBLASLt's ranked heuristic list that a committed table names for the shape
+// (measured on this image's hipBLASLt), else the list's first entry. The list is a
+// deterministic function of the library build and the product's shape, so every process
+// uses the same kernel and gets the same bits; nothing is timed and the host never waits.
+struct LtApi {
+  decltype(&hipblasLtCreate) create = nullptr;
+  decltype(&hipblasLtMatmulDescCreate) desc_create = nullptr;
+  decltype(&hipblasLtMatmulDescSetAttribute) desc_set = nullptr;
+  decltype(&hipblasLtMatmulDescDestroy) desc_destroy = nullptr;
+  decltype(&hipblasLtMatrixLayoutCreate) layout_create = nullptr;
+  decltype(&hipblasLtMatrixLayoutSetAttribute) layout_set = nullptr;
+  decltype(&hipblasLtMatrixLayoutDestroy) layout_destroy = nullptr;
+  decltype(&hipblasLtMatmulPreferenceCreate) pref_create = nullptr;
+  decltype(&hipblasLtMatmulPreferenceSetAttribute) pref_set = nullptr;
+  decltype(&hipblasLtMatmulPreferenceDestroy) pref_destroy = nullptr;
+  decltype(&hipblasLtMatmulAlgoGetHeuristic) heuristic = nullptr;
+  decltype(&hipblasLtMatmul) matmul = nullptr;
+  bool ok = false;
+  std::string error;
+};
+const LtApi& lt_api() {
+  static LtApi api;
+  static std::once_flag once;
+  std::call_once(once, [] {
+    void* h = nullptr;
+    for (const char* name : {"libhipblaslt.so.1", "libhipblaslt.so", "/opt/rocm/lib/libhipblaslt.so.1"})
+      if ((h = dlopen(name, RTLD_NOW | RTLD_LOCAL)) != nullptr) break;
+    if (!h) {
+      const char* e = dlerror();
+      api.error = std::string("hipBLASLt could not be loaded: ") + (e ? e : "libhipblaslt.so.1 not found");
+      return;
+    }
+    bool all = true;
+    auto sym = [&](auto& fn, const char* name) {
+      fn = reinterpret_cast<std::remove_reference_t<decltype(fn)>>(dlsym(h, name));
+      all = all && fn != nullptr;
+    };
+    sym(api.create, "hipblasLtCreate");
+    sym(api.desc_create, "hipblasLtMatmulDescCreate");
+    sym(api.desc_set, "hipblasLtMatmulDescSetAttribute");
+    sym(api.desc_destroy, "hipblasLtMatmulDescDestroy");
+    sym(api.layout_create, "hipblasLtMatrixLayoutCreate");
+    sym(api.layout_set, "hipblasLtMatrixLayoutSetAttribute");
+    sym(api.layout_destroy, "hipblasLtMatrixLayoutDestroy");
+    sym(api.pref_create, "hipblasLtMatmulPreferenceCreate");
+    sym(api.pref_set, "hipblasLtMatmulPreferenceSetAttribute");
+    sym(api.pref_destroy, "hipblasLtMatmulPreferenceDestroy");
+    sym(api.heuristic, "hipblasLtMatmulAlgoGetHeuristic");
+    sym(api.matmul, "hipblasLtMatmul");
+    if (!all) {
+      api.error = "hipBLASLt is missing an entry point this library uses";
+      return;
+    }
+    api.ok = true;
+  });
+  return api;
+}
+
+// Committed algorithm choices: the position in the heuristic's ranked list for a product
+// shape (element size, output columns, key rows, contraction, dense row stride, split).
+// Measured at the reference's grad perf shape (perf_sfa_grad_triton.py:23) on this image's
+// hipBLASLt: the [d_key | d_key_rope] product runs 0.167 ms with entry 38 against 0.198 ms
+// with the first entry; for the d_value product the first entry is within 1% of the best.
+struct LtPick {
+  int esize, n_cols, nk, k;
+  int64_t kp;
+  int split, index;
+};
+constexpr LtPick LT_PICKS[] = {
+    {2, 576, 4096, 32768, 32768, 4, 38},
+};
+
 struct LtCache {
   std::mutex mu;
   std::map<int, hipblasLtHandle_t> handle;
@@ -635,24 +714,43 @@ LtCache& lt_cache() {
   return c;
 }
 
-// staged[c][t, col] = sum over j in chunk c of dense[t, j] b_rows[j, col] (fp32), for the
-// `split` equal chunks of the contraction k, as one strided-batched product.
-hipError_t lt_gemm(hipDataType dt, int n_cols, int nk, int k, int split, const void* b_rows, const void* dense,
-                   int64_t kp, float* staged, int64_t split_stride, void* ws, hipStream_t s) {
+// The device's hipBLASLt handle; the first call on a device creates it and must not be
+// under stream capture (hipErrorStreamCaptureUnsupported).
+hipError_t lt_handle(hipStream_t s, hipblasLtHandle_t* h) {
+  const LtApi& api = lt_api();
+  if (!api.ok) return hipErrorSharedObjectInitFailed;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return hipErrorInvalidDevice;
   LtCache& c = lt_cache();
-  hipblasLtHandle_t h;
-  {
-    std::lock_guard<std::mutex> g(c.mu);
-    auto it = c.handle.find(dev);
-    if (it == c.handle.end()) {
-      if (hipblasLtCreate(&h) != HIPBLAS_STATUS_SUCCESS) return hipErrorNotInitialized;
-      c.handle[dev] = h;
-    } else {
-      h = it->second;
-    }
+  std::lock_guard<std::mutex> g(c.mu);
+  auto it = c.handle.find(dev);
+  if (it != c.handle.end()) {
+    *h = it->second;
+    return hipSuccess;
   }
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cap) != hipSuccess) return hipErrorInvalidValue;
+  if (cap != hipStreamCaptureStatusNone) return hipErrorStreamCaptureUnsupported;
+  if (api.create(h) != HIPBLAS_STATUS_SUCCESS) return hipErrorNotInitialized;
+  c.handle[dev] = *h;
+  return hipSuccess;
+}
+
+// staged[c][t, col] = sum over j in chunk c of dense[t, j] b_rows[j, col] (fp32), for the
+// `split` equal chunks of the contraction k, as one strided-batched product. In
+// column-major terms the product of a batch is C^T [N x nk] = B^T [N x K] * A^T [K x nk]:
+// B^T is the row-major [K x N] operand (q | q_rope or d_out rows of the batch, ld N), A^T
+// the row-major dense [nk x kp] buffer (ld kp, its first K = nq * N1 columns), C^T the
+// row-major staged [nk x N] rows (ld N).
+hipError_t lt_gemm(hipDataType dt, int n_cols, int nk, int k, int split, const void* b_rows, const void* dense,
+                   int64_t kp, float* staged, int64_t split_stride, void* ws, hipStream_t s) {
+  const LtApi& api = lt_api();
+  hipblasLtHandle_t h;
+  hipError_t he = lt_handle(s, &h);
+  if (he != hipSuccess) return he;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return hipErrorInvalidDevice;
+  LtCache& c = lt_cache();
   hipblasLtMatmulDesc_t desc = nullptr;
   hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
   hipblasLtMatmulPreference_t pref = nullptr;
@@ -661,30 +759,24 @@ hipError_t lt_gemm(hipDataType dt, int n_cols, int nk, int k, int split, const v
   const uint64_t wsb = LT_WS;
   const float alpha = 1.f, beta = 0.f;
   do {
-    if (hipblasLtMatmulDescCreate(&desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS) break;
-    if (hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_TRANSA, &op, sizeof(op)) != HIPBLAS_STATUS_SUCCESS ||
-        hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_TRANSB, &op, sizeof(op)) != HIPBLAS_STATUS_SUCCESS)
+    if (api.desc_create(&desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS) break;
+    if (api.desc_set(desc, HIPBLASLT_MATMUL_DESC_TRANSA, &op, sizeof(op)) != HIPBLAS_STATUS_SUCCESS ||
+        api.desc_set(desc, HIPBLASLT_MATMUL_DESC_TRANSB, &op, sizeof(op)) != HIPBLAS_STATUS_SUCCESS)
       break;
     const int kc = k / split;
-    if (hipblasLtMatrixLayoutCreate(&la, dt, n_cols, kc, n_cols) != HIPBLAS_STATUS_SUCCESS ||
-        hipblasLtMatrixLayoutCreate(&lb, dt, kc, nk, kp) != HIPBLAS_STATUS_SUCCESS ||
-        hipblasLtMatrixLayoutCreate(&lc, HIP_R_32F, n_cols, nk, n_cols) != HIPBLAS_STATUS_SUCCESS)
+    if (api.layout_create(&la, dt, n_cols, kc, n_cols) != HIPBLAS_STATUS_SUCCESS ||
+        api.layout_create(&lb, dt, kc, nk, kp) != HIPBLAS_STATUS_SUCCESS ||
+        api.layout_create(&lc, HIP_R_32F, n_cols, nk, n_cols) != HIPBLAS_STATUS_SUCCESS)
       break;
     if (split > 1) {
       const int32_t bc = split;
       const int64_t sa = (int64_t)kc * n_cols, sb = kc, sc = split_stride;
-      if (hipblasLtMatrixLayoutSetAttribute(la, HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &bc, sizeof(bc)) !=
-              HIPBLAS_STATUS_SUCCESS ||
-          hipblasLtMatrixLayoutSetAttribute(la, HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &sa, sizeof(sa)) !=
-              HIPBLAS_STATUS_SUCCESS ||
-          hipblasLtMatrixLayoutSetAttribute(lb, HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &bc, sizeof(bc)) !=
-              HIPBLAS_STATUS_SUCCESS ||
-          hipblasLtMatrixLayoutSetAttribute(lb, HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &sb, sizeof(sb)) !=
-              HIPBLAS_STATUS_SUCCESS ||
-          hipblasLtMatrixLayoutSetAttribute(lc, HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &bc, sizeof(bc)) !=
-              HIPBLAS_STATUS_SUCCESS ||
-          hipblasLtMatrixLayoutSetAttribute(lc, HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &sc, sizeof(sc)) !=
-              HIPBLAS_STATUS_SUCCESS)
+      if (api.layout_set(la, HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &bc, sizeof(bc)) != HIPBLAS_STATUS_SUCCESS ||
+          api.layout_set(la, HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &sa, sizeof(sa)) != HIPBLAS_STATUS_SUCCESS ||
+          api.layout_set(lb, HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &bc, sizeof(bc)) != HIPBLAS_STATUS_SUCCESS ||
+          api.layout_set(lb, HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &sb, sizeof(sb)) != HIPBLAS_STATUS_SUCCESS ||
+          api.layout_set(lc, HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &bc, sizeof(bc)) != HIPBLAS_STATUS_SUCCESS ||
+          api.layout_set(lc, HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &sc, sizeof(sc)) != HIPBLAS_STATUS_SUCCESS)
         break;
     }
     hipblasLtMatmulAlgo_t algo;
@@ -698,62 +790,35 @@ hipError_t lt_gemm(hipDataType dt, int n_cols, int nk, int k, int split, const v
         have = true;
       }
     }
-    if (!have) {
-      if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS ||
-          hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb, sizeof(wsb)) !=
-              HIPBLAS_STATUS_SUCCESS)
+    if (!have) {   // host-side query only: no GPU work, no synchronisation
+      if (api.pref_create(&pref) != HIPBLAS_STATUS_SUCCESS ||
+          api.pref_set(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb, sizeof(wsb)) != HIPBLAS_STATUS_SUCCESS)
         break;
       hipblasLtMatmulHeuristicResult_t res[LT_CANDIDATES];
       int nres = 0;
-      if (hipblasLtMatmulAlgoGetHeuristic(h, desc, la, lb, lc, lc, pref, LT_CANDIDATES, res, &nres) !=
-              HIPBLAS_STATUS_SUCCESS ||
+      if (api.heuristic(h, desc, la, lb, lc, lc, pref, LT_CANDIDATES, res, &nres) != HIPBLAS_STATUS_SUCCESS ||
           nres < 1)
         break;
-      algo = res[0].algo;
-      // The heuristic's first choice is not reliably the fastest here (measured up to
-      // 3x slower than others in its own list on these shapes): the first call of a
-      // shape times every candidate on the caller's stream and keeps the fastest. Under
-      // stream capture it keeps the heuristic's choice (timing needs a synchronisation).
-      hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-      if (hipStreamIsCapturing(s, &cap) == hipSuccess && cap == hipStreamCaptureStatusNone && nres > 1) {
-        hipEvent_t e0 = nullptr, e1 = nullptr;
-        if (hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess) {
-          float best = 1e30f;
-          for (int i = 0; i < nres; ++i) {
-            if (res[i].workspaceSize > LT_WS) continue;
-            auto run = [&]() {
-              return hipblasLtMatmul(h, desc, &alpha, b_rows, la, dense, lb, &beta, staged, lc, staged, lc,
-                                     &res[i].algo, ws, LT_WS, s);
-            };
-            if (run() != HIPBLAS_STATUS_SUCCESS) continue;   // warm-up; skips an algorithm that fails
-            float ms = 0.f;
-            if (hipEventRecord(e0, s) != hipSuccess) break;
-            for (int rep = 0; rep < 2; ++rep) run();
-            if (hipEventRecord(e1, s) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
-                hipEventElapsedTime(&ms, e0, e1) != hipSuccess)
-              break;
-            if (ms < best) {
-              best = ms;
-              algo = res[i].algo;
-            }
-          }
-        }
-        if (e0) hipEventDestroy(e0);
-        if (e1) hipEventDestroy(e1);
-      }
+      int pick = 0;
+      const int esize = 2;   // bf16 / fp16 operands
+      for (const LtPick& p : LT_PICKS)
+        if (p.esize == esize && p.n_cols == n_cols && p.nk == nk && p.k == k && p.kp == kp && p.split == split &&
+            p.index < nres && res[p.index].workspaceSize <= LT_WS)
+          pick = p.index;
+      algo = res[pick].algo;
       std::lock_guard<std::mutex> g(c.mu);
       c.algo[key] = algo;
     }
-    if (hipblasLtMatmul(h, desc, &alpha, b_rows, la, dense, lb, &beta, staged, lc, staged, lc, &algo, ws, LT_WS, s) !=
+    if (api.matmul(h, desc, &alpha, b_rows, la, dense, lb, &beta, staged, lc, staged, lc, &algo, ws, LT_WS, s) !=
         HIPBLAS_STATUS_SUCCESS)
       break;
     ret = hipSuccess;
   } while (false);
-  if (pref) hipblasLtMatmulPreferenceDestroy(pref);
-  if (lc) hipblasLtMatrixLayoutDestroy(lc);
-  if (lb) hipblasLtMatrixLayoutDestroy(lb);
-  if (la) hipblasLtMatrixLayoutDestroy(la);
-  if (desc) hipblasLtMatmulDescDestroy(desc);
+  if (pref) api.pref_destroy(pref);
+  if (lc) api.layout_destroy(lc);
+  if (lb) api.layout_destroy(lb);
+  if (la) api.layout_destroy(la);
+  if (desc) api.desc_destroy(desc);
   return ret;
 }
 
@@ -782,6 +847,7 @@ size_t bwd_fixed_bytes(int total_rows, int batch, int topk, int sbs, int64_t sta
   off += align256((size_t)BSPLIT * staged * (d + BDR) * 4);
   off += align256((size_t)BSPLIT * staged * d * 4);
   off += align256((size_t)(total_rows > 0 ? total_rows : 0) * n1 * (d + BDR) * 2);
+  off += align256((size_t)(total_rows > 0 ? total_rows : 0) * n1 * d * 2);
   off += LT_WS;
   return off;
 }
@@ -822,6 +888,8 @@ hipError_t launch_sfa_bwd(const SfaBwdArgs& a, hipStream_t s) {
   }
   w.qcat = reinterpret_cast<uint16_t*>(base + off);
   off += dsa::align256((size_t)(f.total_rows > 0 ? f.total_rows : 0) * f.n1 * (f.d + dsa::BDR) * 2);
+  w.gocat = reinterpret_cast<uint16_t*>(base + off);
+  off += dsa::align256((size_t)(f.total_rows > 0 ? f.total_rows : 0) * f.n1 * f.d * 2);
   w.lt_ws = base + off;
   off += dsa::LT_WS;
   // the two dense buffers split what is left (256-byte aligned halves)
@@ -856,7 +924,6 @@ hipError_t launch_sfa_bwd(const SfaBwdArgs& a, hipStream_t s) {
   if (e != hipSuccess) return e;
   // the two products of every batch holding query rows and key tokens
   const hipDataType dt = f.io == dsa::IO_BF16 ? HIP_R_16BF : HIP_R_16F;
-  const uint16_t* go = reinterpret_cast<const uint16_t*>(a.d_out);
   int64_t doff = 0, soff = 0;
   for (int b = 0; b < f.batch; ++b) {
     const int rs = a.h_row_start[b], nq = a.h_row_start[b + 1] - rs;
@@ -868,7 +935,7 @@ hipError_t launch_sfa_bwd(const SfaBwdArgs& a, hipStream_t s) {
       const int dt_w = f.d + dsa::BDR;
       if ((e = dsa::lt_gemm(dt, dt_w, nk, k, w.split, w.qcat + brow * dt_w, w.dst + doff, kp, w.skc + soff * dt_w,
                             hg.staged * dt_w, w.lt_ws, s)) != hipSuccess ||
-          (e = dsa::lt_gemm(dt, f.d, nk, k, w.split, go + brow * f.d, w.pt + doff, kp, w.sv + soff * f.d,
+          (e = dsa::lt_gemm(dt, f.d, nk, k, w.split, w.gocat + brow * f.d, w.pt + doff, kp, w.sv + soff * f.d,
                             hg.staged * f.d, w.lt_ws, s)) != hipSuccess)
         return e;
     }
@@ -877,3 +944,5 @@ hipError_t launch_sfa_bwd(const SfaBwdArgs& a, hipStream_t s) {
   }
   return dsa::launch_place(a, w, s);
 }
+
+const char* sfa_bwd_library_error() { return dsa::lt_api().error.c_str(); }

@@ -286,3 +286,26 @@ def test_noalloc_refuses_problems_beyond_the_scratch():
     bad = list(args)
     bad[18] = 64
     assert lib.dsa_sfa_fwd_noalloc(*bad) == _lib.DSA_ERR_INVALID and b"D must be" in lib.dsa_last_error()
+
+
+def test_library_has_no_load_time_hipblaslt_dependency():
+    """hipBLASLt (the SFA backward's library GEMMs) is loaded with dlopen on the first
+    backward call: the indexer / forward library must load without it."""
+    import subprocess
+    out = subprocess.run(["readelf", "-d", str(_lib.LIB_PATH)], capture_output=True, text=True, check=True).stdout
+    needed = re.findall(r"\(NEEDED\)\s+Shared library: \[([^\]]+)\]", out)
+    assert needed, out
+    assert not any("blas" in n for n in needed), needed
+
+
+def test_grad_rejects_decreasing_host_row_start():
+    """The host copies of the row offsets size and place the library GEMMs: an entry out
+    of order is refused before any device work."""
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    rs = (ctypes.c_int32 * 4)(0, 5, 3, 8)
+    ak = (ctypes.c_int32 * 3)(64, 64, 64)
+    st = lib.dsa_sfa_bwd(p, p, p, p, 1, p, 16, 1, p, p, p, p, ctypes.cast(rs, ctypes.c_void_p),
+                         ctypes.cast(ak, ctypes.c_void_p), 3, 8, 8, 128, 64, 64, 192, 3, 0.1, p, p, p, p,
+                         p, p, p, p, p, p, 1 << 30, None)
+    assert st == _lib.DSA_ERR_INVALID and b"non-decreasing" in lib.dsa_last_error()

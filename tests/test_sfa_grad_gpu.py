@@ -238,3 +238,78 @@ def test_grad_poisoned_workspace(dev, N1, D):
     torch.cuda.synchronize()
     for name, a, b in zip(("dq", "dk", "dv", "dqr", "dkr"), got, want):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16)), f"N1={N1} D={D}: {name} differs"
+
+
+def test_grad_nan_in_inactive_rows_does_not_leak(dev):
+    """Rows past act_q take no part in the backward (the reference masks them, row_active at
+    sparse_flash_attention_grad_triton.py:229): NaN in their q, q_rope and d_out must leave
+    every gradient of the batch finite and bit-identical to a run with finite values there."""
+    B, S1, S2, N1, D, count = 2, 12, 256, 16, 512, 64
+    act_q, act_k = [9, 12], [200, 256]
+    q, k, v, qr, kr, do = _inputs(B, S1, S2, N1, D, "bf16", seed=17)
+    si = _ref_indices(B, S1, S2, count, 1, 3, act_q, act_k, seed=4)
+    scale = 1.0 / math.sqrt(D + 64)
+    g = lambda x: x.to(dev)
+    k, kr, sit = g(k), g(kr), g(torch.from_numpy(si))
+
+    def run(qq, qqr, ddo):
+        out, smax, ssum = sparse_flash_attention(qq, k, k, sit, scale_value=scale, actual_seq_lengths_query=act_q,
+                                                 actual_seq_lengths_kv=act_k, query_rope=qqr, key_rope=kr,
+                                                 sparse_mode=3, return_softmax_lse=True)
+        grads = sparse_flash_attention_grad(qq, k, k, sit, ddo, out, smax, ssum, scale_value=scale, query_rope=qqr,
+                                            key_rope=kr, actual_seq_lengths_query=act_q,
+                                            actual_seq_lengths_kv=act_k, sparse_mode=3)
+        torch.cuda.synchronize()
+        return [x.clone() for x in grads]
+
+    clean = run(g(q), g(qr), g(do))
+    qn, qrn, don = g(q), g(qr), g(do)
+    qn[0, 9:] = float("nan")     # rows past act_q of batch 0
+    qrn[0, 9:] = float("nan")
+    don[0, 9:] = float("nan")
+    dirty = run(qn, qrn, don)
+    for name, a, b in zip(("dq", "dk", "dv", "dqr", "dkr"), dirty, clean):
+        assert torch.isfinite(a.float()).all(), f"{name}: NaN leaked"
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), f"{name} differs"
+
+
+_REPRO_SCRIPT = r"""
+import sys, math, numpy as np, torch
+sys.path.insert(0, sys.argv[1])
+from tests.test_sfa_grad_gpu import _inputs, _ref_indices
+from dsa_triton_ascend_amd import sparse_flash_attention, sparse_flash_attention_grad
+dev = torch.device("cuda:0")
+B, S1, S2, N1, D, count = 1, 512, 4096, 64, 512, 2048
+q, k, v, qr, kr, do = _inputs(B, S1, S2, N1, D, "bf16", seed=3)
+si = _ref_indices(B, S1, S2, count, 1, 3)
+scale = 1.0 / math.sqrt(D + 64)
+g = lambda x: x.to(dev)
+out, smax, ssum = sparse_flash_attention(g(q), g(k), g(k), g(torch.from_numpy(si)), scale_value=scale,
+                                         query_rope=g(qr), key_rope=g(kr), sparse_mode=3, return_softmax_lse=True)
+dq, dk, dv, dqr, dkr = sparse_flash_attention_grad(g(q), g(k), g(k), g(torch.from_numpy(si)), g(do), out, smax,
+                                                   ssum, scale_value=scale, query_rope=g(qr), key_rope=g(kr),
+                                                   sparse_mode=3)
+torch.cuda.synchronize()
+np.savez(sys.argv[2], **{n: t.view(torch.int16).cpu().numpy() for n, t in
+                        zip(("dq", "dk", "dv", "dqr", "dkr"), (dq, dk, dv, dqr, dkr))})
+print("saved", flush=True)
+"""
+
+
+def test_grad_bitwise_reproducible_across_processes(tmp_path):
+    """The library GEMMs' algorithm is fixed per shape (no per-process timing), so two fresh
+    processes produce the same gradient bits at the reference's grad perf shape
+    (perf_sfa_grad_triton.py:23)."""
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = str(Path(__file__).resolve().parents[1])
+    files = []
+    for i in range(2):   # one after the other: never more than one extra process on the GPU
+        f = tmp_path / f"g{i}.npz"
+        r = subprocess.run([sys.executable, "-c", _REPRO_SCRIPT, root, str(f)], capture_output=True, text=True,
+                           timeout=240)
+        assert r.returncode == 0, r.stderr[-2000:]
+        files.append(np.load(f))
+    for name in ("dq", "dk", "dv", "dqr", "dkr"):
+        assert np.array_equal(files[0][name], files[1][name]), f"{name} differs between processes"
