@@ -177,17 +177,19 @@ int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key,
  * that cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc). Arguments, semantics and outputs are those
  * of dsa_sfa_fwd (same kernels); the workspace is the library's static per-device
- * scratch array of DSA_SFA_NOALLOC_SCRATCH_BYTES, which each GPU the library runs on
- * holds until the process ends. A problem whose dsa_sfa_workspace_bytes(...) exceeds
- * that size is refused with DSA_ERR_UNSUPPORTED before any device work (e.g. C4 decode,
- * 64 rows x 2048 tokens, and C3 prefill, 4096 rows x 2048 tokens, fit). The call
+ * scratch array of DSA_SFA_NOALLOC_SCRATCH_BYTES (40 MiB), part of the library's code
+ * object: every process that loads the library holds it on every GPU where the module is
+ * loaded, until the process ends, whether or not it calls this entry point. A problem
+ * whose dsa_sfa_workspace_bytes(...) exceeds that size is refused with
+ * DSA_ERR_UNSUPPORTED before any device work (C4 decode, 64 rows x 2048 tokens: 32.9 MiB,
+ * and C3 prefill, 4096 rows x 2048 tokens: 32.0 MiB, fit). The call
  * allocates nothing; its first call on a device looks up that device's copy of the
  * array and clears its zero-row prefix once (synchronising the given stream unless it
  * is capturing). Every call on one GPU shares that GPU's array: calls that overlap on
  * one GPU (different streams, or host threads without ordering) race and must be
  * serialised by the caller.
  */
-#define DSA_SFA_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+#define DSA_SFA_NOALLOC_SCRATCH_BYTES ((size_t)40 << 20)
 
 int dsa_sfa_fwd_noalloc(const void* query, const void* query_rope, const void* key,
                         const void* key_rope, int io_dtype, const int32_t* sparse_indices,

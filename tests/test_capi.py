@@ -270,7 +270,7 @@ def test_noalloc_refuses_problems_beyond_the_scratch():
     exceeds its static scratch, before any device work (no GPU needed)."""
     lib = _lib.load()
     one = ctypes.c_void_p(1)
-    limit = 64 << 20
+    limit = 40 << 20   # DSA_SFA_NOALLOC_SCRATCH_BYTES
     # C5-sized prefill: 18216 rows x 2048 tokens of token lists alone exceed the scratch
     assert lib.dsa_sfa_workspace_bytes(18216, 128, 512, 2048, 1, 0) > limit
     args = [one, one, one, one, 1, one, 2048, 1, None, 0, 0, one, one, one, one, 4, 18216, 128, 512, 64, 8192,
