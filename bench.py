@@ -447,6 +447,25 @@ def main():
         breakdown["indexer_c1"] = {"ms": round(gpu_ms["c1_ms"], 4),
                                    "rows_per_s": round(256 / (gpu_ms["c1_ms"] * 1e-3), 1)}
         del p1, i1
+        log("[bench] lightning_indexer at the reference's perf_li shape ...")
+        # perf_li_triton.py:43: B=1, S1=512, S2=4096, N1=64, N2=1, D=128, top-k 2048, fp16
+        # inputs, fp32 weights N(0,1), the cell's default causal mode 3
+        ip = W.indexer_inputs(B=1, S1=512, S2=4096, N1=64, N2=1, D=128, sparse_count=2048, sparse_mode=3,
+                              w_scale=1.0, dtype=torch.float16, device="cuda:0", seed=42)
+        pp = IndexerPlan(ip.query, ip.key, ip.weights, sparse_count=2048, sparse_mode=3, return_value=True)
+        warm(pp.run, torch)
+        ms_li, ms_li_score, ms_li_topk = event_time([pp.run, pp.score, pp.topk], 50, torch)
+        pairs_li = sum(4096 - 512 + s + 1 for s in range(512))
+        f_li = 2.0 * pairs_li * 64 * 128
+        breakdown["indexer_perf_li"] = {"ms": round(ms_li, 4), "score_ms": round(ms_li_score, 4),
+                                        "topk_ms": round(ms_li_topk, 4),
+                                        "rows_per_s": round(512 / (ms_li * 1e-3), 1),
+                                        "score_tflops": round(f_li / ms_li_score / 1e9, 2),
+                                        "score_frac_mfma": round(f_li / ms_li_score / 1e9 / PEAK_BF16_TFLOPS, 4),
+                                        "algorithmic_flop": f_li,
+                                        "shape": "BSND B=1 S1=512 S2=4096 N1=64 N2=1 D=128 top-k 2048 causal fp16 "
+                                                 "(perf_li_triton.py:43)"}
+        del pp, ip
         steps = max(3, args.steps // 4)
         try:
             log("[bench] C3 SFA prefill ...")

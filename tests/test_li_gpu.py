@@ -186,6 +186,16 @@ def test_c2_full_size_sampled(dev):
     assert stats.flips <= max(4, 0.01 * stats.elements), stats
 
 
+@pytest.mark.slow
+@pytest.mark.parametrize("S1,S2", [(4096, 4096), (4096, 8192), (16384, 16384)])
+def test_reference_production_shapes(dev, S1, S2):
+    """The reference's production shapes (test_li_triton.py:49-51): 4096 x 4096, S2 > S1
+    (non-square causal, the reference's grid-overflow regression point) and 16K x 16K, 64
+    heads, D=128, top-2048: top-k invariants on every row, oracle parity on stride-sampled
+    rows spanning the causal triangle."""
+    run_case(dev, 1, S1, S2, 64, 1, 128, 2048, 3, "bf16", max_rows=48)
+
+
 @pytest.mark.parametrize("mode", [0, 3])
 def test_rows_longer_than_register_cache(dev, mode):
     """S2 = 12,000 > 8,192: the top-k streams a row's keys from memory in two chunks (the

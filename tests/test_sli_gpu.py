@@ -175,6 +175,17 @@ def test_kl_loss_target_shape(dev, dtype):
     run(dev, 1, 512, 4096, 64, 512, 64, 128, 2048, dtype, pattern="causal_continuous", loose=True)
 
 
+@pytest.mark.slow
+@pytest.mark.parametrize("shape,dtype", [((1, 1024, 1024, 32, 512, 8, 128, 1024), "fp16"),
+                                         ((1, 1024, 1024, 32, 512, 8, 128, 1024), "bf16"),
+                                         ((1, 4096, 4096, 64, 512, 64, 128, 2048), "bf16")])
+def test_kl_loss_large_loose_shapes(dev, shape, dtype):
+    """The reference's two largest loose-group shapes (test_sli_grad_kl_loss_triton.py:31-32),
+    causal_continuous ids: every row against the full fp32 oracle pass; d_key_index (summed
+    over 1024 / 4096 query rows through the key-major pass) by relative Frobenius norm."""
+    run(dev, *shape, dtype, pattern="causal_continuous", loose=True)
+
+
 @pytest.mark.parametrize("pattern", ["causal_random", "repeated"])
 def test_kl_loss_loose_shapes(dev, pattern):
     """The reference's loose group shapes with S2 = 4096 (:27-33): ids drawn from each row's
