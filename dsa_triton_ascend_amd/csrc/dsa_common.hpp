@@ -245,6 +245,7 @@ struct LiScoreArgs {
   // PA_BSND keys (block_table != nullptr): token t of batch b is row
   // block_table[b * max_blocks + t / page_bs] * page_bs + t % page_bs of `k`
   const int32_t* block_table = nullptr; int max_blocks = 0; int page_bs = 0; int64_t key_rows = 0;
+  int key_split = 1;   // work-groups per row block, each over a share of its key tiles (set by the launcher)
 };
 constexpr int LI_MAX_BLOCKS = 8192;   // block-table row held in LDS by the paged score kernel
 constexpr int LI_TOPK_MAX_K = 16384;  // top-k: the selected keys and their indices sorted in LDS

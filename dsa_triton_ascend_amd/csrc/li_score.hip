@@ -91,7 +91,12 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int b = blockIdx.z;
   const int n2 = blockIdx.y;
-  const int rb = gridDim.x - 1 - blockIdx.x;  // heaviest row block first
+  // blockIdx.x = (row block, key chunk): with few row blocks (short query batches) the
+  // visible keys of a row block are split over `ksplit` work-groups, each writing the
+  // scores of its own tiles (no reduction: every key's score is independent)
+  const int ksplit = a.key_split > 1 ? a.key_split : 1;
+  const int kc = (int)blockIdx.x % ksplit;
+  const int rb = (int)(gridDim.x / ksplit) - 1 - (int)blockIdx.x / ksplit;  // heaviest row block first
   const int G = a.n1 / a.n2;
 
   const int rows_b = a.row_start[b + 1] - a.row_start[b];
@@ -143,7 +148,11 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
   // When the batch's key rows span less than 4 GiB from kbase (S2 * N2 * D < 2^31)
   // the byte offset of a load is a per-lane constant plus one scalar tile offset,
   // and a full tile's loads take the SGPR-base form: one VALU add per load.
-  const int ntiles = (L_blk + T::BN - 1) / T::BN;
+  const int ntiles_all = (L_blk + T::BN - 1) / T::BN;
+  const int tiles_per = (ntiles_all + ksplit - 1) / ksplit;
+  const int t0 = kc * tiles_per;                  // this work-group's tiles [t0, ntiles)
+  const int ntiles = t0 + tiles_per < ntiles_all ? t0 + tiles_per : ntiles_all;
+  if (t0 >= ntiles) return;
   const uint32_t ksb = (uint32_t)(a.n2 * D * 2);   // key row stride in bytes
   const bool off32 = !PAGED && (uint64_t)(uint32_t)a.s2 * ksb <= 0xFFFFFFFFull;
   int dk[T::IPW];          // key row of load j within the tile
@@ -176,7 +185,7 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
     for (int j = 0; j < T::IPW; ++j) dma_part(tile, buf, j);
   };
 #pragma unroll
-  for (int j = 0; j < T::NBUF - 1; ++j) dma(j, kt[j]);
+  for (int j = 0; j < T::NBUF - 1; ++j) dma(t0 + j, kt[j]);
 
   // ---- per-row operands: Q fragments (A) and head weights
   uint4 qf[QREG ? MT : 1][QREG ? KK : 1];
@@ -388,7 +397,7 @@ __global__ __launch_bounds__(NW * 64) void li_score_kernel(LiScoreArgs a) {
   static_assert(T::NBUF == 3, "the ring below is unrolled for three buffers");
   wait_vmcnt<0>();
   lds_barrier();
-  for (int t = 0; t < ntiles; t += 3) {
+  for (int t = t0; t < ntiles; t += 3) {
     tile_body(std::integral_constant<int, 0>{}, t);
     if (t + 1 >= ntiles) break;
     tile_body(std::integral_constant<int, 1>{}, t + 1);
@@ -413,8 +422,16 @@ void launch_mt(const LiScoreArgs& a, hipStream_t s, int MT, dim3 grid, dim3 bloc
 }
 
 template <int IO, int D>
-hipError_t launch_d(const LiScoreArgs& a, hipStream_t s, int MT) {
-  dim3 grid((a.max_rows_per_batch + NW - 1) / NW, a.n2, a.batch), block(NW * 64);
+hipError_t launch_d(const LiScoreArgs& a0, hipStream_t s, int MT) {
+  LiScoreArgs a = a0;
+  // Short query batches leave most CUs idle (one 8-row work-group per CU): split each row
+  // block's keys over enough work-groups for ~2 per CU, keeping at least 4 tiles each.
+  const int64_t blocks = (int64_t)((a.max_rows_per_batch + NW - 1) / NW) * a.n2 * a.batch;
+  const int max_tiles = (a.max_kv + LiTile<D>::BN - 1) / LiTile<D>::BN;
+  int ks = (int)((512 + blocks - 1) / blocks);
+  ks = ks < max_tiles / 4 ? ks : max_tiles / 4;
+  a.key_split = ks > 1 ? (ks < 16 ? ks : 16) : 1;
+  dim3 grid((unsigned)(((a.max_rows_per_batch + NW - 1) / NW) * a.key_split), a.n2, a.batch), block(NW * 64);
   if (a.block_table)
     launch_mt<IO, D, true>(a, s, MT, grid, block);
   else
