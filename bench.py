@@ -352,6 +352,11 @@ def pmc_pass(torch, W):
     plan.run()
     torch.cuda.synchronize()
     del plan, inp
+    li = W.indexer_inputs(B=1, S1=512, S2=4096, N1=64, N2=1, D=128, sparse_count=2048, sparse_mode=3,
+                          w_scale=1.0, dtype=torch.float16, device=dev, seed=42)   # perf_li shape
+    IndexerPlan(li.query, li.key, li.weights, sparse_count=2048, sparse_mode=3, return_value=True).run()
+    torch.cuda.synchronize()
+    del li
     for mk in (W.sfa_prefill_inputs, W.sfa_decode_inputs):
         si = mk(device="cuda:0", seed=42)
         AttentionPlan(query=si.query, key=si.key, value=si.key, sparse_indices=si.sparse_indices,
