@@ -118,6 +118,28 @@ __device__ __forceinline__ void mfma32_vacc(f32x16& c, uint4 a, uint4 b) {   // 
 // Wait states after the last MFMA of a VGPR chain: an 8-pass XDL result read (or
 // its operands overwritten) by VALU needs 11; 18 covers every XDL pass count.
 __device__ __forceinline__ void vacc_drain(f32x16& c) { asm volatile("s_nop 15\n\ts_nop 1" : "+v"(c)); }
+// The last step of a chain with its drain in the same statement: the compiler may copy
+// the accumulator to other registers between two asm statements (a copy it places before
+// a separate vacc_drain would read the MFMA's result in flight), never inside one.
+template <int IO>
+__device__ __forceinline__ void mfma32_vacc_last(f32x16& c, uint4 a, uint4 b) {   // c += A B, drained
+  const i32x4v av = __builtin_bit_cast(i32x4v, a), bv = __builtin_bit_cast(i32x4v, b);
+  if constexpr (IO == IO_BF16)
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0\n\ts_nop 15\n\ts_nop 1" : "+v"(c) : "v"(av), "v"(bv));
+  else
+    asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0\n\ts_nop 15\n\ts_nop 1" : "+v"(c) : "v"(av), "v"(bv));
+}
+// Same with the result in other registers than the accumulator read (c + A B, drained).
+template <int IO>
+__device__ __forceinline__ f32x16 mfma32_vacc_last_to(const f32x16& c, uint4 a, uint4 b) {
+  f32x16 d;
+  const i32x4v av = __builtin_bit_cast(i32x4v, a), bv = __builtin_bit_cast(i32x4v, b);
+  if constexpr (IO == IO_BF16)
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %3\n\ts_nop 15\n\ts_nop 1" : "=&v"(d) : "v"(av), "v"(bv), "v"(c));
+  else
+    asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %3\n\ts_nop 15\n\ts_nop 1" : "=&v"(d) : "v"(av), "v"(bv), "v"(c));
+  return d;
+}
 
 // Output layouts (CDNA3/CDNA4 MFMA, 64 lanes):
 //  32x32: lane l, acc[r] (r < 16) holds C[row = (r/4)*8 + (l/32)*4 + r%4][col = l%32]
@@ -211,6 +233,18 @@ __device__ __forceinline__ uint2 ds_read_tr(const void* lds_ptr) {
   s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (__attribute__((address_space(3))) s16x4*)(const_cast<void*>(lds_ptr)));
   return __builtin_bit_cast(uint2, v);
+}
+
+// The same at a 32-bit LDS byte address (constant offsets added to it fold into the
+// instruction's offset field).
+__device__ __forceinline__ uint2 ds_read_tr_at(uint32_t lds_addr) {
+  s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)lds_addr);
+  return __builtin_bit_cast(uint2, v);
+}
+
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
 // s_waitcnt vmcnt(N) (gfx9 encoding; expcnt and lgkmcnt left unconstrained).

@@ -651,6 +651,7 @@ __device__ __forceinline__ int rope_off(int t, int c) { return (t >> 3) * 1024 +
 struct TileIdx {
   int nope[8];
   int rope;
+  uint32_t zero_rows = 0;   // OFF32: nope rows (bit j: part j) whose id is out of range
 };
 
 // One of the GPW - 1 gather loads of a tile for wave w: part j < 8 copies the
@@ -658,7 +659,11 @@ struct TileIdx {
 // of the wave's 8 tokens (lane -> token lane%8, chunk lane/8). A physical row
 // outside [0, krows) -- -1 for a missing token -- reads the zero row, so no id
 // can address memory outside the key tensors.
-template <int D>
+//
+// OFF32 (key tensor under 4 GiB): a nope part is the key base plus a 32-bit per-lane
+// offset, one VALU op, instead of a 64-bit SGPR address and a zero-row select. Its ids
+// were clamped into range (ix.zero_rows marks the rows the caller zeroes once they land).
+template <int D, bool OFF32 = false>
 __device__ __forceinline__ void gather_part(int j, const uint16_t* kb, const uint16_t* krb,
                                             const uint16_t* zero, int krows, const TileIdx& ix,
                                             uint8_t* nope, uint8_t* rope, int wave_u, int lane) {
@@ -669,6 +674,11 @@ __device__ __forceinline__ void gather_part(int j, const uint16_t* kb, const uin
   if (j < 8) {
     int phys = ix.nope[j];   // wave-uniform: the row base goes in an SGPR pair
     asm volatile("" : "+s"(phys));
+    if constexpr (OFF32) {
+      if (lane < C::LANES_ROW)
+        lds_dma16_sbase_untracked(kb, (uint32_t)phys * (D * 2) + lane * 16, nope + nope_off<D>(wave_u * 8 + j));
+      return;
+    }
     const uint16_t* src = (uint32_t)phys < (uint32_t)krows ? kb + (int64_t)phys * D : zero;
     if (lane < C::LANES_ROW) lds_dma16_sbase_untracked(src, lane * 16, nope + nope_off<D>(wave_u * 8 + j));
   } else {
@@ -709,17 +719,26 @@ __device__ __forceinline__ float agpr_scale(float o, float f) {
 // each tile gives t_p[slot] = (1 / N1) sum_h exp(S scale - t_max[h]) / (t_sum[h] + 1e-8)
 // (in-lane over 16 heads, one lane-half swap, then across the head blocks in LDS), and
 // there is no PV product, softmax state or output.
-template <int IO, int D, int NH, bool TEACH>
+//
+// OWN (128 heads, attention): each wave also runs the PV product of its own 32 heads, over
+// all D columns (O^T[D, 32 heads] in AGPRs). P never leaves the wave's registers: the
+// softmax turns the S^T accumulator into the PV B operands with two lane-half swaps, so
+// no wave waits for another's P, and the transposed V operands of tile t are read ahead
+// during the S^T chain of tile t+1 (four times the V^T reads of the column split, at the
+// LDS rate of conflict-free transposed reads). The softmax of tile t is staged over that
+// chain, and the PV MFMAs of tile t follow it; one barrier per tile guards the ring.
+template <int IO, int D, int NH, bool TEACH, bool OWN = false>
 __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, int splits, int fuse_tok, Ws ws) {
   using C = Cfg<D>;
   static_assert(NH == 128 || NH == 64, "heads per work-group");
+  static_assert(!OWN || (NH == 128 && !TEACH), "per-wave PV: 128-head attention only");
   constexpr int MT = NH / 32;                      // 32-head blocks
   constexpr bool KSPLIT = NH == 64;                // S^T contraction split over wave pairs
   constexpr int KSH = KSPLIT ? C::KS / 2 : C::KS;  // S^T k-steps per wave
   static_assert(!KSPLIT || (C::KS % 2 == 0 && KSH <= C::KSN), "first half of the contraction is nope");
   __shared__ __attribute__((aligned(16))) uint8_t nope_buf[NBUF][C::NOPE];
   __shared__ __attribute__((aligned(16))) uint8_t rope_buf[NBUF][C::ROPE];
-  __shared__ __attribute__((aligned(16))) uint16_t pt[2][NH * PP];   // P of tiles t (PV) and t+1 (softmax)
+  __shared__ __attribute__((aligned(16))) uint16_t pt[2][OWN ? 8 : NH * PP];   // P of tiles t (PV) and t+1 (softmax)
   __shared__ __attribute__((aligned(16))) uint16_t qrs[NH * QRP];   // Q rope of all heads
   __shared__ __attribute__((aligned(16))) int32_t s_ids[4][BN];   // token-id ring (tiles t+2 .. t+4)
   __shared__ float s_alpha[2][NH];   // O rescale factors of tiles t and t+1
@@ -827,16 +846,22 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
       lds_dma16_sbase_untracked(toks + clamp_tile(t) * BN + wave_u * 8, lane * 16, &s_ids[t & 3][wave_u * 8]);
   };
   // ids of tile t from the ring; slots past the token list take the tile's first token
-  auto tile_idx = [&](int t) {
+  // (off32: for gather_part<D, true>, see TileIdx::zero_rows)
+  auto tile_idx = [&](int t, bool off32 = false) {
     const int tb = clamp_tile(t) * BN;
     const int nvalid = ntok - tb < BN ? ntok - tb : BN;
     const int k = wave_u * 8 + (lane & 7);
     int v = s_ids[t & 3][k];
     v = k < nvalid ? v : s_ids[t & 3][0];
     TileIdx ix;
+    ix.rope = v;   // the rope gather selects the zero row itself
+    if (OWN && off32) {   // nope gathers with 32-bit offsets: out-of-range ids read row 0, zeroed later
+      const bool out = (uint32_t)v >= (uint32_t)krows;
+      ix.zero_rows = (uint32_t)__builtin_amdgcn_ballot_w64(out) & 0xFFu;
+      v = out ? 0 : v;
+    }
 #pragma unroll
     for (int i = 0; i < 8; ++i) ix.nope[i] = __builtin_amdgcn_readlane(v, i);
-    ix.rope = v;
     return ix;
   };
   // ---- the ids of tiles 0..3 (copied from the token list, or already written to
@@ -901,44 +926,61 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
     float agpr_hint = 0.f;
     asm volatile("" : "+a"(agpr_hint));
   }
-  f32x16 o[MT][C::NT];
+  // O^T accumulators: [head block][32-column tile] -- all head blocks over this wave's
+  // D/4 columns, or (OWN) this wave's head block over all D columns
+  constexpr int OM = OWN ? 1 : MT;
+  constexpr int ON = OWN ? D / 32 : C::NT;
+  f32x16 o[OM][ON];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+  for (int mt = 0; mt < OM; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < C::NT; ++nt)
+    for (int nt = 0; nt < ON; ++nt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) o[mt][nt][i] = 0.f;
 
   const int tr = lane & 31, kg = lane >> 5;
   const int g16 = lane >> 4, c16 = lane & 15;
   constexpr int KQ = BN / 16;
+  // Token of S^T accumulator row r = 8g + 4h + i (g < 4, h < 2, i < 4). OWN permutes the
+  // rows, 16 (g/2) + 8h + 4 (g%2) + i, so that a lane's 16 scores are tokens 16 kq + 8 (lane/32)
+  // + j (j < 8) of steps kq = 0, 1 -- the PV B operand's order, with no exchange between
+  // lanes; otherwise row r is token r.
+  auto row_tok = [](int r) { return OWN ? 16 * (r >> 4) + 8 * ((r >> 2) & 1) + 4 * ((r >> 3) & 1) + (r & 3) : r; };
+  const int tk_row = row_tok(tr);   // token whose K row this lane supplies to S^T
 
   // ---- S^T[32 tokens, 32 heads] of tile u for this wave over k-steps [K0, K0 + KSH),
   // K0 = KH * KSH; `spread(j)` issues the loads scheduled after the chain's j-th step
   // (the next tile's gathers ride on this chain)
-  auto s_tile_k = [&](int u, auto&& spread, auto khc) __attribute__((always_inline)) -> f32x16 {
+  auto s_tile_k = [&](int u, auto&& spread, auto khc, auto&& pre) __attribute__((always_inline)) -> f32x16 {
     constexpr int K0 = decltype(khc)::value * KSH;
     const uint8_t* nope = nope_buf[u % NBUF];
     const uint8_t* rope = rope_buf[u % NBUF];
     f32x16 sacc = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    const uint8_t* arow = nope + nope_off<D>(tr) + kg * 16;
+    const uint8_t* arow = nope + nope_off<D>(tk_row) + kg * 16;
     // operand loads run 4 k-steps ahead of the MFMA chain; the sched barrier
     // keeps that order (hoisting every load would cost ~4 VGPRs per k-step)
     auto a_frag = [&](int ks) -> uint4 {
       return ks < C::KSN ? *reinterpret_cast<const uint4*>(arow + ks * 32)
-                         : *reinterpret_cast<const uint4*>(rope + rope_off(tr, (ks - C::KSN) * 2 + kg));
+                         : *reinterpret_cast<const uint4*>(rope + rope_off(tk_row, (ks - C::KSN) * 2 + kg));
     };
     // the Q-rope B fragments (LDS) of the chain's rope k-steps are fetched with the
     // first operands, so the rope k-steps at the end of the chain do not wait on LDS
+    // (OWN: with the K operands, as its registers are needed for the V^T operands read
+    // during the chain)
     constexpr int NR = C::KS - C::KSN;
     uint4 qr[NR];
+    auto qr_frag = [&](int j) -> uint4 { return *reinterpret_cast<const uint4*>(qrs + hq * QRP + j * 16 + kg * 8); };
+    if constexpr (!OWN) {
 #pragma unroll
-    for (int j = 0; j < NR; ++j)
-      if (C::KSN + j >= K0 && C::KSN + j < K0 + KSH)
-        qr[j] = *reinterpret_cast<const uint4*>(qrs + hq * QRP + j * 16 + kg * 8);
-    uint4 af[4];
+      for (int j = 0; j < NR; ++j)
+        if (C::KSN + j >= K0 && C::KSN + j < K0 + KSH) qr[j] = qr_frag(j);
+    }
+    // (OWN: five steps ahead -- LDS reads take ~200 cycles under load, four steps ~130)
+    constexpr int KPF = OWN ? 5 : 4;
+    uint4 af[KPF];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) af[j] = a_frag(K0 + j);
+    for (int j = 0; j < KPF; ++j) af[j] = a_frag(K0 + j);
+    pre();   // (OWN: MFMAs that cover the first operands' LDS latency)
 #pragma unroll
     for (int j = 0; j < KSH; ++j) {
       const int ks = K0 + j;
@@ -946,11 +988,17 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
       if constexpr (TEACH) {
         sacc = Mfma<IO>::m32(bq, af[j & 3], sacc);   // S[head, token]
       } else {                                         // S^T[token, head], accumulator in VGPRs
+        // the last step drains in its own statement, before the last step's loads and any VALU
+        // (OWN: into fresh registers, which can be those of the loop-carried scores of the
+        // previous tile -- dead by then -- so the compiler never copies an accumulator in flight)
         if (j == 0) sacc = mfma32_vacc_first<IO>(af[0], bq);
-        else mfma32_vacc<IO>(sacc, af[j & 3], bq);
-        if (j == KSH - 1) vacc_drain(sacc);   // before the last step's loads and any VALU
+        else if (j < KSH - 1) mfma32_vacc<IO>(sacc, af[j % KPF], bq);
+        else if constexpr (OWN) sacc = mfma32_vacc_last_to<IO>(sacc, af[j % KPF], bq);
+        else mfma32_vacc_last<IO>(sacc, af[j % KPF], bq);
       }
-      if (j + 4 < KSH) af[j & 3] = a_frag(ks + 4);
+      if (j + KPF < KSH) af[j % KPF] = a_frag(ks + KPF);
+      if constexpr (OWN)
+        if (j + KPF < KSH && ks + KPF >= C::KSN) qr[ks + KPF - C::KSN] = qr_frag(ks + KPF - C::KSN);
       spread(j);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -961,8 +1009,8 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   auto s_tile = [&](int u, auto&& spread) __attribute__((always_inline)) -> f32x16 {
     if constexpr (KSPLIT) {
       const int kh_u = __builtin_amdgcn_readfirstlane(kh);
-      f32x16 sv = kh_u == 0 ? s_tile_k(u, spread, std::integral_constant<int, 0>{})
-                            : s_tile_k(u, spread, std::integral_constant<int, 1>{});
+      f32x16 sv = kh_u == 0 ? s_tile_k(u, spread, std::integral_constant<int, 0>{}, [] {})
+                            : s_tile_k(u, spread, std::integral_constant<int, 1>{}, [] {});
       const int w_u = __builtin_amdgcn_readfirstlane(wave);
       float* mine = &s_xch[w_u][0];
 #pragma unroll
@@ -981,7 +1029,7 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
       }
       return sv;
     } else {
-      return s_tile_k(u, spread, std::integral_constant<int, 0>{});
+      return s_tile_k(u, spread, std::integral_constant<int, 0>{}, [] {});
     }
   };
 
@@ -991,7 +1039,7 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
     if (nvalid < BN) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int tk = (i >> 2) * 8 + kg * 4 + (i & 3);
+        const int tk = row_tok((i >> 2) * 8 + kg * 4 + (i & 3));
         sv[i] = tk < nvalid ? sv[i] : -INFINITY;
       }
     }
@@ -1123,6 +1171,153 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
     teach_store(ntiles - 1);
     return;
   }
+  if constexpr (OWN) {
+    // Lane's transposed-read base inside a nope buffer: tokens (g16/2)*8 + c16/4 (and +4,
+    // the operand's upper half), columns (g16%2)*16 + 4(c16%4) of a 32-column tile -- the
+    // pattern whose reads land on distinct banks. Token bit 2 is clear there, so
+    // nope_off(t + 4) = nope_off(t) + 4 ROW + 16 and the 16-token steps add 16 ROW.
+    const int vlane = nope_off<D>((g16 >> 1) * 8 + (c16 >> 2)) + ((g16 & 1) * 16 + 4 * (c16 & 3)) * 2;
+    constexpr int NPV = 2 * ON;   // PV MFMAs per tile: two 16-token steps x ON column tiles
+    constexpr int VR = 8;         // V^T operands in flight (8 MFMAs ahead: ~250 cycles)
+    static_assert(NPV >= VR, "V^T operand ring");
+    // the lane's LDS address in buffer `nope`, laundered so that each read's constant
+    // offset goes into the instruction (the compiler would otherwise keep one
+    // precomputed address per read in a VGPR)
+    auto v_base = [&](const uint8_t* nope) __attribute__((always_inline)) -> uint32_t {
+      uint32_t b = lds_addr(nope) + vlane;
+      asm volatile("" : "+v"(b));
+      return b;
+    };
+    auto v_frag = [&](uint32_t b, int m) __attribute__((always_inline)) -> uint4 {
+      const uint32_t p = b + (m / ON) * 16 * C::ROW + (m % ON) * 64;
+      const uint2 lo = ds_read_tr_at(p);
+      const uint2 hi = ds_read_tr_at(p + 4 * C::ROW + 16);
+      return make_uint4(lo.x, lo.y, hi.x, hi.y);
+    };
+    uint4 pb[2];         // P^T of the tile whose PV runs: B operands of its two 16-token steps
+    uint4 pn[2];         // the same for the next tile (the softmax's output)
+    float alpha = 1.f;   // O rescale factor of the next tile (the lane's head)
+    float sm_mx = 0.f, sm_mb = 0.f, sm_sum = 0.f;
+    uint32_t sm_d[4][2];
+    constexpr int NST = 14;   // softmax stages, spread over the previous tile's PV MFMAs
+    // Stage st of the online softmax of raw scores sv (lane: head hq, tokens 16 kq +
+    // 8(lane/32) + j at sv[8 kq + j], see row_tok), each a few VALU ops: 0-3 the max over
+    // four scores each, 4 the tile max and exponent reference, 5-12 two exponentials
+    // each, 13 the row sum and the B operands of the two 16-token steps.
+    auto smx = [&](int st, const f32x16& sv) __attribute__((always_inline)) {
+      if (st < 4) {
+        const int b = 4 * st;
+        sm_mx = st == 0 ? fmaxf(fmaxf(sv[b], sv[b + 1]), fmaxf(sv[b + 2], sv[b + 3]))
+                        : fmaxf(fmaxf(fmaxf(sm_mx, sv[b]), sv[b + 1]), fmaxf(sv[b + 2], sv[b + 3]));
+      } else if (st == 4) {
+        // every tile holds at least one valid token: the max is finite; max(c s) = c max(s), c > 0
+        const float mx = max_half_swap(sm_mx) * cpos;
+        m_true = fmaxf(m_true, mx);
+        const float m_new = mx > m_used + lazy_tau<IO>() ? mx : m_used;   // lazy rescaling
+        alpha = m_used == -INFINITY ? 1.f : __builtin_amdgcn_exp2f((m_used - m_new) * LOG2E);
+        m_used = m_new;
+        sm_mb = m_used * LOG2E;
+        sm_sum = 0.f;
+      } else if (st < NST - 1) {
+        const int i = 2 * (st - 5);
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[i], cl2, -sm_mb));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[i + 1], cl2, -sm_mb));
+        sm_sum += p0;
+        sm_sum += p1;
+        sm_d[i >> 2][(i >> 1) & 1] = pack2<IO>(p0, p1);
+      } else {
+        l_part = l_part * alpha + sm_sum;
+        pn[0] = make_uint4(sm_d[0][0], sm_d[0][1], sm_d[1][0], sm_d[1][1]);
+        pn[1] = make_uint4(sm_d[2][0], sm_d[2][1], sm_d[3][0], sm_d[3][1]);
+      }
+    };
+    // O *= alpha when the lane's head moved its exponent reference (rare: lazy rescaling)
+    auto rescale = [&]() __attribute__((always_inline)) {
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
+#pragma unroll
+        for (int nt = 0; nt < ON; ++nt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) o[0][nt][i] = agpr_scale(o[0][nt][i], alpha);
+      }
+    };
+    // PV MFMAs [m0, m1) of a tile. The V^T operands run VR MFMAs ahead in one ring across
+    // tiles: past the tile's last MFMA the reads continue with the next tile's first
+    // operands (at LDS address `vnext`, resident since the barrier that preceded them).
+    // `between(m)` runs after the m-th MFMA.
+    constexpr int NPRE = 6;   // PV MFMAs issued before the next S^T chain (cover its operand latency)
+    uint4 vb[VR];
+    auto pv_run = [&](int m0, int m1, uint32_t vbase, uint32_t vnext, bool next, auto&& between)
+        __attribute__((always_inline)) {
+#pragma unroll
+      for (int m = m0; m < m1; ++m) {
+        o[0][m % ON] = Mfma<IO>::m32(vb[m % VR], pb[m / ON], o[0][m % ON]);
+        if (m + VR < NPV) vb[m % VR] = v_frag(vbase, m + VR);
+        else if (next) vb[m % VR] = v_frag(vnext, m + VR - NPV);
+        between(m);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    wait_vmcnt<C::GPW - 1>();   // this wave's part of tile 0 landed; tile 1 may be in flight
+    lds_barrier();              // tile 0 visible
+    {
+      f32x16 s0 = s_tile(0, [&](int) {});
+      mask_tile(0, s0);
+#pragma unroll
+      for (int st = 0; st < NST; ++st) smx(st, s0);
+      const uint32_t vb0 = v_base(nope_buf[0]);
+#pragma unroll
+      for (int m = 0; m < VR; ++m) vb[m] = v_frag(vb0, m);
+    }
+    // Iteration t: O rescaled for tile t; after the barrier the first NPRE PV MFMAs of tile
+    // t, the S^T chain of tile t+1 (carrying the gathers of tile t+2), then the other PV
+    // MFMAs of tile t with the softmax of tile t+1 staged among them; the ring ends with
+    // the first V^T operands of tile t+1.
+    uint32_t zero_rows = 0;   // this wave's rows of tile t+1 to zero (ids out of range)
+    for (int t = 0; t + 1 < ntiles; ++t) {
+      pb[0] = pn[0];
+      pb[1] = pn[1];
+      rescale();   // tile t's factor (its softmax ran in the previous iteration)
+      if (t == 0) wait_vmcnt<0>(); else wait_vmcnt<1>();   // this wave's gathers of tile t+1
+      if (zero_rows) {   // rare: such rows read as zeros, as the zero row gives
+        wait_vmcnt<0>();
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (((zero_rows >> j) & 1u) && lane < C::LANES_ROW)
+            *reinterpret_cast<uint4*>(nope_buf[(t + 1) % NBUF] + nope_off<D>(wave_u * 8 + j) + lane * 16) =
+                make_uint4(0, 0, 0, 0);
+      }
+      lds_barrier();   // tile t+1 resident; every wave's PV reads of tile t-1 done, so its buffer is free
+      const TileIdx ix = tile_idx(t + 2, true);
+      zero_rows = ix.zero_rows;
+      uint8_t* gnope = nope_buf[(t + 2) % NBUF];
+      uint8_t* grope = rope_buf[(t + 2) % NBUF];
+      const uint32_t vbase = v_base(nope_buf[t % NBUF]);
+      const uint32_t vnext = v_base(nope_buf[(t + 1) % NBUF]);
+      f32x16 s1 = s_tile_k(
+          t + 1,
+          [&](int ks) {
+#pragma unroll
+            for (int j = 0; j < C::GPW; ++j)
+              if (j * KSH / C::GPW == ks) {
+                if (j < C::GPW - 1) gather_part<D, true>(j, kb, krb, ws.zero, krows, ix, gnope, grope, wave_u, lane);
+                else ids_dma(t + 4);   // slot (t+4)%4 held the ids of tile t, read two iterations ago
+              }
+          },
+          std::integral_constant<int, 0>{}, [&] { pv_run(0, NPRE, vbase, vnext, true, [](int) {}); });
+      mask_tile(t + 1, s1);
+      pv_run(NPRE, NPV, vbase, vnext, true, [&](int m) {
+#pragma unroll
+        for (int st = 0; st < NST; ++st)
+          if (st * (NPV - NPRE) / NST == m - NPRE) smx(st, s1);
+      });
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    pb[0] = pn[0];
+    pb[1] = pn[1];
+    rescale();
+    pv_run(0, NPV, v_base(nope_buf[(ntiles - 1) % NBUF]), 0u, false, [](int) {});
+    wait_vmcnt<0>();   // the ring's last (unused) gathers must land before the LDS is released
+  } else {
   wait_vmcnt<C::GPW - 1>();   // this wave's part of tile 0 landed; tile 1 may be in flight
   lds_barrier();   // tile 0 visible
   {
@@ -1144,10 +1339,10 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
     if (__builtin_amdgcn_ballot_w64(a0 != 1.f || a1 != 1.f)) {
       // O^T layout: every element a lane holds in M tile mt belongs to head mt*32 + lane%32
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
+      for (int mt = 0; mt < OM; ++mt) {
         const float al = s_alpha[t & 1][mt * 32 + (lane & 31)];
 #pragma unroll
-        for (int nt = 0; nt < C::NT; ++nt)
+        for (int nt = 0; nt < ON; ++nt)
 #pragma unroll
           for (int i = 0; i < 16; ++i) o[mt][nt][i] = agpr_scale(o[mt][nt][i], al);
       }
@@ -1175,11 +1370,12 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   tile_top(ntiles - 1);
   pv_tile(ntiles - 1, [&]() {});
   wait_vmcnt<0>();   // the ring's last (unused) gathers must land before the LDS is released
+  }
 
   // ---- epilogue
   const float l_tot = l_part + __shfl_xor(l_part, 32);
   const bool owner = lane < 32 && kh == 0;   // one lane per head (a pair holds equal values)
-  if (owner) s_l[hq] = 1.f / l_tot;   // l > 0: a row or split holds at least one token
+  if (!OWN && owner) s_l[hq] = 1.f / l_tot;   // l > 0: a row or split holds at least one token
   if (direct) {
     if (owner && hq < n1 && a.sm_max) {
       a.sm_max[(int64_t)r * n1 + hq] = m_true;
@@ -1192,23 +1388,23 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
     ps[2] = l_tot;
   }
   // s_l (written only here) visible to every wave; an LDS-only barrier, so the
-  // statistics stores above are not waited for
-  lds_barrier();
-  // O^T layout: in accumulator (mt, nt) lane l holds head h = mt*32 + l%32 and, at
-  // index 4g + j, column wave*DW + nt*32 + 8g + 4(l/32) + j (g, j < 4). After scaling
-  // and packing, two lane-half swaps leave lanes l < 32 with columns [0,8) and
-  // [16,24) of the 32-column group and lanes l >= 32 with [8,16) and [24,32): two
-  // 16-byte stores per accumulator instead of sixteen 2-byte ones.
+  // statistics stores above are not waited for (OWN: every lane holds its own head's l)
+  if constexpr (!OWN) lds_barrier();
+  // O^T layout: in accumulator (mt, nt) lane l holds head h = mt*32 + l%32 (OWN: the
+  // wave's block) and, at index 4g + j, column c0 + nt*32 + 8g + 4(l/32) + j (g, j < 4;
+  // c0 = wave*DW, or 0 for OWN). After scaling and packing, two lane-half swaps leave
+  // lanes l < 32 with columns [0,8) and [16,24) of the 32-column group and lanes l >= 32
+  // with [8,16) and [24,32): two 16-byte stores per accumulator instead of sixteen 2-byte ones.
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int h = mt * 32 + (lane & 31);
-    const float inv = s_l[h];
+  for (int mt = 0; mt < OM; ++mt) {
+    const int h = (OWN ? wave : mt) * 32 + (lane & 31);
+    const float inv = OWN ? 1.f / l_tot : s_l[h];
     // one split: the output row; several: this split's normalised partial
     uint16_t* orow = (direct ? out + ((int64_t)r * n1 + min(h, n1 - 1)) * D
                              : ws.part_o + (((int64_t)r * splits + sp) * n1 + min(h, n1 - 1)) * D) +
-                     wave * C::DW + (lane >> 5) * 8;
+                     (OWN ? 0 : wave * C::DW) + (lane >> 5) * 8;
 #pragma unroll
-    for (int nt = 0; nt < C::NT; ++nt) {
+    for (int nt = 0; nt < ON; ++nt) {
       uint32_t d[4][2];
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
@@ -1644,6 +1840,9 @@ hipError_t launch_attn_d(const SfaArgs& a, hipStream_t s, int cap, int splits, i
   } else if (a.n1 <= 64)
     hipLaunchKernelGGL((sfa_attn_kernel<IO, D, 64, false>), dim3(a.total_rows, splits), dim3(NWV * 64), 0, s, a,
                        cap, splits, fuse_tok, ws);
+  else if ((uint64_t)a.key_rows * D * 2 <= (1ull << 32))   // its gathers use 32-bit row offsets
+    hipLaunchKernelGGL((sfa_attn_kernel<IO, D, 128, false, true>), dim3(a.total_rows, splits), dim3(NWV * 64), 0, s,
+                       a, cap, splits, fuse_tok, ws);
   else
     hipLaunchKernelGGL((sfa_attn_kernel<IO, D, 128, false>), dim3(a.total_rows, splits), dim3(NWV * 64), 0, s, a,
                        cap, splits, fuse_tok, ws);
