@@ -21,11 +21,17 @@
 //      exclusive scans of the per-thread counts. Rows of up to 65536 entries carry
 //      x = 0xFFFF - index; longer rows (WIDE) carry x = p and keep the 32-bit index
 //      in a second LDS array at p (p, like the index, increases along the row).
-//   4. A stable LSD radix sort on the 16-bit score (4 passes of 4 bits, digits
-//      of the inverted key so larger scores come first; per-thread counter
-//      columns in LDS, no atomics). Stability preserves the index order of
-//      equal scores, which is exactly the golden's tie rule.
+//   4. A stable LSD radix sort on the 16-bit score (passes of 4 bits, digits of
+//      the inverted key so larger scores come first). Each thread counts the digits
+//      of its keys in registers (packed counters: no LDS read-modify-write chain),
+//      one block scan turns the per-thread counts into scatter offsets. Passes over
+//      bits that every selected key shares are identities and are skipped: with u
+//      in [umin, umax], pass p runs only if umin >> 4p != umax >> 4p. Stability
+//      preserves the index order of equal scores, which is exactly the golden's tie
+//      rule.
 //   5. One pass writes the indices and 16-bit values in rank order.
+// The selection histogram and the sort's counters share one LDS array (they are
+// never live together), so a work-group needs ~16 KB and more of them fit a CU.
 #include "dsa_common.hpp"
 
 namespace dsa {
@@ -34,9 +40,6 @@ namespace {
 constexpr int TPB = 256;
 constexpr int RPT = 32;                 // row entries per thread held in VGPRs
 constexpr int ROW_CACHED = TPB * RPT;   // 8192
-// Histogram bins are split into HSUB counters picked by lane % HSUB: scores cluster
-// in few high-byte bins, and same-address LDS atomics of one instruction serialise.
-constexpr int HSUB = 8;
 
 __device__ __forceinline__ int visible_len(int s1, int aq, int ak, int S2, int mode) {
   int L;
@@ -92,57 +95,109 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* red, u
   return off + x - v;
 }
 
-__device__ __forceinline__ void load_keys(const uint16_t* row, int L, int base, uint32_t (&u)[RPT]) {
+// ord16 of both 16-bit halves of w (see ord16): -0 becomes +0, then negative values
+// are inverted and positive ones get the top bit, with 32-bit operations on the pair.
+__device__ __forceinline__ uint32_t ord16x2(uint32_t w) {
+  const uint32_t mag = w & 0x7FFF7FFFu;
+  const uint32_t nz = __builtin_amdgcn_ubfe(mag, 0, 15) != 0 ? 1u : 0u;   // low half nonzero
+  const uint32_t nzh = (mag >> 16) != 0 ? 0x10000u : 0u;                 // high half nonzero
+  const uint32_t sgn = w & ((nz | nzh) << 15);                             // sign bits of nonzero halves
+  const uint32_t inv = (sgn >> 15) * 0x7FFFu;                              // 0x7FFF in negative halves
+  return (mag | sgn) ^ 0x80008000u ^ inv;
+}
+// key e of a thread's packed pairs (w[e / 2], low half = even e)
+__device__ __forceinline__ uint32_t kh(const uint32_t* w, int e) { return (e & 1) ? w[e >> 1] >> 16 : w[e >> 1] & 0xFFFFu; }
+
+// Keys [base + 32t, +32) of the row as packed ord16 pairs; entries at or past L are 0
+// (below every real key).
+__device__ __forceinline__ void load_keys(const uint16_t* row, int L, int base, uint32_t (&w)[RPT / 2]) {
   const int i0 = base + threadIdx.x * RPT;
   if (i0 + RPT <= L) {
 #pragma unroll
     for (int c = 0; c < RPT / 8; ++c) {
       const uint4 v = ldg16(row + i0 + c * 8);
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        u[c * 8 + 2 * j] = ord16((uint16_t)(w[j] & 0xFFFFu));
-        u[c * 8 + 2 * j + 1] = ord16((uint16_t)(w[j] >> 16));
-      }
+      w[c * 4 + 0] = ord16x2(v.x);
+      w[c * 4 + 1] = ord16x2(v.y);
+      w[c * 4 + 2] = ord16x2(v.z);
+      w[c * 4 + 3] = ord16x2(v.w);
     }
   } else {
 #pragma unroll
-    for (int e = 0; e < RPT; ++e) u[e] = (i0 + e < L) ? ord16(row[i0 + e]) : 0u;  // 0 < every real key
+    for (int e = 0; e < RPT; e += 2) {
+      const uint32_t lo = (i0 + e < L) ? ord16(row[i0 + e]) : 0u;
+      const uint32_t hi = (i0 + e + 1 < L) ? ord16(row[i0 + e + 1]) : 0u;
+      w[e >> 1] = lo | (hi << 16);
+    }
   }
 }
 
-// Stable LSD radix sort of E keys per thread (blocked: thread t holds ranks
-// [E t, E t + E)), ascending on the inverted upper 16 bits = score descending.
+// Digit counters of one thread's E keys, packed: 4-bit fields (E < 16) in one 64-bit
+// word, else 8-bit fields (E < 256) in two.
 template <int E>
-__device__ __forceinline__ void radix_sort_desc16(uint32_t (&key)[E], uint32_t* sbuf, uint16_t* cnt,
+struct DigitCount {
+  static constexpr bool NIB = E < 16;
+  uint64_t c0 = 0, c1 = 0;
+  // rank of this key among the thread's earlier keys with digit d, then count it
+  __device__ __forceinline__ uint32_t take(uint32_t d) {
+    if constexpr (NIB) {
+      const uint32_t sh = d * 4;
+      const uint32_t r = (uint32_t)(c0 >> sh) & 15u;
+      c0 += 1ull << sh;
+      return r;
+    } else {
+      const uint32_t sh = (d & 7) * 8;
+      const bool hi = d >= 8;
+      const uint64_t w = hi ? c1 : c0;
+      const uint32_t r = (uint32_t)(w >> sh) & 255u;
+      const uint64_t inc = 1ull << sh;
+      c0 += hi ? 0ull : inc;
+      c1 += hi ? inc : 0ull;
+      return r;
+    }
+  }
+  __device__ __forceinline__ uint32_t count(int d) const {
+    if constexpr (NIB) return (uint32_t)(c0 >> (d * 4)) & 15u;
+    else return (uint32_t)((d < 8 ? c0 : c1) >> ((d & 7) * 8)) & 255u;
+  }
+};
+
+// Stable LSD radix sort of E keys per thread (blocked: thread t holds ranks
+// [E t, E t + E)), ascending on the inverted upper 16 bits = score descending, over
+// passes [0, npass) (4 bits each, from the low bits up). `cnt` holds 16 x TPB 16-bit
+// counters in [digit][thread] order.
+template <int E>
+__device__ __forceinline__ void radix_sort_desc16(uint32_t (&key)[E], int npass, uint32_t* sbuf, uint16_t* cnt,
                                                   uint32_t* red) {
   const int t = threadIdx.x;
 #pragma unroll 1
-  for (int pass = 0; pass < 4; ++pass) {
+  for (int pass = 0; pass < npass; ++pass) {
     const int shift = 16 + 4 * pass;
+    DigitCount<E> dc;
+    uint32_t lrank[E];
 #pragma unroll
-    for (int d = 0; d < 16; ++d) cnt[d * TPB + t] = 0;
-    uint16_t lrank[E];
+    for (int e = 0; e < E; ++e) lrank[e] = dc.take(((~key[e]) >> shift) & 15u);
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const int d = ((~key[e]) >> shift) & 15;
-      const uint16_t r = cnt[d * TPB + t];
-      lrank[e] = r;
-      cnt[d * TPB + t] = r + 1;
-    }
+    for (int d = 0; d < 16; ++d) cnt[d * TPB + t] = (uint16_t)dc.count(d);
     __syncthreads();
     // exclusive scan over cnt in [digit][thread] order: thread t scans entries 16t..16t+15
-    uint32_t loc[16];
+    const uint4 q0 = *reinterpret_cast<const uint4*>(cnt + t * 16);
+    const uint4 q1 = *reinterpret_cast<const uint4*>(cnt + t * 16 + 8);
+    const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
     uint32_t s = 0;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      loc[j] = s;
-      s += cnt[t * 16 + j];
-    }
+    for (int j = 0; j < 8; ++j) s += (w[j] & 0xFFFFu) + (w[j] >> 16);
     uint32_t tot;
-    const uint32_t off = block_excl_scan(s, red, &tot);
+    uint32_t run = block_excl_scan(s, red, &tot);   // offset of this thread's first entry
+    uint32_t o[8];   // running offsets, re-derived from the counts (no second array live across the scan)
 #pragma unroll
-    for (int j = 0; j < 16; ++j) cnt[t * 16 + j] = (uint16_t)(off + loc[j]);
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t lo = run;
+      run += w[j] & 0xFFFFu;
+      o[j] = lo | (run << 16);
+      run += w[j] >> 16;
+    }
+    *reinterpret_cast<uint4*>(cnt + t * 16) = make_uint4(o[0], o[1], o[2], o[3]);
+    *reinterpret_cast<uint4*>(cnt + t * 16 + 8) = make_uint4(o[4], o[5], o[6], o[7]);
     __syncthreads();
 #pragma unroll
     for (int e = 0; e < E; ++e) {
@@ -152,19 +207,57 @@ __device__ __forceinline__ void radix_sort_desc16(uint32_t (&key)[E], uint32_t* 
     __syncthreads();
 #pragma unroll
     for (int e = 0; e < E; ++e) key[e] = sbuf[E * t + e];
-    __syncthreads();
+    // the next pass writes cnt (read above, before the barrier) and sbuf (after two barriers)
   }
+}
+
+// Block-wide exclusive scan of v together with the maxima of m1 and m2 (every thread
+// gets the scan total and both maxima): one LDS exchange for the three.
+__device__ __forceinline__ uint32_t block_scan_max2(uint32_t v, uint32_t m1, uint32_t m2, uint32_t* red,
+                                                    uint32_t* total, uint32_t* max1, uint32_t* max2) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t n = __shfl_up(x, o);
+    if (lane >= o) x += n;
+    m1 = max(m1, (uint32_t)__shfl_xor(m1, o));
+    m2 = max(m2, (uint32_t)__shfl_xor(m2, o));
+  }
+  __syncthreads();
+  if (lane == 63) {
+    red[wave] = x;
+    red[TPB / 64 + wave] = m1;
+    red[2 * (TPB / 64) + wave] = m2;
+  }
+  __syncthreads();
+  uint32_t off = 0, tot = 0, a = 0, b = 0;
+#pragma unroll
+  for (int w = 0; w < TPB / 64; ++w) {
+    off += (w < wave) ? red[w] : 0u;
+    tot += red[w];
+    a = max(a, red[TPB / 64 + w]);
+    b = max(b, red[2 * (TPB / 64) + w]);
+  }
+  *total = tot;
+  *max1 = a;
+  *max2 = b;
+  return off + x - v;
 }
 
 template <int E, bool WIDE>
 __global__ __launch_bounds__(TPB) void li_topk_kernel(LiTopkArgs a) {
   static_assert(E * TPB <= 65536, "compacted positions are 16-bit");
+  constexpr int HWORDS = 2048;         // selection histogram (u >> 5), then the candidate list
+  constexpr int CWORDS = 16 * TPB / 2;   // sort counters (16-bit)
   __shared__ __attribute__((aligned(16))) uint32_t sbuf[E * TPB];
   __shared__ int32_t sidx[WIDE ? E * TPB : 1];   // WIDE: row index of compacted position p
-  __shared__ uint16_t cnt[16 * TPB];
-  __shared__ uint32_t red[TPB / 64];
-  __shared__ uint32_t hist[256 * HSUB];
-  __shared__ uint32_t pick[2];
+  __shared__ __attribute__((aligned(16))) uint32_t work[HWORDS > CWORDS ? HWORDS : CWORDS];
+  __shared__ uint32_t red[3 * (TPB / 64)];
+  __shared__ uint32_t pick[3];
+  __shared__ uint32_t chist[32];
+  uint32_t* hist = work;
+  uint16_t* cnt = reinterpret_cast<uint16_t*>(work);
 
   const int sr = blockIdx.x;
   const int r = sr / a.n2;
@@ -189,93 +282,210 @@ __global__ __launch_bounds__(TPB) void li_topk_kernel(LiTopkArgs a) {
 
   // ---- selection + order-preserving compaction into sbuf[0, nout)
   const int nchunks = (L + ROW_CACHED - 1) / ROW_CACHED;
-  uint32_t u[RPT];
-  if (nchunks == 1) load_keys(row, L, 0, u);
+  uint32_t w[RPT / 2];   // the thread's keys, packed pairs
+  if (nchunks == 1) load_keys(row, L, 0, w);
   uint32_t T = 0;  // keys > T are all taken; keys == T up to `need`
   uint32_t need = 0xFFFFFFFFu;
+  uint32_t umin = 0, umax = 0xFFFFu;   // bounds of the selected keys (the sort's pass range)
+  bool compacted = false;
   if (L > k) {
-    // 256-bin histogram over (u >> shift) of the keys whose high byte is `match`
-    // (every key for the first pass), then a scan from the top bin: the bin that
-    // holds the `want`-th largest and the count of keys in higher bins
-    auto select_byte = [&](int shift, int match, uint32_t want, uint32_t& above) -> int {
+    // 2048-bin histogram of u >> 5, scanned from the top bin: bin b holds the k-th
+    // largest key, `above` keys lie in higher bins (all taken)
 #pragma unroll
-      for (int i = 0; i < HSUB; ++i) hist[i * TPB + t] = 0;
-      __syncthreads();
-      const int sub = t & (HSUB - 1);
+    for (int i = 0; i < 8; ++i) hist[t * 8 + i] = 0;
+    __syncthreads();
 #pragma unroll 1
-      for (int ch = 0; ch < nchunks; ++ch) {
-        if (nchunks > 1) load_keys(row, L, ch * ROW_CACHED, u);
+    for (int ch = 0; ch < nchunks; ++ch) {
+      if (nchunks > 1) load_keys(row, L, ch * ROW_CACHED, w);
 #pragma unroll
-        for (int e = 0; e < RPT; ++e)
-          if (u[e] != 0u && (match < 0 || (int)(u[e] >> 8) == match))
-            atomicAdd(&hist[((u[e] >> shift) & 255u) * HSUB + sub], 1u);
-      }
-      __syncthreads();
-      uint32_t h = 0;   // thread t: bin 255 - t, so the scan runs from the top
-#pragma unroll
-      for (int i = 0; i < HSUB; ++i) h += hist[(255 - t) * HSUB + i];
-      uint32_t tot;
-      const uint32_t before = block_excl_scan(h, red, &tot);
-      if (before < want && before + h >= want) {
-        pick[0] = 255 - t;
-        pick[1] = before;
-      }
-      __syncthreads();
-      above = pick[1];
-      return (int)pick[0];
-    };
-    uint32_t above_hi, above_lo;
-    const int hb = select_byte(8, -1, (uint32_t)k, above_hi);
-    const int lb = select_byte(0, hb, (uint32_t)k - above_hi, above_lo);
-    T = ((uint32_t)hb << 8) | (uint32_t)lb;
-    need = (uint32_t)k - (above_hi + above_lo);   // keys == T to take, in index order
-  }
-  // positions: selected-before = greater-before + min(ties-before, need)
-  uint32_t run_g = 0, run_e = 0;  // totals of previous chunks
-#pragma unroll 1
-  for (int ch = 0; ch < nchunks; ++ch) {
-    if (nchunks > 1) load_keys(row, L, ch * ROW_CACHED, u);
-    uint32_t cg = 0, ce = 0;
-#pragma unroll
-    for (int e = 0; e < RPT; ++e) {
-      cg += u[e] > T ? 1u : 0u;
-      ce += (u[e] == T && T != 0) ? 1u : 0u;
+      for (int e = 0; e < RPT; ++e)
+        if (kh(w, e) != 0u) atomicAdd(&hist[kh(w, e) >> 5], 1u);
     }
-    uint32_t tot_g, tot_e;
-    uint32_t pg = block_excl_scan(cg, red, &tot_g) + run_g;
-    uint32_t pe = block_excl_scan(ce, red, &tot_e) + run_e;
-    const int i0 = ch * ROW_CACHED + t * RPT;
+    __syncthreads();
+    uint32_t h[8];   // thread t: bins 2047 - 8t - j, j < 8 (the scan runs from the top)
+    {
+      const uint4 lo4 = *reinterpret_cast<const uint4*>(&hist[2040 - 8 * t]);
+      const uint4 hi4 = *reinterpret_cast<const uint4*>(&hist[2044 - 8 * t]);
+      h[0] = hi4.w; h[1] = hi4.z; h[2] = hi4.y; h[3] = hi4.x;
+      h[4] = lo4.w; h[5] = lo4.z; h[6] = lo4.y; h[7] = lo4.x;
+    }
+    uint32_t hs = 0, top1 = 0;   // top1: highest non-empty bin + 1 (0: none)
 #pragma unroll
-    for (int e = 0; e < RPT; ++e) {
-      // x: the index (rows up to 65536) or the position, whose index goes to sidx
-      auto put = [&](uint32_t p) {
-        if constexpr (WIDE) {
-          sbuf[p] = (u[e] << 16) | p;
-          sidx[p] = i0 + e;
-        } else {
-          sbuf[p] = (u[e] << 16) | (0xFFFFu - (uint32_t)(i0 + e));
+    for (int j = 7; j >= 0; --j) {
+      hs += h[j];
+      top1 = h[j] ? (uint32_t)(2048 - 8 * t - j) : top1;
+    }
+    uint32_t tot, btop1, unused;
+    uint32_t cum = block_scan_max2(hs, top1, 0u, red, &tot, &btop1, &unused);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (cum < (uint32_t)k && cum + h[j] >= (uint32_t)k) {
+        pick[0] = 2047 - 8 * t - j;
+        pick[1] = cum;
+        pick[2] = h[j];
+      }
+      cum += h[j];
+    }
+    __syncthreads();
+    const uint32_t bin = pick[0], above = pick[1], nc = pick[2];
+    umax = ((btop1 - 1) << 5) | 31u;
+    const uint32_t need_c = (uint32_t)k - above;   // keys of bin `bin` to take
+    // the k-th largest within bin `bin`: a 32-bin histogram of the low 5 bits of its
+    // keys, scanned from the top by wave 0; sets T and `need`
+    auto resolve = [&](auto&& count_keys) {
+      if (t < 32) chist[t] = 0;
+      __syncthreads();
+      count_keys();
+      __syncthreads();
+      if (t < 64) {
+        const uint32_t hh = t < 32 ? chist[31 - t] : 0u;
+        uint32_t incl = hh;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const uint32_t n = __shfl_up(incl, o);
+          if (t >= o) incl += n;
         }
-      };
-      if (u[e] > T) {
-        put(pg + (pe < need ? pe : need));
-        ++pg;
-      } else if (u[e] == T && T != 0) {
-        if (pe < need) put(pg + pe);
-        ++pe;
+        if (t < 32 && incl - hh < need_c && incl >= need_c) {
+          pick[0] = 31 - t;
+          pick[1] = incl - hh;
+        }
       }
+      __syncthreads();
+      T = (bin << 5) | pick[0];
+      need = need_c - pick[1];
+    };
+    if (!WIDE && nchunks == 1 && nc <= (uint32_t)HWORDS) {
+      // one pass over the row: keys of higher bins go to sbuf[0, above) in index order,
+      // the keys of bin `bin` to a candidate list (key << 16 | index, index order) in
+      // the histogram's place; T is then found among the candidates only, and the
+      // selected ones follow in sbuf, in index order. The two groups hold different
+      // keys, so their relative order is irrelevant to the stable sort.
+      uint32_t* cand = work;
+      const int i0 = t * RPT;
+      uint32_t cg = 0, cc = 0;
+#pragma unroll
+      for (int e = 0; e < RPT; ++e) {
+        const uint32_t v = kh(w, e) >> 5;
+        cg += v > bin ? 1u : 0u;
+        cc += (v == bin && kh(w, e) != 0u) ? 1u : 0u;
+      }
+      uint32_t tot1;
+      const uint32_t pgc = block_excl_scan((cg << 16) | cc, red, &tot1);
+      uint32_t pg = pgc >> 16, pc = pgc & 0xFFFFu;
+#pragma unroll
+      for (int e = 0; e < RPT; ++e) {
+        const uint32_t ue = kh(w, e), v = ue >> 5;
+        if (v > bin) sbuf[pg++] = (ue << 16) | (0xFFFFu - (uint32_t)(i0 + e));
+        else if (v == bin && ue != 0u) cand[pc++] = (ue << 16) | (uint32_t)(i0 + e);
+      }
+      // candidates [c0, c1) of this thread (at most 8: nc <= 2048)
+      const uint32_t m = (nc + TPB - 1) / TPB, c0 = min((uint32_t)t * m, nc), c1 = min(c0 + m, nc);
+      resolve([&] {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (c0 + j < c1) atomicAdd(&chist[(cand[c0 + j] >> 16) & 31u], 1u);
+      });
+      uint32_t cv[8];
+      uint32_t g2 = 0, e2 = 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        cv[j] = c0 + j < c1 ? cand[c0 + j] : 0u;
+        g2 += (c0 + j < c1 && (cv[j] >> 16) > T) ? 1u : 0u;
+        e2 += (c0 + j < c1 && (cv[j] >> 16) == T) ? 1u : 0u;
+      }
+      uint32_t tot2;
+      const uint32_t pge = block_excl_scan((g2 << 16) | e2, red, &tot2);
+      uint32_t qg = above + (pge >> 16), qe = pge & 0xFFFFu;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (c0 + j >= c1) continue;
+        const uint32_t key16 = cv[j] >> 16, x = 0xFFFFu - (cv[j] & 0xFFFFu);
+        if (key16 > T) {
+          sbuf[qg + (qe < need ? qe : need)] = (key16 << 16) | x;
+          ++qg;
+        } else if (key16 == T) {
+          if (qe < need) sbuf[qg + qe] = (key16 << 16) | x;
+          ++qe;
+        }
+      }
+      compacted = true;
+    } else {   // rows longer than 8192 or a crowded bin: one more pass over the row
+      resolve([&] {
+#pragma unroll 1
+        for (int ch = 0; ch < nchunks; ++ch) {
+          if (nchunks > 1) load_keys(row, L, ch * ROW_CACHED, w);
+#pragma unroll
+          for (int e = 0; e < RPT; ++e)
+            if (kh(w, e) != 0u && (kh(w, e) >> 5) == bin) atomicAdd(&chist[kh(w, e) & 31u], 1u);
+        }
+      });
     }
-    run_g += tot_g;
-    run_e += tot_e;
+    umin = T;
+  }
+  if (!compacted) {
+    // positions: selected-before = greater-before + min(ties-before, need); one scan of
+    // (greater << 16 | ties) per chunk (a chunk holds at most 8192 of each), which also
+    // gives the largest and smallest key (the sort's pass range when every key is taken)
+    uint32_t run_g = 0, run_e = 0;  // totals of previous chunks
+    uint32_t kmax = 0, kmin_inv = 0;   // max of u, max of 0xFFFF - u over nonzero keys
+#pragma unroll 1
+    for (int ch = 0; ch < nchunks; ++ch) {
+      if (nchunks > 1) load_keys(row, L, ch * ROW_CACHED, w);
+      const int i0 = ch * ROW_CACHED + t * RPT;
+      uint32_t cg = 0, ce = 0, mx = 0, mn = 0;
+#pragma unroll
+      for (int e = 0; e < RPT; ++e) {
+        const uint32_t ue = kh(w, e);
+        cg += ue > T ? 1u : 0u;
+        ce += (ue == T && T != 0) ? 1u : 0u;
+        mx = max(mx, ue);
+        mn = ue != 0u ? max(mn, 0xFFFFu - ue) : mn;
+      }
+      uint32_t tot, cmx, cmn;
+      const uint32_t pgs = block_scan_max2((cg << 16) | ce, mx, mn, red, &tot, &cmx, &cmn);
+      kmax = max(kmax, cmx);
+      kmin_inv = max(kmin_inv, cmn);
+      uint32_t pg = (pgs >> 16) + run_g;
+      uint32_t pe = (pgs & 0xFFFFu) + run_e;
+#pragma unroll
+      for (int e = 0; e < RPT; ++e) {
+        const uint32_t ue = kh(w, e);
+        // x: the index (rows up to 65536) or the position, whose index goes to sidx
+        auto put = [&](uint32_t p) {
+          if constexpr (WIDE) {
+            sbuf[p] = (ue << 16) | p;
+            sidx[p] = i0 + e;
+          } else {
+            sbuf[p] = (ue << 16) | (0xFFFFu - (uint32_t)(i0 + e));
+          }
+        };
+        if (ue > T) {
+          put(pg + (pe < need ? pe : need));
+          ++pg;
+        } else if (ue == T && T != 0) {
+          if (pe < need) put(pg + pe);
+          ++pe;
+        }
+      }
+      run_g += tot >> 16;
+      run_e += tot & 0xFFFFu;
+    }
+    if (L <= k) {
+      umax = kmax;
+      umin = 0xFFFFu - kmin_inv;
+    }
   }
   for (int i = nout + t; i < E * TPB; i += TPB) sbuf[i] = 0u;  // pads sort last
   __syncthreads();
 
-  // ---- stable radix sort of the selected keys, then write in rank order
+  // ---- stable radix sort of the selected keys, then write in rank order. Passes over
+  // digits every selected key shares (a common prefix of umin and umax) are skipped.
+  int npass = 4;
+  while (npass > 0 && (umin >> (4 * (npass - 1))) == (umax >> (4 * (npass - 1)))) --npass;
   uint32_t key[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) key[e] = sbuf[E * t + e];
-  __syncthreads();
-  radix_sort_desc16<E>(key, sbuf, cnt, red);
+  radix_sort_desc16<E>(key, npass, sbuf, cnt, red);
   // ranks E t .. E t + E - 1 of thread t: their index (or -1) and 16-bit value (or 0)
   int32_t oi[E];
   uint16_t ov[E];
