@@ -224,6 +224,35 @@ __device__ __forceinline__ void swap_halves(uint32_t& a, uint32_t& b) {
   asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
 }
 
+// Wave-wide inclusive prefix sum / max over the 64 lanes with DPP, VALU only (the
+// __shfl_* intrinsics lower to ds_bpermute: a dependent LDS round trip per step). Row
+// shifts by 1, 2, 4, 8 scan each 16-lane row (lanes shifted in from outside the row
+// read 0); row_bcast:15 then adds row 0's last lane to row 1 (and row 2's to row 3),
+// row_bcast:31 adds lane 31 to rows 2 and 3. Unsigned max uses the same steps (0 is its
+// identity).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_shift(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, ROW_MASK, 0xF, false);
+}
+__device__ __forceinline__ uint32_t wave_incl_sum(uint32_t x) {
+  x += dpp_shift<0x111, 0xF>(x);   // row_shr:1
+  x += dpp_shift<0x112, 0xF>(x);   // row_shr:2
+  x += dpp_shift<0x114, 0xF>(x);   // row_shr:4
+  x += dpp_shift<0x118, 0xF>(x);   // row_shr:8
+  x += dpp_shift<0x142, 0xA>(x);   // row_bcast:15 into rows 1, 3
+  x += dpp_shift<0x143, 0xC>(x);   // row_bcast:31 into rows 2, 3
+  return x;
+}
+__device__ __forceinline__ uint32_t wave_incl_max(uint32_t x) {
+  x = max(x, dpp_shift<0x111, 0xF>(x));
+  x = max(x, dpp_shift<0x112, 0xF>(x));
+  x = max(x, dpp_shift<0x114, 0xF>(x));
+  x = max(x, dpp_shift<0x118, 0xF>(x));
+  x = max(x, dpp_shift<0x142, 0xA>(x));
+  x = max(x, dpp_shift<0x143, 0xC>(x));
+  return x;
+}
+
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 // ds_read_b64_tr_b16: 8 bytes per lane, transposed within groups of 16 lanes.
@@ -238,7 +267,7 @@ __device__ __forceinline__ uint2 ds_read_tr(const void* lds_ptr) {
 // The same at a 32-bit LDS byte address (constant offsets added to it fold into the
 // instruction's offset field).
 __device__ __forceinline__ uint2 ds_read_tr_at(uint32_t lds_addr) {
-  s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)lds_addr);
+  s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(uintptr_t)lds_addr);
   return __builtin_bit_cast(uint2, v);
 }
 

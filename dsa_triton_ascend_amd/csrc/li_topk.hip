@@ -32,6 +32,8 @@
 //   5. One pass writes the indices and 16-bit values in rank order.
 // The selection histogram and the sort's counters share one LDS array (they are
 // never live together), so a work-group needs ~16 KB and more of them fit a CU.
+#include <type_traits>
+
 #include "dsa_common.hpp"
 
 namespace dsa {
@@ -54,34 +56,10 @@ __device__ __forceinline__ int visible_len(int s1, int aq, int ak, int S2, int m
   return L < 0 ? 0 : L;
 }
 
-__device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-
-// Block-wide sum (all threads get the total). `red` holds TPB/64 words.
-__device__ __forceinline__ uint32_t block_sum(uint32_t v, uint32_t* red) {
-  v = wave_sum(v);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  __syncthreads();
-  if (lane == 0) red[wave] = v;
-  __syncthreads();
-  uint32_t t = 0;
-#pragma unroll
-  for (int w = 0; w < TPB / 64; ++w) t += red[w];
-  return t;
-}
-
-// Block-wide exclusive scan; also returns the total.
+// Block-wide exclusive scan (wave scans with DPP, one LDS exchange); also returns the total.
 __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* red, uint32_t* total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  uint32_t x = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t n = __shfl_up(x, o);
-    if (lane >= o) x += n;
-  }
+  const uint32_t x = wave_incl_sum(v);
   __syncthreads();
   if (lane == 63) red[wave] = x;
   __syncthreads();
@@ -131,33 +109,27 @@ __device__ __forceinline__ void load_keys(const uint16_t* row, int L, int base, 
   }
 }
 
-// Digit counters of one thread's E keys, packed: 4-bit fields (E < 16) in one 64-bit
-// word, else 8-bit fields (E < 256) in two.
+// Digit counters of one thread's E keys, packed in two words (digits 0-7, 8-15): 4-bit
+// fields (E < 16, 32-bit shifts only) or 8-bit fields in two 64-bit words (E < 256).
 template <int E>
 struct DigitCount {
   static constexpr bool NIB = E < 16;
-  uint64_t c0 = 0, c1 = 0;
+  using W = typename std::conditional<NIB, uint32_t, uint64_t>::type;
+  static constexpr uint32_t FB = NIB ? 4 : 8;   // field bits
+  W c0 = 0, c1 = 0;
   // rank of this key among the thread's earlier keys with digit d, then count it
   __device__ __forceinline__ uint32_t take(uint32_t d) {
-    if constexpr (NIB) {
-      const uint32_t sh = d * 4;
-      const uint32_t r = (uint32_t)(c0 >> sh) & 15u;
-      c0 += 1ull << sh;
-      return r;
-    } else {
-      const uint32_t sh = (d & 7) * 8;
-      const bool hi = d >= 8;
-      const uint64_t w = hi ? c1 : c0;
-      const uint32_t r = (uint32_t)(w >> sh) & 255u;
-      const uint64_t inc = 1ull << sh;
-      c0 += hi ? 0ull : inc;
-      c1 += hi ? inc : 0ull;
-      return r;
-    }
+    const uint32_t sh = (d & 7) * FB;
+    const bool hi = d >= 8;
+    const W w = hi ? c1 : c0;
+    const uint32_t r = (uint32_t)(w >> sh) & ((1u << FB) - 1);
+    const W inc = (W)1 << sh;
+    c0 += hi ? (W)0 : inc;
+    c1 += hi ? inc : (W)0;
+    return r;
   }
   __device__ __forceinline__ uint32_t count(int d) const {
-    if constexpr (NIB) return (uint32_t)(c0 >> (d * 4)) & 15u;
-    else return (uint32_t)((d < 8 ? c0 : c1) >> ((d & 7) * 8)) & 255u;
+    return (uint32_t)((d < 8 ? c0 : c1) >> ((d & 7) * FB)) & ((1u << FB) - 1);
   }
 };
 
@@ -216,14 +188,9 @@ __device__ __forceinline__ void radix_sort_desc16(uint32_t (&key)[E], int npass,
 __device__ __forceinline__ uint32_t block_scan_max2(uint32_t v, uint32_t m1, uint32_t m2, uint32_t* red,
                                                     uint32_t* total, uint32_t* max1, uint32_t* max2) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  uint32_t x = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t n = __shfl_up(x, o);
-    if (lane >= o) x += n;
-    m1 = max(m1, (uint32_t)__shfl_xor(m1, o));
-    m2 = max(m2, (uint32_t)__shfl_xor(m2, o));
-  }
+  const uint32_t x = wave_incl_sum(v);
+  m1 = wave_incl_max(m1);   // lane 63: the wave's maximum
+  m2 = wave_incl_max(m2);
   __syncthreads();
   if (lane == 63) {
     red[wave] = x;
@@ -245,8 +212,15 @@ __device__ __forceinline__ uint32_t block_scan_max2(uint32_t v, uint32_t m1, uin
   return off + x - v;
 }
 
-template <int E, bool WIDE>
-__global__ __launch_bounds__(TPB) void li_topk_kernel(LiTopkArgs a) {
+// SHORT: rows of at most ROW_CACHED entries (s2 <= 8192), held in registers in one chunk;
+// the chunked paths for longer rows are compiled out. Short rows with k <= 2048 are
+// compiled for eight waves per SIMD (64 VGPRs, 96 SGPRs: more SGPR spills to VGPR lanes,
+// which cost less than the latency an eighth work-group per CU hides; 0.128 -> 0.121 ms
+// at C2). The kernel is bound by the latency of its barrier/LDS chain, not throughput.
+template <int E, bool WIDE, bool SHORT = false>
+__global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(SHORT && E <= 8 ? 8 : 1, 8)))
+void li_topk_kernel(LiTopkArgs a) {
+  static_assert(!(SHORT && WIDE), "short rows use 16-bit indices");
   static_assert(E * TPB <= 65536, "compacted positions are 16-bit");
   constexpr int HWORDS = 2048;         // selection histogram (u >> 5), then the candidate list
   constexpr int CWORDS = 16 * TPB / 2;   // sort counters (16-bit)
@@ -281,7 +255,7 @@ __global__ __launch_bounds__(TPB) void li_topk_kernel(LiTopkArgs a) {
   }
 
   // ---- selection + order-preserving compaction into sbuf[0, nout)
-  const int nchunks = (L + ROW_CACHED - 1) / ROW_CACHED;
+  const int nchunks = SHORT ? 1 : (L + ROW_CACHED - 1) / ROW_CACHED;
   uint32_t w[RPT / 2];   // the thread's keys, packed pairs
   if (nchunks == 1) load_keys(row, L, 0, w);
   uint32_t T = 0;  // keys > T are all taken; keys == T up to `need`
@@ -337,14 +311,9 @@ __global__ __launch_bounds__(TPB) void li_topk_kernel(LiTopkArgs a) {
       __syncthreads();
       count_keys();
       __syncthreads();
-      if (t < 64) {
+      if (t < 64) {   // wave 0, all lanes active (DPP)
         const uint32_t hh = t < 32 ? chist[31 - t] : 0u;
-        uint32_t incl = hh;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-          const uint32_t n = __shfl_up(incl, o);
-          if (t >= o) incl += n;
-        }
+        const uint32_t incl = wave_incl_sum(hh);
         if (t < 32 && incl - hh < need_c && incl >= need_c) {
           pick[0] = 31 - t;
           pick[1] = incl - hh;
@@ -523,16 +492,16 @@ __global__ __launch_bounds__(TPB) void li_topk_kernel(LiTopkArgs a) {
 }  // namespace
 }  // namespace dsa
 
-template <bool WIDE>
+template <bool WIDE, bool SHORT>
 static hipError_t launch_topk_e(const LiTopkArgs& a, int e, unsigned rows, hipStream_t s) {
   const dim3 grid(rows), block(dsa::TPB);
-  if (e <= 1) hipLaunchKernelGGL((dsa::li_topk_kernel<1, WIDE>), grid, block, 0, s, a);
-  else if (e <= 2) hipLaunchKernelGGL((dsa::li_topk_kernel<2, WIDE>), grid, block, 0, s, a);
-  else if (e <= 4) hipLaunchKernelGGL((dsa::li_topk_kernel<4, WIDE>), grid, block, 0, s, a);
-  else if (e <= 8) hipLaunchKernelGGL((dsa::li_topk_kernel<8, WIDE>), grid, block, 0, s, a);
-  else if (e <= 16) hipLaunchKernelGGL((dsa::li_topk_kernel<16, WIDE>), grid, block, 0, s, a);
-  else if (e <= 32) hipLaunchKernelGGL((dsa::li_topk_kernel<32, WIDE>), grid, block, 0, s, a);
-  else hipLaunchKernelGGL((dsa::li_topk_kernel<64, WIDE>), grid, block, 0, s, a);
+  if (e <= 1) hipLaunchKernelGGL((dsa::li_topk_kernel<1, WIDE, SHORT>), grid, block, 0, s, a);
+  else if (e <= 2) hipLaunchKernelGGL((dsa::li_topk_kernel<2, WIDE, SHORT>), grid, block, 0, s, a);
+  else if (e <= 4) hipLaunchKernelGGL((dsa::li_topk_kernel<4, WIDE, SHORT>), grid, block, 0, s, a);
+  else if (e <= 8) hipLaunchKernelGGL((dsa::li_topk_kernel<8, WIDE, SHORT>), grid, block, 0, s, a);
+  else if (e <= 16) hipLaunchKernelGGL((dsa::li_topk_kernel<16, WIDE, SHORT>), grid, block, 0, s, a);
+  else if (e <= 32) hipLaunchKernelGGL((dsa::li_topk_kernel<32, WIDE, SHORT>), grid, block, 0, s, a);
+  else hipLaunchKernelGGL((dsa::li_topk_kernel<64, WIDE, SHORT>), grid, block, 0, s, a);
   return hipGetLastError();
 }
 
@@ -540,5 +509,7 @@ hipError_t launch_li_topk(const LiTopkArgs& a, hipStream_t s) {
   const int64_t rows = (int64_t)a.total_rows * a.n2;
   if (rows <= 0) return hipSuccess;
   const int e = (a.k + dsa::TPB - 1) / dsa::TPB;
-  return a.s2 > 65536 ? launch_topk_e<true>(a, e, (unsigned)rows, s) : launch_topk_e<false>(a, e, (unsigned)rows, s);
+  if (a.s2 > 65536) return launch_topk_e<true, false>(a, e, (unsigned)rows, s);
+  if (a.s2 > dsa::ROW_CACHED) return launch_topk_e<false, false>(a, e, (unsigned)rows, s);
+  return launch_topk_e<false, true>(a, e, (unsigned)rows, s);   // every visible row fits the registers
 }
