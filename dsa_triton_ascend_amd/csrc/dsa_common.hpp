@@ -230,9 +230,11 @@ __device__ __forceinline__ void swap_halves(uint32_t& a, uint32_t& b) {
 // read 0); row_bcast:15 then adds row 0's last lane to row 1 (and row 2's to row 3),
 // row_bcast:31 adds lane 31 to rows 2 and 3. Unsigned max uses the same steps (0 is its
 // identity).
-template <int CTRL, int ROW_MASK>
+// (OLD: the value lanes shifted in from outside a row, or rows the mask leaves out, read:
+// the operation's identity)
+template <int CTRL, int ROW_MASK, int OLD = 0>
 __device__ __forceinline__ uint32_t dpp_shift(uint32_t x) {
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, ROW_MASK, 0xF, false);
+  return (uint32_t)__builtin_amdgcn_update_dpp(OLD, (int)x, CTRL, ROW_MASK, 0xF, false);
 }
 __device__ __forceinline__ uint32_t wave_incl_sum(uint32_t x) {
   x += dpp_shift<0x111, 0xF>(x);   // row_shr:1
@@ -241,6 +243,17 @@ __device__ __forceinline__ uint32_t wave_incl_sum(uint32_t x) {
   x += dpp_shift<0x118, 0xF>(x);   // row_shr:8
   x += dpp_shift<0x142, 0xA>(x);   // row_bcast:15 into rows 1, 3
   x += dpp_shift<0x143, 0xC>(x);   // row_bcast:31 into rows 2, 3
+  return x;
+}
+// signed minimum (identity INT_MAX); lane 63 holds the wave's minimum
+__device__ __forceinline__ int wave_incl_min_i32(int x) {
+  constexpr int I = 0x7FFFFFFF;
+  x = min(x, (int)dpp_shift<0x111, 0xF, I>((uint32_t)x));
+  x = min(x, (int)dpp_shift<0x112, 0xF, I>((uint32_t)x));
+  x = min(x, (int)dpp_shift<0x114, 0xF, I>((uint32_t)x));
+  x = min(x, (int)dpp_shift<0x118, 0xF, I>((uint32_t)x));
+  x = min(x, (int)dpp_shift<0x142, 0xA, I>((uint32_t)x));
+  x = min(x, (int)dpp_shift<0x143, 0xC, I>((uint32_t)x));
   return x;
 }
 __device__ __forceinline__ uint32_t wave_incl_max(uint32_t x) {

@@ -126,11 +126,10 @@ __device__ __forceinline__ void red_barrier() {
 
 template <bool LDS_ONLY = false>
 __device__ __forceinline__ int block_min_i(int v, int* red) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o));
+  v = wave_incl_min_i32(v);   // lane 63: the wave's minimum (DPP, no LDS round trips)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   red_barrier<LDS_ONLY>();
-  if (lane == 0) red[wave] = v;
+  if (lane == 63) red[wave] = v;
   red_barrier<LDS_ONLY>();
   int m = red[0];
 #pragma unroll
@@ -140,11 +139,10 @@ __device__ __forceinline__ int block_min_i(int v, int* red) {
 
 template <bool LDS_ONLY = false>
 __device__ __forceinline__ int block_sum_i(int v, int* red) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  v = (int)wave_incl_sum((uint32_t)v);   // lane 63: the wave's sum
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   red_barrier<LDS_ONLY>();
-  if (lane == 0) red[wave] = v;
+  if (lane == 63) red[wave] = v;
   red_barrier<LDS_ONLY>();
   int t = 0;
 #pragma unroll
@@ -156,12 +154,7 @@ __device__ __forceinline__ int block_sum_i(int v, int* red) {
 template <bool LDS_ONLY = false>
 __device__ __forceinline__ int block_excl_scan_i(int v, int* red, int* tot) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int x = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int n = __shfl_up(x, o);
-    if (lane >= o) x += n;
-  }
+  const int x = (int)wave_incl_sum((uint32_t)v);
   red_barrier<LDS_ONLY>();
   if (lane == 63) red[wave] = x;
   red_barrier<LDS_ONLY>();
@@ -319,8 +312,7 @@ __global__ __launch_bounds__(64 * TOK1_ROWS) void sfa_tokens1_kernel(SfaArgs a, 
     for (int i = 7; i >= 0; --i)
 #pragma unroll
       for (int j = 3; j >= 0; --j) fneg = v[i][j] == -1 ? c0 + (i * 64 + lane) * 4 + j : fneg;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) fneg = min(fneg, __shfl_xor(fneg, o));   // only -1 stops the scan
+    fneg = __builtin_amdgcn_readlane(wave_incl_min_i32(fneg), 63);   // only -1 stops the scan
     bool ok[8][4];
     int32_t pr[8][4];
 #pragma unroll
