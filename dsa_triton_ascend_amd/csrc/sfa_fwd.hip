@@ -783,6 +783,19 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
     // follow and issue only once the token count has arrived
     asm volatile("" ::: "memory");
   };
+  // Unsplit rows: the ids of tiles 0..3 are copied into the id ring before the token count
+  // is known (one memory round trip instead of two before the first gathers). Copies stay
+  // inside the row's token-list stride; ids past the row's tokens are never used for a
+  // tile that is consumed (their gathers are bounded like any other).
+  const bool early_ids = !fuse_tok && splits == 1;
+  if (early_ids) {
+    const int w_u = __builtin_amdgcn_readfirstlane(wave);
+    const int32_t* toks0 = ws.tokens + (int64_t)r * ws.tstride;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      if ((t + 1) * BN <= ws.tstride && lane < 2)
+        lds_dma16_sbase_untracked(toks0 + t * BN + w_u * 8, lane * 16, &s_ids[t][w_u * 8]);
+  }
   int ntok_all = ntok_pre;
   if (fuse_tok) {   // KV-split rows with sparse_block_size 1: this split lists its own tokens
     ntok_all = split_token_list(a, r, sp, splits, ws, reinterpret_cast<int*>(&s_alpha[0][0]), pre, s_ids,
@@ -861,7 +874,8 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   // rope to LDS and the first two gathers
   if (!fuse_tok) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) ids_dma(t);
+    for (int t = 0; t < 4; ++t)
+      if (!early_ids || (t + 1) * BN > ws.tstride) ids_dma(t);
   }
   wait_vmcnt<0>();
   if (hq >= n1)
