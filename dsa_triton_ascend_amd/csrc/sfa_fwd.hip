@@ -728,7 +728,12 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   constexpr bool KSPLIT = NH == 64;                // S^T contraction split over wave pairs
   constexpr int KSH = KSPLIT ? C::KS / 2 : C::KS;  // S^T k-steps per wave
   static_assert(!KSPLIT || (C::KS % 2 == 0 && KSH <= C::KSN), "first half of the contraction is nope");
-  __shared__ __attribute__((aligned(16))) uint8_t nope_buf[NBUF][C::NOPE];
+  // OWN: before the first gathers the ring is the staging area of Q^T nope (NH * D * 2
+  // bytes, which may exceed the ring)
+  constexpr int QSTAGE = OWN ? NH * D * 2 : 0;
+  constexpr int NOPE_RAW = NBUF * C::NOPE > QSTAGE ? NBUF * C::NOPE : QSTAGE;
+  __shared__ __attribute__((aligned(16))) uint8_t nope_raw[NOPE_RAW];
+  uint8_t(*const nope_buf)[C::NOPE] = reinterpret_cast<uint8_t(*)[C::NOPE]>(nope_raw);
   __shared__ __attribute__((aligned(16))) uint8_t rope_buf[NBUF][C::ROPE];
   __shared__ __attribute__((aligned(16))) uint16_t pt[2][OWN ? 8 : NH * PP];   // P of tiles t (PV) and t+1 (softmax)
   __shared__ __attribute__((aligned(16))) uint16_t qrs[NH * QRP];   // Q rope of all heads
@@ -762,12 +767,40 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
   uint4 qf[QF];
   uint4 qrv[NH * (DR / 8) / (NWV * 64)];
   float t_stat[2] = {0.f, 0.f};   // TEACH: max and sum of head threadIdx.x
-  auto issue_q = [&]() __attribute__((always_inline)) {
-    const uint16_t* qn = reinterpret_cast<const uint16_t*>(a.q) + ((int64_t)r * n1 + min(hq, n1 - 1)) * D;
+  // OWN: Q^T nope goes through LDS (q_frags reads the fragments once it has landed). Wave
+  // w copies its 32 heads to bytes [w * 32 D * 2, +32 D * 2) of the staging area, head
+  // rows D * 2 bytes apart, with whole head rows per instruction (coalesced); the lane
+  // that copies 16-byte chunk c of head h writes it at chunk c ^ (h % 16) of the row, so
+  // that a fragment read (16 heads, the same chunk) lands on 16 distinct bank groups.
+  constexpr int QLPR = D / 8;                                // lanes per head row
+  auto q_stage = [&]() __attribute__((always_inline)) {
+    const int w_u = __builtin_amdgcn_readfirstlane(wave);
+    const uint16_t* q0 = reinterpret_cast<const uint16_t*>(a.q) + (int64_t)r * n1 * D;
+    const int hl = lane / QLPR, c = lane % QLPR;             // head of the instruction, chunk
 #pragma unroll
-    for (int j = 0; j < QF; ++j) {
-      const int ks = kh * KSH + j;
-      qf[j] = ldg16(qn + (ks < C::KSN ? ks : 0) * 16 + (lane >> 5) * 8);
+    for (int j = 0; j < 32 * QLPR / 64; ++j) {
+      const int hb = j * (64 / QLPR);                       // the instruction's first head
+      const int h = min(w_u * 32 + hb + hl, n1 - 1);
+      lds_dma16_untracked(q0 + (int64_t)h * D + (c ^ ((hb + hl) & 15)) * 8,
+                          nope_raw + w_u * (32 * D * 2) + hb * (D * 2));
+    }
+  };
+  auto q_frags = [&]() __attribute__((always_inline)) {
+    const uint8_t* row = nope_raw + __builtin_amdgcn_readfirstlane(wave) * (32 * D * 2) + (lane & 31) * (D * 2);
+#pragma unroll
+    for (int j = 0; j < QF; ++j)
+      qf[j] = *reinterpret_cast<const uint4*>(row + (((2 * j + (lane >> 5)) ^ (lane & 15)) * 16));
+  };
+  auto issue_q = [&]() __attribute__((always_inline)) {
+    if constexpr (OWN) {
+      q_stage();
+    } else {
+      const uint16_t* qn = reinterpret_cast<const uint16_t*>(a.q) + ((int64_t)r * n1 + min(hq, n1 - 1)) * D;
+#pragma unroll
+      for (int j = 0; j < QF; ++j) {
+        const int ks = kh * KSH + j;
+        qf[j] = ldg16(qn + (ks < C::KSN ? ks : 0) * 16 + (lane >> 5) * 8);
+      }
     }
 #pragma unroll
     for (int j = 0; j < NH * (DR / 8) / (NWV * 64); ++j) {
@@ -878,6 +911,7 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
       if (!early_ids || (t + 1) * BN > ws.tstride) ids_dma(t);
   }
   wait_vmcnt<0>();
+  if constexpr (OWN) q_frags();   // this wave's own staging rows: no barrier needed
   if (hq >= n1)
 #pragma unroll
     for (int j = 0; j < QF; ++j) qf[j] = make_uint4(0, 0, 0, 0);
@@ -921,7 +955,7 @@ __global__ __launch_bounds__(NWV * 64) void sfa_attn_kernel(SfaArgs a, int cap, 
       t_il[threadIdx.x] = real ? 1.f / (t_stat[1] + 1e-8f) : 0.f;   // padded heads contribute 0
     }
   }
-  lds_barrier();
+  lds_barrier();   // (OWN: also every wave's Q^T reads of the staging area done)
   gather_tile<D>(kb, krb, ws.zero, krows, tile_idx(0), nope_buf[0], rope_buf[0], wave_u, lane);
   gather_tile<D>(kb, krb, ws.zero, krows, tile_idx(1), nope_buf[1], rope_buf[1], wave_u, lane);
 
