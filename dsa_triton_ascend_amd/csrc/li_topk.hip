@@ -73,15 +73,39 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* red, u
   return off + x - v;
 }
 
-// ord16 of both 16-bit halves of w (see ord16): -0 becomes +0, then negative values
-// are inverted and positive ones get the top bit, with 32-bit operations on the pair.
+typedef short i16x2 __attribute__((ext_vector_type(2)));
+
+// ord16 of both 16-bit halves of w (see ord16), five VALU ops for the pair: a half whose
+// magnitude is zero loses its sign bit (-0 becomes +0: magnitude + 0x7FFF sets the half's
+// top bit exactly when the magnitude is nonzero, and the halves cannot carry into each
+// other), then h ^ (sign-extended sign | 0x8000) inverts negative halves and sets the top
+// bit of positive ones.
 __device__ __forceinline__ uint32_t ord16x2(uint32_t w) {
-  const uint32_t mag = w & 0x7FFF7FFFu;
-  const uint32_t nz = __builtin_amdgcn_ubfe(mag, 0, 15) != 0 ? 1u : 0u;   // low half nonzero
-  const uint32_t nzh = (mag >> 16) != 0 ? 0x10000u : 0u;                 // high half nonzero
-  const uint32_t sgn = w & ((nz | nzh) << 15);                             // sign bits of nonzero halves
-  const uint32_t inv = (sgn >> 15) * 0x7FFFu;                              // 0x7FFF in negative halves
-  return (mag | sgn) ^ 0x80008000u ^ inv;
+  const uint32_t nzt = (w & 0x7FFF7FFFu) + 0x7FFF7FFFu;
+  const uint32_t h = w & (nzt | 0x7FFF7FFFu);
+  const uint32_t s = __builtin_bit_cast(uint32_t, __builtin_bit_cast(i16x2, h) >> (i16x2){15, 15});
+  return h ^ (s | 0x80008000u);
+}
+
+// Per 16-bit half of the packed keys w: 1 if the key is above c (c in both halves of
+// cc), else 0 -- a saturating packed subtraction and a packed minimum with 1.
+__device__ __forceinline__ uint32_t pk_above(uint32_t w, uint32_t cc) {
+  uint32_t d;
+  asm("v_pk_sub_u16 %0, %1, %2 clamp\n\tv_pk_min_u16 %0, %0, %3" : "=&v"(d) : "v"(w), "s"(cc), "s"(0x00010001u));
+  return d;
+}
+// sum of the two 16-bit halves of packed counters (each at most 0x7FFF)
+__device__ __forceinline__ uint32_t pk_hsum(uint32_t c) { return (c & 0xFFFFu) + (c >> 16); }
+// packed 16-bit unsigned max, min and wrapping subtraction (v_pk_max_u16, v_pk_min_u16, v_pk_sub_u16)
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pk_max(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, a), __builtin_bit_cast(u16x2, b)));
+}
+__device__ __forceinline__ uint32_t pk_min(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_min(__builtin_bit_cast(u16x2, a), __builtin_bit_cast(u16x2, b)));
+}
+__device__ __forceinline__ uint32_t pk_sub(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) - __builtin_bit_cast(u16x2, b));
 }
 // key e of a thread's packed pairs (w[e / 2], low half = even e)
 __device__ __forceinline__ uint32_t kh(const uint32_t* w, int e) { return (e & 1) ? w[e >> 1] >> 16 : w[e >> 1] & 0xFFFFu; }
@@ -331,13 +355,16 @@ void li_topk_kernel(LiTopkArgs a) {
       // keys, so their relative order is irrelevant to the stable sort.
       uint32_t* cand = work;
       const int i0 = t * RPT;
-      uint32_t cg = 0, cc = 0;
+      // cg: keys of higher bins (>= (bin + 1) << 5); cc: nonzero keys of bin `bin` (keys
+      // >= max(bin << 5, 1), minus cg), counted per packed pair (per-half sums <= 16)
+      const uint32_t g1 = ((bin + 1) << 5) - 1, b1 = bin == 0 ? 0u : (bin << 5) - 1;
+      uint32_t ag = 0, ab = 0;
 #pragma unroll
-      for (int e = 0; e < RPT; ++e) {
-        const uint32_t v = kh(w, e) >> 5;
-        cg += v > bin ? 1u : 0u;
-        cc += (v == bin && kh(w, e) != 0u) ? 1u : 0u;
+      for (int i = 0; i < RPT / 2; ++i) {
+        ag += pk_above(w[i], g1 * 0x10001u);
+        ab += pk_above(w[i], b1 * 0x10001u);
       }
+      const uint32_t cg = pk_hsum(ag), cc = pk_hsum(ab) - cg;
       uint32_t tot1;
       const uint32_t pgc = block_excl_scan((cg << 16) | cc, red, &tot1);
       uint32_t pg = pgc >> 16, pc = pgc & 0xFFFFu;
@@ -390,6 +417,41 @@ void li_topk_kernel(LiTopkArgs a) {
       });
     }
     umin = T;
+  }
+  if constexpr (SHORT) {
+    if (L <= k) {
+      // every visible entry is taken, at its own index (the keys past L are 0 and are
+      // not written); the largest key and the smallest nonzero one bound the sort's
+      // passes, as in the general path below
+      const int i0 = t * RPT;
+      uint32_t mx2 = 0, mn2 = 0xFFFFFFFFu;   // per half: largest key, smallest key - 1 (0 wraps to 0xFFFF)
+#pragma unroll
+      for (int i = 0; i < RPT / 2; ++i) {
+        mx2 = pk_max(mx2, w[i]);
+        mn2 = pk_min(mn2, pk_sub(w[i], 0x00010001u));
+      }
+      const uint32_t mx = max(mx2 & 0xFFFFu, mx2 >> 16), mnm1 = min(mn2 & 0xFFFFu, mn2 >> 16);
+      const uint32_t mninv = mnm1 == 0xFFFFu ? 0u : 0xFFFEu - mnm1;   // 0xFFFF - smallest nonzero key
+      if (i0 + RPT <= L) {
+        const uint32_t xb = 0xFFFFu - (uint32_t)i0;
+#pragma unroll
+        for (int c = 0; c < RPT / 4; ++c) {   // entries 4c .. 4c + 3: words 2c, 2c + 1
+          const uint32_t w0 = w[2 * c], w1 = w[2 * c + 1];
+          *reinterpret_cast<uint4*>(&sbuf[i0 + 4 * c]) =
+              make_uint4((w0 << 16) | (xb - 4 * c), (w0 & 0xFFFF0000u) | (xb - 4 * c - 1),
+                         (w1 << 16) | (xb - 4 * c - 2), (w1 & 0xFFFF0000u) | (xb - 4 * c - 3));
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < RPT; ++e)
+          if (i0 + e < L) sbuf[i0 + e] = (kh(w, e) << 16) | (0xFFFFu - (uint32_t)(i0 + e));
+      }
+      uint32_t tot, cmx, cmn;
+      block_scan_max2(0u, mx, mninv, red, &tot, &cmx, &cmn);
+      umax = cmx;
+      umin = 0xFFFFu - cmn;
+      compacted = true;
+    }
   }
   if (!compacted) {
     // positions: selected-before = greater-before + min(ties-before, need); one scan of
