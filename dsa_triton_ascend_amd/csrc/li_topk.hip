@@ -158,12 +158,11 @@ struct DigitCount {
 };
 
 // Stable LSD radix sort of E keys per thread (blocked: thread t holds ranks
-// [E t, E t + E)), ascending on the inverted upper 16 bits = score descending, over
-// passes [0, npass) (4 bits each, from the low bits up). `cnt` holds 16 x TPB 16-bit
-// counters in [digit][thread] order.
+// [E t, E t + E)), ascending on the upper 16 bits, over passes [0, npass) (4 bits each,
+// from the low bits up). `cnt` holds 16 x TPB 16-bit counters in [digit][thread] order.
 template <int E>
-__device__ __forceinline__ void radix_sort_desc16(uint32_t (&key)[E], int npass, uint32_t* sbuf, uint16_t* cnt,
-                                                  uint32_t* red) {
+__device__ __forceinline__ void radix_sort_asc16(uint32_t (&key)[E], int npass, uint32_t* sbuf, uint16_t* cnt,
+                                                 uint32_t* red) {
   const int t = threadIdx.x;
 #pragma unroll 1
   for (int pass = 0; pass < npass; ++pass) {
@@ -171,7 +170,7 @@ __device__ __forceinline__ void radix_sort_desc16(uint32_t (&key)[E], int npass,
     DigitCount<E> dc;
     uint32_t lrank[E];
 #pragma unroll
-    for (int e = 0; e < E; ++e) lrank[e] = dc.take(((~key[e]) >> shift) & 15u);
+    for (int e = 0; e < E; ++e) lrank[e] = dc.take(__builtin_amdgcn_ubfe(key[e], shift, 4));
 #pragma unroll
     for (int d = 0; d < 16; ++d) cnt[d * TPB + t] = (uint16_t)dc.count(d);
     __syncthreads();
@@ -197,7 +196,7 @@ __device__ __forceinline__ void radix_sort_desc16(uint32_t (&key)[E], int npass,
     __syncthreads();
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-      const int d = ((~key[e]) >> shift) & 15;
+      const int d = __builtin_amdgcn_ubfe(key[e], shift, 4);
       sbuf[cnt[d * TPB + t] + lrank[e]] = key[e];
     }
     __syncthreads();
@@ -367,12 +366,15 @@ void li_topk_kernel(LiTopkArgs a) {
       const uint32_t cg = pk_hsum(ag), cc = pk_hsum(ab) - cg;
       uint32_t tot1;
       const uint32_t pgc = block_excl_scan((cg << 16) | cc, red, &tot1);
-      uint32_t pg = pgc >> 16, pc = pgc & 0xFFFFu;
+      uint32_t* ps = sbuf + (pgc >> 16);
+      uint32_t* pcd = cand + (pgc & 0xFFFFu);
+      const uint32_t xb = 0xFFFFu - (uint32_t)i0;
 #pragma unroll
       for (int e = 0; e < RPT; ++e) {
-        const uint32_t ue = kh(w, e), v = ue >> 5;
-        if (v > bin) sbuf[pg++] = (ue << 16) | (0xFFFFu - (uint32_t)(i0 + e));
-        else if (v == bin && ue != 0u) cand[pc++] = (ue << 16) | (uint32_t)(i0 + e);
+        // the key compared as it lies in its half; ku = key << 16
+        const uint32_t ue = kh(w, e), ku = (e & 1) ? (w[e >> 1] & 0xFFFF0000u) : (w[e >> 1] << 16);
+        if (ue > g1) *ps++ = ku | (xb - e);                      // a higher bin
+        else if (ue > b1) *pcd++ = ku | (uint32_t)(i0 + e);      // bin `bin`, nonzero
       }
       // candidates [c0, c1) of this thread (at most 8: nc <= 2048)
       const uint32_t m = (nc + TPB - 1) / TPB, c0 = min((uint32_t)t * m, nc), c1 = min(c0 + m, nc);
@@ -441,7 +443,7 @@ void li_topk_kernel(LiTopkArgs a) {
               make_uint4((w0 << 16) | (xb - 4 * c), (w0 & 0xFFFF0000u) | (xb - 4 * c - 1),
                          (w1 << 16) | (xb - 4 * c - 2), (w1 & 0xFFFF0000u) | (xb - 4 * c - 3));
         }
-      } else {
+      } else if (i0 < L) {   // the one thread holding the row's end
 #pragma unroll
         for (int e = 0; e < RPT; ++e)
           if (i0 + e < L) sbuf[i0 + e] = (kh(w, e) << 16) | (0xFFFFu - (uint32_t)(i0 + e));
@@ -509,14 +511,20 @@ void li_topk_kernel(LiTopkArgs a) {
   for (int i = nout + t; i < E * TPB; i += TPB) sbuf[i] = 0u;  // pads sort last
   __syncthreads();
 
-  // ---- stable radix sort of the selected keys, then write in rank order. Passes over
-  // digits every selected key shares (a common prefix of umin and umax) are skipped.
-  int npass = 4;
-  while (npass > 0 && (umin >> (4 * (npass - 1))) == (umax >> (4 * (npass - 1)))) --npass;
+  // ---- stable radix sort of the selected keys, then write in rank order. The sort runs
+  // ascending on v = umax - key (score descending), over the 4-bit digits that
+  // umax - umin spans; the padding entries (key 0) take v = 16^npass - 1, the largest
+  // value those digits hold, and being last in the input they stay last among equals.
+  const uint32_t urange = umax > umin ? umax - umin : 0u;
+  const int npass = urange == 0 ? 0 : (35 - __builtin_clz(urange)) / 4;
+  const uint32_t vmax = (1u << (4 * npass)) - 1u;
   uint32_t key[E];
 #pragma unroll
-  for (int e = 0; e < E; ++e) key[e] = sbuf[E * t + e];
-  radix_sort_desc16<E>(key, npass, sbuf, cnt, red);
+  for (int e = 0; e < E; ++e) {
+    const uint32_t x = sbuf[E * t + e];
+    key[e] = (min(umax - (x >> 16), vmax) << 16) | (x & 0xFFFFu);
+  }
+  radix_sort_asc16<E>(key, npass, sbuf, cnt, red);
   // ranks E t .. E t + E - 1 of thread t: their index (or -1) and 16-bit value (or 0)
   int32_t oi[E];
   uint16_t ov[E];
@@ -525,7 +533,7 @@ void li_topk_kernel(LiTopkArgs a) {
     const bool ok = E * t + e < nout;
     if constexpr (WIDE) oi[e] = ok ? sidx[key[e] & 0xFFFFu] : -1;
     else oi[e] = ok ? (int32_t)(0xFFFFu - (key[e] & 0xFFFFu)) : -1;
-    ov[e] = ok ? unord16(key[e] >> 16) : (uint16_t)0;
+    ov[e] = ok ? unord16(umax - (key[e] >> 16)) : (uint16_t)0;
   }
   // 16-byte stores when the thread's whole run lies inside the row and rows are
   // 16-byte aligned (k % 8 == 0); the rest element by element
