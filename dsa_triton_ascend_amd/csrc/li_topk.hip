@@ -111,7 +111,7 @@ __device__ __forceinline__ uint32_t pk_sub(uint32_t a, uint32_t b) {
 __device__ __forceinline__ uint32_t kh(const uint32_t* w, int e) { return (e & 1) ? w[e >> 1] >> 16 : w[e >> 1] & 0xFFFFu; }
 
 // Keys [base + 32t, +32) of the row as packed ord16 pairs; entries at or past L are 0
-// (below every real key).
+// (below every real key). Threads whose entries all lie past L load nothing.
 __device__ __forceinline__ void load_keys(const uint16_t* row, int L, int base, uint32_t (&w)[RPT / 2]) {
   const int i0 = base + threadIdx.x * RPT;
   if (i0 + RPT <= L) {
@@ -123,13 +123,16 @@ __device__ __forceinline__ void load_keys(const uint16_t* row, int L, int base, 
       w[c * 4 + 2] = ord16x2(v.z);
       w[c * 4 + 3] = ord16x2(v.w);
     }
-  } else {
+  } else if (i0 < L) {
 #pragma unroll
     for (int e = 0; e < RPT; e += 2) {
       const uint32_t lo = (i0 + e < L) ? ord16(row[i0 + e]) : 0u;
       const uint32_t hi = (i0 + e + 1 < L) ? ord16(row[i0 + e + 1]) : 0u;
       w[e >> 1] = lo | (hi << 16);
     }
+  } else {
+#pragma unroll
+    for (int e = 0; e < RPT / 2; ++e) w[e] = 0u;
   }
 }
 
@@ -281,6 +284,9 @@ void li_topk_kernel(LiTopkArgs a) {
   const int nchunks = SHORT ? 1 : (L + ROW_CACHED - 1) / ROW_CACHED;
   uint32_t w[RPT / 2];   // the thread's keys, packed pairs
   if (nchunks == 1) load_keys(row, L, 0, w);
+  // one chunk: whether this wave holds any entry of the row (the per-entry loops of the
+  // others are skipped: every key they hold is 0)
+  const bool wv = nchunks > 1 || __builtin_amdgcn_readfirstlane(t >> 6) * 64 * RPT < L;
   uint32_t T = 0;  // keys > T are all taken; keys == T up to `need`
   uint32_t need = 0xFFFFFFFFu;
   uint32_t umin = 0, umax = 0xFFFFu;   // bounds of the selected keys (the sort's pass range)
@@ -294,9 +300,13 @@ void li_topk_kernel(LiTopkArgs a) {
 #pragma unroll 1
     for (int ch = 0; ch < nchunks; ++ch) {
       if (nchunks > 1) load_keys(row, L, ch * ROW_CACHED, w);
+      if (wv)
 #pragma unroll
-      for (int e = 0; e < RPT; ++e)
-        if (kh(w, e) != 0u) atomicAdd(&hist[kh(w, e) >> 5], 1u);
+        for (int i = 0; i < RPT / 2; ++i) {   // the bins of both keys of a pair, straight from the word
+          const uint32_t x = w[i];
+          if (x & 0xFFFFu) atomicAdd(&hist[(x >> 5) & 0x7FFu], 1u);
+          if (x >> 16) atomicAdd(&hist[x >> 21], 1u);
+        }
     }
     __syncthreads();
     uint32_t h[8];   // thread t: bins 2047 - 8t - j, j < 8 (the scan runs from the top)
@@ -358,24 +368,26 @@ void li_topk_kernel(LiTopkArgs a) {
       // >= max(bin << 5, 1), minus cg), counted per packed pair (per-half sums <= 16)
       const uint32_t g1 = ((bin + 1) << 5) - 1, b1 = bin == 0 ? 0u : (bin << 5) - 1;
       uint32_t ag = 0, ab = 0;
+      if (wv)
 #pragma unroll
-      for (int i = 0; i < RPT / 2; ++i) {
-        ag += pk_above(w[i], g1 * 0x10001u);
-        ab += pk_above(w[i], b1 * 0x10001u);
-      }
+        for (int i = 0; i < RPT / 2; ++i) {
+          ag += pk_above(w[i], g1 * 0x10001u);
+          ab += pk_above(w[i], b1 * 0x10001u);
+        }
       const uint32_t cg = pk_hsum(ag), cc = pk_hsum(ab) - cg;
       uint32_t tot1;
       const uint32_t pgc = block_excl_scan((cg << 16) | cc, red, &tot1);
       uint32_t* ps = sbuf + (pgc >> 16);
       uint32_t* pcd = cand + (pgc & 0xFFFFu);
       const uint32_t xb = 0xFFFFu - (uint32_t)i0;
+      if (wv)
 #pragma unroll
-      for (int e = 0; e < RPT; ++e) {
-        // the key compared as it lies in its half; ku = key << 16
-        const uint32_t ue = kh(w, e), ku = (e & 1) ? (w[e >> 1] & 0xFFFF0000u) : (w[e >> 1] << 16);
-        if (ue > g1) *ps++ = ku | (xb - e);                      // a higher bin
-        else if (ue > b1) *pcd++ = ku | (uint32_t)(i0 + e);      // bin `bin`, nonzero
-      }
+        for (int e = 0; e < RPT; ++e) {
+          // the key compared as it lies in its half; ku = key << 16
+          const uint32_t ue = kh(w, e), ku = (e & 1) ? (w[e >> 1] & 0xFFFF0000u) : (w[e >> 1] << 16);
+          if (ue > g1) *ps++ = ku | (xb - e);                      // a higher bin
+          else if (ue > b1) *pcd++ = ku | (uint32_t)(i0 + e);      // bin `bin`, nonzero
+        }
       // candidates [c0, c1) of this thread (at most 8: nc <= 2048)
       const uint32_t m = (nc + TPB - 1) / TPB, c0 = min((uint32_t)t * m, nc), c1 = min(c0 + m, nc);
       resolve([&] {
