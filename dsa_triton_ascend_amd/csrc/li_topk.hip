@@ -163,17 +163,23 @@ struct DigitCount {
 // Stable LSD radix sort of E keys per thread (blocked: thread t holds ranks
 // [E t, E t + E)), ascending on the upper 16 bits, over passes [0, npass) (4 bits each,
 // from the low bits up). `cnt` holds 16 x TPB 16-bit counters in [digit][thread] order.
+// Entries at ranks >= n are padding whose digits are all 15 (and whose values are
+// never read back): they stay behind every real key in each pass, so they affect no
+// real key's position, and a wave holding padding only neither counts nor moves it
+// (the ranks past the active waves' slots are then left stale).
 template <int E>
-__device__ __forceinline__ void radix_sort_asc16(uint32_t (&key)[E], int npass, uint32_t* sbuf, uint16_t* cnt,
-                                                 uint32_t* red) {
+__device__ __forceinline__ void radix_sort_asc16(uint32_t (&key)[E], int npass, int n, uint32_t* sbuf,
+                                                 uint16_t* cnt, uint32_t* red) {
   const int t = threadIdx.x;
+  const bool act = (int)__builtin_amdgcn_readfirstlane(t >> 6) * 64 * E < n;
 #pragma unroll 1
   for (int pass = 0; pass < npass; ++pass) {
     const int shift = 16 + 4 * pass;
     DigitCount<E> dc;
     uint32_t lrank[E];
+    if (act)
 #pragma unroll
-    for (int e = 0; e < E; ++e) lrank[e] = dc.take(__builtin_amdgcn_ubfe(key[e], shift, 4));
+      for (int e = 0; e < E; ++e) lrank[e] = dc.take(__builtin_amdgcn_ubfe(key[e], shift, 4));
 #pragma unroll
     for (int d = 0; d < 16; ++d) cnt[d * TPB + t] = (uint16_t)dc.count(d);
     __syncthreads();
@@ -197,14 +203,16 @@ __device__ __forceinline__ void radix_sort_asc16(uint32_t (&key)[E], int npass, 
     *reinterpret_cast<uint4*>(cnt + t * 16) = make_uint4(o[0], o[1], o[2], o[3]);
     *reinterpret_cast<uint4*>(cnt + t * 16 + 8) = make_uint4(o[4], o[5], o[6], o[7]);
     __syncthreads();
+    if (act)
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const int d = __builtin_amdgcn_ubfe(key[e], shift, 4);
-      sbuf[cnt[d * TPB + t] + lrank[e]] = key[e];
-    }
+      for (int e = 0; e < E; ++e) {
+        const int d = __builtin_amdgcn_ubfe(key[e], shift, 4);
+        sbuf[cnt[d * TPB + t] + lrank[e]] = key[e];
+      }
     __syncthreads();
+    if (act)
 #pragma unroll
-    for (int e = 0; e < E; ++e) key[e] = sbuf[E * t + e];
+      for (int e = 0; e < E; ++e) key[e] = sbuf[E * t + e];
     // the next pass writes cnt (read above, before the barrier) and sbuf (after two barriers)
   }
 }
@@ -536,7 +544,7 @@ void li_topk_kernel(LiTopkArgs a) {
     const uint32_t x = sbuf[E * t + e];
     key[e] = (min(umax - (x >> 16), vmax) << 16) | (x & 0xFFFFu);
   }
-  radix_sort_asc16<E>(key, npass, sbuf, cnt, red);
+  radix_sort_asc16<E>(key, npass, nout, sbuf, cnt, red);
   // ranks E t .. E t + E - 1 of thread t: their index (or -1) and 16-bit value (or 0)
   int32_t oi[E];
   uint16_t ov[E];
