@@ -9,26 +9,26 @@
 // One 256-thread work-group per score row (any length: indices are 32-bit):
 //   1. Thread t owns the contiguous index range [32t, 32t+32) of the row; the
 //      16-bit scores are mapped to order-preserving keys u (ord16) and kept in
-//      VGPRs (rows longer than 8192 entries are streamed from memory instead, in
-//      chunks of 8192).
-//   2. L > k: the k-th largest key T is found with two 256-bin LDS histograms:
-//      one over the high byte of the keys picks the bin holding the k-th largest
-//      (a scan from the top bin), one over the low byte of the keys in that bin
-//      picks T; the same scans give the number of keys above T.
-//   3. Order-preserving compaction: entries with u > T and the first
-//      k - count(u > T) entries with u == T (in index order) are written, in
-//      index order, to positions p < k as keys (u << 16 | x); p comes from block
-//      exclusive scans of the per-thread counts. Rows of up to 65536 entries carry
+//      VGPRs as packed pairs (rows longer than 8192 entries are streamed from
+//      memory instead, in chunks of 8192). Waves holding no entry of the row skip
+//      the per-entry loops below.
+//   2. L > k: a 2048-bin LDS histogram of u >> 5, scanned from the top bin, gives
+//      the bin holding the k-th largest key and the number of keys above that bin.
+//   3. Order-preserving compaction: keys of higher bins go, in index order, to
+//      positions p < k as (u << 16 | x), p from a block exclusive scan of the
+//      per-thread counts (packed 16-bit counting on the key pairs); the keys of the
+//      bin go to a candidate list, among which a 32-bin histogram of the low 5 bits
+//      finds the exact threshold T and how many keys equal to T to take; those
+//      follow, also in index order. Rows of up to 65536 entries carry
 //      x = 0xFFFF - index; longer rows (WIDE) carry x = p and keep the 32-bit index
 //      in a second LDS array at p (p, like the index, increases along the row).
-//   4. A stable LSD radix sort on the 16-bit score (passes of 4 bits, digits of
-//      the inverted key so larger scores come first). Each thread counts the digits
-//      of its keys in registers (packed counters: no LDS read-modify-write chain),
-//      one block scan turns the per-thread counts into scatter offsets. Passes over
-//      bits that every selected key shares are identities and are skipped: with u
-//      in [umin, umax], pass p runs only if umin >> 4p != umax >> 4p. Stability
-//      preserves the index order of equal scores, which is exactly the golden's tie
-//      rule.
+//      Rows with L <= k take every entry at its own index.
+//   4. A stable LSD radix sort ascending on v = umax - u (score descending; umax
+//      and umin bound the selected keys), 4-bit digits, over only the digits that
+//      umax - umin spans. Each thread counts the digits of its keys in registers
+//      (packed counters: no LDS read-modify-write chain), one block scan turns the
+//      per-thread counts into scatter offsets. Stability preserves the index order
+//      of equal scores, which is exactly the golden's tie rule.
 //   5. One pass writes the indices and 16-bit values in rank order.
 // The selection histogram and the sort's counters share one LDS array (they are
 // never live together), so a work-group needs ~16 KB and more of them fit a CU.
