@@ -329,3 +329,62 @@ def test_pa_bsnd_decode_shape(dev):
     stats = check_li(gi, gv, _np(q).reshape(B, 1, N1, D), dense, _np(w).reshape(B, 1, N1), np.ones(B, int),
                      np.asarray(lens), K, 3, dtype)
     assert stats.flips <= max(4, 0.02 * stats.elements), stats
+
+
+def _crafted_bits(family, rows, S2, rng):
+    """16-bit bf16 patterns of a crafted score matrix [rows, S2] (uint16)."""
+    f32 = dict(dtype=np.float32)
+    if family == "equal":   # one value: no sort pass runs
+        return np.full((rows, S2), 0x3F80, np.uint16)
+    if family == "signed_zeros":   # +0 / -0 (equal keys) with a few real values
+        b = np.where(rng.random((rows, S2), **f32) < 0.5, 0x0000, 0x8000).astype(np.uint16)
+        x = ((rng.standard_normal((rows, S2), **f32) * 0.1).view(np.uint32) >> 16).astype(np.uint16)
+        return np.where(rng.random((rows, S2), **f32) < 0.05, x, b)
+    if family == "extremes":   # +inf, the largest finite values, subnormals, both signs
+        pool = np.array([0x7F80, 0x7F7F, 0xFF7F, 0x0001, 0x8001, 0x3F80, 0xBF80, 0x0000], np.uint16)
+        return pool[rng.integers(0, len(pool), (rows, S2))]
+    if family == "two_values":   # adjacent keys: the threshold sits in a long run of ties
+        return np.where(rng.random((rows, S2), **f32) < 0.5, 0x3F80, 0x3F81).astype(np.uint16)
+    if family == "wide":   # both signs over forty binades: every digit pass runs
+        x = rng.standard_normal((rows, S2), **f32) * np.exp2(rng.uniform(-20, 20, (rows, S2))).astype(np.float32)
+        return (x.view(np.uint32) >> 16).astype(np.uint16)
+    if family == "narrow":   # a few dozen keys either side of a 16-key digit boundary
+        key = 0xBF80 + rng.integers(-24, 24, (rows, S2))   # ord16 keys of positive values
+        return (key & 0x7FFF).astype(np.uint16)
+    raise ValueError(family)
+
+
+@pytest.mark.parametrize("S1,S2", [(8192, 8192), (64, 12000), (8, 70000)])
+@pytest.mark.parametrize("family", ["equal", "signed_zeros", "extremes", "two_values", "wide", "narrow"])
+def test_topk_crafted_score_rows(dev, S1, S2, family):
+    """The top-k kernel alone on crafted score rows, against the golden's stable sort
+    (oracle select_topk): ties, +0/-0, infinities and subnormals, rows of one value
+    (no digit pass), both signs over many binades (every pass), and rows of every
+    visible length around k, in the register-cached (S2 <= 8192), chunked and 32-bit
+    index paths. -inf is left out: the golden drops -inf entries (its mask value)."""
+    from dsa_triton_ascend_amd.lightning_indexer import IndexerPlan
+    K = 2048
+    rng = np.random.default_rng(11)
+    q = torch.zeros(1, S1, 8, 128, dtype=torch.bfloat16, device=dev)
+    k = torch.zeros(1, S2, 1, 128, dtype=torch.bfloat16, device=dev)
+    w = torch.zeros(1, S1, 8, dtype=torch.float32, device=dev)
+    plan = IndexerPlan(q, k, w, sparse_count=K, sparse_mode=3, return_value=True)
+    bits = _crafted_bits(family, S1, S2, rng)
+    sc = torch.from_numpy(bits.view(np.int16)).to(dev)
+    plan.scores.zero_()
+    plan.scores[:S1, :S2] = sc
+    plan.topk()
+    torch.cuda.synchronize()
+    gi = plan.idx.reshape(S1, K).cpu().numpy()
+    gv = plan.vals.reshape(S1, K).float().cpu().numpy()
+    vals = (bits.astype(np.uint32) << 16).view(np.float32)
+    rows = sorted({0, 1, 2, 63, 64, 255, 1023, 2046, 2047, 2048, 2049, 3000, 4095, 4096, 6143,
+                   6144, 8190, 8191} | set(range(0, S1, 97)))
+    rows = [r for r in rows if r < S1]
+    for r in rows:
+        L = S2 - S1 + r + 1
+        s = np.full(S2, -np.inf, np.float32)
+        s[:L] = vals[r, :L]
+        ei, ev = LI.select_topk(s, S2, K)
+        assert np.array_equal(gi[r], ei), (family, S2, r, L, np.flatnonzero(gi[r] != ei)[:8])
+        assert np.array_equal(gv[r], ev), (family, S2, r, L)
