@@ -396,17 +396,21 @@ void li_topk_kernel(LiTopkArgs a) {
           if (ue > g1) *ps++ = ku | (xb - e);                      // a higher bin
           else if (ue > b1) *pcd++ = ku | (uint32_t)(i0 + e);      // bin `bin`, nonzero
         }
-      // candidates [c0, c1) of this thread (at most 8: nc <= 2048)
+      // candidates [c0, c1) of this thread (at most 8: nc <= 2048; the loops stop at the
+      // block-uniform m, typically 1 or 2)
       const uint32_t m = (nc + TPB - 1) / TPB, c0 = min((uint32_t)t * m, nc), c1 = min(c0 + m, nc);
       resolve([&] {
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
+        for (int j = 0; j < 8; ++j) {
+          if (j >= (int)m) break;
           if (c0 + j < c1) atomicAdd(&chist[(cand[c0 + j] >> 16) & 31u], 1u);
+        }
       });
       uint32_t cv[8];
       uint32_t g2 = 0, e2 = 0;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
+        if (j >= (int)m) break;
         cv[j] = c0 + j < c1 ? cand[c0 + j] : 0u;
         g2 += (c0 + j < c1 && (cv[j] >> 16) > T) ? 1u : 0u;
         e2 += (c0 + j < c1 && (cv[j] >> 16) == T) ? 1u : 0u;
@@ -416,6 +420,7 @@ void li_topk_kernel(LiTopkArgs a) {
       uint32_t qg = above + (pge >> 16), qe = pge & 0xFFFFu;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
+        if (j >= (int)m) break;
         if (c0 + j >= c1) continue;
         const uint32_t key16 = cv[j] >> 16, x = 0xFFFFu - (cv[j] & 0xFFFFu);
         if (key16 > T) {
