@@ -541,15 +541,18 @@ __global__ __launch_bounds__(256) void sfa_merge_kernel(SfaArgs a, int splits, W
   // of two; the entries of splits past the row's tokens are in bounds and never used
   uint4 v[MU][MERGE_MAX_SPLITS];
   float sm_u[MU][MERGE_MAX_SPLITS], sm_t[MU][MERGE_MAX_SPLITS], sm_l[MU][MERGE_MAX_SPLITS];
+  static_assert(CH % 64 == 0 || 64 % CH == 0, "a wave's units cover whole heads or divide one");
 #pragma unroll
   for (int k = 0; k < MU; ++k) {
     const int u = u0 + k * 256;
     const int uc = u < units ? u : units - 1;
+    // D >= 512: one head per wave, so its statistics are scalar loads
+    const int hw = CH >= 64 ? __builtin_amdgcn_readfirstlane(uc / CH) : uc / CH;
 #pragma unroll
     for (int sp = 0; sp < MERGE_MAX_SPLITS; ++sp)
       if (sp < splits) {
         v[k][sp] = ldg16(po + ((int64_t)sp * n1 + uc / CH) * D + (uc % CH) * 8);
-        const float* q = ps + ((int64_t)sp * n1 + uc / CH) * 3;
+        const float* q = ps + ((int64_t)sp * n1 + hw) * 3;
         sm_u[k][sp] = q[0];
         sm_t[k][sp] = q[1];
         sm_l[k][sp] = q[2];
