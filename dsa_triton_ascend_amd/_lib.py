@@ -31,6 +31,8 @@ SIGNATURES = {
     "dsa_li_score": (_I, [_P, _P, _P, _I, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I,
                           _P, _I64, _P]),
     "dsa_li_topk": (_I, [_P, _I64, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P]),
+    "dsa_li_topk_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
+    "dsa_li_topk_ws": (_I, [_P, _I64, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _SZ, _P]),
     "dsa_sfa_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I, _I]),
     "dsa_sfa_workspace_zero_bytes": (_SZ, []),
     "dsa_sfa_fwd": (_I, [_P, _P, _P, _P, _I, _P, _I, _I, _P, _I, _I, _P, _P, _P, _P, _I, _I, _I,

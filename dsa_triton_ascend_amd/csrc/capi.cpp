@@ -108,24 +108,58 @@ int dsa_li_score_paged(const void* query, const void* key_cache, const void* wei
   return hip_status(launch_li_score(a, (hipStream_t)stream), "dsa_li_score_paged launch");
 }
 
+namespace {
+// Argument checks of dsa_li_topk / dsa_li_topk_ws; DSA_OK when the call may proceed.
+int check_li_topk(const char* fn, const uint16_t* scores, int64_t score_ld, int io_dtype,
+                  const int32_t* row_start, const int32_t* act_q, const int32_t* act_k, int batch,
+                  int total_rows, int n2, int s2, int sparse_mode, int sparse_count, const int32_t* indices) {
+  if (!scores || !row_start || !act_q || !act_k || !indices)
+    return fail(DSA_ERR_INVALID, "%s: null pointer argument", fn);
+  if (!is16(io_dtype)) return fail(DSA_ERR_INVALID, "%s: io_dtype must be fp16 or bf16", fn);
+  if (batch <= 0 || total_rows < 0 || n2 <= 0 || s2 < 0)
+    return fail(DSA_ERR_INVALID, "%s: non-positive shape", fn);
+  if (sparse_count <= 0) return fail(DSA_ERR_INVALID, "%s: sparse_count must be positive", fn);
+  if (sparse_mode != 0 && sparse_mode != 3)
+    return fail(DSA_ERR_INVALID, "%s: sparse_mode must be 0 or 3", fn);
+  if (score_ld < s2) return fail(DSA_ERR_INVALID, "%s: score_ld < S2", fn);
+  return DSA_OK;
+}
+}  // namespace
+
 int dsa_li_topk(const uint16_t* scores, int64_t score_ld, int io_dtype, const int32_t* row_start,
                 const int32_t* act_q, const int32_t* act_k, int batch, int total_rows, int n2,
                 int s2, int sparse_mode, int sparse_count, int32_t* indices, uint16_t* values,
                 void* stream) {
-  if (!scores || !row_start || !act_q || !act_k || !indices)
-    return fail(DSA_ERR_INVALID, "dsa_li_topk: null pointer argument");
-  if (!is16(io_dtype)) return fail(DSA_ERR_INVALID, "dsa_li_topk: io_dtype must be fp16 or bf16");
-  if (batch <= 0 || total_rows < 0 || n2 <= 0 || s2 < 0)
-    return fail(DSA_ERR_INVALID, "dsa_li_topk: non-positive shape");
-  if (sparse_count <= 0) return fail(DSA_ERR_INVALID, "dsa_li_topk: sparse_count must be positive");
+  const int st = check_li_topk("dsa_li_topk", scores, score_ld, io_dtype, row_start, act_q, act_k, batch,
+                               total_rows, n2, s2, sparse_mode, sparse_count, indices);
+  if (st != DSA_OK) return st;
   if (sparse_count > LI_TOPK_MAX_K)
-    return fail(DSA_ERR_UNSUPPORTED, "dsa_li_topk: sparse_count=%d > %d", sparse_count, LI_TOPK_MAX_K);
-  if (sparse_mode != 0 && sparse_mode != 3)
-    return fail(DSA_ERR_INVALID, "dsa_li_topk: sparse_mode must be 0 or 3");
-  if (score_ld < s2) return fail(DSA_ERR_INVALID, "dsa_li_topk: score_ld < S2");
+    return fail(DSA_ERR_UNSUPPORTED, "dsa_li_topk: sparse_count=%d > %d (use dsa_li_topk_ws)", sparse_count,
+                LI_TOPK_MAX_K);
   LiTopkArgs a{scores, score_ld, io_dtype, row_start, act_q, act_k, batch, total_rows, n2, s2,
                sparse_mode, sparse_count, indices, values};
   return hip_status(launch_li_topk(a, (hipStream_t)stream), "dsa_li_topk launch");
+}
+
+size_t dsa_li_topk_workspace_bytes(int total_rows, int n2, int s2, int sparse_count) {
+  return li_topk_workspace_bytes(total_rows, n2, s2, sparse_count);
+}
+
+int dsa_li_topk_ws(const uint16_t* scores, int64_t score_ld, int io_dtype, const int32_t* row_start,
+                   const int32_t* act_q, const int32_t* act_k, int batch, int total_rows, int n2,
+                   int s2, int sparse_mode, int sparse_count, int32_t* indices, uint16_t* values,
+                   void* workspace, size_t workspace_bytes, void* stream) {
+  const int st = check_li_topk("dsa_li_topk_ws", scores, score_ld, io_dtype, row_start, act_q, act_k, batch,
+                               total_rows, n2, s2, sparse_mode, sparse_count, indices);
+  if (st != DSA_OK) return st;
+  LiTopkArgs a{scores, score_ld, io_dtype, row_start, act_q, act_k, batch, total_rows, n2, s2,
+               sparse_mode, sparse_count, indices, values};
+  if (sparse_count <= LI_TOPK_MAX_K)
+    return hip_status(launch_li_topk(a, (hipStream_t)stream), "dsa_li_topk_ws launch");
+  const size_t need = li_topk_workspace_bytes(total_rows, n2, s2, sparse_count);
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return fail(DSA_ERR_INVALID, "dsa_li_topk_ws: workspace of %zu bytes < %zu", workspace_bytes, need);
+  return hip_status(launch_li_topk_big(a, workspace, (hipStream_t)stream), "dsa_li_topk_ws launch");
 }
 
 size_t dsa_sfa_workspace_bytes(int total_rows, int n1, int d, int sparse_count,

@@ -345,6 +345,9 @@ struct SfaArgs {
 };
 hipError_t launch_li_score(const LiScoreArgs& a, hipStream_t s);
 hipError_t launch_li_topk(const LiTopkArgs& a, hipStream_t s);
+// sparse_count > LI_TOPK_MAX_K: every visible entry sorted in caller-provided scratch
+size_t li_topk_workspace_bytes(int total_rows, int n2, int s2, int k);
+hipError_t launch_li_topk_big(const LiTopkArgs& a, void* ws, hipStream_t s);
 hipError_t launch_sfa_fwd(const SfaArgs& a, hipStream_t s);
 // Teacher sums of the indexer KL losses on the attention kernel's S^T path (BSND keys
 // [B, S2, 1, D | 64]): slot i of row r is key row b * S2 + clip(sidx[r][i], 0, S2 - 1) (slot i

@@ -584,6 +584,126 @@ void li_topk_kernel(LiTopkArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- sparse_count > LI_TOPK_MAX_K
+// Rows whose top-k does not fit the LDS sort (k > 16384): one 1024-thread work-group
+// per score row sorts every visible entry in global scratch (two buffers of S2 entries
+// per row, caller-provided) and writes the first min(L, k). Entries are
+// (v << 32 | index), v = umax - key (score descending), written in index order; a
+// stable LSD radix sort on v (4-bit digits, over the digits umax - umin spans) then
+// keeps the index order of equal scores, the golden's tie rule. Thread t owns the
+// contiguous input range [t C, t C + C) of each pass; its per-digit counters and, after
+// the block scan in (digit, thread) order, its scatter offsets are LDS words of its own.
+constexpr int BIG_TPB = 1024;
+
+__device__ __forceinline__ uint32_t big_block_scan(uint32_t v, uint32_t* red, uint32_t* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t x = wave_incl_sum(v);
+  __syncthreads();
+  if (lane == 63) red[wave] = x;
+  __syncthreads();
+  uint32_t off = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < BIG_TPB / 64; ++w) {
+    off += (w < wave) ? red[w] : 0u;
+    tot += red[w];
+  }
+  *total = tot;
+  return off + x - v;
+}
+
+__global__ __launch_bounds__(BIG_TPB) void li_topk_big_kernel(LiTopkArgs a, uint64_t* ws) {
+  __shared__ uint32_t cnt[16 * BIG_TPB];   // [digit][thread]: counts, then scatter offsets
+  __shared__ uint32_t red[2 * (BIG_TPB / 64)];
+  const int sr = blockIdx.x;
+  const int r = sr / a.n2;
+  const int b = batch_of_row(a.row_start, a.batch, r);
+  const int s1 = r - a.row_start[b];
+  const int aq = a.act_q[b], ak = a.act_k[b];
+  const int L = s1 < aq ? visible_len(s1, aq, ak, a.s2, a.sparse_mode) : 0;
+  const int k = a.k;
+  const int nout = L < k ? L : k;
+  int32_t* iout = a.idx + (int64_t)sr * k;
+  uint16_t* vout = a.val ? a.val + (int64_t)sr * k : nullptr;
+  const uint16_t* row = a.scores + (int64_t)sr * a.ld;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  if (nout == 0) {
+    for (int i = t; i < k; i += BIG_TPB) {
+      iout[i] = -1;
+      if (vout) vout[i] = 0;
+    }
+    return;
+  }
+  uint64_t* src = ws + (int64_t)sr * 2 * a.s2;
+  uint64_t* dst = src + a.s2;
+  // the range of the row's keys: largest key, and 0xFFFF - the smallest
+  uint32_t mx = 0, mi = 0;
+  for (int i = t; i < L; i += BIG_TPB) {
+    const uint32_t u = ord16(row[i]);
+    mx = max(mx, u);
+    mi = max(mi, 0xFFFFu - u);
+  }
+  mx = wave_incl_max(mx);
+  mi = wave_incl_max(mi);
+  if (lane == 63) {
+    red[wave] = mx;
+    red[BIG_TPB / 64 + wave] = mi;
+  }
+  __syncthreads();
+  uint32_t umax = 0, uminv = 0;
+#pragma unroll
+  for (int w = 0; w < BIG_TPB / 64; ++w) {
+    umax = max(umax, red[w]);
+    uminv = max(uminv, red[BIG_TPB / 64 + w]);
+  }
+  const uint32_t urange = umax - (0xFFFFu - uminv);
+  const int npass = urange == 0 ? 0 : (35 - __builtin_clz(urange)) / 4;
+  for (int i = t; i < L; i += BIG_TPB) src[i] = ((uint64_t)(umax - ord16(row[i])) << 32) | (uint32_t)i;
+  __syncthreads();   // (also: every read of red above is done before the scans reuse it)
+  const int C = (L + BIG_TPB - 1) / BIG_TPB;
+  const int c0 = min(t * C, L), c1 = min(c0 + C, L);
+  for (int pass = 0; pass < npass; ++pass) {
+    const int shift = 32 + 4 * pass;
+#pragma unroll
+    for (int d = 0; d < 16; ++d) cnt[d * BIG_TPB + t] = 0;
+    for (int i = c0; i < c1; ++i) ++cnt[(int)((src[i] >> shift) & 15u) * BIG_TPB + t];
+    __syncthreads();
+    // exclusive scan in (digit, thread) order: thread t scans words 16t .. 16t + 15
+    uint32_t w[16], s = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      w[j] = cnt[16 * t + j];
+      s += w[j];
+    }
+    uint32_t tot;
+    uint32_t run = big_block_scan(s, red, &tot);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      cnt[16 * t + j] = run;
+      run += w[j];
+    }
+    __syncthreads();
+    for (int i = c0; i < c1; ++i) {
+      const uint64_t e = src[i];
+      const int d = (int)((e >> shift) & 15u);
+      dst[cnt[d * BIG_TPB + t]++] = e;
+    }
+    __syncthreads();   // the pass's output is complete (and visible) before the next reads it
+    uint64_t* tmp = src;
+    src = dst;
+    dst = tmp;
+  }
+  for (int i = t; i < k; i += BIG_TPB) {
+    if (i < nout) {
+      const uint64_t e = src[i];
+      iout[i] = (int32_t)(uint32_t)e;
+      if (vout) vout[i] = unord16(umax - (uint32_t)(e >> 32));
+    } else {
+      iout[i] = -1;
+      if (vout) vout[i] = 0;
+    }
+  }
+}
+
 }  // namespace
 }  // namespace dsa
 
@@ -597,6 +717,19 @@ static hipError_t launch_topk_e(const LiTopkArgs& a, int e, unsigned rows, hipSt
   else if (e <= 16) hipLaunchKernelGGL((dsa::li_topk_kernel<16, WIDE, SHORT>), grid, block, 0, s, a);
   else if (e <= 32) hipLaunchKernelGGL((dsa::li_topk_kernel<32, WIDE, SHORT>), grid, block, 0, s, a);
   else hipLaunchKernelGGL((dsa::li_topk_kernel<64, WIDE, SHORT>), grid, block, 0, s, a);
+  return hipGetLastError();
+}
+
+size_t li_topk_workspace_bytes(int total_rows, int n2, int s2, int k) {
+  if (k <= LI_TOPK_MAX_K || total_rows <= 0 || n2 <= 0 || s2 <= 0) return 0;
+  return (size_t)total_rows * n2 * 2 * s2 * sizeof(uint64_t);
+}
+
+hipError_t launch_li_topk_big(const LiTopkArgs& a, void* ws, hipStream_t s) {
+  const int64_t rows = (int64_t)a.total_rows * a.n2;
+  if (rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL(dsa::li_topk_big_kernel, dim3((unsigned)rows), dim3(dsa::BIG_TPB), 0, s, a,
+                     reinterpret_cast<uint64_t*>(ws));
   return hipGetLastError();
 }
 

@@ -106,6 +106,8 @@ class IndexerPlan:
                      if return_value else torch.zeros(out_lead + (N2, self.k), dtype=query.dtype, device=dev))
         self.ld = _score_ld(S2)
         self.scores = torch.empty((max(total_rows, 1) * N2, self.ld), dtype=torch.int16, device=dev)
+        tw = int(self.lib.dsa_li_topk_workspace_bytes(total_rows, N2, S2, self.k))
+        self.topk_ws = torch.empty(tw, dtype=torch.uint8, device=dev) if tw > 0 else None
         self.d_row_start = H.i32(row_start, dev)
         self.d_key_start = H.i32(key_start, dev)
         self.d_aq = H.i32(act_q, dev)
@@ -133,6 +135,14 @@ class IndexerPlan:
 
     def topk(self):
         if self.total_rows == 0:
+            return
+        if self.topk_ws is not None:   # sparse_count above the LDS sort's cap
+            _lib.check(self.lib.dsa_li_topk_ws(
+                self.scores.data_ptr(), self.ld, self.io, self.d_row_start.data_ptr(),
+                self.d_aq.data_ptr(), self.d_ak.data_ptr(), self.B, self.total_rows, self.N2, self.S2,
+                self.sparse_mode, self.k, self.idx.data_ptr(),
+                self.vals.data_ptr() if self.return_value else None, self.topk_ws.data_ptr(),
+                self.topk_ws.numel(), H.stream_ptr(self.dev)), "dsa_li_topk_ws")
             return
         _lib.check(self.lib.dsa_li_topk(
             self.scores.data_ptr(), self.ld, self.io, self.d_row_start.data_ptr(),

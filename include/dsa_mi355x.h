@@ -106,12 +106,32 @@ int dsa_li_score_paged(const void* query, const void* key_cache, const void* wei
  * min(L, sparse_count) are written to indices[(r*N2+n2)*sparse_count + i]
  * (int32) and, if `values` is not NULL, their 16-bit score to values[...];
  * the remaining slots get index -1 and value 0. Rows with s1 >= act_q are all -1 / 0.
- * Any S2 (int32 indices); sparse_count <= 16384.
+ * Any S2 (int32 indices); sparse_count <= 16384 (DSA_ERR_UNSUPPORTED above: use
+ * dsa_li_topk_ws).
  */
 int dsa_li_topk(const uint16_t* scores, int64_t score_ld, int io_dtype,
                 const int32_t* row_start, const int32_t* act_q, const int32_t* act_k,
                 int batch, int total_rows, int n2, int s2, int sparse_mode, int sparse_count,
                 int32_t* indices, uint16_t* values, void* stream);
+
+/*
+ * Bytes of device workspace dsa_li_topk_ws needs: 0 for sparse_count <= 16384, else two
+ * buffers of S2 8-byte entries per score row (total_rows * N2 * 16 * S2).
+ */
+size_t dsa_li_topk_workspace_bytes(int total_rows, int n2, int s2, int sparse_count);
+
+/*
+ * dsa_li_topk for any sparse_count (the reference's _stable_topk,
+ * lightning_indexer_triton.py:343-361, has no cap): sparse_count <= 16384 runs
+ * dsa_li_topk's kernel and ignores the workspace; above, every visible entry of a row
+ * is sorted (stable, score descending) in `workspace`, which must hold
+ * dsa_li_topk_workspace_bytes (DSA_ERR_INVALID otherwise). Same outputs and ordering.
+ */
+int dsa_li_topk_ws(const uint16_t* scores, int64_t score_ld, int io_dtype,
+                   const int32_t* row_start, const int32_t* act_q, const int32_t* act_k,
+                   int batch, int total_rows, int n2, int s2, int sparse_mode, int sparse_count,
+                   int32_t* indices, uint16_t* values, void* workspace, size_t workspace_bytes,
+                   void* stream);
 
 /*
  * Bytes of device workspace dsa_sfa_fwd needs for this problem (token lists and,

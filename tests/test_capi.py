@@ -45,6 +45,14 @@ def test_invalid_arguments_return_status_without_gpu():
     assert st == _lib.DSA_ERR_UNSUPPORTED
     st = lib.dsa_li_topk(p, 70000, 1, p, p, p, 1, 1, 1, 70000, 3, 16385, p, None, None)
     assert st == _lib.DSA_ERR_UNSUPPORTED and b"16384" in lib.dsa_last_error()
+    # above the LDS sort's cap: the workspace entry point sizes and checks its scratch
+    assert lib.dsa_li_topk_workspace_bytes(4, 2, 70000, 16384) == 0
+    assert lib.dsa_li_topk_workspace_bytes(4, 2, 70000, 16385) == 4 * 2 * 2 * 70000 * 8
+    st = lib.dsa_li_topk_ws(p, 70000, 1, p, p, p, 1, 4, 2, 70000, 3, 16385, p, None, None, 0, None)
+    assert st == _lib.DSA_ERR_INVALID and b"workspace" in lib.dsa_last_error()
+    st = lib.dsa_li_topk_ws(p, 70000, 1, p, p, p, 1, 4, 2, 70000, 3, 16385, p, None, p,
+                            4 * 2 * 2 * 70000 * 8 - 1, None)
+    assert st == _lib.DSA_ERR_INVALID and b"workspace" in lib.dsa_last_error()
     base = [p, p, p, p, 1, p, 64, 1, None, 0, 0, p, p, p, p, 1, 1, 128, 512, 64, 16, 16, 3, 0.1,
             p, None, None, p, 1 << 30, 0, None]
     # `base` itself is valid and is never called: each case below breaks one field

@@ -214,6 +214,16 @@ def test_long_context_rows(dev, S2, K):
     run_case(dev, B, S1, S2, N1, N2, D, K, 3, "bf16", act_q=[S1], act_k=[S2], max_rows=4, w_scale=1 / 8)
 
 
+@pytest.mark.parametrize("S2,K,mode", [(20000, 18000, 3), (70000, 40000, 0), (17000, 17000, 3)])
+def test_sparse_count_above_the_lds_sort(dev, S2, K, mode):
+    """sparse_count > 16,384 (the reference's mint.topk path has no cap): every visible entry of
+    a row is sorted in global scratch (dsa_li_topk_ws), 32-bit indices past 65,535 included,
+    and rows shorter than k (the 17,000-key case) pad with -1. Oracle on sampled rows, the
+    top-k invariants on all."""
+    B, S1, N1, N2, D = 1, 8, 8, 1, 64
+    run_case(dev, B, S1, S2, N1, N2, D, K, mode, "bf16", act_q=[S1], act_k=[S2], max_rows=4, w_scale=1 / 8)
+
+
 def test_pa_bsnd_128k_context(dev):
     """Decode-time indexing over a 128K paged context with 32-token pages (4,097 block-table
     entries per batch), one query row per batch."""
@@ -354,16 +364,17 @@ def _crafted_bits(family, rows, S2, rng):
     raise ValueError(family)
 
 
-@pytest.mark.parametrize("S1,S2", [(8192, 8192), (64, 12000), (8, 70000)])
+@pytest.mark.parametrize("S1,S2,K", [(8192, 8192, 2048), (64, 12000, 2048), (8, 70000, 2048),
+                                     (16, 20000, 18000), (8, 70000, 40000)])
 @pytest.mark.parametrize("family", ["equal", "signed_zeros", "extremes", "two_values", "wide", "narrow"])
-def test_topk_crafted_score_rows(dev, S1, S2, family):
+def test_topk_crafted_score_rows(dev, S1, S2, K, family):
     """The top-k kernel alone on crafted score rows, against the golden's stable sort
     (oracle select_topk): ties, +0/-0, infinities and subnormals, rows of one value
     (no digit pass), both signs over many binades (every pass), and rows of every
     visible length around k, in the register-cached (S2 <= 8192), chunked and 32-bit
-    index paths. -inf is left out: the golden drops -inf entries (its mask value)."""
+    index paths, and with k above the LDS sort's cap (sorted in global scratch). -inf is
+    left out: the golden drops -inf entries (its mask value)."""
     from dsa_triton_ascend_amd.lightning_indexer import IndexerPlan
-    K = 2048
     rng = np.random.default_rng(11)
     q = torch.zeros(1, S1, 8, 128, dtype=torch.bfloat16, device=dev)
     k = torch.zeros(1, S2, 1, 128, dtype=torch.bfloat16, device=dev)
