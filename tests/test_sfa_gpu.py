@@ -106,6 +106,25 @@ def test_golden_matrix(dev, B, S1, S2, N1, count, bs, mode, D, dtype):
     compare(out, smax, ssum, *o, what=f"B{B} S1={S1} S2={S2} N1={N1} k={count} bs={bs} m{mode} D{D} {dtype}")
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("D", [128, 256])
+@pytest.mark.parametrize("S1,S2,count", [(6, 300, 200), (1, 2100, 2048)])
+def test_per_wave_pv_form_smaller_d(dev, S1, S2, count, D, dtype):
+    """128 heads at D = 128 / 256: the per-wave PV form with its Q^T staged through the gather
+    ring at those row widths (two or four heads per copy instruction), on unsplit rows with a
+    partial last tile and on a single decode-like row that is split over KV."""
+    B, N1 = 1, 128
+    q, k, v, qr, kr = _inputs(B, S1, S2, N1, D, dtype, seed=21)
+    si = _ref_indices(B, S1, S2, count, 1, 3, seed=22)
+    scale = 1.0 / math.sqrt(D + 64)
+    out, smax, ssum = sparse_flash_attention(q.to(dev), k.to(dev), v.to(dev), torch.from_numpy(si).to(dev),
+                                             scale_value=scale, query_rope=qr.to(dev), key_rope=kr.to(dev),
+                                             sparse_mode=3, return_softmax_lse=True)
+    o = SFA.sparse_flash_attention(_np(q), _np(k), None, si, scale, query_rope=_np(qr), key_rope=_np(kr),
+                                   sparse_mode=3, return_softmax_lse=True, io_dtype=dtype)
+    compare(out, smax, ssum, *o, what=f"N1=128 D={D} S1={S1} S2={S2} k={count} {dtype}")
+
+
 @pytest.mark.parametrize("N1", [1, 2, 32, 64, 128])
 def test_head_counts(dev, N1):
     B, S1, S2, D, count = 1, 6, 96, 512, 48
