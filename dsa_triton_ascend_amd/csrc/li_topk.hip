@@ -25,15 +25,14 @@
 //      Rows with L <= k take every entry at its own index.
 //   4. A stable LSD radix sort ascending on v = umax - u (score descending; umax
 //      and umin bound the selected keys), 4-bit digits, over only the digits that
-//      umax - umin spans. Each thread counts the digits of its keys in registers
-//      (packed counters: no LDS read-modify-write chain), one block scan turns the
-//      per-thread counts into scatter offsets. Stability preserves the index order
-//      of equal scores, which is exactly the golden's tie rule.
+//      umax - umin spans. Each thread counts the digits of its keys with LDS atomics
+//      on its own 16-bit counters (the returned value is the key's rank among the
+//      thread's earlier keys of that digit), one block scan turns the per-thread
+//      counts into scatter offsets. Stability preserves the index order of equal
+//      scores, which is exactly the golden's tie rule.
 //   5. One pass writes the indices and 16-bit values in rank order.
 // The selection histogram and the sort's counters share one LDS array (they are
 // never live together), so a work-group needs ~16 KB and more of them fit a CU.
-#include <type_traits>
-
 #include "dsa_common.hpp"
 
 namespace dsa {
@@ -136,33 +135,12 @@ __device__ __forceinline__ void load_keys(const uint16_t* row, int L, int base, 
   }
 }
 
-// Digit counters of one thread's E keys, packed in two words (digits 0-7, 8-15): 4-bit
-// fields (E < 16, 32-bit shifts only) or 8-bit fields in two 64-bit words (E < 256).
-template <int E>
-struct DigitCount {
-  static constexpr bool NIB = E < 16;
-  using W = typename std::conditional<NIB, uint32_t, uint64_t>::type;
-  static constexpr uint32_t FB = NIB ? 4 : 8;   // field bits
-  W c0 = 0, c1 = 0;
-  // rank of this key among the thread's earlier keys with digit d, then count it
-  __device__ __forceinline__ uint32_t take(uint32_t d) {
-    const uint32_t sh = (d & 7) * FB;
-    const bool hi = d >= 8;
-    const W w = hi ? c1 : c0;
-    const uint32_t r = (uint32_t)(w >> sh) & ((1u << FB) - 1);
-    const W inc = (W)1 << sh;
-    c0 += hi ? (W)0 : inc;
-    c1 += hi ? inc : (W)0;
-    return r;
-  }
-  __device__ __forceinline__ uint32_t count(int d) const {
-    return (uint32_t)((d < 8 ? c0 : c1) >> ((d & 7) * FB)) & ((1u << FB) - 1);
-  }
-};
-
 // Stable LSD radix sort of E keys per thread (blocked: thread t holds ranks
 // [E t, E t + E)), ascending on the upper 16 bits, over passes [0, npass) (4 bits each,
-// from the low bits up). `cnt` holds 16 x TPB 16-bit counters in [digit][thread] order.
+// from the low bits up). `cnt` holds 16 x TPB 16-bit counters in [digit][thread] order;
+// a thread counts its keys with LDS atomics on its own counter (a 32-bit add of 1 or
+// 1 << 16 on the word it shares with the neighbouring thread), whose returned value is
+// the key's rank among the thread's earlier keys of that digit.
 // Entries at ranks >= n are padding whose digits are all 15 (and whose values are
 // never read back): they stay behind every real key in each pass, so they affect no
 // real key's position, and a wave holding padding only neither counts nor moves it
@@ -172,16 +150,23 @@ __device__ __forceinline__ void radix_sort_asc16(uint32_t (&key)[E], int npass, 
                                                  uint16_t* cnt, uint32_t* red) {
   const int t = threadIdx.x;
   const bool act = (int)__builtin_amdgcn_readfirstlane(t >> 6) * 64 * E < n;
+  const uint32_t inc = (t & 1) ? 0x10000u : 1u, hsh = (t & 1) ? 16u : 0u;
+  uint32_t* cw = reinterpret_cast<uint32_t*>(cnt) + (t >> 1);   // digit 0's word of this thread pair
 #pragma unroll 1
   for (int pass = 0; pass < npass; ++pass) {
     const int shift = 16 + 4 * pass;
-    DigitCount<E> dc;
+    // the pair's counter words, digits 8 (t & 1) .. +8 by this thread: both threads of a
+    // pair sit in one wave, whose LDS operations run in order, and no other wave touches
+    // these words before the barrier below (the last pass's scatter read only its own)
+#pragma unroll
+    for (int d = 0; d < 8; ++d) cw[(8 * (t & 1) + d) * (TPB / 2)] = 0u;
     uint32_t lrank[E];
     if (act)
 #pragma unroll
-      for (int e = 0; e < E; ++e) lrank[e] = dc.take(__builtin_amdgcn_ubfe(key[e], shift, 4));
-#pragma unroll
-    for (int d = 0; d < 16; ++d) cnt[d * TPB + t] = (uint16_t)dc.count(d);
+      for (int e = 0; e < E; ++e) {
+        const uint32_t d = __builtin_amdgcn_ubfe(key[e], shift, 4);
+        lrank[e] = (atomicAdd(cw + d * (TPB / 2), inc) >> hsh) & 0xFFFFu;
+      }
     __syncthreads();
     // exclusive scan over cnt in [digit][thread] order: thread t scans entries 16t..16t+15
     const uint4 q0 = *reinterpret_cast<const uint4*>(cnt + t * 16);
