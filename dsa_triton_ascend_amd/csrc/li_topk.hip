@@ -535,7 +535,33 @@ void li_topk_kernel(LiTopkArgs a) {
     key[e] = (min(umax - (x >> 16), vmax) << 16) | (x & 0xFFFFu);
   }
   radix_sort_asc16<E>(key, npass, nout, sbuf, cnt, red);
-  // ranks E t .. E t + E - 1 of thread t: their index (or -1) and 16-bit value (or 0)
+  // ranks E t .. E t + E - 1 of thread t: their index (or -1) and 16-bit value (or 0).
+  // A run of 8 ranks inside the row's output, all below nout (the usual case): indices
+  // 0xFFFF - x, values unord16(umax - v) computed on packed pairs.
+  if (!WIDE && E % 8 == 0 && k % 8 == 0 && E * t + E <= nout) {
+    const uint32_t um2 = umax * 0x10001u;
+#pragma unroll
+    for (int e = 0; e < E; e += 8) {
+      uint32_t pv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // upper halves (v) of keys e + 2j and e + 2j + 1, then umax - v per half: the keys
+        const uint32_t vv = __builtin_amdgcn_perm(key[e + 2 * j + 1], key[e + 2 * j], 0x07060302u);
+        const uint32_t kk = pk_sub(um2, vv);
+        // unord16 per half: a set top bit is cleared, otherwise the half is inverted
+        const uint32_t sg = __builtin_bit_cast(uint32_t, __builtin_bit_cast(i16x2, kk) >> (i16x2){15, 15});
+        pv[j] = kk ^ ~(sg & 0x7FFF7FFFu);
+      }
+      *reinterpret_cast<int4*>(iout + E * t + e) =
+          make_int4((int)(~key[e] & 0xFFFFu), (int)(~key[e + 1] & 0xFFFFu), (int)(~key[e + 2] & 0xFFFFu),
+                    (int)(~key[e + 3] & 0xFFFFu));
+      *reinterpret_cast<int4*>(iout + E * t + e + 4) =
+          make_int4((int)(~key[e + 4] & 0xFFFFu), (int)(~key[e + 5] & 0xFFFFu), (int)(~key[e + 6] & 0xFFFFu),
+                    (int)(~key[e + 7] & 0xFFFFu));
+      if (vout) *reinterpret_cast<uint4*>(vout + E * t + e) = make_uint4(pv[0], pv[1], pv[2], pv[3]);
+    }
+    return;
+  }
   int32_t oi[E];
   uint16_t ov[E];
 #pragma unroll
