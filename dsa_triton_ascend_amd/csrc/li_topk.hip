@@ -56,10 +56,13 @@ __device__ __forceinline__ int visible_len(int s1, int aq, int ak, int S2, int m
 }
 
 // Block-wide exclusive scan (wave scans with DPP, one LDS exchange); also returns the total.
+// One barrier: every caller has a block barrier between the previous reads of `red` (the
+// last scan's) and this call (the compaction and candidate scans follow the barriers of
+// the bin pick and of the candidate resolution, each sort pass's scan the pass's count
+// barrier), so the words are free to overwrite.
 __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* red, uint32_t* total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t x = wave_incl_sum(v);
-  __syncthreads();
   if (lane == 63) red[wave] = x;
   __syncthreads();
   uint32_t off = 0, tot = 0;
