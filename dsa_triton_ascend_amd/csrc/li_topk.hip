@@ -237,8 +237,9 @@ __device__ __forceinline__ uint32_t block_scan_max2(uint32_t v, uint32_t m1, uin
 // SHORT: rows of at most ROW_CACHED entries (s2 <= 8192), held in registers in one chunk;
 // the chunked paths for longer rows are compiled out. Short rows with k <= 2048 are
 // compiled for eight waves per SIMD (64 VGPRs, 96 SGPRs: more SGPR spills to VGPR lanes,
-// which cost less than the latency an eighth work-group per CU hides; 0.128 -> 0.121 ms
-// at C2). The kernel is bound by the latency of its barrier/LDS chain, not throughput.
+// which cost less than the latency an eighth work-group per CU hides). At eight waves per
+// SIMD the VALU issues for about two thirds of the kernel's time; LDS bank conflicts and
+// the chain of block barriers take most of the rest.
 template <int E, bool WIDE, bool SHORT = false>
 __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(SHORT && E <= 8 ? 8 : 1, 8)))
 void li_topk_kernel(LiTopkArgs a) {
