@@ -175,9 +175,10 @@ __device__ __forceinline__ void radix_sort_asc16(uint32_t (&key)[E], int npass, 
     const uint4 q0 = *reinterpret_cast<const uint4*>(cnt + t * 16);
     const uint4 q1 = *reinterpret_cast<const uint4*>(cnt + t * 16 + 8);
     const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-    uint32_t s = 0;
+    uint32_t s = 0;   // both halves at once: a half sums at most 8 counts of at most E keys
 #pragma unroll
-    for (int j = 0; j < 8; ++j) s += (w[j] & 0xFFFFu) + (w[j] >> 16);
+    for (int j = 0; j < 8; ++j) s += w[j];
+    s = (s & 0xFFFFu) + (s >> 16);
     uint32_t tot;
     uint32_t run = block_excl_scan(s, red, &tot);   // offset of this thread's first entry
     uint32_t o[8];   // running offsets, re-derived from the counts (no second array live across the scan)
