@@ -57,14 +57,16 @@ template <int IO> __device__ __forceinline__ uint16_t from_f32(float f) {
   return IO == IO_BF16 ? f32_to_bf16_rne(f) : f32_to_f16_rne(f);
 }
 
-// Monotone map of a 16-bit float pattern to an unsigned key: larger float ->
-// larger key; +0 and -0 map to the same key (the goldens compare them equal).
+// Monotone map of a 16-bit float pattern (sign, magnitude m) to an unsigned key:
+// 0x8000 + m for a positive value, 0x8000 - m for a negative one. Larger float ->
+// larger key; +0 and -0 map to the same key 0x8000 (the goldens compare them equal),
+// and no pattern maps to 0, which marks entries outside a row.
 __device__ __forceinline__ uint32_t ord16(uint16_t h) {
-  if (h == 0x8000u) h = 0;
-  return (h & 0x8000u) ? (uint32_t)(uint16_t)(~h) : (uint32_t)(h | 0x8000u);
+  return (h & 0x8000u) ? (uint32_t)(uint16_t)(0x10000u - h) : (uint32_t)(h | 0x8000u);
 }
+// inverse of ord16 on keys 1..0xFFFF (0x8000 gives +0)
 __device__ __forceinline__ uint16_t unord16(uint32_t k) {
-  return (k & 0x8000u) ? (uint16_t)(k & 0x7FFFu) : (uint16_t)(~k);
+  return (k & 0x8000u) ? (uint16_t)(k & 0x7FFFu) : (uint16_t)(0x10000u - k);
 }
 
 // ------------------------------------------------------------------ MFMA

@@ -77,16 +77,15 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* red, u
 
 typedef short i16x2 __attribute__((ext_vector_type(2)));
 
-// ord16 of both 16-bit halves of w (see ord16), five VALU ops for the pair: a half whose
-// magnitude is zero loses its sign bit (-0 becomes +0: magnitude + 0x7FFF sets the half's
-// top bit exactly when the magnitude is nonzero, and the halves cannot carry into each
-// other), then h ^ (sign-extended sign | 0x8000) inverts negative halves and sets the top
-// bit of positive ones.
+// ord16 of both 16-bit halves of w (see ord16), four VALU ops for the pair: a half h
+// becomes h ^ (sign-extended sign | 0x8000) plus its sign bit, i.e. h | 0x8000 when
+// positive and ~h + 1 = 0x10000 - h when negative (-0 lands on +0's 0x8000). No half
+// carries into the next: a negative half gives at most 0x7FFF + 1.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t ord16x2(uint32_t w) {
-  const uint32_t nzt = (w & 0x7FFF7FFFu) + 0x7FFF7FFFu;
-  const uint32_t h = w & (nzt | 0x7FFF7FFFu);
-  const uint32_t s = __builtin_bit_cast(uint32_t, __builtin_bit_cast(i16x2, h) >> (i16x2){15, 15});
-  return h ^ (s | 0x80008000u);
+  const uint32_t s = __builtin_bit_cast(uint32_t, __builtin_bit_cast(i16x2, w) >> (i16x2){15, 15});
+  const uint32_t sb = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, w) >> (u16x2){15, 15});
+  return (w ^ (s | 0x80008000u)) + sb;
 }
 
 // Per 16-bit half of the packed keys w: 1 if the key is above c (c in both halves of
@@ -99,7 +98,6 @@ __device__ __forceinline__ uint32_t pk_above(uint32_t w, uint32_t cc) {
 // sum of the two 16-bit halves of packed counters (each at most 0x7FFF)
 __device__ __forceinline__ uint32_t pk_hsum(uint32_t c) { return (c & 0xFFFFu) + (c >> 16); }
 // packed 16-bit unsigned max, min and wrapping subtraction (v_pk_max_u16, v_pk_min_u16, v_pk_sub_u16)
-typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pk_max(uint32_t a, uint32_t b) {
   return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, a), __builtin_bit_cast(u16x2, b)));
 }
@@ -108,6 +106,14 @@ __device__ __forceinline__ uint32_t pk_min(uint32_t a, uint32_t b) {
 }
 __device__ __forceinline__ uint32_t pk_sub(uint32_t a, uint32_t b) {
   return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) - __builtin_bit_cast(u16x2, b));
+}
+// Stores v at *p and advances p by one word in place, for the active lanes of a divergent
+// branch. Written in C++ (`*p++ = v`) the compiler computes the new pointer into another
+// register before the store and copies it back: two VALU ops per store instead of one.
+typedef __attribute__((address_space(3))) uint32_t lds_u32;
+__device__ __forceinline__ void lds_push(lds_u32*& p, uint32_t v) {
+  *p = v;
+  asm volatile("v_add_u32 %0, 4, %0" : "+v"(p));
 }
 // key e of a thread's packed pairs (w[e / 2], low half = even e)
 __device__ __forceinline__ uint32_t kh(const uint32_t* w, int e) { return (e & 1) ? w[e >> 1] >> 16 : w[e >> 1] & 0xFFFFu; }
@@ -298,12 +304,15 @@ void li_topk_kernel(LiTopkArgs a) {
 #pragma unroll 1
     for (int ch = 0; ch < nchunks; ++ch) {
       if (nchunks > 1) load_keys(row, L, ch * ROW_CACHED, w);
-      if (wv)
+      // every key of a thread holding part of the row is counted, with no per-key test:
+      // the padding past L of the one thread straddling L lands in bin 0 and is taken
+      // out below (threads wholly past L count nothing, so bin 0 sees no pile-up)
+      if (ch * ROW_CACHED + t * RPT < L)
 #pragma unroll
         for (int i = 0; i < RPT / 2; ++i) {   // the bins of both keys of a pair, straight from the word
           const uint32_t x = w[i];
-          if (x & 0xFFFFu) atomicAdd(&hist[(x >> 5) & 0x7FFu], 1u);
-          if (x >> 16) atomicAdd(&hist[x >> 21], 1u);
+          atomicAdd(&hist[(x >> 5) & 0x7FFu], 1u);
+          atomicAdd(&hist[x >> 21], 1u);
         }
     }
     __syncthreads();
@@ -314,6 +323,7 @@ void li_topk_kernel(LiTopkArgs a) {
       h[0] = hi4.w; h[1] = hi4.z; h[2] = hi4.y; h[3] = hi4.x;
       h[4] = lo4.w; h[5] = lo4.z; h[6] = lo4.y; h[7] = lo4.x;
     }
+    if (t == TPB - 1) h[7] -= (uint32_t)(-L & (RPT - 1));   // bin 0: the padding counted above
     uint32_t hs = 0, top1 = 0;   // top1: highest non-empty bin + 1 (0: none)
 #pragma unroll
     for (int j = 7; j >= 0; --j) {
@@ -356,8 +366,8 @@ void li_topk_kernel(LiTopkArgs a) {
     };
     if (!WIDE && nchunks == 1 && nc <= (uint32_t)HWORDS) {
       // one pass over the row: keys of higher bins go to sbuf[0, above) in index order,
-      // the keys of bin `bin` to a candidate list (key << 16 | index, index order) in
-      // the histogram's place; T is then found among the candidates only, and the
+      // the keys of bin `bin` to a candidate list (the same key << 16 | 0xFFFF - index,
+      // index order) in the histogram's place; T is then found among the candidates only, and the
       // selected ones follow in sbuf, in index order. The two groups hold different
       // keys, so their relative order is irrelevant to the stable sort.
       uint32_t* cand = work;
@@ -375,16 +385,22 @@ void li_topk_kernel(LiTopkArgs a) {
       const uint32_t cg = pk_hsum(ag), cc = pk_hsum(ab) - cg;
       uint32_t tot1;
       const uint32_t pgc = block_excl_scan((cg << 16) | cc, red, &tot1);
-      uint32_t* ps = sbuf + (pgc >> 16);
-      uint32_t* pcd = cand + (pgc & 0xFFFFu);
+      lds_u32* ps = (lds_u32*)(sbuf + (pgc >> 16));
+      lds_u32* pcd = (lds_u32*)(cand + (pgc & 0xFFFFu));
       const uint32_t xb = 0xFFFFu - (uint32_t)i0;
       if (wv)
 #pragma unroll
         for (int e = 0; e < RPT; ++e) {
-          // the key compared as it lies in its half; ku = key << 16
-          const uint32_t ue = kh(w, e), ku = (e & 1) ? (w[e >> 1] & 0xFFFF0000u) : (w[e >> 1] << 16);
-          if (ue > g1) *ps++ = ku | (xb - e);                      // a higher bin
-          else if (ue > b1) *pcd++ = ku | (uint32_t)(i0 + e);      // bin `bin`, nonzero
+          // key << 16 | (0xFFFF - index), built from the key's half in two ops (the empty
+          // asm keeps the compiler from splitting xb - e around the shift); the compares
+          // read the key in its half
+          uint32_t x = xb - e;
+          asm("" : "+v"(x));
+          const uint32_t v = (e & 1) ? ((w[e >> 1] & 0xFFFF0000u) | x) : ((w[e >> 1] << 16) | x);
+          const uint32_t ue = kh(w, e);
+          const bool hi = ue > g1;
+          if (hi) lds_push(ps, v);               // a higher bin
+          if (ue > b1 && !hi) lds_push(pcd, v);  // bin `bin`, nonzero
         }
       // candidates [c0, c1) of this thread (at most 8: nc <= 2048; the loops stop at the
       // block-uniform m, typically 1 or 2)
@@ -412,7 +428,7 @@ void li_topk_kernel(LiTopkArgs a) {
       for (int j = 0; j < 8; ++j) {
         if (j >= (int)m) break;
         if (c0 + j >= c1) continue;
-        const uint32_t key16 = cv[j] >> 16, x = 0xFFFFu - (cv[j] & 0xFFFFu);
+        const uint32_t key16 = cv[j] >> 16, x = cv[j] & 0xFFFFu;
         if (key16 > T) {
           sbuf[qg + (qe < need ? qe : need)] = (key16 << 16) | x;
           ++qg;
@@ -544,18 +560,19 @@ void li_topk_kernel(LiTopkArgs a) {
   // A run of 8 ranks inside the row's output, all below nout (the usual case): indices
   // 0xFFFF - x, values unord16(umax - v) computed on packed pairs.
   if (!WIDE && E % 8 == 0 && k % 8 == 0 && E * t + E <= nout) {
-    const uint32_t um2 = umax * 0x10001u;
+    const uint32_t um2x = (umax ^ 0x8000u) * 0x10001u;   // umax - 0x8000 in both halves
 #pragma unroll
     for (int e = 0; e < E; e += 8) {
       uint32_t pv[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        // upper halves (v) of keys e + 2j and e + 2j + 1, then umax - v per half: the keys
+        // upper halves (v) of keys e + 2j and e + 2j + 1; the key is umax - v per half
         const uint32_t vv = __builtin_amdgcn_perm(key[e + 2 * j + 1], key[e + 2 * j], 0x07060302u);
-        const uint32_t kk = pk_sub(um2, vv);
-        // unord16 per half: a set top bit is cleared, otherwise the half is inverted
-        const uint32_t sg = __builtin_bit_cast(uint32_t, __builtin_bit_cast(i16x2, kk) >> (i16x2){15, 15});
-        pv[j] = kk ^ ~(sg & 0x7FFF7FFFu);
+        // unord16 per half from d = key - 0x8000 (signed: the value's magnitude, negated
+        // for a negative value): |d| with d's sign bit
+        const i16x2 d = __builtin_bit_cast(i16x2, pk_sub(um2x, vv));
+        const uint32_t ad = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(d, (i16x2){0, 0} - d));
+        pv[j] = ad | (__builtin_bit_cast(uint32_t, d) & 0x80008000u);
       }
       *reinterpret_cast<int4*>(iout + E * t + e) =
           make_int4((int)(~key[e] & 0xFFFFu), (int)(~key[e + 1] & 0xFFFFu), (int)(~key[e + 2] & 0xFFFFu),
