@@ -144,12 +144,18 @@ __device__ __forceinline__ void load_keys(const uint16_t* row, int L, int base, 
   }
 }
 
+// Rank block of thread t in the sort: lanes l and l + 32 of a wave hold the neighbouring
+// blocks 2m, 2m + 1 (m = 32 w + l), so the thread pair sharing a 32-bit counter word sits
+// in different half-waves, and the 32 lanes of a half-wave reach 32 different banks.
+__device__ __forceinline__ int rank_block(int t) { return (t & ~63) | ((t & 31) << 1) | ((t >> 5) & 1); }
+
 // Stable LSD radix sort of E keys per thread (blocked: thread t holds ranks
-// [E t, E t + E)), ascending on the upper 16 bits, over passes [0, npass) (4 bits each,
-// from the low bits up). `cnt` holds 16 x TPB 16-bit counters in [digit][thread] order;
-// a thread counts its keys with LDS atomics on its own counter (a 32-bit add of 1 or
-// 1 << 16 on the word it shares with the neighbouring thread), whose returned value is
-// the key's rank among the thread's earlier keys of that digit.
+// [E b, E b + E), b = rank_block(t)), ascending on the upper 16 bits, over passes
+// [0, npass) (4 bits each, from the low bits up). `cnt` holds 16 x TPB 16-bit counters in
+// [digit][block] order; a thread counts its keys with LDS atomics on its own counter (a
+// 32-bit add of 1 or 1 << 16 on the word it shares with the thread of the neighbouring
+// block), whose returned value is the key's rank among the thread's earlier keys of that
+// digit.
 // Entries at ranks >= n are padding whose digits are all 15 (and whose values are
 // never read back): they stay behind every real key in each pass, so they affect no
 // real key's position, and a wave holding padding only neither counts nor moves it
@@ -157,18 +163,18 @@ __device__ __forceinline__ void load_keys(const uint16_t* row, int L, int base, 
 template <int E>
 __device__ __forceinline__ void radix_sort_asc16(uint32_t (&key)[E], int npass, int n, uint32_t* sbuf,
                                                  uint16_t* cnt, uint32_t* red) {
-  const int t = threadIdx.x;
+  const int t = threadIdx.x, tb = rank_block(t);
   const bool act = (int)__builtin_amdgcn_readfirstlane(t >> 6) * 64 * E < n;
-  const uint32_t inc = (t & 1) ? 0x10000u : 1u, hsh = (t & 1) ? 16u : 0u;
-  uint32_t* cw = reinterpret_cast<uint32_t*>(cnt) + (t >> 1);   // digit 0's word of this thread pair
+  const uint32_t inc = (tb & 1) ? 0x10000u : 1u, hsh = (tb & 1) ? 16u : 0u;
+  uint32_t* cw = reinterpret_cast<uint32_t*>(cnt) + (tb >> 1);   // digit 0's word of this thread pair
 #pragma unroll 1
   for (int pass = 0; pass < npass; ++pass) {
     const int shift = 16 + 4 * pass;
-    // the pair's counter words, digits 8 (t & 1) .. +8 by this thread: both threads of a
+    // the pair's counter words, digits 8 (tb & 1) .. +8 by this thread: both threads of a
     // pair sit in one wave, whose LDS operations run in order, and no other wave touches
     // these words before the barrier below (the last pass's scatter read only its own)
 #pragma unroll
-    for (int d = 0; d < 8; ++d) cw[(8 * (t & 1) + d) * (TPB / 2)] = 0u;
+    for (int d = 0; d < 8; ++d) cw[(8 * (tb & 1) + d) * (TPB / 2)] = 0u;
     uint32_t lrank[E];
     if (act)
 #pragma unroll
@@ -177,7 +183,7 @@ __device__ __forceinline__ void radix_sort_asc16(uint32_t (&key)[E], int npass, 
         lrank[e] = (atomicAdd(cw + d * (TPB / 2), inc) >> hsh) & 0xFFFFu;
       }
     __syncthreads();
-    // exclusive scan over cnt in [digit][thread] order: thread t scans entries 16t..16t+15
+    // exclusive scan over cnt in [digit][block] order: thread t scans entries 16t..16t+15
     const uint4 q0 = *reinterpret_cast<const uint4*>(cnt + t * 16);
     const uint4 q1 = *reinterpret_cast<const uint4*>(cnt + t * 16 + 8);
     const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
@@ -202,25 +208,31 @@ __device__ __forceinline__ void radix_sort_asc16(uint32_t (&key)[E], int npass, 
 #pragma unroll
       for (int e = 0; e < E; ++e) {
         const int d = __builtin_amdgcn_ubfe(key[e], shift, 4);
-        sbuf[cnt[d * TPB + t] + lrank[e]] = key[e];
+        // byte offset (offset + rank) * 4 in one op (the compiler shifts both terms)
+        uint32_t bo;
+        asm("v_add_lshl_u32 %0, %1, %2, 2" : "=v"(bo) : "v"((uint32_t)cnt[d * TPB + tb]), "v"(lrank[e]));
+        *reinterpret_cast<lds_u32*>((__attribute__((address_space(3))) uint8_t*)sbuf + bo) = key[e];
       }
     __syncthreads();
     if (act)
 #pragma unroll
-      for (int e = 0; e < E; ++e) key[e] = sbuf[E * t + e];
+      for (int e = 0; e < E; ++e) key[e] = sbuf[E * tb + e];
     // the next pass writes cnt (read above, before the barrier) and sbuf (after two barriers)
   }
 }
 
 // Block-wide exclusive scan of v together with the maxima of m1 and m2 (every thread
-// gets the scan total and both maxima): one LDS exchange for the three.
+// gets the scan total and both maxima): one LDS exchange for the three. LEAD: a barrier
+// first, for callers whose threads may still be reading `red` from an earlier scan (a
+// caller's first scan of the row needs none). M2 = false: m2 is unused (max2 gets 0).
+template <bool LEAD = true, bool M2 = true>
 __device__ __forceinline__ uint32_t block_scan_max2(uint32_t v, uint32_t m1, uint32_t m2, uint32_t* red,
                                                     uint32_t* total, uint32_t* max1, uint32_t* max2) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t x = wave_incl_sum(v);
   m1 = wave_incl_max(m1);   // lane 63: the wave's maximum
-  m2 = wave_incl_max(m2);
-  __syncthreads();
+  if constexpr (M2) m2 = wave_incl_max(m2);
+  if constexpr (LEAD) __syncthreads();
   if (lane == 63) {
     red[wave] = x;
     red[TPB / 64 + wave] = m1;
@@ -233,7 +245,7 @@ __device__ __forceinline__ uint32_t block_scan_max2(uint32_t v, uint32_t m1, uin
     off += (w < wave) ? red[w] : 0u;
     tot += red[w];
     a = max(a, red[TPB / 64 + w]);
-    b = max(b, red[2 * (TPB / 64) + w]);
+    if constexpr (M2) b = max(b, red[2 * (TPB / 64) + w]);
   }
   *total = tot;
   *max1 = a;
@@ -331,7 +343,7 @@ void li_topk_kernel(LiTopkArgs a) {
       top1 = h[j] ? (uint32_t)(2048 - 8 * t - j) : top1;
     }
     uint32_t tot, btop1, unused;
-    uint32_t cum = block_scan_max2(hs, top1, 0u, red, &tot, &btop1, &unused);
+    uint32_t cum = block_scan_max2<false, false>(hs, top1, 0u, red, &tot, &btop1, &unused);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       if (cum < (uint32_t)k && cum + h[j] >= (uint32_t)k) {
@@ -480,7 +492,7 @@ void li_topk_kernel(LiTopkArgs a) {
           if (i0 + e < L) sbuf[i0 + e] = (kh(w, e) << 16) | (0xFFFFu - (uint32_t)(i0 + e));
       }
       uint32_t tot, cmx, cmn;
-      block_scan_max2(0u, mx, mninv, red, &tot, &cmx, &cmn);
+      block_scan_max2<false>(0u, mx, mninv, red, &tot, &cmx, &cmn);
       umax = cmx;
       umin = 0xFFFFu - cmn;
       compacted = true;
@@ -550,16 +562,17 @@ void li_topk_kernel(LiTopkArgs a) {
   const int npass = urange == 0 ? 0 : (35 - __builtin_clz(urange)) / 4;
   const uint32_t vmax = (1u << (4 * npass)) - 1u;
   uint32_t key[E];
+  const int tb = rank_block(t);   // the thread's rank block in the sort and the output
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    const uint32_t x = sbuf[E * t + e];
+    const uint32_t x = sbuf[E * tb + e];
     key[e] = (min(umax - (x >> 16), vmax) << 16) | (x & 0xFFFFu);
   }
   radix_sort_asc16<E>(key, npass, nout, sbuf, cnt, red);
-  // ranks E t .. E t + E - 1 of thread t: their index (or -1) and 16-bit value (or 0).
+  // ranks E tb .. E tb + E - 1 of thread t: their index (or -1) and 16-bit value (or 0).
   // A run of 8 ranks inside the row's output, all below nout (the usual case): indices
   // 0xFFFF - x, values unord16(umax - v) computed on packed pairs.
-  if (!WIDE && E % 8 == 0 && k % 8 == 0 && E * t + E <= nout) {
+  if (!WIDE && E % 8 == 0 && k % 8 == 0 && E * tb + E <= nout) {
     const uint32_t um2x = (umax ^ 0x8000u) * 0x10001u;   // umax - 0x8000 in both halves
 #pragma unroll
     for (int e = 0; e < E; e += 8) {
@@ -574,13 +587,13 @@ void li_topk_kernel(LiTopkArgs a) {
         const uint32_t ad = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(d, (i16x2){0, 0} - d));
         pv[j] = ad | (__builtin_bit_cast(uint32_t, d) & 0x80008000u);
       }
-      *reinterpret_cast<int4*>(iout + E * t + e) =
+      *reinterpret_cast<int4*>(iout + E * tb + e) =
           make_int4((int)(~key[e] & 0xFFFFu), (int)(~key[e + 1] & 0xFFFFu), (int)(~key[e + 2] & 0xFFFFu),
                     (int)(~key[e + 3] & 0xFFFFu));
-      *reinterpret_cast<int4*>(iout + E * t + e + 4) =
+      *reinterpret_cast<int4*>(iout + E * tb + e + 4) =
           make_int4((int)(~key[e + 4] & 0xFFFFu), (int)(~key[e + 5] & 0xFFFFu), (int)(~key[e + 6] & 0xFFFFu),
                     (int)(~key[e + 7] & 0xFFFFu));
-      if (vout) *reinterpret_cast<uint4*>(vout + E * t + e) = make_uint4(pv[0], pv[1], pv[2], pv[3]);
+      if (vout) *reinterpret_cast<uint4*>(vout + E * tb + e) = make_uint4(pv[0], pv[1], pv[2], pv[3]);
     }
     return;
   }
@@ -588,27 +601,27 @@ void li_topk_kernel(LiTopkArgs a) {
   uint16_t ov[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    const bool ok = E * t + e < nout;
+    const bool ok = E * tb + e < nout;
     if constexpr (WIDE) oi[e] = ok ? sidx[key[e] & 0xFFFFu] : -1;
     else oi[e] = ok ? (int32_t)(0xFFFFu - (key[e] & 0xFFFFu)) : -1;
     ov[e] = ok ? unord16(umax - (key[e] >> 16)) : (uint16_t)0;
   }
   // 16-byte stores when the thread's whole run lies inside the row and rows are
   // 16-byte aligned (k % 8 == 0); the rest element by element
-  if (E % 8 == 0 && k % 8 == 0 && E * t + E <= k) {
+  if (E % 8 == 0 && k % 8 == 0 && E * tb + E <= k) {
 #pragma unroll
     for (int e = 0; e < E; e += 4)
-      *reinterpret_cast<int4*>(iout + E * t + e) = make_int4(oi[e], oi[e + 1], oi[e + 2], oi[e + 3]);
+      *reinterpret_cast<int4*>(iout + E * tb + e) = make_int4(oi[e], oi[e + 1], oi[e + 2], oi[e + 3]);
     if (vout)
 #pragma unroll
       for (int e = 0; e < E; e += 8)
-        *reinterpret_cast<uint4*>(vout + E * t + e) =
+        *reinterpret_cast<uint4*>(vout + E * tb + e) =
             make_uint4(ov[e] | ((uint32_t)ov[e + 1] << 16), ov[e + 2] | ((uint32_t)ov[e + 3] << 16),
                        ov[e + 4] | ((uint32_t)ov[e + 5] << 16), ov[e + 6] | ((uint32_t)ov[e + 7] << 16));
   } else {
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-      const int i = E * t + e;
+      const int i = E * tb + e;
       if (i < k) {
         iout[i] = oi[e];
         if (vout) vout[i] = ov[e];
