@@ -106,6 +106,9 @@ int dsa_li_score_paged(const void* query, const void* key_cache, const void* wei
  * min(L, sparse_count) are written to indices[(r*N2+n2)*sparse_count + i]
  * (int32) and, if `values` is not NULL, their 16-bit score to values[...];
  * the remaining slots get index -1 and value 0. Rows with s1 >= act_q are all -1 / 0.
+ * Scores compare as the floats their bit patterns encode, with +0 == -0 (a -0 is
+ * returned as +0); NaN patterns, which the golden's contract excludes, order by their
+ * bits: negative ones below -inf, positive ones above +inf.
  * Any S2 (int32 indices); sparse_count <= 16384 (DSA_ERR_UNSUPPORTED above: use
  * dsa_li_topk_ws).
  */
