@@ -399,3 +399,40 @@ def test_topk_crafted_score_rows(dev, S1, S2, K, family):
         ei, ev = LI.select_topk(s, S2, K)
         assert np.array_equal(gi[r], ei), (family, S2, r, L, np.flatnonzero(gi[r] != ei)[:8])
         assert np.array_equal(gv[r], ev), (family, S2, r, L)
+
+
+@pytest.mark.parametrize("S1,S2,K", [(4096, 4096, 2048), (16, 20000, 2048), (8, 70000, 2048)])
+def test_topk_order_of_nan_and_signed_zero_patterns(dev, S1, S2, K):
+    """Bit patterns outside the golden's contract (NaNs), next to +-0 and +-inf: the top-k
+    orders every 16-bit pattern as sign-magnitude (0x8000 + m / 0x8000 - m), so negative
+    NaNs fall below -inf (0xFFFF lowest of all) and positive ones above +inf, +0 ties -0
+    and a -0 comes back as +0. Expected order: a numpy stable sort on that key, rows with
+    L <= k and L > k, in the register-cached, chunked and 32-bit index paths."""
+    from dsa_triton_ascend_amd.lightning_indexer import IndexerPlan
+    rng = np.random.default_rng(5)
+    q = torch.zeros(1, S1, 8, 128, dtype=torch.bfloat16, device=dev)
+    k = torch.zeros(1, S2, 1, 128, dtype=torch.bfloat16, device=dev)
+    w = torch.zeros(1, S1, 8, dtype=torch.float32, device=dev)
+    plan = IndexerPlan(q, k, w, sparse_count=K, sparse_mode=3, return_value=True)
+    pool = np.array([0xFFFF, 0xFFC0, 0xFF81, 0x7FC0, 0x7F81, 0x7FFF, 0xFF80, 0x7F80, 0x0000, 0x8000],
+                    np.uint16)
+    normal = ((rng.standard_normal((S1, S2), dtype=np.float32)).view(np.uint32) >> 16).astype(np.uint16)
+    bits = np.where(rng.random((S1, S2)) < 0.3, pool[rng.integers(0, len(pool), (S1, S2))], normal)
+    plan.scores.zero_()
+    plan.scores[:S1, :S2] = torch.from_numpy(bits.view(np.int16)).to(dev)
+    plan.topk()
+    torch.cuda.synchronize()
+    gi = plan.idx.reshape(S1, K).cpu().numpy()
+    gv = plan.vals.reshape(S1, K).view(torch.int16).cpu().numpy().view(np.uint16)
+    m = bits.astype(np.int64) & 0x7FFF
+    key = np.where(bits & 0x8000, 0x8000 - m, 0x8000 + m)
+    rows = sorted({0, 1, 2047, 2048, 2049, 3000, S1 - 1} | set(range(0, S1, 257)))
+    for r in (r for r in rows if r < S1):
+        L = S2 - S1 + r + 1
+        order = np.lexsort((np.arange(L), -key[r, :L]))[:min(L, K)]
+        n = len(order)
+        assert np.array_equal(gi[r, :n], order), (S2, r, L, np.flatnonzero(gi[r, :n] != order)[:8])
+        assert np.all(gi[r, n:] == -1)
+        ev = np.where(bits[r, order] == 0x8000, 0, bits[r, order])
+        assert np.array_equal(gv[r, :n], ev), (S2, r, L)
+        assert np.all(gv[r, n:] == 0)
